@@ -1,0 +1,166 @@
+/*
+ * keep_amd -- C ABI of the MI355X (gfx950) routed E8P expert path.
+ *
+ * Every entry point takes caller-owned device pointers, explicit shapes and a
+ * hipStream_t (passed as void*), allocates no device memory, validates its
+ * arguments on the host before any launch and returns 0 or a negative
+ * KEEP_E* code; keep_last_error() then holds a message (thread-local).
+ *
+ * Dtype enums: KEEP_F32 = 0, KEEP_F16 = 1, KEEP_BF16 = 2.
+ * Index arrays are int32. Codes are uint16 (E8P, code_bits = 16) or uint8
+ * (E8 1-bit table, code_bits = 8). Codebooks are the packed uint32[256]
+ * nibble tables of the reference (src/keep/vq/e8.py:127-139, :169-179).
+ * A route index outside [0, num_experts) never faults: that route's output
+ * row is written as NaN.
+ */
+#ifndef KEEP_AMD_H
+#define KEEP_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { KEEP_F32 = 0, KEEP_F16 = 1, KEEP_BF16 = 2 };
+enum { KEEP_OK = 0, KEEP_EINVAL = -1, KEEP_ELAUNCH = -2, KEEP_EUNSUPPORTED = -3 };
+enum { KEEP_SCORE_SOFTMAX = 0, KEEP_SCORE_SIGMOID = 1, KEEP_SCORE_SQRTSOFTPLUS = 2 };
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* keep_last_error(void);
+/* ABI version (bumped on any signature change). */
+int keep_abi_version(void);
+
+/* Host-side: the E8P packed absolute table, uint32[256], built from its closed
+ * form. Replaces keep.vq.e8.e8p_packed_abs_grid (src/keep/vq/e8.py:127-139). */
+int keep_e8p_packed_abs_grid(uint32_t* out256);
+/* Host-side: the packed 8-bit E8 residual table, uint32[256].
+ * Replaces keep.vq.e8.e8_1bit_packed (src/keep/vq/e8.py:169-179). */
+int keep_e8_1bit_packed(uint32_t* out256);
+
+/* Decode n E8P codewords to float32 [n, 8], optionally times per-group scales
+ * (scales != NULL: codes viewed as rows of codewords_per_row codewords, one
+ * scale per group_codewords consecutive codewords). Bit-exact with
+ * keep.vq.e8.decode_e8p / decode_weight_matrix (src/keep/vq/e8.py:210-234,
+ * :542-571). */
+int keep_e8p_decode(const uint16_t* codes, int64_t n, const uint32_t* table,
+                    const void* scales, int scale_dtype, int64_t codewords_per_row,
+                    int64_t group_codewords, float* out, void* stream);
+
+/* Routed VQ mat-vec: out[r, :] = W[rhs[r]] . x[row(r), :] for r < routes,
+ * row(r) = lhs ? lhs[r] : r / x_div. W[e] is [N, K] given by codes [E, N, K/8]
+ * and scales [E, N, K/group_size]. fp32 accumulate.
+ * Optional nested residual (res_codes != NULL): 8-bit E8 codes [H, N, K/8],
+ * res_scales [H, N, K/res_group_size], res_table = half2 pairs uint32[256*4]
+ * (fp16 bits of dims 2k | 2k+1 << 16) and hot_of_slot[E] (row in the residual
+ * arrays or 0xFFFFFFFF); base and residual accumulate separately.
+ * Replaces ramp.kernels.e8p_m1.e8p_m1_token_layout / e8p_m1_per_route
+ * (src/ramp/kernels/e8p_m1.py:134-183), e8p_nested_m1_* (e8p_nested_m1.py:90-112),
+ * vq_qmv (vq_qmv.py:163-232, routes = 1), vq_qmm (vq_qmm.py:93-152) and the
+ * direct / per_route_decoded branches of gather_vqmm (src/ramp/ops/vq_switch.py:916-1221). */
+int keep_vq_matvec(const void* x, int x_dtype, int64_t x_rows,
+                   const void* codes, int code_bits, const void* scales, int scale_dtype,
+                   const uint32_t* table,
+                   const int32_t* rhs, const int32_t* lhs, int64_t routes, int64_t x_div,
+                   int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
+                   const uint8_t* res_codes, const void* res_scales, int64_t res_group_size,
+                   const uint32_t* res_table, const uint32_t* hot_of_slot, int64_t num_hot,
+                   void* out, int out_dtype, void* stream);
+
+/* Expert-grouped verify rows: each tile holds up to m_rows routes of one
+ * expert (tile_offset/tile_count index the sorted routes; tile_expert is
+ * the expert). Routes of a tile share every code load and decode. Output row
+ * sorted_route is written at out[sorted_route] (sorted order). Bit-identical
+ * per route with keep_vq_matvec (same lane accumulation order).
+ * Replaces gather_vqmm_verify_rows (src/ramp/ops/vq_switch.py:286-377) and
+ * its kernel gather_vqmm_verify_mrows (src/ramp/kernels/gather_vqmm.py:287-419). */
+int keep_vq_matvec_tiles(const void* x, int x_dtype, int64_t x_rows,
+                         const uint16_t* codes, const void* scales, int scale_dtype,
+                         const uint32_t* table, const int32_t* sorted_lhs, int64_t routes,
+                         const int32_t* tile_expert, const int32_t* tile_offset,
+                         const int32_t* tile_count, int64_t n_tiles, int64_t m_rows,
+                         int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
+                         void* out, int out_dtype, void* stream);
+
+/* Residency-biased dual top-k router, one evaluation per token:
+ * scores = score_func(logits[T, E]); served idx/w = top-k of scores + bias_served
+ * (an expert with bias_served <= -1e30 is absent: weight 0 if picked), weights
+ * renormalised (if renormalize) and times route_scale; demand want/want_score =
+ * top-k of scores + bias_demand with raw scores; admit[t, j] = want absent and
+ * its normalised demand weight >= tau. Ties: larger key, then lower index.
+ * bias_* may be NULL (zeros); want/want_score/admit may be NULL.
+ * Replaces MoEGate._expert_select (src/ramp/models/deepseek_v4_flash_adapter.py:923-940),
+ * gate_masked (scripts/runpod/v41_reap/local_eval.py:69-91) and the dual top-k
+ * kernel _TOPK (scripts/v41_build/omlx_lattice.py:77-97). */
+int keep_router_dual_topk(const float* logits, int64_t T, int64_t E, int64_t k,
+                          const float* bias_served, const float* bias_demand,
+                          int score_func, int renormalize, float route_scale, float tau,
+                          int32_t* idx, float* w, int32_t* want, float* want_score,
+                          uint8_t* admit, void* stream);
+
+/* Device route plan: stable sort of routes by expert, its inverse, per-expert
+ * counts/offsets and tile descriptors of at most `tile` routes (tiles in
+ * expert order; entries past the last real tile have count 0, offset 0).
+ * n_tiles_out[0] receives the real tile count. Buffers: order/inverse [R],
+ * counts/offsets [E], tile_* [max_tiles], max_tiles >= ceil(R/tile) + E.
+ * Replaces argsort + _inverse_permutation + _expert_block_tile_descriptors
+ * (src/ramp/ops/vq_switch.py:100-152) and _verify_row_tile_descriptors (:186-225). */
+int keep_route_plan(const int32_t* rhs, int64_t R, int64_t E, int64_t tile,
+                    int32_t* order, int32_t* inverse, int32_t* counts, int32_t* offsets,
+                    int32_t* tile_expert, int32_t* tile_offset, int32_t* tile_count,
+                    int64_t max_tiles, int32_t* n_tiles_out, void* stream);
+
+/* Prefill grouped GEMM over expert-sorted routes on MFMA: for every tile t and
+ * route i < tile_count[t]: out[tile_offset[t] + i, :] =
+ * W[tile_expert[t]] . x[lhs[tile_offset[t] + i], :] (lhs NULL: identity).
+ * E8P decoded into fp16/bf16 LDS tiles (exact), fp32 accumulate, scales applied
+ * per group in fp32. Tiles hold at most 64 routes.
+ * Replaces gather_vqmm_sorted_routes with the NAX E8P kernels
+ * (src/ramp/ops/vq_switch.py:620-913; native/vq_nax_ext/kernels/nax_fp16_matmul.metal:904-1062). */
+int keep_vq_grouped_gemm(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
+                         const uint16_t* codes, const void* scales, int scale_dtype,
+                         const uint32_t* table,
+                         const int32_t* tile_expert, const int32_t* tile_offset,
+                         const int32_t* tile_count, int64_t n_tiles, int64_t routes,
+                         int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
+                         void* out, int out_dtype, void* stream);
+
+/* Fused routed SwiGLU MoE for few tokens (decode / verify):
+ * h[t, j, :] = swiglu(Wg[e] x_t, Wu[e] x_t) (clamped by swiglu_limit if > 0),
+ * out[t, :] = sum_j w[t, j] * Wd[e] h[t, j, :], e = idx[t, j].
+ * Gate/up codes [E, I, H/8], down codes [E, H, I/8]; h_work is caller-provided
+ * [T * k * I] in x_dtype (fp16 or bf16). Two launches on `stream`.
+ * Replaces QuantizedVQSwitchGLU.__call__ (src/ramp/models/glm4_moe_adapter.py:367-372)
+ * plus the weighted combine of DeepseekV4FlashVQMoE.__call__
+ * (src/ramp/models/deepseek_v4_flash_adapter.py:1776-1784) and the decode step
+ * of scripts/v41_build/omlx_lattice.py:359-371. */
+int keep_moe_decode(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
+                    const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
+                    const uint16_t* gate_codes, const void* gate_scales,
+                    const uint16_t* up_codes, const void* up_scales,
+                    const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                    int64_t group_size_h, int64_t group_size_i, const uint32_t* table,
+                    float swiglu_limit, void* h_work, void* out, int out_dtype, void* stream);
+
+/* The two launches of keep_moe_decode as separate entry points (same kernels,
+ * same arguments): gate/up/SwiGLU into h_work, then down + weighted combine
+ * from h_work (h_dtype = the activation dtype h_work holds). A route with
+ * weight 0 is skipped by both. Replace the e8p_m1_token_layout gate/up pair
+ * and the e8p_m1_per_route down + fp32 sum of scripts/v41_build/omlx_lattice.py:366-371. */
+int keep_moe_gateup(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
+                    const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
+                    const uint16_t* gate_codes, const void* gate_scales,
+                    const uint16_t* up_codes, const void* up_scales, int scale_dtype,
+                    int64_t group_size_h, const uint32_t* table, float swiglu_limit,
+                    void* h_work, void* stream);
+int keep_moe_down(int h_dtype, int64_t T, int64_t H, int64_t I,
+                  const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
+                  const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                  int64_t group_size_i, const uint32_t* table, const void* h_work,
+                  void* out, int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KEEP_AMD_H */

@@ -1,0 +1,36 @@
+"""keep_amd -- MI355X (gfx950) routed E8P expert path.
+
+Python host code over torch device tensors calling hand-written HIP kernels
+through the C ABI of ``libkeep_amd.so`` (``include/keep_amd.h``). No CPU
+fallback: without the library every operator raises ``RuntimeError``.
+"""
+
+from keep_amd._lib import is_available
+from keep_amd.nn import LimitedSwiGLU, QuantizedVQSwitchGLU, QuantizedVQSwitchLinear, RoutedVQMoE, moe_decode
+from keep_amd.ops import (
+    decode_e8p,
+    decode_weight_matrix,
+    e8_1bit_packed,
+    e8p_m1_per_route,
+    e8p_m1_token_layout,
+    e8p_nested_m1_per_route,
+    e8p_nested_m1_token_layout,
+    e8p_packed_abs_grid,
+    gather_vqmm,
+    gather_vqmm_sorted_routes,
+    gather_vqmm_verify_rows,
+    half2_pairs,
+    route_plan,
+    trace_gather_vqmm_calls,
+    vq_qmm,
+    vq_qmv,
+)
+from keep_amd.router import expert_select, resident_bias, router_dual_topk
+
+__all__ = [
+    "LimitedSwiGLU", "QuantizedVQSwitchGLU", "QuantizedVQSwitchLinear", "RoutedVQMoE", "decode_e8p",
+    "decode_weight_matrix", "e8_1bit_packed", "e8p_m1_per_route", "e8p_m1_token_layout", "e8p_nested_m1_per_route",
+    "e8p_nested_m1_token_layout", "e8p_packed_abs_grid", "expert_select", "gather_vqmm", "gather_vqmm_sorted_routes",
+    "gather_vqmm_verify_rows", "half2_pairs", "is_available", "moe_decode", "resident_bias", "route_plan",
+    "router_dual_topk", "trace_gather_vqmm_calls", "vq_qmm", "vq_qmv",
+]

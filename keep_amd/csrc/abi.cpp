@@ -1,0 +1,148 @@
+// Host-side pieces of the C ABI: thread-local error text, launch status and the
+// closed-form codebook builders (no device code here).
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "../../include/keep_amd.h"
+
+namespace keep {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return KEEP_ELAUNCH;
+  }
+  return KEEP_OK;
+}
+
+// Pack eight half-unit values v (|v| <= 7) as nibbles v + 8, nibble d in bits 4d..4d+3.
+static uint32_t pack_row(const int* v) {
+  uint32_t p = 0;
+  for (int d = 0; d < 8; ++d) p |= (uint32_t)(v[d] + 8) << (4 * d);
+  return p;
+}
+
+// QuIP#'s 29 norm-12 padding rows in half units (five 3s and three 1s each),
+// the fixed completion of the E8P abs table to 256 entries.
+static const char* const kPadRows[29] = {
+    "31113333", "13113333", "11313333", "11133333", "33313311", "33313131", "33311331", "33313113",
+    "33311313", "33311133", "33133311", "33133131", "33131331", "33133113", "33131313", "33131133",
+    "31333311", "31333131", "31331331", "31333113", "31331313", "13331133", "13333311", "13333131",
+    "13331331", "13333113", "13331313", "11331333", "33113331"};
+
+static std::array<uint32_t, 256> build_e8p_table() {
+  std::vector<std::array<int, 8>> rows;
+  const int vals[4] = {1, 3, 5, 7};
+  // {1,3,5,7}^8 in lexicographic (itertools.product) order, sum of squares <= 40
+  for (int i = 0; i < 65536; ++i) {
+    std::array<int, 8> r;
+    int ss = 0;
+    for (int d = 0; d < 8; ++d) {
+      r[d] = vals[(i >> (2 * (7 - d))) & 3];
+      ss += r[d] * r[d];
+    }
+    if (ss <= 40) rows.push_back(r);
+  }
+  for (const char* s : kPadRows) {
+    std::array<int, 8> r;
+    for (int d = 0; d < 8; ++d) r[d] = s[d] - '0';
+    rows.push_back(r);
+  }
+  std::array<uint32_t, 256> out{};
+  if (rows.size() != 256) return out;  // caught by the caller's SHA test
+  const int order[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+  for (int i = 0; i < 256; ++i) {
+    int v[8], sum = 0;
+    for (int j = 0; j < 8; ++j) {
+      v[j] = rows[i][order[j]];
+      sum += v[j];
+    }
+    if (sum % 4 == 2) v[7] = -v[7];
+    out[i] = pack_row(v);
+  }
+  return out;
+}
+
+static std::array<uint32_t, 256> build_e8_1bit_table() {
+  std::vector<std::array<int, 8>> rows;
+  // integer rows: {-1,0,1}^8 (product order), sum of squares <= 2, even sum; x2 to half units
+  for (int i = 0; i < 6561; ++i) {
+    std::array<int, 8> r;
+    int t = i, ss = 0, sum = 0;
+    for (int d = 7; d >= 0; --d) {
+      r[d] = (t % 3) - 1;
+      t /= 3;
+    }
+    for (int d = 0; d < 8; ++d) {
+      ss += r[d] * r[d];
+      sum += r[d];
+    }
+    if (ss <= 2 && ((sum % 2) + 2) % 2 == 0) {
+      for (int d = 0; d < 8; ++d) r[d] *= 2;
+      rows.push_back(r);
+    }
+  }
+  // half rows: {-1,1}^8 with sum = 0 mod 4
+  for (int i = 0; i < 256; ++i) {
+    std::array<int, 8> r;
+    int sum = 0;
+    for (int d = 0; d < 8; ++d) {
+      r[d] = ((i >> (7 - d)) & 1) ? 1 : -1;
+      sum += r[d];
+    }
+    if (((sum % 4) + 4) % 4 == 0) rows.push_back(r);
+  }
+  // pads: +4 on axes 0..7, then -4 on axes 0..6
+  for (int s = 0; s < 2; ++s)
+    for (int d = 0; d < 8; ++d) {
+      if (s == 1 && d == 7) break;
+      std::array<int, 8> r{};
+      r[d] = s == 0 ? 4 : -4;
+      rows.push_back(r);
+    }
+  std::array<uint32_t, 256> out{};
+  if (rows.size() != 256) return out;
+  for (int i = 0; i < 256; ++i) out[i] = pack_row(rows[i].data());
+  return out;
+}
+
+}  // namespace keep
+
+extern "C" const char* keep_last_error(void) { return keep::g_err; }
+
+extern "C" int keep_abi_version(void) { return 1; }
+
+extern "C" int keep_e8p_packed_abs_grid(uint32_t* out256) {
+  if (!out256) {
+    keep::set_error("out256 is null");
+    return KEEP_EINVAL;
+  }
+  static const std::array<uint32_t, 256> t = keep::build_e8p_table();
+  std::memcpy(out256, t.data(), sizeof(uint32_t) * 256);
+  return KEEP_OK;
+}
+
+extern "C" int keep_e8_1bit_packed(uint32_t* out256) {
+  if (!out256) {
+    keep::set_error("out256 is null");
+    return KEEP_EINVAL;
+  }
+  static const std::array<uint32_t, 256> t = keep::build_e8_1bit_table();
+  std::memcpy(out256, t.data(), sizeof(uint32_t) * 256);
+  return KEEP_OK;
+}

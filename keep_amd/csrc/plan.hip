@@ -1,0 +1,121 @@
+// Device route plan: stable counting sort of routes by expert plus tile
+// descriptors, in one workgroup of 1024 threads (no host sync, no device
+// allocation). Routes with an expert outside [0, E) sort after every valid
+// route and belong to no tile.
+//
+// Stability: routes are taken in chunks of 1024 in route order. Inside a
+// chunk, a route's rank among same-expert routes is (routes of its expert in
+// earlier waves of the chunk, from per-wave histograms) + (earlier lanes of
+// its own wave with the same expert, by a 64-step shuffle scan).
+#include "common.h"
+
+namespace keep {
+
+constexpr int PLAN_THREADS = 1024;
+constexpr int PLAN_WAVES = PLAN_THREADS / 64;
+constexpr int PLAN_MAX_E = 1024;
+
+__global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs, int R, int E, int tile,
+                                                             int32_t* order, int32_t* inverse, int32_t* counts,
+                                                             int32_t* offsets, int32_t* te, int32_t* to, int32_t* tc,
+                                                             int max_tiles, int32_t* n_tiles_out) {
+  __shared__ int cnt[PLAN_MAX_E + 1];
+  __shared__ int run[PLAN_MAX_E + 1];
+  __shared__ int tbase[PLAN_MAX_E + 1];
+  __shared__ int wh[PLAN_WAVES][PLAN_MAX_E + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int EB = E + 1;  // bucket E collects invalid expert ids
+  for (int e = tid; e < EB; e += PLAN_THREADS) cnt[e] = 0;
+  __syncthreads();
+  for (int r = tid; r < R; r += PLAN_THREADS) {
+    int e = rhs[r];
+    if (e < 0 || e >= E) e = E;
+    atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0, tacc = 0;
+    for (int e = 0; e < EB; ++e) {
+      run[e] = acc;
+      acc += cnt[e];
+      tbase[e] = tacc;
+      if (e < E) tacc += (cnt[e] + tile - 1) / tile;
+    }
+    tbase[E] = tacc;
+    n_tiles_out[0] = tacc;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += PLAN_THREADS) {
+    counts[e] = cnt[e];
+    offsets[e] = run[e];
+    const int nt = (cnt[e] + tile - 1) / tile;
+    for (int i = 0; i < nt; ++i) {
+      const int ti = tbase[e] + i;
+      if (ti < max_tiles) {
+        te[ti] = e;
+        to[ti] = run[e] + i * tile;
+        tc[ti] = min(tile, cnt[e] - i * tile);
+      }
+    }
+  }
+  for (int ti = tbase[E] + tid; ti < max_tiles; ti += PLAN_THREADS) {
+    te[ti] = 0;
+    to[ti] = 0;
+    tc[ti] = 0;
+  }
+  for (int base = 0; base < R; base += PLAN_THREADS) {
+    for (int i = tid; i < PLAN_WAVES * EB; i += PLAN_THREADS) wh[i / EB][i % EB] = 0;
+    __syncthreads();
+    const int r = base + tid;
+    int e = -1;
+    if (r < R) {
+      e = rhs[r];
+      if (e < 0 || e >= E) e = E;
+    }
+    int rank = 0;
+    for (int l = 0; l < 64; ++l) {
+      const int el = __shfl(e, l, 64);
+      if (l < lane && el == e) ++rank;
+    }
+    if (e >= 0) atomicAdd(&wh[wv][e], 1);
+    __syncthreads();
+    for (int q = tid; q < EB; q += PLAN_THREADS) {
+      int acc = run[q];
+      for (int w = 0; w < PLAN_WAVES; ++w) {
+        const int c = wh[w][q];
+        wh[w][q] = acc;
+        acc += c;
+      }
+      run[q] = acc;
+    }
+    __syncthreads();
+    if (e >= 0) {
+      const int pos = wh[wv][e] + rank;
+      order[pos] = r;
+      inverse[r] = pos;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace keep
+
+using namespace keep;
+
+extern "C" int keep_route_plan(const int32_t* rhs, int64_t R, int64_t E, int64_t tile, int32_t* order,
+                               int32_t* inverse, int32_t* counts, int32_t* offsets, int32_t* tile_expert,
+                               int32_t* tile_offset, int32_t* tile_count, int64_t max_tiles, int32_t* n_tiles_out,
+                               void* stream) {
+  KEEP_REQUIRE(R >= 0 && R <= 0x7fffffffLL, "bad route count");
+  KEEP_REQUIRE(E >= 1 && E <= PLAN_MAX_E, "E must be in 1..%d", PLAN_MAX_E);
+  KEEP_REQUIRE(tile >= 1 && tile <= 4096, "tile must be in 1..4096");
+  KEEP_REQUIRE(max_tiles >= (R + tile - 1) / tile + E, "max_tiles must be >= ceil(R/tile) + E");
+  KEEP_REQUIRE(max_tiles <= 0x7fffffffLL, "max_tiles too large");
+  KEEP_REQUIRE((R == 0 || (rhs && order && inverse)) && counts && offsets && tile_expert && tile_offset &&
+                   tile_count && n_tiles_out,
+               "null pointer argument");
+  hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(PLAN_THREADS), 0, (hipStream_t)stream, rhs, (int)R, (int)E,
+                     (int)tile, order, inverse, counts, offsets, tile_expert, tile_offset, tile_count, (int)max_tiles,
+                     n_tiles_out);
+  return launch_status("keep_route_plan");
+}

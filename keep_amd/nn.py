@@ -1,0 +1,261 @@
+"""Module layer of the routed E8P expert path (torch, GPU).
+
+- ``QuantizedVQSwitchLinear`` -- stacked E8P/E8 expert projection, drop-in for
+  ``src/ramp/nn/switch_linear.py:93-463`` (core routing; the continuous
+  sidecars -- scale delta, low-rank and sparse-row residuals, rotation
+  matrices -- are outside this path and rejected with ``ValueError``).
+- ``QuantizedVQSwitchGLU`` -- gate/up/down with SwiGLU, drop-in for
+  ``src/ramp/models/glm4_moe_adapter.py:113-390``: few-token calls run the
+  decode mat-vec per projection, prefill runs one device route plan shared by
+  the three MFMA grouped GEMMs (``_shared_sorted_route_prefill``).
+- ``LimitedSwiGLU`` -- ``deepseek_v4_flash_adapter.py:962-986``.
+- ``RoutedVQMoE`` -- router + experts + weighted combine
+  (``DeepseekV4FlashVQMoE.__call__``, ``deepseek_v4_flash_adapter.py:1776-1784``),
+  whose decode path is the fused two-launch ``keep_moe_decode``.
+"""
+
+from __future__ import annotations
+
+from typing import Callable
+
+import torch
+
+from keep_amd import _lib, ops
+from keep_amd.router import router_dual_topk
+
+CODEWORD_DIM = 8
+
+
+class LimitedSwiGLU:
+    """``silu(min(g, L)) * clip(u, -L, L)``; plain SwiGLU for ``L <= 0``.
+    Called as ``act(up, gate)`` like the reference (``x`` first)."""
+
+    def __init__(self, limit: float = 0.0, *, fp32: bool = False):
+        self.limit = float(limit)
+        self.fp32 = bool(fp32)
+
+    def __call__(self, up: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        dtype = up.dtype
+        g = gate.float() if self.fp32 else gate
+        u = up.float() if self.fp32 else up
+        if self.limit > 0:
+            g = torch.clamp(g, max=self.limit)
+            u = torch.clamp(u, -self.limit, self.limit)
+        return (torch.nn.functional.silu(g) * u).to(dtype)
+
+
+class QuantizedVQSwitchLinear:
+    """Switch-linear layer backed by stacked VQ expert tensors (torch, GPU)."""
+
+    def __init__(self, *, input_dims: int, output_dims: int, num_experts: int, codes: torch.Tensor,
+                 scales: torch.Tensor, codebook: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+                 group_size: int = 512, code_bits: int = 8, use_gather_vqmm: bool = True,
+                 route_strategy: str = "auto", gather_codebook_duplication: int = 8,
+                 rht_signs: torch.Tensor | None = None, **sidecars):
+        if input_dims <= 0 or output_dims <= 0 or num_experts <= 0:
+            raise ValueError("input_dims, output_dims, and num_experts must be positive")
+        if input_dims % CODEWORD_DIM != 0:
+            raise ValueError("input_dims must be divisible by 8")
+        if input_dims % group_size != 0:
+            raise ValueError("input_dims must be divisible by group_size")
+        if code_bits not in (8, 16):
+            raise ValueError("code_bits must be 8 or 16")
+        if gather_codebook_duplication not in (1, 4, 8):
+            raise ValueError("gather_codebook_duplication must be 1, 4, or 8")
+        if route_strategy not in ("auto", "direct", "sorted_tiled", "per_route_decoded"):
+            raise ValueError("route_strategy must be 'auto', 'direct', 'sorted_tiled', or 'per_route_decoded'")
+        unsupported = [k for k, v in sidecars.items() if v is not None]
+        if unsupported:
+            raise ValueError(f"continuous sidecars are not part of the routed E8P path: {sorted(unsupported)}")
+        expected_codes = (num_experts, output_dims, input_dims // CODEWORD_DIM)
+        expected_scales = (num_experts, output_dims, input_dims // group_size)
+        if tuple(codes.shape) != expected_codes:
+            raise ValueError(f"codes must have shape {expected_codes}, found {tuple(codes.shape)}")
+        if tuple(scales.shape) != expected_scales:
+            raise ValueError(f"scales must have shape {expected_scales}, found {tuple(scales.shape)}")
+        if bias is not None and tuple(bias.shape) != (num_experts, output_dims):
+            raise ValueError(f"bias must have shape ({num_experts}, {output_dims}), found {tuple(bias.shape)}")
+        if rht_signs is not None and tuple(rht_signs.shape) != (input_dims,):
+            raise ValueError(f"rht_signs must have shape ({input_dims},), found {tuple(rht_signs.shape)}")
+        device = codes.device if isinstance(codes, torch.Tensor) and codes.is_cuda else ops._device_of(codes)
+        self.input_dims, self.output_dims, self.num_experts = input_dims, output_dims, num_experts
+        self.group_size, self.code_bits = group_size, code_bits
+        self.use_gather_vqmm, self.route_strategy = use_gather_vqmm, route_strategy
+        self.gather_codebook_duplication = gather_codebook_duplication
+        self.codes = ops._codes_tensor(codes, code_bits, device)
+        self.scales = ops._to_dev(scales, device)
+        self.codebook = ops._codebook_tensor(codebook, code_bits, device)
+        self.bias = None if bias is None else ops._to_dev(bias, device)
+        self.rht_signs = None if rht_signs is None else ops._to_dev(rht_signs, device, torch.float32)
+
+    def effective_scales(self) -> torch.Tensor:
+        return self.scales
+
+    def _rht(self, x: torch.Tensor) -> torch.Tensor:
+        if self.rht_signs is None:
+            return x
+        from keep_amd.rht import apply_rht
+        return apply_rht(x, self.rht_signs)
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor, *, sorted_indices: bool = False) -> torch.Tensor:
+        x = self._rht(x)
+        kw = dict(input_dims=self.input_dims, output_dims=self.output_dims, group_size=self.group_size,
+                  code_bits=self.code_bits, route_strategy=self.route_strategy, sorted_indices=sorted_indices,
+                  codebook_duplication=self.gather_codebook_duplication)
+        if x.ndim >= 2 and indices.ndim >= 2 and tuple(x.shape[:-1]) == tuple(indices.shape[:-1]):
+            lead, k = tuple(x.shape[:-1]), indices.shape[-1]
+            y = ops.gather_vqmm(x.reshape(-1, self.input_dims), self.codes, self.scales, self.codebook,
+                                indices.reshape(-1, k), **kw)
+            y = y.reshape(lead + (k, self.output_dims))
+        elif x.ndim >= 2 and tuple(x.shape[:-1]) == tuple(indices.shape):
+            shape = tuple(indices.shape)
+            flat_x = x.reshape(-1, self.input_dims)
+            lhs = torch.arange(flat_x.shape[0], dtype=torch.int32, device=flat_x.device)
+            y = ops.gather_vqmm(flat_x, self.codes, self.scales, self.codebook, indices.reshape(-1),
+                                lhs_indices=lhs, **kw).reshape(shape + (self.output_dims,))
+        else:
+            raise ValueError(f"x {tuple(x.shape)} and indices {tuple(indices.shape)} match neither the token nor "
+                             "the per-route layout")
+        if self.bias is not None:
+            y = y + self.bias[indices.long()].to(y.dtype)
+        return y
+
+
+class QuantizedVQSwitchGLU:
+    """Routed SwiGLU experts: ``down(act(up(x), gate(x)))`` per route -> ``[..., k, H]``."""
+
+    def __init__(self, *, gate_proj: QuantizedVQSwitchLinear, up_proj: QuantizedVQSwitchLinear,
+                 down_proj: QuantizedVQSwitchLinear, prefill_engine: str = "auto",
+                 activation: Callable | None = None):
+        if gate_proj.input_dims != up_proj.input_dims:
+            raise ValueError("gate_proj and up_proj input dimensions must match")
+        if gate_proj.output_dims != up_proj.output_dims:
+            raise ValueError("gate_proj and up_proj output dimensions must match")
+        if down_proj.input_dims != gate_proj.output_dims:
+            raise ValueError("down_proj input dimension must match routed hidden dimension")
+        if down_proj.output_dims != gate_proj.input_dims:
+            raise ValueError("down_proj output dimension must match routed input dimension")
+        if prefill_engine not in ("auto", "vq_metal", "nax_e8", "nax_e8p", "mfma"):
+            raise ValueError("prefill_engine must be 'auto' or 'mfma'")
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+        self.prefill_engine = prefill_engine
+        self.activation = activation
+        self.input_dims = gate_proj.input_dims
+        self.hidden_dims = gate_proj.output_dims
+        self.num_experts = gate_proj.num_experts
+
+    def _apply_activation(self, up: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        if self.activation is None:
+            return torch.nn.functional.silu(gate) * up
+        return self.activation(up, gate)
+
+    def _all_e8p(self) -> bool:
+        return all(p.code_bits == 16 and p.bias is None and p.rht_signs is None
+                   for p in (self.gate_proj, self.up_proj, self.down_proj))
+
+    def _can_use_shared_sorted_route_prefill(self, x: torch.Tensor, indices: torch.Tensor) -> bool:
+        routes = indices.numel()
+        return (self._all_e8p() and routes >= ops.GEMM_ROUTE_THRESHOLD
+                and all(ops.gemm_eligible(code_bits=16, x_dtype=x.dtype, input_dims=p.input_dims,
+                                          group_size=p.group_size)
+                        for p in (self.gate_proj, self.up_proj, self.down_proj)))
+
+    def _shared_sorted_route_prefill(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        lead, k = tuple(x.shape[:-1]), indices.shape[-1]
+        flat_x = x.reshape(-1, self.input_dims).contiguous()
+        flat_rhs = indices.reshape(-1).to(torch.int32).contiguous()
+        R = flat_rhs.numel()
+        flat_lhs = torch.arange(R, dtype=torch.int32, device=x.device) // k
+        order, inverse, _, _, te, to, tc, _ = ops.route_plan(flat_rhs, self.num_experts, ops.GEMM_ROUTE_TILE)
+        sorted_lhs = flat_lhs[order.long()].contiguous()
+        tiles = (te, to, tc)
+        g, u, d = self.gate_proj, self.up_proj, self.down_proj
+        gate = ops.grouped_gemm(flat_x, g.codes, g.scales, g.codebook, tiles, lhs=sorted_lhs, routes=R,
+                                input_dims=g.input_dims, output_dims=g.output_dims, group_size=g.group_size)
+        up = ops.grouped_gemm(flat_x, u.codes, u.scales, u.codebook, tiles, lhs=sorted_lhs, routes=R,
+                              input_dims=u.input_dims, output_dims=u.output_dims, group_size=u.group_size)
+        hidden = self._apply_activation(up, gate).contiguous()
+        y = ops.grouped_gemm(hidden, d.codes, d.scales, d.codebook, tiles, lhs=None, routes=R,
+                             input_dims=d.input_dims, output_dims=d.output_dims, group_size=d.group_size)
+        return y[inverse.long()].reshape(lead + (k, d.output_dims))
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        if self._can_use_shared_sorted_route_prefill(x, indices):
+            return self._shared_sorted_route_prefill(x, indices)
+        gate = self.gate_proj(x, indices)
+        up = self.up_proj(x, indices)
+        return self.down_proj(self._apply_activation(up, gate), indices)
+
+
+def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, up, down, *, limit: float = 0.0,
+               codebook: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+               h_work: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused routed SwiGLU MoE for few tokens (``keep_moe_decode``, two launches).
+
+    ``gate``/``up``/``down`` are ``(codes, scales)``: gate/up ``[E, I, H/8]``,
+    down ``[E, H, I/8]``. ``out[t] = sum_j w[t,j] * down_e(swiglu(gate_e x_t, up_e x_t))``
+    with fp32 accumulation; h is held in the activation dtype.
+    """
+
+    device = x.device
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("moe_decode needs float16 or bfloat16 activations")
+    (gc, gs), (uc, us), (dc, ds) = gate, up, down
+    E, I, Hc = gc.shape
+    H = Hc * 8
+    if x.ndim != 2 or x.shape[1] != H:
+        raise ValueError(f"x must be [tokens, {H}], found {tuple(x.shape)}")
+    if tuple(uc.shape) != (E, I, Hc) or tuple(dc.shape) != (E, H, I // 8):
+        raise ValueError("gate/up codes must be [E, I, H/8] and down codes [E, H, I/8]")
+    if not (gs.dtype == us.dtype == ds.dtype):
+        raise ValueError("gate/up/down scales must share a dtype")
+    T, k = idx.shape
+    cb = ops._codebook_tensor(codebook, 16, device)
+    od = out_dtype or ops.output_dtype(x.dtype)
+    out = torch.empty((T, H), dtype=od, device=device)
+    if h_work is None:
+        h_work = torch.empty((T * k * I,), dtype=x.dtype, device=device)
+    elif h_work.numel() < T * k * I or h_work.dtype != x.dtype:
+        raise ValueError("h_work must hold T*k*I elements of the activation dtype")
+    idx32 = idx.to(torch.int32).contiguous()
+    w32 = weight.to(torch.float32).contiguous()
+    _lib.call("keep_moe_decode", x.data_ptr(), ops._DT[x.dtype], T, H, I, idx32.data_ptr(), w32.data_ptr(), k, E,
+              gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
+              ops._DT[gs.dtype], H // gs.shape[-1], I // ds.shape[-1], cb.data_ptr(), float(limit),
+              h_work.data_ptr(), out.data_ptr(), ops._DT[od], ops._stream(device))
+    return out
+
+
+class RoutedVQMoE:
+    """Router + routed E8P SwiGLU experts + weighted combine (one MoE layer).
+
+    ``__call__(x, logits)`` evaluates the residency-biased dual top-k router
+    once, then runs the experts: the fused decode pair for few tokens, the
+    shared-plan MFMA path for prefill. Returns ``(out [T, H], RouterOutput)``.
+    """
+
+    def __init__(self, glu: QuantizedVQSwitchGLU, *, top_k: int, score_func: str = "softmax",
+                 renormalize: bool = True, route_scale: float = 1.0, swiglu_limit: float = 0.0,
+                 bias_served: torch.Tensor | None = None, bias_demand: torch.Tensor | None = None,
+                 tau: float = float("inf"), decode_max_tokens: int = 64):
+        self.glu, self.top_k, self.score_func = glu, top_k, score_func
+        self.renormalize, self.route_scale, self.limit = renormalize, route_scale, float(swiglu_limit)
+        self.bias_served, self.bias_demand, self.tau = bias_served, bias_demand, tau
+        self.decode_max_tokens = decode_max_tokens
+        if glu.activation is None and self.limit > 0:
+            glu.activation = LimitedSwiGLU(self.limit)
+
+    def experts(self, x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        g, u, d = self.glu.gate_proj, self.glu.up_proj, self.glu.down_proj
+        T = x.shape[0]
+        if T <= self.decode_max_tokens and self.glu._all_e8p() and x.dtype in (torch.float16, torch.bfloat16):
+            return moe_decode(x, idx, weight, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
+                              limit=self.limit, codebook=g.codebook)
+        y = self.glu(x, idx)  # [T, k, H]
+        return (y.float() * weight[..., None].float()).sum(-2).to(ops.output_dtype(x.dtype))
+
+    def __call__(self, x: torch.Tensor, logits: torch.Tensor):
+        r = router_dual_topk(logits, self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
+                             score_func=self.score_func, renormalize=self.renormalize, route_scale=self.route_scale,
+                             tau=self.tau)
+        return self.experts(x, r.idx, r.weight), r

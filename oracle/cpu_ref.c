@@ -1,0 +1,129 @@
+/*
+ * CPU restatement of the routed E8P expert path -- TEST INFRASTRUCTURE ONLY
+ * (the oracle's C form and the timed CPU baseline of bench.py; never linked
+ * into keep_amd).
+ *
+ * Decode follows the reference decoder src/keep/vq/e8.py:203-234 bit by bit
+ * (signs = c & 0xFF, idx = c >> 8, p = popcount(signs) & 1, eff = signs ^ p,
+ * dim d reads nibble {0,4,1,5,2,6,3,7}[d], negated by bit of eff, +-1/4 by p).
+ * The mat-vec decodes on the fly through a 65,536 x 8 float lookup table built
+ * from that decoder (2 MiB, cache resident; no dense weight matrix), with
+ * fp32 accumulation per scale group, OpenMP over (route, row). The MoE layer
+ * is router outputs -> gate/up -> SwiGLU -> down -> weighted fp32 combine
+ * (src/ramp/models/glm4_moe_adapter.py:367-372,
+ * src/ramp/models/deepseek_v4_flash_adapter.py:962-967,1776-1784).
+ *
+ * Pins: oracle_e8p_decode is compared with the numpy oracle over all 65,536
+ * codewords (tests/test_oracle_cpu.py), which is itself pinned by the
+ * reference's golden vectors; the mat-vec and MoE layer against the float64
+ * dense oracle.
+ */
+#include <math.h>
+#include <omp.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+static const int kShuffle[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+
+void oracle_e8p_decode(const uint16_t* codes, int64_t n, const uint32_t* table, float* out) {
+  for (int64_t i = 0; i < n; ++i) {
+    uint32_t c = codes[i];
+    uint32_t signs = c & 0xffu, idx = c >> 8;
+    uint32_t p = 0;
+    for (int b = 0; b < 8; ++b) p ^= (signs >> b) & 1u;
+    uint32_t eff = signs ^ p;
+    uint32_t word = table[idx];
+    for (int d = 0; d < 8; ++d) {
+      int s = kShuffle[d];
+      float v = (float)((int)((word >> (4 * s)) & 15u) - 8) * 0.5f;
+      if ((eff >> s) & 1u) v = -v;
+      out[i * 8 + d] = v + (p ? -0.25f : 0.25f);
+    }
+  }
+}
+
+/* 65,536 x 8 decoded-value table for one codebook, cached across calls. */
+static float* g_lut = NULL;
+static uint32_t g_lut_table[256];
+
+static const float* get_lut(const uint32_t* table) {
+  if (g_lut && memcmp(g_lut_table, table, sizeof g_lut_table) == 0) return g_lut;
+  if (!g_lut) g_lut = (float*)aligned_alloc(64, sizeof(float) * 65536 * 8);
+  uint16_t* all = (uint16_t*)malloc(sizeof(uint16_t) * 65536);
+  for (int i = 0; i < 65536; ++i) all[i] = (uint16_t)i;
+  oracle_e8p_decode(all, 65536, table, g_lut);
+  free(all);
+  memcpy(g_lut_table, table, sizeof g_lut_table);
+  return g_lut;
+}
+
+/* Dot of one code row (C codewords, G groups) with x (fp32). */
+static inline float row_dot(const uint16_t* crow, const float* srow, int64_t C, int64_t cpg, const float* x,
+                            const float* lut) {
+  float total = 0.f;
+  for (int64_t g0 = 0; g0 < C; g0 += cpg) {
+    float acc = 0.f;
+    for (int64_t c = g0; c < g0 + cpg; ++c) {
+      const float* w = lut + (size_t)crow[c] * 8;
+      const float* xv = x + c * 8;
+      acc += w[0] * xv[0] + w[1] * xv[1] + w[2] * xv[2] + w[3] * xv[3] + w[4] * xv[4] + w[5] * xv[5] +
+             w[6] * xv[6] + w[7] * xv[7];
+    }
+    total += acc * srow[g0 / cpg];
+  }
+  return total;
+}
+
+/* out[r, n] = W[rhs[r]][n, :] . x[lhs ? lhs[r] : r / x_div, :] */
+void oracle_routed_matvec(const float* x, const uint16_t* codes, const float* scales, const uint32_t* table,
+                          const int32_t* rhs, const int32_t* lhs, int64_t routes, int64_t x_div, int64_t N, int64_t K,
+                          int64_t group_size, float* out, int threads) {
+  const float* lut = get_lut(table);
+  const int64_t C = K / 8, G = K / group_size, cpg = group_size / 8;
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < routes * N; ++i) {
+    const int64_t r = i / N, n = i % N;
+    const int64_t e = rhs[r];
+    const int64_t xr = lhs ? lhs[r] : r / x_div;
+    out[i] = row_dot(codes + (e * N + n) * C, scales + (e * N + n) * G, C, cpg, x + xr * K, lut);
+  }
+}
+
+/* Routed SwiGLU MoE for T tokens; x [T, H] fp32, scales fp32, out [T, H]. */
+void oracle_moe_decode(const float* x, int64_t T, int64_t H, int64_t I, const int32_t* idx, const float* w,
+                       int64_t k, const uint16_t* gc, const float* gs, const uint16_t* uc, const float* us,
+                       const uint16_t* dc, const float* ds, int64_t group_h, int64_t group_i,
+                       const uint32_t* table, float limit, float* out, int threads) {
+  const float* lut = get_lut(table);
+  float* h = (float*)malloc(sizeof(float) * T * k * I);
+  const int64_t Ch = H / 8, Ci = I / 8, Gh = H / group_h, Gi = I / group_i;
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < T * k * I; ++i) {
+    const int64_t route = i / I, n = i % I, t = route / k;
+    const int64_t e = idx[route];
+    float g = row_dot(gc + (e * I + n) * Ch, gs + (e * I + n) * Gh, Ch, group_h / 8, x + t * H, lut);
+    float u = row_dot(uc + (e * I + n) * Ch, us + (e * I + n) * Gh, Ch, group_h / 8, x + t * H, lut);
+    if (limit > 0.f) {
+      g = fminf(g, limit);
+      u = fminf(fmaxf(u, -limit), limit);
+    }
+    h[i] = g / (1.f + expf(-g)) * u;
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < T * H; ++i) {
+    const int64_t t = i / H, n = i % H;
+    float acc = 0.f;
+    for (int64_t j = 0; j < k; ++j) {
+      const int64_t route = t * k + j;
+      const int64_t e = idx[route];
+      acc += w[route] * row_dot(dc + (e * H + n) * Ci, ds + (e * H + n) * Gi, Ci, group_i / 8, h + route * I, lut);
+    }
+    out[i] = acc;
+  }
+  free(h);
+}
+
+int oracle_max_threads(void) { return omp_get_max_threads(); }

@@ -1,0 +1,65 @@
+"""Random-sign Walsh-Hadamard transform -- CPU oracle (test infrastructure).
+
+Restated from the reference's ``src/keep/quant/rht.py:24-66``.
+
+Pins: the FWHT is checked against ``scipy.linalg.hadamard`` (Sylvester order)
+and by round-trip / norm preservation (``tests/test_glm45_air_rht.py:14-28``).
+``deterministic_rht_signs`` is pinned only by its closed form
+(``shake_256(str(seed))``, little-endian bit unpack, 0 -> -1): no golden sign
+vector exists in the reference, so its exact bit stream is "parity unpinned"
+beyond that closed form (the synthetic inputs use their own seeded signs, so
+no hot-path parity claim depends on it).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+
+import numpy as np
+
+
+def _check_pow2(n: int) -> None:
+    if n <= 0 or n & (n - 1):
+        raise ValueError("RHT dimension must be a positive power of two")
+
+
+def deterministic_rht_signs(dim: int, *, seed: int | str) -> np.ndarray:
+    """+-1 int8 signs from ``shake_256(str(seed))`` (``rht.py:24-31``)."""
+
+    _check_pow2(dim)
+    raw = hashlib.shake_256(str(seed).encode("utf-8")).digest((dim + 7) // 8)
+    bits = [(raw[i // 8] >> (i % 8)) & 1 for i in range(dim)]
+    return np.array([1 if b else -1 for b in bits], dtype=np.int8)
+
+
+def fwht(x: np.ndarray) -> np.ndarray:
+    """Orthonormal fast Walsh-Hadamard transform over the last axis, float64
+    (Sylvester order, ``rht.py:34-48``)."""
+
+    v = np.array(x, dtype=np.float64, copy=True)
+    n = v.shape[-1]
+    _check_pow2(n)
+    h = 1
+    while h < n:
+        v = v.reshape(v.shape[:-1] + (n // (2 * h), 2, h))
+        a = v[..., 0, :].copy()
+        b = v[..., 1, :].copy()
+        v[..., 0, :] = a + b
+        v[..., 1, :] = a - b
+        v = v.reshape(v.shape[:-3] + (n,))
+        h *= 2
+    return v / math.sqrt(n)
+
+
+def apply_rht(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """``FWHT(x * signs)`` over the last axis (``rht.py:51-57``), float64."""
+
+    s = np.asarray(signs, dtype=np.float64)
+    return fwht(np.asarray(x, dtype=np.float64) * s)
+
+
+def apply_inverse_rht(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """``FWHT(x) * signs`` (``rht.py:60-66``), float64."""
+
+    return fwht(x) * np.asarray(signs, dtype=np.float64)

@@ -1,0 +1,85 @@
+"""The C-ABI library loads and exports every entry point ``include/keep_amd.h``
+declares; host-only entry points and argument validation work without a GPU
+(every validation error returns before any launch)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from keep_amd import _lib
+from oracle import e8p
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "keep_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(keep_\w+)\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in keep_amd.h but not exported"
+    assert set(names) == set(_lib.EXPORTED)
+
+
+def test_abi_version_and_empty_error():
+    lib = _lib.load()
+    assert lib.keep_abi_version() == 1
+    assert isinstance(lib.keep_last_error(), bytes)
+
+
+def test_host_codebooks_match_oracle():
+    lib = _lib.load()
+    out = (ctypes.c_uint32 * 256)()
+    assert lib.keep_e8p_packed_abs_grid(out) == 0
+    np.testing.assert_array_equal(np.frombuffer(out, dtype=np.uint32), e8p.e8p_packed_abs_grid())
+    assert lib.keep_e8_1bit_packed(out) == 0
+    np.testing.assert_array_equal(np.frombuffer(out, dtype=np.uint32), e8p.e8_1bit_packed())
+    assert lib.keep_e8p_packed_abs_grid(None) == _lib.KEEP_EINVAL
+
+
+def _matvec(**over):
+    args = dict(x=16, x_dtype=1, x_rows=1, codes=16, code_bits=16, scales=16, scale_dtype=1, table=16, rhs=16, lhs=None,
+                routes=1, x_div=1, E=1, N=16, K=64, gs=64, rc=None, rs=None, rgs=0, rt=None, hot=None, nhot=0,
+                out=16, out_dtype=1, stream=None)
+    args.update(over)
+    return _lib.load().keep_vq_matvec(*args.values())
+
+
+@pytest.mark.parametrize("over, msg", [
+    (dict(code_bits=7), "code_bits"),
+    (dict(K=60), "divisible by 8"),
+    (dict(gs=24), "group_size"),
+    (dict(x_dtype=9), "dtype"),
+    (dict(x=None), "null"),
+    (dict(x=3), "aligned"),
+    (dict(rc=16, rs=None), "nested"),
+])
+def test_matvec_argument_validation_before_launch(over, msg):
+    assert _matvec(**over) == _lib.KEEP_EINVAL
+    assert msg in _lib.load().keep_last_error().decode()
+
+
+def test_zero_routes_is_a_no_op():
+    assert _matvec(routes=0, x=None) == 0
+
+
+def test_other_entry_points_validate():
+    lib = _lib.load()
+    assert lib.keep_router_dual_topk(1, 1, 2000, 6, None, None, 0, 1, 1.0, 0.3, 1, 1, None, None, None, None) == -1
+    assert b"E must be" in lib.keep_last_error()
+    assert lib.keep_route_plan(1, 10, 4, 4, 1, 1, 1, 1, 1, 1, 1, 2, 1, None) == -1
+    assert b"max_tiles" in lib.keep_last_error()
+    assert lib.keep_vq_grouped_gemm(16, 0, 1, None, 16, 16, 1, 16, 1, 1, 1, 1, 1, 1, 16, 256, 256, 16, 1, None) == -1
+    assert b"fp16 or bf16" in lib.keep_last_error()
+    assert lib.keep_moe_decode(16, 1, 1, 4096, 2048, 1, 1, 6, 384, 16, 16, 16, 16, 16, 16, 1, 100, 2048, 16, 0.0,
+                               16, 16, 1, None) == -1
+    assert b"group_size_h" in lib.keep_last_error()
+    assert lib.keep_e8p_decode(16, 10, 16, 16, 1, 3, 1, 16, None) == -1

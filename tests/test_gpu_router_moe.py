@@ -1,0 +1,203 @@
+"""GPU parity: dual top-k router (exact indices), device route plan (exact),
+MFMA grouped GEMM, verify rows and the fused MoE decode layer."""
+
+import numpy as np
+import pytest
+import torch
+
+import keep_amd
+from keep_amd import synth
+from oracle import cpu, e8p, ops
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _t(a, dev):
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    elif a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _check(got, want, tol=TOL):
+    g = got.float().cpu().numpy()
+    err = ops.max_rel_err(g, want)
+    assert err <= tol, f"max rel err {err:.3e}"
+    assert ops.elementwise_ok(g, want, rtol=tol), "elementwise bound violated"
+    return err
+
+
+@pytest.mark.parametrize("T,E,k,func", [(1, 384, 6, "softmax"), (64, 384, 6, "softmax"), (33, 288, 8, "sigmoid"),
+                                        (17, 256, 8, "sqrtsoftplus"), (5, 1024, 32, "softmax")])
+def test_router_indices_exact_unmasked(dev, T, E, k, func):
+    z = synth.router_logits(T, E, seed=T + E, device=dev)
+    r = keep_amd.router_dual_topk(z, k, score_func=func, route_scale=2.5)
+    idx, w, want, ws, admit = ops.router_dual_topk(z.cpu().numpy(), np.zeros(E), np.zeros(E), k, func=func,
+                                                   route_scale=2.5)
+    np.testing.assert_array_equal(r.idx.cpu().numpy(), idx)
+    np.testing.assert_array_equal(r.want.cpu().numpy(), want)
+    np.testing.assert_allclose(r.weight.cpu().numpy(), w, rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(r.want_score.cpu().numpy(), ws, rtol=2e-6, atol=1e-9)
+
+
+@pytest.mark.parametrize("T", [1, 512])
+def test_router_residency_config5(dev, T):
+    E, k, tau = 288, 8, 0.3
+    z = synth.router_logits(T, E, seed=7, device=dev)
+    mask = synth.resident_mask(E, frac=0.5, seed=8)
+    bias = keep_amd.resident_bias(torch.from_numpy(mask).to(dev))
+    r = keep_amd.router_dual_topk(z, k, bias_served=bias, tau=tau)
+    idx, w, want, ws, admit = ops.router_dual_topk(z.cpu().numpy(), bias.cpu().numpy(), np.zeros(E), k, tau=tau)
+    np.testing.assert_array_equal(r.idx.cpu().numpy(), idx)
+    np.testing.assert_array_equal(r.want.cpu().numpy(), want)
+    np.testing.assert_array_equal(r.admit.cpu().numpy().astype(bool), admit)
+    assert mask[r.idx.cpu().numpy()].all()  # served is always resident here (144 > k)
+    np.testing.assert_allclose(r.weight.cpu().numpy().sum(-1), 1.0, rtol=1e-5)
+
+
+def test_router_fewer_resident_than_k(dev):
+    E, k = 64, 6
+    z = synth.router_logits(9, E, seed=3, device=dev)
+    bias = torch.full((E,), float("-inf"), device=dev)
+    bias[[5, 40]] = 0.0
+    r = keep_amd.router_dual_topk(z, k, bias_served=bias)
+    idx, w, *_ = ops.router_dual_topk(z.cpu().numpy(), bias.cpu().numpy(), np.zeros(E), k)
+    np.testing.assert_array_equal(r.idx.cpu().numpy(), idx)
+    wg = r.weight.cpu().numpy()
+    assert ((wg > 0).sum(-1) == 2).all()
+    np.testing.assert_allclose(wg, w, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("R,E,tile", [(6, 384, 64), (384, 384, 4), (12288, 384, 64), (1000, 7, 16), (0, 5, 8)])
+def test_route_plan_exact(dev, R, E, tile):
+    rng = np.random.default_rng(R + E)
+    rhs = rng.integers(0, E, size=R).astype(np.int32)
+    order, inv, counts, offsets, te, to, tc, nt = keep_amd.route_plan(_t(rhs, dev), E, tile)
+    o_order, o_inv, o_counts, o_offsets, o_te, o_to, o_tc = ops.route_plan(rhs, E, tile)
+    np.testing.assert_array_equal(order.cpu().numpy(), o_order)
+    np.testing.assert_array_equal(inv.cpu().numpy(), o_inv)
+    np.testing.assert_array_equal(counts.cpu().numpy(), o_counts)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), o_offsets)
+    n = int(nt.item())
+    assert n == len(o_te)
+    np.testing.assert_array_equal(te.cpu().numpy()[:n], o_te)
+    np.testing.assert_array_equal(to.cpu().numpy()[:n], o_to)
+    np.testing.assert_array_equal(tc.cpu().numpy()[:n], o_tc)
+    assert (tc.cpu().numpy()[n:] == 0).all()
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("G", [1, 4])
+def test_grouped_gemm_sorted_routes(dev, xdt, G):
+    E, N, K, T, k = 12, 320, 512, 70, 4
+    codes, scales = synth.projection_np(E, N, K, group_size=K // G, seed=G)
+    rhs = synth.zipf_routes(T, E, k, seed=3)
+    x = synth.rht_activations(T, K, seed=4, device=dev, dtype=xdt)
+    with keep_amd.trace_gather_vqmm_calls() as tr:
+        y = keep_amd.gather_vqmm(x, _t(codes, dev), _t(scales, dev), None, _t(rhs, dev), input_dims=K,
+                                 output_dims=N, group_size=K // G, code_bits=16, route_strategy="sorted_tiled")
+    assert tr[0]["implementation"] == "mfma_grouped_gemm"
+    _check(y, ops.gather_token(x.float().cpu().numpy(), codes, scales, rhs))
+
+
+def test_sorted_routes_entry_with_presorted_x(dev):
+    E, N, K, R = 5, 256, 256, 150
+    codes, scales = synth.projection_np(E, N, K, seed=9)
+    rng = np.random.default_rng(10)
+    rhs = np.sort(rng.integers(0, E, size=R)).astype(np.int32)
+    x = torch.from_numpy(rng.standard_normal((R, K)).astype(np.float16)).to(dev)
+    lhs = np.arange(R, dtype=np.int32)
+    y = keep_amd.gather_vqmm_sorted_routes(x, _t(codes, dev), _t(scales, dev), None, _t(rhs, dev), _t(lhs, dev),
+                                           input_dims=K, output_dims=N, group_size=K, code_bits=16,
+                                           x_pre_sorted=True, validate_indices=True)
+    _check(y, ops.gather_routes(x.float().cpu().numpy(), codes, scales, rhs, lhs))
+
+
+@pytest.mark.parametrize("M", [8, 16, 64])
+def test_verify_rows_expert_grouping_bit_identical_to_flat(dev, M):
+    E, N, K, k = 384, 64, 4096, 6
+    codes = torch.randint(-32768, 32768, (E, N, K // 8), dtype=torch.int16, device=dev)
+    scales = torch.exp(torch.randn((E, N, 1), device=dev) * 0.3).half()
+    x = synth.rht_activations(M, K, seed=M, device=dev)
+    z = synth.router_logits(M, E, seed=M + 1, device=dev)
+    rhs = keep_amd.router_dual_topk(z, k).idx
+    flat = keep_amd.gather_vqmm_verify_rows(x, codes, scales, None, rhs, input_dims=K, output_dims=N,
+                                            group_size=K, grouping="flat")
+    grouped = keep_amd.gather_vqmm_verify_rows(x, codes, scales, None, rhs, input_dims=K, output_dims=N,
+                                               group_size=K, grouping="expert", m_rows=4)
+    assert torch.equal(flat, grouped)
+    r = rhs.cpu().numpy()
+    used = np.unique(r)
+    c_np = codes.cpu().numpy().view(np.uint16)
+    s_np = scales.cpu().numpy()
+    want = np.zeros((M, k, N))
+    for e in used:
+        W = ops.dense(c_np[e], s_np[e])
+        for t, j in zip(*np.nonzero(r == e)):
+            want[t, j] = W @ x[t].float().cpu().numpy()
+    _check(flat, want)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_moe_decode_small_vs_oracle(dev, xdt):
+    E, H, I, k, T = 16, 512, 256, 4, 3
+    gate = synth.projection_np(E, I, H, group_size=256, seed=1)
+    up = synth.projection_np(E, I, H, group_size=256, seed=2)
+    down = synth.projection_np(E, H, I, seed=3)
+    x = synth.rht_activations(T, H, seed=4, device=dev, dtype=xdt)
+    z = synth.router_logits(T, E, seed=5, device=dev)
+    r = keep_amd.router_dual_topk(z, k)
+    tt = lambda p: (_t(p[0], dev), _t(p[1], dev))  # noqa: E731
+    out = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=10.0)
+    hr = np.float16 if xdt == torch.float16 else None
+    want = ops.moe_layer(x.float().cpu().numpy(), r.idx.cpu().numpy(), r.weight.cpu().numpy(), gate, up, down,
+                         limit=10.0, h_round=hr)
+    _check(out, want)
+
+
+def test_moe_layer_config2_full_shape_vs_c_oracle(dev):
+    """Config 2 at its real shape: 384 experts, 4096/2048, top-6, batch 1."""
+    E, H, I, k = 384, 4096, 2048, 6
+    gate = synth.projection(E, I, H, seed=1, device=dev)
+    up = synth.projection(E, I, H, seed=2, device=dev)
+    down = synth.projection(E, H, I, seed=3, device=dev)
+    x = synth.rht_activations(1, H, seed=4, device=dev)
+    z = synth.router_logits(1, E, seed=5, device=dev)
+    r = keep_amd.router_dual_topk(z, k)
+    out = keep_amd.moe_decode(x, r.idx, r.weight, (gate.codes, gate.scales), (up.codes, up.scales),
+                              (down.codes, down.scales))
+    idx = r.idx.cpu().numpy()
+    used = np.unique(idx)
+    sub = {e: i for i, e in enumerate(used)}
+    pick = lambda p: (p.codes[torch.from_numpy(used).to(dev).long()].cpu().numpy().view(np.uint16),  # noqa: E731
+                      p.scales[torch.from_numpy(used).to(dev).long()].float().cpu().numpy())
+    g, u, d = pick(gate), pick(up), pick(down)
+    local = np.vectorize(sub.get)(idx).astype(np.int32)
+    want = cpu.moe_decode(x.float().cpu().numpy(), local, r.weight.cpu().numpy(), g, u, d, e8p.e8p_packed_abs_grid())
+    _check(out, want)
+    zi, zw, *_ = ops.router_dual_topk(z.cpu().numpy(), np.zeros(E), np.zeros(E), k)
+    np.testing.assert_array_equal(idx, zi)
+
+
+def test_routed_moe_module_prefill_matches_decode_path(dev):
+    E, H, I, k, T = 32, 512, 256, 6, 48  # 288 routes -> MFMA prefill path
+    gate = synth.projection_np(E, I, H, seed=11)
+    up = synth.projection_np(E, I, H, seed=12)
+    down = synth.projection_np(E, H, I, seed=13)
+    mk = lambda p, i, o: keep_amd.QuantizedVQSwitchLinear(input_dims=i, output_dims=o, num_experts=E,  # noqa: E731
+                                                          codes=_t(p[0], dev), scales=_t(p[1], dev), group_size=i,
+                                                          code_bits=16)
+    glu = keep_amd.QuantizedVQSwitchGLU(gate_proj=mk(gate, H, I), up_proj=mk(up, H, I), down_proj=mk(down, I, H),
+                                        activation=keep_amd.LimitedSwiGLU(10.0, fp32=True))
+    x = synth.rht_activations(T, H, seed=14, device=dev)
+    z = synth.router_logits(T, E, seed=15, device=dev)
+    moe = keep_amd.RoutedVQMoE(glu, top_k=k, swiglu_limit=10.0, decode_max_tokens=0)
+    out, r = moe(x, z)
+    want = ops.moe_layer(x.float().cpu().numpy(), r.idx.cpu().numpy(), r.weight.cpu().numpy(), gate, up, down,
+                         limit=10.0, h_round=np.float16)
+    _check(out, want)
+    moe_dec = keep_amd.RoutedVQMoE(glu, top_k=k, swiglu_limit=10.0, decode_max_tokens=64)
+    out2, _ = moe_dec(x, z)
+    _check(out2, want)
