@@ -62,7 +62,7 @@ def main() -> int:
 
     import keep_amd
     from keep_amd import _lib, synth
-    from keep_amd.ops import _default_codebook
+    from keep_amd.ops import _default_codebook, prepared_table
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -73,6 +73,7 @@ def main() -> int:
     up = synth.projection(E, I, H, seed=2, device=dev)
     down = synth.projection(E, H, I, seed=3, device=dev)
     table = _default_codebook(16, dev)
+    prep = prepared_table(table)
     x = synth.rht_activations(1, H, seed=4, device=dev)
     logits = synth.router_logits(N_SETS, E, seed=5, device=dev).reshape(N_SETS, 1, E).contiguous()
     idx = torch.empty((N_SETS, 1, K_TOP), dtype=torch.int32, device=dev)
@@ -80,9 +81,9 @@ def main() -> int:
     want = torch.empty_like(idx)
     want_s = torch.empty_like(w)
     admit = torch.empty((N_SETS, 1, K_TOP), dtype=torch.uint8, device=dev)
-    h = torch.empty((N_SETS, K_TOP * I), dtype=torch.float16, device=dev)
-    out = torch.empty((N_SETS, H), dtype=torch.float16, device=dev)
-    F16 = _lib.KEEP_F16
+    h = torch.empty((N_SETS, K_TOP * I), dtype=torch.bfloat16, device=dev)  # SwiGLU output held in bf16
+    out = torch.empty((N_SETS, H), dtype=torch.float32, device=dev)  # routed sum in fp32
+    F16, BF16, F32 = _lib.KEEP_F16, _lib.KEEP_BF16, _lib.KEEP_F32
 
     def router(i):
         _lib.check(lib.keep_router_dual_topk(logits[i].data_ptr(), 1, E, K_TOP, None, None, 0, 1, 1.0,
@@ -93,13 +94,14 @@ def main() -> int:
     def gateup(i):
         _lib.check(lib.keep_moe_gateup(x.data_ptr(), F16, 1, H, I, idx[i].data_ptr(), w[i].data_ptr(), K_TOP, E,
                                        gate.codes.data_ptr(), gate.scales.data_ptr(), up.codes.data_ptr(),
-                                       up.scales.data_ptr(), F16, H, table.data_ptr(), 0.0, h[i].data_ptr(),
-                                       stream.cuda_stream), "gateup")
+                                       up.scales.data_ptr(), F16, H, table.data_ptr(), prep.data_ptr(), 0.0,
+                                       h[i].data_ptr(), stream.cuda_stream), "gateup")
 
     def down_(i):
-        _lib.check(lib.keep_moe_down(F16, 1, H, I, idx[i].data_ptr(), w[i].data_ptr(), K_TOP, E,
+        _lib.check(lib.keep_moe_down(BF16, 1, H, I, idx[i].data_ptr(), w[i].data_ptr(), K_TOP, E,
                                      down.codes.data_ptr(), down.scales.data_ptr(), F16, I, table.data_ptr(),
-                                     h[i].data_ptr(), out[i].data_ptr(), F16, stream.cuda_stream), "down")
+                                     prep.data_ptr(), h[i].data_ptr(), out[i].data_ptr(), F32, stream.cuda_stream),
+                   "down")
 
     def layer(i):
         router(i)

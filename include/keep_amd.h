@@ -125,11 +125,25 @@ int keep_vq_grouped_gemm(const void* x, int x_dtype, int64_t x_rows, const int32
                          int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
                          void* out, int out_dtype, void* stream);
 
+/* Expanded E8P table for the fused MoE decode kernels: 2 x 128 KiB (fp16 then
+ * bf16), 16384 entries of four packed values each, addressed by
+ * (parity, abs index, 4 sign bits) so one decode is two lookups with the
+ * signs, parity and +-1/4 shift already applied (src/keep/vq/e8.py:203-234).
+ * `prepared` must hold keep_e8p_prepared_bytes() bytes. No reference
+ * counterpart: it replaces the per-threadgroup half2 pair decode of
+ * src/ramp/kernels/e8p_m1.metal:36-45 at a larger scale. */
+int keep_e8p_prepare(const uint32_t* table, void* prepared, void* stream);
+int keep_e8p_prepared_bytes(void);
+
 /* Fused routed SwiGLU MoE for few tokens (decode / verify):
  * h[t, j, :] = swiglu(Wg[e] x_t, Wu[e] x_t) (clamped by swiglu_limit if > 0),
  * out[t, :] = sum_j w[t, j] * Wd[e] h[t, j, :], e = idx[t, j].
  * Gate/up codes [E, I, H/8], down codes [E, H, I/8]; h_work is caller-provided
- * [T * k * I] in x_dtype (fp16 or bf16). Two launches on `stream`.
+ * [T * k * I] bf16 (SwiGLU in fp32, stored as bf16 as the reference's serving
+ * step stores it; fp16 would overflow). Two launches on `stream`. With
+ * `prepared` (keep_e8p_prepare of `table`) and a served shape the kernels
+ * decode through the expanded table (1024-thread blocks, one per CU);
+ * `prepared` = NULL uses the packed-table kernels.
  * Replaces QuantizedVQSwitchGLU.__call__ (src/ramp/models/glm4_moe_adapter.py:367-372)
  * plus the weighted combine of DeepseekV4FlashVQMoE.__call__
  * (src/ramp/models/deepseek_v4_flash_adapter.py:1776-1784) and the decode step
@@ -140,24 +154,25 @@ int keep_moe_decode(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
                     const uint16_t* up_codes, const void* up_scales,
                     const uint16_t* down_codes, const void* down_scales, int scale_dtype,
                     int64_t group_size_h, int64_t group_size_i, const uint32_t* table,
-                    float swiglu_limit, void* h_work, void* out, int out_dtype, void* stream);
+                    const void* prepared, float swiglu_limit, void* h_work, void* out,
+                    int out_dtype, void* stream);
 
 /* The two launches of keep_moe_decode as separate entry points (same kernels,
  * same arguments): gate/up/SwiGLU into h_work, then down + weighted combine
- * from h_work (h_dtype = the activation dtype h_work holds). A route with
+ * from h_work (h_dtype must be KEEP_BF16). A route with
  * weight 0 is skipped by both. Replace the e8p_m1_token_layout gate/up pair
  * and the e8p_m1_per_route down + fp32 sum of scripts/v41_build/omlx_lattice.py:366-371. */
 int keep_moe_gateup(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
                     const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
                     const uint16_t* gate_codes, const void* gate_scales,
                     const uint16_t* up_codes, const void* up_scales, int scale_dtype,
-                    int64_t group_size_h, const uint32_t* table, float swiglu_limit,
-                    void* h_work, void* stream);
+                    int64_t group_size_h, const uint32_t* table, const void* prepared,
+                    float swiglu_limit, void* h_work, void* stream);
 int keep_moe_down(int h_dtype, int64_t T, int64_t H, int64_t I,
                   const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
                   const uint16_t* down_codes, const void* down_scales, int scale_dtype,
-                  int64_t group_size_i, const uint32_t* table, const void* h_work,
-                  void* out, int out_dtype, void* stream);
+                  int64_t group_size_i, const uint32_t* table, const void* prepared,
+                  const void* h_work, void* out, int out_dtype, void* stream);
 
 #ifdef __cplusplus
 }

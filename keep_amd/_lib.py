@@ -36,11 +36,13 @@ _SIGS = {
     "keep_vq_grouped_gemm": [_P, c_int, c_int64, _P, _P, _P, c_int, _P, _P, _P, _P, c_int64, c_int64, c_int64,
                              c_int64, c_int64, c_int64, _P, c_int, _P],
     "keep_moe_decode": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
-                        c_int, c_int64, c_int64, _P, c_float, _P, _P, c_int, _P],
+                        c_int, c_int64, c_int64, _P, _P, c_float, _P, _P, c_int, _P],
     "keep_moe_gateup": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, c_int,
-                        c_int64, _P, c_float, _P, _P],
+                        c_int64, _P, _P, c_float, _P, _P],
     "keep_moe_down": [c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, c_int, c_int64, _P, _P, _P,
-                      c_int, _P],
+                      _P, c_int, _P],
+    "keep_e8p_prepare": [_P, _P, _P],
+    "keep_e8p_prepared_bytes": [],
 }
 _RESTYPE = {"keep_last_error": c_char_p}
 EXPORTED = tuple(_SIGS)

@@ -309,9 +309,10 @@ __device__ __forceinline__ float swiglu(float g, float u, float limit) {
   return g / (1.f + __expf(-g)) * u;
 }
 
-// Gate and up for MV_ROWS intermediate rows of one route, then SwiGLU; h is
-// stored in the activation dtype. A route with weight 0 is skipped (its h is
-// never read).
+// Gate and up for MV_ROWS intermediate rows of one route, then SwiGLU in
+// fp32; h is stored as bf16 (the SwiGLU product of unit-scale activations can
+// exceed the fp16 range; bf16 keeps fp32's exponent, as the reference's
+// serving step does). A route with weight 0 is skipped (its h is never read).
 template <typename XT, int CH>
 __global__ __launch_bounds__(256) void k_moe_gateup(MoeArgs a) {
   constexpr int PK = PairOf<XT>::value;
@@ -328,9 +329,9 @@ __global__ __launch_bounds__(256) void k_moe_gateup(MoeArgs a) {
   if (a.w[route] == 0.f) return;
   const int64_t t = route / a.k;
   const int64_t e = a.idx[route];
-  XT* hrow = (XT*)a.h + route * a.I;
+  bf16s* hrow = (bf16s*)a.h + route * a.I;
   if (e < 0 || e >= a.E) {
-    if (lane < MV_ROWS && row0 + lane < a.I) hrow[row0 + lane] = from_float<XT>(__builtin_nanf(""));
+    if (lane < MV_ROWS && row0 + lane < a.I) hrow[row0 + lane] = from_float<bf16s>(__builtin_nanf(""));
     return;
   }
   const int64_t C = a.H >> 3;
@@ -372,13 +373,15 @@ __global__ __launch_bounds__(256) void k_moe_gateup(MoeArgs a) {
     au[r] = wave_sum(au[r]);
   }
   if (lane < MV_ROWS && row0 + lane < a.I)
-    hrow[row0 + lane] = from_float<XT>(swiglu(select_row(ag, lane), select_row(au, lane), a.limit));
+    hrow[row0 + lane] = from_float<bf16s>(swiglu(select_row(ag, lane), select_row(au, lane), a.limit));
 }
 
 // Down projection of every route of one token for MV_ROWS output rows, with
 // the routing-weighted combine in fp32 (no atomics: one wave owns its rows).
-template <typename XT, int CH>
+// Reads the bf16 h of k_moe_gateup (bf16 codebook pairs, v_dot2_f32_bf16).
+template <int CH>
 __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
+  using XT = bf16s;
   constexpr int NW = (CH * 2 + 3) / 4;
   constexpr int PK = PairOf<XT>::value;
   __shared__ uint4 tab[256];
@@ -438,6 +441,12 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
 }
 
 // ------------------------------------------------------------------ host side
+
+bool moe_v2_supported(int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i);
+int moe_v2_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
+                  const int32_t* idx, const float* w, int64_t k, int64_t E, const uint16_t* gc, const void* gs,
+                  const uint16_t* uc, const void* us, const uint16_t* dc, const void* ds, int sdt, int64_t group_h,
+                  int64_t group_i, const void* prepared, float limit, void* h, void* out, int odt, hipStream_t s);
 
 // Codewords per lane chunk: must divide the codewords of a scale group (and of
 // the residual's group) so a chunk never straddles two scales; prefer the
@@ -598,10 +607,10 @@ static void launch_moe(int ch_h, int ch_i, bool gateup, bool down, hipStream_t s
   }
   if (down) {
     switch (ch_i) {
-      case 8: hipLaunchKernelGGL((k_moe_down<XT, 8>), g2, dim3(256), 0, s, a); break;
-      case 4: hipLaunchKernelGGL((k_moe_down<XT, 4>), g2, dim3(256), 0, s, a); break;
-      case 2: hipLaunchKernelGGL((k_moe_down<XT, 2>), g2, dim3(256), 0, s, a); break;
-      default: hipLaunchKernelGGL((k_moe_down<XT, 1>), g2, dim3(256), 0, s, a); break;
+      case 8: hipLaunchKernelGGL((k_moe_down<8>), g2, dim3(256), 0, s, a); break;
+      case 4: hipLaunchKernelGGL((k_moe_down<4>), g2, dim3(256), 0, s, a); break;
+      case 2: hipLaunchKernelGGL((k_moe_down<2>), g2, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL((k_moe_down<1>), g2, dim3(256), 0, s, a); break;
     }
   }
 }
@@ -610,9 +619,10 @@ static int moe_common(bool gateup, bool down, const char* what, const void* x, i
                       int64_t I, const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
                       const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
                       const void* up_scales, const uint16_t* down_codes, const void* down_scales, int scale_dtype,
-                      int64_t group_size_h, int64_t group_size_i, const uint32_t* table, float swiglu_limit,
-                      void* h_work, void* out, int out_dtype, void* stream) {
-  KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "fused MoE needs fp16 or bf16 activations");
+                      int64_t group_size_h, int64_t group_size_i, const uint32_t* table, const void* prepared,
+                      float swiglu_limit, void* h_work, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE(gateup ? (x_dtype == KEEP_F16 || x_dtype == KEEP_BF16) : x_dtype == KEEP_BF16,
+               gateup ? "fused MoE needs fp16 or bf16 activations" : "h_work must be bf16 (h_dtype = KEEP_BF16)");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(T >= 0 && k > 0 && num_experts > 0, "need T >= 0, k > 0, num_experts > 0");
   KEEP_REQUIRE(H > 0 && I > 0 && H % 8 == 0 && I % 8 == 0, "H and I must be positive multiples of 8");
@@ -628,6 +638,14 @@ static int moe_common(bool gateup, bool down, const char* what, const void* x, i
   KEEP_REQUIRE((!gateup || (aligned(gate_codes, ch_h * 2) && aligned(up_codes, ch_h * 2))) &&
                    (!down || aligned(down_codes, ch_i * 2)),
                "codes misaligned");
+  KEEP_REQUIRE(!prepared || aligned(prepared, 16), "prepared table must be 16-byte aligned");
+  if (prepared && moe_v2_supported(H, I, k, group_size_h, group_size_i)) {
+    KEEP_REQUIRE((int64_t)T * k * I <= 0x7fffffffLL * 16LL && T * ((H + 15) / 16) <= 0x7fffffffLL, "too many blocks");
+    moe_v2_launch(gateup, down, x, x_dtype, T, H, I, idx, w, k, num_experts, gate_codes, gate_scales, up_codes,
+                  up_scales, down_codes, down_scales, scale_dtype, group_size_h, group_size_i, prepared,
+                  swiglu_limit, h_work, out, out_dtype, (hipStream_t)stream);
+    return launch_status(what);
+  }
   MoeArgs a{};
   a.x = x; a.T = T; a.H = H; a.I = I; a.idx = idx; a.w = w; a.k = k; a.E = num_experts;
   a.gc = gate_codes; a.uc = up_codes; a.dc = down_codes; a.gs = gate_scales; a.us = up_scales; a.ds = down_scales;
@@ -646,28 +664,29 @@ extern "C" int keep_moe_decode(const void* x, int x_dtype, int64_t T, int64_t H,
                                const float* w, int64_t k, int64_t num_experts, const uint16_t* gate_codes,
                                const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
                                const uint16_t* down_codes, const void* down_scales, int scale_dtype,
-                               int64_t group_size_h, int64_t group_size_i, const uint32_t* table, float swiglu_limit,
-                               void* h_work, void* out, int out_dtype, void* stream) {
+                               int64_t group_size_h, int64_t group_size_i, const uint32_t* table,
+                               const void* prepared, float swiglu_limit, void* h_work, void* out, int out_dtype,
+                               void* stream) {
   return moe_common(true, true, "keep_moe_decode", x, x_dtype, T, H, I, idx, w, k, num_experts, gate_codes,
                     gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype, group_size_h,
-                    group_size_i, table, swiglu_limit, h_work, out, out_dtype, stream);
+                    group_size_i, table, prepared, swiglu_limit, h_work, out, out_dtype, stream);
 }
 
 extern "C" int keep_moe_gateup(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, const int32_t* idx,
                                const float* w, int64_t k, int64_t num_experts, const uint16_t* gate_codes,
                                const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
-                               int scale_dtype, int64_t group_size_h, const uint32_t* table, float swiglu_limit,
-                               void* h_work, void* stream) {
+                               int scale_dtype, int64_t group_size_h, const uint32_t* table, const void* prepared,
+                               float swiglu_limit, void* h_work, void* stream) {
   return moe_common(true, false, "keep_moe_gateup", x, x_dtype, T, H, I, idx, w, k, num_experts, gate_codes,
                     gate_scales, up_codes, up_scales, nullptr, nullptr, scale_dtype, group_size_h, I, table,
-                    swiglu_limit, h_work, nullptr, KEEP_F32, stream);
+                    prepared, swiglu_limit, h_work, nullptr, KEEP_F32, stream);
 }
 
 extern "C" int keep_moe_down(int h_dtype, int64_t T, int64_t H, int64_t I, const int32_t* idx, const float* w,
                              int64_t k, int64_t num_experts, const uint16_t* down_codes, const void* down_scales,
-                             int scale_dtype, int64_t group_size_i, const uint32_t* table, const void* h_work,
-                             void* out, int out_dtype, void* stream) {
+                             int scale_dtype, int64_t group_size_i, const uint32_t* table, const void* prepared,
+                             const void* h_work, void* out, int out_dtype, void* stream) {
   return moe_common(false, true, "keep_moe_down", nullptr, h_dtype, T, H, I, idx, w, k, num_experts, nullptr,
-                    nullptr, nullptr, nullptr, down_codes, down_scales, scale_dtype, H, group_size_i, table, 0.f,
-                    const_cast<void*>(h_work), out, out_dtype, stream);
+                    nullptr, nullptr, nullptr, down_codes, down_scales, scale_dtype, H, group_size_i, table,
+                    prepared, 0.f, const_cast<void*>(h_work), out, out_dtype, stream);
 }

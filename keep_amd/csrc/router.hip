@@ -41,10 +41,12 @@ __device__ __forceinline__ float score_of(float z, int func) {
   return sqrtf(fmaxf(z, 0.f) + log1pf(expf(-fabsf(z))));
 }
 
-// k rounds of selection over keys; returns the winners in order.
+// k rounds of selection over keys. The winners are wave-uniform; lane
+// `slot0 + j` keeps winner j in a register (no dynamically indexed arrays).
 template <int PER>
-__device__ __forceinline__ void select_topk(const float (&key)[PER], int E, int k, int lane, int* out_idx) {
+__device__ __forceinline__ int select_topk(const float (&key)[PER], int E, int k, int lane, int slot0) {
   uint32_t taken = 0u;
+  int mine = 0;
   for (int j = 0; j < k; ++j) {
     float bk = -__builtin_inff();
     int bi = 0x7fffffff;
@@ -61,9 +63,10 @@ __device__ __forceinline__ void select_topk(const float (&key)[PER], int E, int 
       }
     }
     const KeyIdx w = wave_argmax(bk, bi);
-    out_idx[j] = w.idx;
+    if (lane == slot0 + j) mine = w.idx;
     if ((w.idx & 63) == lane) taken |= 1u << (w.idx >> 6);
   }
+  return mine;
 }
 
 template <int PER>
@@ -101,27 +104,31 @@ __global__ __launch_bounds__(256) void k_router(const float* logits, int T, int 
   }
 
   float key[PER];
-  // Winners are wave-uniform: every lane ends up with both lists.
-  int served[32], demand[32];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int e = lane + 64 * i;
     key[i] = s[i] + (bias_s && e < E ? bias_s[e] : 0.f);
   }
-  select_topk<PER>(key, E, k, lane, served);
+  // lanes 0..k-1 receive the served winners, lanes 32..32+k-1 the demand winners
+  int e_sel = select_topk<PER>(key, E, k, lane, 0);
+  if (bias_d == bias_s) {
+    const int same = __shfl(e_sel, lane - 32 < 0 ? 0 : lane - 32, 64);
+    if (lane >= 32) e_sel = same;
+  } else {
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = s[i] + (bias_d && e < E ? bias_d[e] : 0.f);
+    for (int i = 0; i < PER; ++i) {
+      const int e = lane + 64 * i;
+      key[i] = s[i] + (bias_d && e < E ? bias_d[e] : 0.f);
+    }
+    const int d = select_topk<PER>(key, E, k, lane, 32);
+    if (lane >= 32) e_sel = d;
   }
-  select_topk<PER>(key, E, k, lane, demand);
 
   // Lanes j < k handle served slot j, lanes 32 + j handle demand slot j. Each
   // fetches its expert's score from the owner lane (e & 63), slot e >> 6.
   const bool is_served = lane < 32;
   const int j = is_served ? lane : lane - 32;
-  int e_sel = 0;
-  if (j < k) e_sel = is_served ? served[j] : demand[j];
+  if (j >= k) e_sel = 0;
   float mine = 0.f;
   {
     const int owner = e_sel & 63;

@@ -161,6 +161,8 @@ class QuantizedVQSwitchGLU:
                         for p in (self.gate_proj, self.up_proj, self.down_proj)))
 
     def _shared_sorted_route_prefill(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """One device route plan shared by the gate, up and down MFMA GEMMs
+        (``glm4_moe_adapter.py:274-353``); per-route outputs are float32."""
         lead, k = tuple(x.shape[:-1]), indices.shape[-1]
         flat_x = x.reshape(-1, self.input_dims).contiguous()
         flat_rhs = indices.reshape(-1).to(torch.int32).contiguous()
@@ -170,13 +172,18 @@ class QuantizedVQSwitchGLU:
         sorted_lhs = flat_lhs[order.long()].contiguous()
         tiles = (te, to, tc)
         g, u, d = self.gate_proj, self.up_proj, self.down_proj
+        f32 = torch.float32
         gate = ops.grouped_gemm(flat_x, g.codes, g.scales, g.codebook, tiles, lhs=sorted_lhs, routes=R,
-                                input_dims=g.input_dims, output_dims=g.output_dims, group_size=g.group_size)
+                                input_dims=g.input_dims, output_dims=g.output_dims, group_size=g.group_size,
+                                out_dtype=f32)
         up = ops.grouped_gemm(flat_x, u.codes, u.scales, u.codebook, tiles, lhs=sorted_lhs, routes=R,
-                              input_dims=u.input_dims, output_dims=u.output_dims, group_size=u.group_size)
-        hidden = self._apply_activation(up, gate).contiguous()
+                              input_dims=u.input_dims, output_dims=u.output_dims, group_size=u.group_size,
+                              out_dtype=f32)
+        # activation in fp32, hidden held in bf16 (fp16 would overflow the SwiGLU product)
+        hidden = self._apply_activation(up, gate).to(torch.bfloat16).contiguous()
         y = ops.grouped_gemm(hidden, d.codes, d.scales, d.codebook, tiles, lhs=None, routes=R,
-                             input_dims=d.input_dims, output_dims=d.output_dims, group_size=d.group_size)
+                             input_dims=d.input_dims, output_dims=d.output_dims, group_size=d.group_size,
+                             out_dtype=f32)
         return y[inverse.long()].reshape(lead + (k, d.output_dims))
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
@@ -189,12 +196,15 @@ class QuantizedVQSwitchGLU:
 
 def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, up, down, *, limit: float = 0.0,
                codebook: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-               h_work: torch.Tensor | None = None) -> torch.Tensor:
+               h_work: torch.Tensor | None = None, prepared: bool = True) -> torch.Tensor:
     """Fused routed SwiGLU MoE for few tokens (``keep_moe_decode``, two launches).
 
     ``gate``/``up``/``down`` are ``(codes, scales)``: gate/up ``[E, I, H/8]``,
     down ``[E, H, I/8]``. ``out[t] = sum_j w[t,j] * down_e(swiglu(gate_e x_t, up_e x_t))``
-    with fp32 accumulation; h is held in the activation dtype.
+    with fp32 accumulation; h is held in bf16 and the routed sum is returned in
+    float32 by default, as the reference's decode step keeps them
+    (``scripts/v41_build/omlx_lattice.py:368-371``). ``prepared`` selects the
+    expanded-table kernels (served shapes); ``False`` forces the packed-table ones.
     """
 
     device = x.device
@@ -211,18 +221,19 @@ def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, u
         raise ValueError("gate/up/down scales must share a dtype")
     T, k = idx.shape
     cb = ops._codebook_tensor(codebook, 16, device)
-    od = out_dtype or ops.output_dtype(x.dtype)
+    od = out_dtype or torch.float32
     out = torch.empty((T, H), dtype=od, device=device)
     if h_work is None:
-        h_work = torch.empty((T * k * I,), dtype=x.dtype, device=device)
-    elif h_work.numel() < T * k * I or h_work.dtype != x.dtype:
-        raise ValueError("h_work must hold T*k*I elements of the activation dtype")
+        h_work = torch.empty((T * k * I,), dtype=torch.bfloat16, device=device)
+    elif h_work.numel() < T * k * I or h_work.dtype != torch.bfloat16:
+        raise ValueError("h_work must hold T*k*I bfloat16 elements")
     idx32 = idx.to(torch.int32).contiguous()
     w32 = weight.to(torch.float32).contiguous()
+    prep = ops.prepared_table(cb) if prepared else None
     _lib.call("keep_moe_decode", x.data_ptr(), ops._DT[x.dtype], T, H, I, idx32.data_ptr(), w32.data_ptr(), k, E,
               gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
-              ops._DT[gs.dtype], H // gs.shape[-1], I // ds.shape[-1], cb.data_ptr(), float(limit),
-              h_work.data_ptr(), out.data_ptr(), ops._DT[od], ops._stream(device))
+              ops._DT[gs.dtype], H // gs.shape[-1], I // ds.shape[-1], cb.data_ptr(), ops._ptr(prep),
+              float(limit), h_work.data_ptr(), out.data_ptr(), ops._DT[od], ops._stream(device))
     return out
 
 
@@ -237,11 +248,12 @@ class RoutedVQMoE:
     def __init__(self, glu: QuantizedVQSwitchGLU, *, top_k: int, score_func: str = "softmax",
                  renormalize: bool = True, route_scale: float = 1.0, swiglu_limit: float = 0.0,
                  bias_served: torch.Tensor | None = None, bias_demand: torch.Tensor | None = None,
-                 tau: float = float("inf"), decode_max_tokens: int = 64):
+                 tau: float = float("inf"), decode_max_tokens: int = 64, out_dtype=torch.float32):
         self.glu, self.top_k, self.score_func = glu, top_k, score_func
         self.renormalize, self.route_scale, self.limit = renormalize, route_scale, float(swiglu_limit)
         self.bias_served, self.bias_demand, self.tau = bias_served, bias_demand, tau
         self.decode_max_tokens = decode_max_tokens
+        self.out_dtype = out_dtype
         if glu.activation is None and self.limit > 0:
             glu.activation = LimitedSwiGLU(self.limit)
 
@@ -250,9 +262,9 @@ class RoutedVQMoE:
         T = x.shape[0]
         if T <= self.decode_max_tokens and self.glu._all_e8p() and x.dtype in (torch.float16, torch.bfloat16):
             return moe_decode(x, idx, weight, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
-                              limit=self.limit, codebook=g.codebook)
+                              limit=self.limit, codebook=g.codebook, out_dtype=self.out_dtype)
         y = self.glu(x, idx)  # [T, k, H]
-        return (y.float() * weight[..., None].float()).sum(-2).to(ops.output_dtype(x.dtype))
+        return (y.float() * weight[..., None].float()).sum(-2).to(self.out_dtype)
 
     def __call__(self, x: torch.Tensor, logits: torch.Tensor):
         r = router_dual_topk(logits, self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,

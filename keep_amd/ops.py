@@ -97,6 +97,24 @@ def _default_codebook(code_bits: int, device: torch.device) -> torch.Tensor:
     return _DEVICE_TABLES[key]
 
 
+_PREPARED: dict[tuple[int, str], tuple[torch.Tensor, torch.Tensor]] = {}
+
+
+def prepared_table(codebook: torch.Tensor) -> torch.Tensor:
+    """Expanded E8P table of ``codebook`` for the fused MoE decode kernels
+    (``keep_e8p_prepare``: 2 x 128 KiB, fp16 then bf16), cached per codebook tensor."""
+
+    key = (codebook.data_ptr(), str(codebook.device))
+    hit = _PREPARED.get(key)
+    if hit is not None and hit[0] is codebook:
+        return hit[1]
+    nbytes = _lib.load().keep_e8p_prepared_bytes()
+    out = torch.empty(nbytes, dtype=torch.uint8, device=codebook.device)
+    _lib.call("keep_e8p_prepare", codebook.data_ptr(), out.data_ptr(), _stream(codebook.device))
+    _PREPARED[key] = (codebook, out)
+    return out
+
+
 def half2_pairs(grid: np.ndarray) -> np.ndarray:
     """``[256, 8]`` codebook exact in fp16 -> ``uint32[256, 4]`` (entry k = fp16
     bits of dim 2k | dim 2k+1 << 16), as ``e8p_nested_m1.half2_pairs``."""

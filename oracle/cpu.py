@@ -33,7 +33,7 @@ def load():
         lib.oracle_routed_matvec.restype = None
         lib.oracle_moe_decode.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                           c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
-                                          c_int64, c_void_p, c_float, c_void_p, c_int]
+                                          c_int64, c_void_p, c_float, c_int, c_void_p, c_int]
         lib.oracle_moe_decode.restype = None
         lib.oracle_max_threads.restype = c_int
         _lib = lib
@@ -70,7 +70,7 @@ def routed_matvec(x, codes, scales, table, rhs, lhs=None, *, x_div=1, group_size
     return out
 
 
-def moe_decode(x, idx, w, gate, up, down, table, *, limit=0.0, threads=0) -> np.ndarray:
+def moe_decode(x, idx, w, gate, up, down, table, *, limit=0.0, h_bf16=True, threads=0) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     idx = np.ascontiguousarray(idx, dtype=np.int32)
     w = np.ascontiguousarray(w, dtype=np.float32)
@@ -82,5 +82,6 @@ def moe_decode(x, idx, w, gate, up, down, table, *, limit=0.0, threads=0) -> np.
     I = gc.shape[1]
     out = np.empty((T, H), dtype=np.float32)
     load().oracle_moe_decode(_p(x), T, H, I, _p(idx), _p(w), k, _p(gc), _p(gs), _p(uc), _p(us), _p(dc), _p(ds),
-                             H // gs.shape[-1], I // ds.shape[-1], _p(t), float(limit), _p(out), int(threads))
+                             H // gs.shape[-1], I // ds.shape[-1], _p(t), float(limit), int(bool(h_bf16)), _p(out),
+                             int(threads))
     return out

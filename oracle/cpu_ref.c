@@ -91,11 +91,12 @@ void oracle_routed_matvec(const float* x, const uint16_t* codes, const float* sc
   }
 }
 
-/* Routed SwiGLU MoE for T tokens; x [T, H] fp32, scales fp32, out [T, H]. */
+/* Routed SwiGLU MoE for T tokens; x [T, H] fp32, scales fp32, out [T, H].
+ * h_bf16 != 0 rounds the SwiGLU output to bf16 before the down projection. */
 void oracle_moe_decode(const float* x, int64_t T, int64_t H, int64_t I, const int32_t* idx, const float* w,
                        int64_t k, const uint16_t* gc, const float* gs, const uint16_t* uc, const float* us,
                        const uint16_t* dc, const float* ds, int64_t group_h, int64_t group_i,
-                       const uint32_t* table, float limit, float* out, int threads) {
+                       const uint32_t* table, float limit, int h_bf16, float* out, int threads) {
   const float* lut = get_lut(table);
   float* h = (float*)malloc(sizeof(float) * T * k * I);
   const int64_t Ch = H / 8, Ci = I / 8, Gh = H / group_h, Gi = I / group_i;
@@ -110,7 +111,14 @@ void oracle_moe_decode(const float* x, int64_t T, int64_t H, int64_t I, const in
       g = fminf(g, limit);
       u = fminf(fmaxf(u, -limit), limit);
     }
-    h[i] = g / (1.f + expf(-g)) * u;
+    float hv = g / (1.f + expf(-g)) * u;
+    if (h_bf16) { /* round to bfloat16, nearest even (the reference stores h as bf16) */
+      uint32_t b;
+      memcpy(&b, &hv, 4);
+      if ((b & 0x7fffffffu) <= 0x7f800000u) b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+      memcpy(&hv, &b, 4);
+    }
+    h[i] = hv;
   }
 #pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < T * H; ++i) {

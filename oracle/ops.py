@@ -182,6 +182,16 @@ def swiglu(gate, up, limit: float = 0.0) -> np.ndarray:
     return g / (1.0 + np.exp(-g)) * u
 
 
+def round_bf16(a) -> np.ndarray:
+    """Round to bfloat16 (nearest even) and back to float64."""
+
+    f = np.asarray(a, dtype=np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    out = u.astype(np.uint32).view(np.float32).astype(np.float64)
+    return np.where(np.isnan(f), np.nan, out)
+
+
 def moe_layer(x, idx, w, gate, up, down, *, limit=0.0, h_round=None, hot_of_slot=None,
               residual=None) -> np.ndarray:
     """Routed MoE: ``out[t] = sum_j w[t,j] * down_e(swiglu(gate_e x_t, up_e x_t))``
@@ -189,8 +199,9 @@ def moe_layer(x, idx, w, gate, up, down, *, limit=0.0, h_round=None, hot_of_slot
     ``deepseek_v4_flash_adapter.py:1776-1784``).
 
     ``gate``/``up``/``down`` are ``(codes, scales)`` pairs. ``h_round`` (a numpy
-    dtype, e.g. float16) rounds the SwiGLU output as a kernel that stores it in
-    that dtype would. ``residual`` is an optional dict ``{"gate": (rc, rs), ...}``
+    dtype such as float16, or ``"bfloat16"``) rounds the SwiGLU output as a
+    kernel that stores it in that dtype would (the reference's decode step
+    stores it as bf16, ``scripts/v41_build/omlx_lattice.py:368``). ``residual`` is an optional dict ``{"gate": (rc, rs), ...}``
     of 8-bit residual tiers indexed through ``hot_of_slot``.
     """
 
@@ -217,7 +228,9 @@ def moe_layer(x, idx, w, gate, up, down, *, limit=0.0, h_round=None, hot_of_slot
                 g = g + res["gate"][hrow] @ x[t]
                 u = u + res["up"][hrow] @ x[t]
             h = swiglu(g, u, limit)
-            if h_round is not None:
+            if h_round == "bfloat16":
+                h = round_bf16(h)
+            elif h_round is not None:
                 h = h.astype(h_round).astype(np.float64)
             y = Wd[e] @ h
             if hrow != NO_RESIDUAL and "down" in res:

@@ -31,7 +31,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_empty_error():
     lib = _lib.load()
-    assert lib.keep_abi_version() == 1
+    assert lib.keep_abi_version() == 2
+    assert lib.keep_e8p_prepared_bytes() == 2 * 128 * 1024
     assert isinstance(lib.keep_last_error(), bytes)
 
 
@@ -79,7 +80,7 @@ def test_other_entry_points_validate():
     assert b"max_tiles" in lib.keep_last_error()
     assert lib.keep_vq_grouped_gemm(16, 0, 1, None, 16, 16, 1, 16, 1, 1, 1, 1, 1, 1, 16, 256, 256, 16, 1, None) == -1
     assert b"fp16 or bf16" in lib.keep_last_error()
-    assert lib.keep_moe_decode(16, 1, 1, 4096, 2048, 1, 1, 6, 384, 16, 16, 16, 16, 16, 16, 1, 100, 2048, 16, 0.0,
-                               16, 16, 1, None) == -1
+    assert lib.keep_moe_decode(16, 1, 1, 4096, 2048, 1, 1, 6, 384, 16, 16, 16, 16, 16, 16, 1, 100, 2048, 16, None,
+                               0.0, 16, 16, 1, None) == -1
     assert b"group_size_h" in lib.keep_last_error()
     assert lib.keep_e8p_decode(16, 10, 16, 16, 1, 3, 1, 16, None) == -1

@@ -11,6 +11,7 @@ from oracle import cpu, e8p, ops
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
+TOL_BF16_OUT = TOL + 2.0 ** -9  # a bf16-stored output adds at most 2**-9 relative rounding
 
 
 def _t(a, dev):
@@ -99,7 +100,16 @@ def test_grouped_gemm_sorted_routes(dev, xdt, G):
         y = keep_amd.gather_vqmm(x, _t(codes, dev), _t(scales, dev), None, _t(rhs, dev), input_dims=K,
                                  output_dims=N, group_size=K // G, code_bits=16, route_strategy="sorted_tiled")
     assert tr[0]["implementation"] == "mfma_grouped_gemm"
-    _check(y, ops.gather_token(x.float().cpu().numpy(), codes, scales, rhs))
+    want = ops.gather_token(x.float().cpu().numpy(), codes, scales, rhs)
+    _check(y, want, TOL_BF16_OUT if xdt == torch.bfloat16 else TOL)
+    # fp32 output of the same GEMM holds 2e-3
+    flat = _t(rhs.reshape(-1), dev)
+    order, inverse, _, _, te, to, tc, _ = keep_amd.route_plan(flat, E, 64)
+    lhs = (torch.arange(flat.numel(), device=dev, dtype=torch.int32) // k)[order.long()].contiguous()
+    y32 = keep_amd.ops.grouped_gemm(x, _t(codes, dev), _t(scales, dev), keep_amd.ops._default_codebook(16, dev),
+                                    (te, to, tc), lhs=lhs, routes=flat.numel(), input_dims=K, output_dims=N,
+                                    group_size=K // G, out_dtype=torch.float32)
+    _check(y32[inverse.long()].reshape(T, k, N), want)
 
 
 def test_sorted_routes_entry_with_presorted_x(dev):
@@ -151,9 +161,9 @@ def test_moe_decode_small_vs_oracle(dev, xdt):
     r = keep_amd.router_dual_topk(z, k)
     tt = lambda p: (_t(p[0], dev), _t(p[1], dev))  # noqa: E731
     out = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=10.0)
-    hr = np.float16 if xdt == torch.float16 else None
+    assert out.dtype == torch.float32
     want = ops.moe_layer(x.float().cpu().numpy(), r.idx.cpu().numpy(), r.weight.cpu().numpy(), gate, up, down,
-                         limit=10.0, h_round=hr)
+                         limit=10.0, h_round="bfloat16")
     _check(out, want)
 
 
@@ -196,8 +206,54 @@ def test_routed_moe_module_prefill_matches_decode_path(dev):
     moe = keep_amd.RoutedVQMoE(glu, top_k=k, swiglu_limit=10.0, decode_max_tokens=0)
     out, r = moe(x, z)
     want = ops.moe_layer(x.float().cpu().numpy(), r.idx.cpu().numpy(), r.weight.cpu().numpy(), gate, up, down,
-                         limit=10.0, h_round=np.float16)
+                         limit=10.0, h_round="bfloat16")
     _check(out, want)
     moe_dec = keep_amd.RoutedVQMoE(glu, top_k=k, swiglu_limit=10.0, decode_max_tokens=64)
     out2, _ = moe_dec(x, z)
     _check(out2, want)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("gh,gi", [(2048, 1024), (512, 256)])
+def test_moe_decode_expanded_table_path(dev, xdt, gh, gi):
+    """The expanded-table kernels (H=2048, I=1024) against the oracle and the packed-table kernels."""
+    E, H, I, k, T = 32, 2048, 1024, 4, 3
+    gate = synth.projection_np(E, I, H, group_size=gh, seed=21)
+    up = synth.projection_np(E, I, H, group_size=gh, seed=22)
+    down = synth.projection_np(E, H, I, group_size=gi, seed=23)
+    x = synth.rht_activations(T, H, seed=24, device=dev, dtype=xdt)
+    z = synth.router_logits(T, E, seed=25, device=dev)
+    r = keep_amd.router_dual_topk(z, k)
+    tt = lambda p: (_t(p[0], dev), _t(p[1], dev))  # noqa: E731
+    v2 = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=10.0)
+    v1 = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=10.0, prepared=False)
+    want = ops.moe_layer(x.float().cpu().numpy(), r.idx.cpu().numpy(), r.weight.cpu().numpy(), gate, up, down,
+                         limit=10.0, h_round="bfloat16")
+    _check(v2, want)
+    _check(v1, want)
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_decode_config5_shapes_with_absent_experts(dev, T):
+    """288 experts, top-8, 4096/1536, half the pool absent: weight-0 routes are skipped."""
+    E, H, I, k = 288, 4096, 1536, 8
+    gate = synth.projection(E, I, H, seed=31, device=dev)
+    up = synth.projection(E, I, H, seed=32, device=dev)
+    down = synth.projection(E, H, I, seed=33, device=dev)
+    x = synth.rht_activations(T, H, seed=34, device=dev)
+    z = synth.router_logits(T, E, seed=35, device=dev)
+    mask = torch.from_numpy(synth.resident_mask(E, frac=0.5, seed=36)).to(dev)
+    r = keep_amd.router_dual_topk(z, k, bias_served=keep_amd.resident_bias(mask), tau=0.3)
+    w = r.weight.clone()
+    w[:, -1] = 0.0  # one surplus slot with zero weight per token
+    out = keep_amd.moe_decode(x, r.idx, w, (gate.codes, gate.scales), (up.codes, up.scales),
+                              (down.codes, down.scales))
+    idx = r.idx.cpu().numpy()
+    used = np.unique(idx)
+    sub = {e: i for i, e in enumerate(used)}
+    sel = torch.from_numpy(used).to(dev).long()
+    pick = lambda p: (p.codes[sel].cpu().numpy().view(np.uint16), p.scales[sel].float().cpu().numpy())  # noqa: E731
+    local = np.vectorize(sub.get)(idx).astype(np.int32)
+    want = cpu.moe_decode(x.float().cpu().numpy(), local, w.cpu().numpy(), pick(gate), pick(up), pick(down),
+                          e8p.e8p_packed_abs_grid())
+    _check(out, want)

@@ -193,6 +193,9 @@ def test_c_oracle_matvec_and_moe_match_dense():
     want = ops.gather_token(x, gate[0], gate[1], rhs).reshape(6, I)
     assert ops.max_rel_err(y, want) < 1e-5
     w = rng.random((2, k)).astype(np.float32)
-    got = cpu.moe_decode(x, rhs, w, gate, up, down, t, limit=10.0)
+    got = cpu.moe_decode(x, rhs, w, gate, up, down, t, limit=10.0, h_bf16=False)
     want = ops.moe_layer(x, rhs, w, gate, up, down, limit=10.0)
+    assert ops.max_rel_err(got, want) < 1e-5
+    got = cpu.moe_decode(x, rhs, w, gate, up, down, t, limit=0.0, h_bf16=True)
+    want = ops.moe_layer(x, rhs, w, gate, up, down, limit=0.0, h_round="bfloat16")
     assert ops.max_rel_err(got, want) < 1e-5
