@@ -24,6 +24,7 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -39,6 +40,23 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+GATEUP_KERNEL = "k_moe3_gateup"  # the dominant kernel (2/3 of the layer's bytes)
+PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_layer_config2_counters.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary (None if absent)."""
+    try:
+        with open(PROFILE) as f:
+            for line in f:
+                m = re.match(r"traffic_bytes_per_launch\[(\w+)\] = (\d+)", line.strip())
+                if m and m.group(1) == kernel:
+                    return int(m.group(2))
+    except OSError:
+        return None
+    return None
+
+
 def projection_bytes(n: int, k: int, groups: int = 1) -> int:
     return n * (k // 8) * 2 + n * groups * 2
 
@@ -50,6 +68,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy kernel (torch.neg, fp16) 8 times, the known-size "
+                         "reference that scales FETCH_SIZE / WRITE_SIZE counter readings to bytes")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -108,6 +129,13 @@ def main() -> int:
         gateup(i)
         down_(i)
 
+    if args.copy_calibration:
+        a = torch.ones(128 << 20, dtype=torch.float16, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(8):
+            torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        del a, b
     torch.cuda.synchronize()
     # eager pass: routes for every set, sanity
     for i in range(N_SETS):
@@ -195,9 +223,12 @@ def main() -> int:
         "layer_bytes": layer_bytes,
         "layer_code_bytes": code_bytes,
         "kernels_us": {"router": round(rt_us, 3), "moe_gateup": round(gu_us, 3), "moe_down": round(dn_us, 3)},
-        "roofline": {"bound": "hbm", "kernel": "k_moe_gateup", "achieved": round(gu_gbps, 2),
+        "roofline": {"bound": "hbm", "kernel": GATEUP_KERNEL, "achieved": round(gu_gbps, 2),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
-                     "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_us, 3), "traffic": None},
+                     "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_us, 3),
+                     "traffic": measured_traffic(GATEUP_KERNEL),
+                     "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
+                                       "profiles/moe_layer_config2_counters.md"},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

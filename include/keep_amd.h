@@ -141,9 +141,12 @@ int keep_e8p_prepared_bytes(void);
  * Gate/up codes [E, I, H/8], down codes [E, H, I/8]; h_work is caller-provided
  * [T * k * I] bf16 (SwiGLU in fp32, stored as bf16 as the reference's serving
  * step stores it; fp16 would overflow). Two launches on `stream`. With
- * `prepared` (keep_e8p_prepare of `table`) and a served shape the kernels
- * decode through the expanded table (1024-thread blocks, one per CU);
- * `prepared` = NULL uses the packed-table kernels.
+ * `prepared` (keep_e8p_prepare of `table`) the kernels decode through the
+ * expanded table: one token (T = 1; H <= 4096 and a multiple of 256, I a
+ * multiple of 512 up to 2048, k <= 8, scale groups of 256-element multiples)
+ * on the matrix cores, other served shapes with 1024-thread blocks;
+ * `prepared` = NULL uses the packed-table kernels. h_work holds h in natural
+ * [T, k, I] order whichever kernels ran.
  * Replaces QuantizedVQSwitchGLU.__call__ (src/ramp/models/glm4_moe_adapter.py:367-372)
  * plus the weighted combine of DeepseekV4FlashVQMoE.__call__
  * (src/ramp/models/deepseek_v4_flash_adapter.py:1776-1784) and the decode step

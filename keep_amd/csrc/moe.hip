@@ -134,7 +134,7 @@ struct MoeV2Args {
   const uint4* xt_x;  // expanded table in the activation pair kind
   const uint4* xt_h;  // expanded table in bf16 (for h)
   float limit;
-  uint16_t* h;  // [T, k, I] bf16, each group of 8 in table order (x0,x2,x4,x6,x1,x3,x5,x7)
+  uint16_t* h;  // [T, k, I] bf16, natural order (the layout every MoE path shares)
   void* out;
   int odt;
   int32_t units, rows_per_token;
@@ -197,8 +197,6 @@ __device__ __forceinline__ void load_cw(const uint16_t* p, uint32_t* w) {
   }
 }
 
-// Table-order position of dim d inside a group of 8.
-__device__ __forceinline__ uint32_t table_pos(uint32_t d) { return (d & 1) ? 4 + (d >> 1) : (d >> 1); }
 
 // ------------------------------------------------------------------ gate/up/SwiGLU
 
@@ -324,7 +322,7 @@ __global__ __launch_bounds__(NWAV * 64) void k_moe_gateup_v2(MoeV2Args a) {
     const float u = wave_total(au[r]);
     if (lane == r && rok[r]) {
       const uint32_t rf = rf0 + r;
-      a.h[(rf & ~7u) + table_pos(rf & 7u)] = from_float<bf16s>(silu_mul(g, u, a.limit)).bits;
+      a.h[rf] = from_float<bf16s>(silu_mul(g, u, a.limit)).bits;
     }
   }
 }
@@ -421,8 +419,7 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down_v2(MoeV2Args a) {
       uint32_t xp[CH][4];
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
-        const uint4 q = hsh[j * C + cw0 + i];
-        xp[i][0] = q.x; xp[i][1] = q.y; xp[i][2] = q.z; xp[i][3] = q.w;
+        permute_x(hsh[j * C + cw0 + i], xp[i]);
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -453,6 +450,272 @@ __global__ __launch_bounds__(MOE_THREADS) void k_moe_down_v2(MoeV2Args a) {
       else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;
       else ((float*)a.out)[oi] = o;
     }
+  }
+}
+
+// ------------------------------------------------------------------ v3: matrix-core layer (one token)
+//
+// Rows go through v_mfma_f32_16x16x32_{f16,bf16} in tiles of 16. Lane l
+// decodes one codeword of tile row l % 16 at codeword slot l / 16 (its H and
+// L table entries are exactly the eight operand values of that slot) into
+// the B operand; A holds the activation chunk of the same slot, permuted to
+// the table's pair order. Gate/up: every A row is the token. Down: A row i is
+// route i's SwiGLU output, so one A fragment serves all routes of a block and
+// row i of tile i's result is the useful one. Waves split K (256 elements per
+// wave) and meet in one small LDS reduction; each wave issues all of its code
+// loads before it touches LDS, so the whole code stream of the block is in
+// flight while the table is staged.
+
+typedef _Float16 m3h8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 m3b8_t __attribute__((ext_vector_type(8)));
+typedef float m3f4_t __attribute__((ext_vector_type(4)));
+
+constexpr int M3_MAXW = 16;          // waves per block (K-slices of 256)
+constexpr int M3_HCHUNKS = 1544;     // down: k * (I / 8 + 1) h chunks staged in LDS
+
+template <int PK>
+__device__ __forceinline__ m3f4_t mfma16(uint4 a, uint4 b, m3f4_t c) {
+  if constexpr (PK == PAIR_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(m3h8_t, a), __builtin_bit_cast(m3h8_t, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(m3b8_t, a), __builtin_bit_cast(m3b8_t, b), c,
+                                                   0, 0, 0);
+}
+
+// Codeword in bits [LO, LO + 16) of w -> the B operand: L entry (dims 0,2,4,6)
+// then H entry (dims 1,3,5,7), matching permute_x's activation order.
+template <int LO>
+__device__ __forceinline__ uint4 xt_decode(const char* tab, uint32_t w) {
+  uint32_t ah, al;
+  xt_addr<LO>(w, ah, al);
+  const uint2 eh = *(const uint2*)(tab + ah);
+  const uint2 el = *(const uint2*)(tab + al + 0x8000);
+  return make_uint4(el.x, el.y, eh.x, eh.y);
+}
+
+__device__ __forceinline__ uint32_t dword_of(const uint4& q, int i) {
+  return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+}
+
+__device__ __forceinline__ uint4 permuted(const uint4 q) {
+  uint32_t xp[4];
+  permute_x(q, xp);
+  return make_uint4(xp[0], xp[1], xp[2], xp[3]);
+}
+
+struct M3Args {
+  const void* x;  // [H] fp16 / bf16 (one token)
+  int32_t H, I, k, E;
+  const int32_t* idx;
+  const float* w;
+  const uint16_t *gc, *uc, *dc;
+  const void *gs, *us, *ds;
+  int sdt;
+  int32_t Gh, gsz_h, Gi, gsz_i;  // scale groups per row and elements per group
+  const uint4* xt;               // expanded table, activation pair kind (gate/up) or bf16 (down)
+  float limit;
+  uint16_t* h;  // [k, I] bf16, natural order
+  void* out;
+  int odt;
+  int32_t qtiles;  // gate/up: k * I / 16
+};
+
+// Block: QT = NT / 2 q-tiles (16 consecutive rows of the flattened [k, I]
+// intermediate space), as NT tiles (gate, up, gate, up, ...). H / 256 waves.
+template <int PK, int NT>
+__global__ __launch_bounds__(1024) void k_moe3_gateup(M3Args a) {
+  __shared__ uint4 tab4[XT_BYTES / 16];
+  __shared__ uint4 xsh[512];  // the token, natural order (H <= 4096)
+  __shared__ float red[M3_MAXW][NT][16];
+  constexpr int QT = NT / 2;
+  const char* tab = (const char*)tab4;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const uint32_t j = lane & 15, g = lane >> 4;
+  const uint32_t C = (uint32_t)a.H >> 3;
+
+  // 0. tiles (scalar)
+  uint32_t rbase[QT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const uint32_t qt = blockIdx.x * QT + u;
+    const bool valid = qt < (uint32_t)a.qtiles;
+    const uint32_t q0 = (valid ? qt : 0u) * 16u;
+    const uint32_t route = q0 / (uint32_t)a.I;
+    const uint32_t i0 = q0 - route * (uint32_t)a.I;
+    const int32_t e = a.idx[route];
+    const bool ok = valid && e >= 0 && e < a.E;
+    rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + i0;
+  }
+
+  // 1. LDS DMA: table and the token
+  for (int i = wv * 64; i < XT_BYTES / 16; i += nw * 64) dma16(a.xt + i + lane, tab4 + i);
+  if (wv * 64 < (int)C) dma16((const uint4*)a.x + min(wv * 64 + lane, (int)C - 1), xsh + wv * 64);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. codes: 8 codewords (16 B) per lane per tile, exactly NT loads
+  const uint32_t kc0 = wv * 32 + g * 8;
+  uint4 q[NT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const size_t off = (size_t)(rbase[u] + j) * C + kc0;
+    q[2 * u] = *(const uint4*)(a.gc + off);
+    q[2 * u + 1] = *(const uint4*)(a.uc + off);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm<NT>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  // scales of this wave's group (consumed after the decode)
+  const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
+  ScaleRaw sr[NT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
+    sr[2 * u] = scale_raw(a.gs, a.sdt, si);
+    sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
+  }
+
+  // 3. decode into B, token chunk in A
+  m3f4_t acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = m3f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const uint4 A = permuted(xsh[kc0 + m]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const uint32_t wd = dword_of(q[t], m >> 1);
+      const uint4 B = (m & 1) ? xt_decode<16>(tab, wd) : xt_decode<0>(tab, wd);
+      acc[t] = mfma16<PK>(A, B, acc[t]);
+    }
+  }
+
+  // 4. scaled per-wave partials (every A row holds the token: D row 0 is the dot)
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
+    if (lane < 16) {
+      red[wv][2 * u][j] = acc[2 * u][0] * scale_cvt(sr[2 * u], a.sdt, si);
+      red[wv][2 * u + 1][j] = acc[2 * u + 1][0] * scale_cvt(sr[2 * u + 1], a.sdt, si);
+    }
+  }
+  __syncthreads();
+
+  // 5. wave sum, SwiGLU, h (bf16, natural order)
+  if (threadIdx.x < QT * 16) {
+    const uint32_t u = threadIdx.x >> 4, jj = threadIdx.x & 15;
+    const uint32_t qt = blockIdx.x * QT + u;
+    float gsum = 0.f, usum = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      gsum += red[w][2 * u][jj];
+      usum += red[w][2 * u + 1][jj];
+    }
+    if (qt < (uint32_t)a.qtiles) {
+      const uint32_t q0 = qt * 16u;
+      const uint32_t route = q0 / (uint32_t)a.I;
+      const int32_t e = a.idx[route];
+      if (e >= 0 && e < a.E) a.h[q0 + jj] = from_float<bf16s>(silu_mul(gsum, usum, a.limit)).bits;
+    }
+  }
+}
+
+// Block: 16 output rows (blockIdx.x * 16 ..) over every route; I / 256 waves.
+template <int KMAX>
+__global__ __launch_bounds__(512) void k_moe3_down(M3Args a) {
+  __shared__ uint4 tab4[XT_BYTES / 16];
+  __shared__ uint4 hsh[M3_HCHUNKS];  // route r's h at r * (I / 8 + 1): the pad spreads routes over banks
+  __shared__ float red[8][KMAX][16];
+  const char* tab = (const char*)tab4;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const uint32_t j = lane & 15, g = lane >> 4;
+  const uint32_t C = (uint32_t)a.I >> 3, S = C + 1;
+  const uint32_t n0 = blockIdx.x * 16;
+
+  // 0. routes (scalar)
+  uint32_t dbase[KMAX];
+  float wt[KMAX];
+  bool bad = false;
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    dbase[r] = n0;
+    wt[r] = 0.f;
+    if (r < a.k) {
+      const int32_t e = a.idx[r];
+      const float wr = a.w[r];
+      const bool ok = e >= 0 && e < a.E;
+      if (wr != 0.f && !ok) bad = true;
+      if (wr != 0.f && ok) {
+        wt[r] = wr;
+        dbase[r] = (uint32_t)e * (uint32_t)a.H + n0;
+      }
+    }
+  }
+
+  // 1. LDS DMA: bf16 table and every route's h
+  for (int i = wv * 64; i < XT_BYTES / 16; i += nw * 64) dma16(a.xt + i + lane, tab4 + i);
+  for (int r = 0; r < a.k; ++r)
+    for (uint32_t c0 = wv * 64; c0 < C; c0 += nw * 64)
+      dma16((const uint4*)(a.h + (size_t)r * a.I) + c0 + lane, hsh + r * S + c0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. codes, exactly KMAX loads
+  const uint32_t kc0 = wv * 32 + g * 8;
+  uint4 q[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) q[r] = *(const uint4*)(a.dc + (size_t)(dbase[r] + j) * C + kc0);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm<KMAX>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_i;
+  ScaleRaw sr[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) sr[r] = scale_raw(a.ds, a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
+
+  // 3. decode; A row i holds route i's h
+  const uint32_t ri = j < (uint32_t)a.k ? j : 0u;
+  m3f4_t acc[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) acc[r] = m3f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const uint4 A = permuted(hsh[ri * S + kc0 + m]);
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {  // branch-free: unused or zero-weight routes are dropped in the sum
+      const uint32_t wd = dword_of(q[r], m >> 1);
+      const uint4 B = (m & 1) ? xt_decode<16>(tab, wd) : xt_decode<0>(tab, wd);
+      acc[r] = mfma16<PAIR_BF16>(A, B, acc[r]);
+    }
+  }
+
+  // 4. route r's dot is D row r: lanes 16 * (r / 4) + j, register r % 4
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    if (r < a.k && g == (uint32_t)(r >> 2))
+      red[wv][r][j] = acc[r][r & 3] * scale_cvt(sr[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
+  }
+  __syncthreads();
+
+  // 5. weighted sum over routes and waves
+  if (threadIdx.x < 16) {
+    float o = 0.f;
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {
+      if (wt[r] == 0.f) continue;
+      float v = 0.f;
+      for (int w = 0; w < nw; ++w) v += red[w][r][threadIdx.x];
+      o = fmaf(wt[r], v, o);
+    }
+    if (bad) o = __builtin_nanf("");
+    const size_t oi = n0 + threadIdx.x;
+    if (a.odt == KEEP_F16) ((_Float16*)a.out)[oi] = (_Float16)o;
+    else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;
+    else ((float*)a.out)[oi] = o;
   }
 }
 
@@ -556,6 +819,64 @@ int moe_v2_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t T,
     launch_down_v2(a, Rd, s);
   }
   return 0;
+}
+
+
+// ------------------------------------------------------------------ v3 host
+
+static int m3_qt(int64_t qtiles) {
+  const int64_t qt = (qtiles + 255) / 256;
+  return (int)(qt < 1 ? 1 : qt);
+}
+
+bool moe_v3_gateup_supported(int64_t T, int64_t H, int64_t I, int64_t k, int64_t group_h) {
+  return T == 1 && H % 256 == 0 && H >= 256 && H <= 4096 && I % 16 == 0 && k >= 1 && group_h % 256 == 0 &&
+         m3_qt(k * I / 16) <= 4;
+}
+
+bool moe_v3_down_supported(int64_t T, int64_t H, int64_t I, int64_t k, int64_t group_i) {
+  return T == 1 && H % 16 == 0 && I % 512 == 0 && I <= 2048 && k >= 1 && k <= 8 && k * (I / 8 + 1) <= M3_HCHUNKS &&
+         group_i % 256 == 0;
+}
+
+void moe_v3_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t H, int64_t I, const int32_t* idx,
+                   const float* w, int64_t k, int64_t E, const uint16_t* gc, const void* gs, const uint16_t* uc,
+                   const void* us, const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
+                   const void* prepared, float limit, void* h, void* out, int odt, hipStream_t s) {
+  M3Args a{};
+  a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.k = (int32_t)k; a.E = (int32_t)E; a.idx = idx; a.w = w;
+  a.gc = gc; a.uc = uc; a.dc = dc; a.gs = gs; a.us = us; a.ds = ds; a.sdt = sdt;
+  a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h; a.Gi = (int32_t)(I / group_i);
+  a.gsz_i = (int32_t)group_i; a.limit = limit; a.h = (uint16_t*)h; a.out = out; a.odt = odt;
+  a.qtiles = (int32_t)(k * I / 16);
+  if (gateup) {
+    a.xt = (const uint4*)((const char*)prepared + (x_dtype == KEEP_BF16 ? XT_BYTES : 0));
+    const int qt = m3_qt(a.qtiles);
+    const dim3 grid((unsigned)((a.qtiles + qt - 1) / qt)), blk((unsigned)(H / 256 * 64));
+#define GU(PK, NT) hipLaunchKernelGGL((k_moe3_gateup<PK, NT>), grid, blk, 0, s, a)
+    if (x_dtype == KEEP_BF16) {
+      if (qt == 1) GU(PAIR_BF16, 2); else if (qt == 2) GU(PAIR_BF16, 4); else if (qt == 3) GU(PAIR_BF16, 6);
+      else GU(PAIR_BF16, 8);
+    } else {
+      if (qt == 1) GU(PAIR_F16, 2); else if (qt == 2) GU(PAIR_F16, 4); else if (qt == 3) GU(PAIR_F16, 6);
+      else GU(PAIR_F16, 8);
+    }
+#undef GU
+  }
+  if (down) {
+    a.xt = (const uint4*)((const char*)prepared + XT_BYTES);
+    const dim3 grid((unsigned)(H / 16)), blk((unsigned)(I / 256 * 64));
+    switch (k) {
+      case 1: hipLaunchKernelGGL((k_moe3_down<1>), grid, blk, 0, s, a); break;
+      case 2: hipLaunchKernelGGL((k_moe3_down<2>), grid, blk, 0, s, a); break;
+      case 3: hipLaunchKernelGGL((k_moe3_down<3>), grid, blk, 0, s, a); break;
+      case 4: hipLaunchKernelGGL((k_moe3_down<4>), grid, blk, 0, s, a); break;
+      case 5: hipLaunchKernelGGL((k_moe3_down<5>), grid, blk, 0, s, a); break;
+      case 6: hipLaunchKernelGGL((k_moe3_down<6>), grid, blk, 0, s, a); break;
+      case 7: hipLaunchKernelGGL((k_moe3_down<7>), grid, blk, 0, s, a); break;
+      default: hipLaunchKernelGGL((k_moe3_down<8>), grid, blk, 0, s, a); break;
+    }
+  }
 }
 
 }  // namespace keep

@@ -257,3 +257,30 @@ def test_moe_decode_config5_shapes_with_absent_experts(dev, T):
     want = cpu.moe_decode(x.float().cpu().numpy(), local, w.cpu().numpy(), pick(gate), pick(up), pick(down),
                           e8p.e8p_packed_abs_grid())
     _check(out, want)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("gh,gi", [(1024, 512), (256, 256), (512, 128)])
+def test_moe_decode_matrix_core_path(dev, xdt, gh, gi):
+    """One token through the MFMA decode kernels (gi = 128 sends down through the expanded-table
+    kernel, so h written by one path is read by the other)."""
+    E, H, I, k, T = 32, 1024, 512, 5, 1
+    gate = synth.projection_np(E, I, H, group_size=gh, seed=41)
+    up = synth.projection_np(E, I, H, group_size=gh, seed=42)
+    down = synth.projection_np(E, H, I, group_size=gi, seed=43)
+    x = synth.rht_activations(T, H, seed=44, device=dev, dtype=xdt)
+    z = synth.router_logits(T, E, seed=45, device=dev)
+    r = keep_amd.router_dual_topk(z, k)
+    w = r.weight.clone()
+    w[0, 2] = 0.0  # a zero-weight route contributes nothing
+    tt = lambda p: (_t(p[0], dev), _t(p[1], dev))  # noqa: E731
+    out = keep_amd.moe_decode(x, r.idx, w, tt(gate), tt(up), tt(down), limit=10.0)
+    ref = keep_amd.moe_decode(x, r.idx, w, tt(gate), tt(up), tt(down), limit=10.0, prepared=False)
+    want = ops.moe_layer(x.float().cpu().numpy(), r.idx.cpu().numpy(), w.cpu().numpy(), gate, up, down,
+                         limit=10.0, h_round="bfloat16")
+    _check(out, want)
+    _check(ref, want)
+    bad = r.idx.clone()
+    bad[0, 1] = E + 3  # out-of-range expert with nonzero weight: the token's row is NaN, not a fault
+    out_bad = keep_amd.moe_decode(x, bad, w, tt(gate), tt(up), tt(down), limit=10.0)
+    assert torch.isnan(out_bad).all()
