@@ -2,18 +2,20 @@
 """Benchmark: one routed 384-expert top-6 E8P-2bit MoE layer at batch-1 decode
 on one MI355X.
 
-A *step* is one pass of the hot path for one token: the dual top-k router over
-384 logits, the fused gate/up/SwiGLU kernel and the down + weighted-combine
-kernel. Every step uses a fresh routing (64 pre-drawn logit sets), so the
-2.42 GB resident code pool streams from HBM, not from the 256 MB Infinity
-Cache. Steps are captured in HIP graphs (64 per graph) and replayed; inputs
-are resident in HBM before the timed region.
+A *step* is one pass of the hot path for one token: the whole layer
+(``keep_moe_layer``: dual top-k router over 384 logits fused with
+gate/up/SwiGLU in one launch, then down + weighted combine in a second). Every step uses a fresh routing (64 pre-drawn logit
+sets), so the 2.42 GB resident code pool streams from HBM, not from the
+256 MB Infinity Cache. Steps are captured in HIP graphs (64 per graph) and
+replayed; inputs are resident in HBM before the timed region. The same layer
+as three launches (router, gate/up, down) is timed alongside for reference.
 
 ``value`` = code-stream bytes of one layer (37,847,040 B: 18 projections of
 2048 x 512 uint16 codes plus fp16 row scales) / time per layer, in GB/s.
-``roofline`` covers the dominant kernel (gate/up/SwiGLU, 2/3 of the bytes),
-timed with HIP events on the stream it is launched on. ``cpu_baseline`` times
-the C/OpenMP restatement of the same layer (``oracle/cpu_ref.c``) on the host.
+``roofline`` covers the layer's two launches (``k_moe3_route_gateup`` then
+``k_moe3_down``) as one unit, timed with HIP events on the stream they are
+launched on. ``cpu_baseline`` times the C/OpenMP restatement
+of the same layer (``oracle/cpu_ref.c``) on the host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 """
@@ -40,21 +42,25 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-GATEUP_KERNEL = "k_moe3_gateup"  # the dominant kernel (2/3 of the layer's bytes)
+LAYER_KERNELS = ("k_moe3_route_gateup", "k_moe3_down")  # the two launches of one layer
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_layer_config2_counters.md")
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary (None if absent)."""
+def measured_traffic(kernels):
+    """HBM bytes of one launch of each of `kernels`, summed, from the committed rocprofv3 counter
+    summary (None if any is absent)."""
+    found = {}
     try:
         with open(PROFILE) as f:
             for line in f:
                 m = re.match(r"traffic_bytes_per_launch\[(\w+)\] = (\d+)", line.strip())
-                if m and m.group(1) == kernel:
-                    return int(m.group(2))
+                if m:
+                    found[m.group(1)] = int(m.group(2))
     except OSError:
         return None
-    return None
+    if not all(k in found for k in kernels):
+        return None
+    return sum(found[k] for k in kernels)
 
 
 def projection_bytes(n: int, k: int, groups: int = 1) -> int:
@@ -104,6 +110,7 @@ def main() -> int:
     admit = torch.empty((N_SETS, 1, K_TOP), dtype=torch.uint8, device=dev)
     h = torch.empty((N_SETS, K_TOP * I), dtype=torch.bfloat16, device=dev)  # SwiGLU output held in bf16
     out = torch.empty((N_SETS, H), dtype=torch.float32, device=dev)  # routed sum in fp32
+    idx1, w1, h1, out1 = torch.empty_like(idx), torch.empty_like(w), torch.empty_like(h), torch.empty_like(out)
     F16, BF16, F32 = _lib.KEEP_F16, _lib.KEEP_BF16, _lib.KEEP_F32
 
     def router(i):
@@ -124,10 +131,18 @@ def main() -> int:
                                      prep.data_ptr(), h[i].data_ptr(), out[i].data_ptr(), F32, stream.cuda_stream),
                    "down")
 
-    def layer(i):
+    def layer(i):  # the split path: router, gate/up, down as three launches
         router(i)
         gateup(i)
         down_(i)
+
+    def layer1(i):  # the whole layer: router + gate/up in one launch, down in a second
+        _lib.check(lib.keep_moe_layer(logits[i].data_ptr(), None, None, 0, 1, 1.0, float("inf"), E, K_TOP,
+                                      x.data_ptr(), F16, H, I, gate.codes.data_ptr(), gate.scales.data_ptr(),
+                                      up.codes.data_ptr(), up.scales.data_ptr(), down.codes.data_ptr(),
+                                      down.scales.data_ptr(), F16, H, I, prep.data_ptr(), 0.0, idx1[i].data_ptr(),
+                                      w1[i].data_ptr(), None, None, None, h1[i].data_ptr(), out1[i].data_ptr(), F32,
+                                      stream.cuda_stream), "moe_layer")
 
     if args.copy_calibration:
         a = torch.ones(128 << 20, dtype=torch.float16, device=dev)
@@ -140,9 +155,15 @@ def main() -> int:
     # eager pass: routes for every set, sanity
     for i in range(N_SETS):
         layer(i)
+        layer1(i)
     torch.cuda.synchronize()
-    if not torch.isfinite(out.float()).all():
+    if not torch.isfinite(out.float()).all() or not torch.isfinite(out1).all():
         raise RuntimeError("non-finite layer output")
+    if not torch.equal(idx1, idx):
+        raise RuntimeError("layer kernel routed differently from the router kernel")
+    rel = ((out1 - out).abs().max() / out.abs().max()).item()
+    if not rel <= 2e-3:
+        raise RuntimeError(f"layer kernels differ from the split path: max rel {rel:.3e}")
 
     def capture(fn, n, offset=0):
         g = torch.cuda.CUDAGraph()
@@ -166,9 +187,10 @@ def main() -> int:
 
     # capture graphs inside the torch stream context so our raw calls use the capture stream
     with torch.cuda.stream(stream):
-        full = capture(layer, GRAPH_STEPS)
+        full = capture(layer1, GRAPH_STEPS)
         tail_n = args.steps % GRAPH_STEPS
-        tail = capture(layer, tail_n, GRAPH_STEPS) if tail_n else None
+        tail = capture(layer1, tail_n, GRAPH_STEPS) if tail_n else None
+        g_split = capture(layer, GRAPH_STEPS)
         g_gateup = capture(gateup, GRAPH_STEPS)
         g_down = capture(down_, GRAPH_STEPS)
         g_router = capture(router, GRAPH_STEPS)
@@ -189,6 +211,7 @@ def main() -> int:
 
     # per-kernel averages (HIP events over graph replays on the launch stream)
     reps = max(2, min(16, args.steps // GRAPH_STEPS))
+    split_us = timed_replay([g_split], reps) * 1e3 / (reps * GRAPH_STEPS)
     gu_us = timed_replay([g_gateup], reps) * 1e3 / (reps * GRAPH_STEPS)
     dn_us = timed_replay([g_down], reps) * 1e3 / (reps * GRAPH_STEPS)
     rt_us = timed_replay([g_router], reps) * 1e3 / (reps * GRAPH_STEPS)
@@ -196,8 +219,9 @@ def main() -> int:
     dn_bytes = K_TOP * projection_bytes(H, I)
     gu_gbps = gu_bytes / (gu_us * 1e-6) / 1e9
     dn_gbps = dn_bytes / (dn_us * 1e-6) / 1e9
-    log(f"bench: layer {ms_per_step * 1e3:.2f} us  gateup {gu_us:.2f} us ({gu_gbps:.0f} GB/s)  "
-        f"down {dn_us:.2f} us ({dn_gbps:.0f} GB/s)  router {rt_us:.2f} us")
+    layer_us = ms_per_step * 1e3
+    log(f"bench: layer {layer_us:.2f} us ({value:.0f} GB/s) | split path {split_us:.2f} us: "
+        f"router {rt_us:.2f}  gateup {gu_us:.2f} ({gu_gbps:.0f} GB/s)  down {dn_us:.2f} ({dn_gbps:.0f} GB/s)")
 
     result = {
         "metric": "routed VQ-GEMM HBM GB/s (% of 8 TB/s) + MoE-layer decode tok/s, 384e top-6",
@@ -222,11 +246,12 @@ def main() -> int:
         "tok_per_s": round(1.0 / (ms_per_step * 1e-3), 1),
         "layer_bytes": layer_bytes,
         "layer_code_bytes": code_bytes,
-        "kernels_us": {"router": round(rt_us, 3), "moe_gateup": round(gu_us, 3), "moe_down": round(dn_us, 3)},
-        "roofline": {"bound": "hbm", "kernel": GATEUP_KERNEL, "achieved": round(gu_gbps, 2),
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
-                     "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_us, 3),
-                     "traffic": measured_traffic(GATEUP_KERNEL),
+        "kernels_us": {"moe_layer (route_gateup + down)": round(layer_us, 3), "split_path_total": round(split_us, 3),
+                       "router": round(rt_us, 3), "moe_gateup": round(gu_us, 3), "moe_down": round(dn_us, 3)},
+        "roofline": {"bound": "hbm", "kernel": " + ".join(LAYER_KERNELS), "achieved": round(value, 2),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(value / HBM_PEAK_GBPS, 4),
+                     "bytes_per_launch": layer_bytes, "us_per_launch": round(layer_us, 3),
+                     "traffic": measured_traffic(LAYER_KERNELS),
                      "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
                                        "profiles/moe_layer_config2_counters.md"},
         "cpu_baseline": None,

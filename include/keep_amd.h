@@ -177,6 +177,29 @@ int keep_moe_down(int h_dtype, int64_t T, int64_t H, int64_t I,
                   int64_t group_size_i, const uint32_t* table, const void* prepared,
                   const void* h_work, void* out, int out_dtype, void* stream);
 
+/* One routed MoE decode layer for one token in two launches on `stream`:
+ * first the router (as keep_router_dual_topk with T = 1; outputs written to
+ * idx/w/want/want_score/admit, the last three optional) fused with
+ * gate/up/SwiGLU into h_work, then down + weighted combine into out[H]. The
+ * first launch also pulls the routed experts' down codes into the device's
+ * last-level cache so that the second launch reads them from there. No
+ * state is kept between calls. `prepared` is keep_e8p_prepare of the E8P
+ * table. Serves H = 4096, I a multiple of 512 up to 2048, k <= 8, E <= 1024
+ * and scale groups of 256-element multiples (keep_moe_layer_supported).
+ * Replaces the serving decode step of scripts/v41_build/omlx_lattice.py:327-371
+ * (router, gate/up, SwiGLU, down, fp32 combine) for batch 1. */
+int keep_moe_layer_supported(int64_t num_experts, int64_t H, int64_t I, int64_t k,
+                             int64_t group_size_h, int64_t group_size_i);
+int keep_moe_layer(const float* logits, const float* bias_served, const float* bias_demand,
+                   int score_func, int renormalize, float route_scale, float tau,
+                   int64_t num_experts, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
+                   const uint16_t* gate_codes, const void* gate_scales,
+                   const uint16_t* up_codes, const void* up_scales,
+                   const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                   int64_t group_size_h, int64_t group_size_i, const void* prepared,
+                   float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                   uint8_t* admit, void* h_work, void* out, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

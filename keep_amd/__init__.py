@@ -6,7 +6,8 @@ fallback: without the library every operator raises ``RuntimeError``.
 """
 
 from keep_amd._lib import is_available
-from keep_amd.nn import LimitedSwiGLU, QuantizedVQSwitchGLU, QuantizedVQSwitchLinear, RoutedVQMoE, moe_decode
+from keep_amd.nn import (LimitedSwiGLU, QuantizedVQSwitchGLU, QuantizedVQSwitchLinear, RoutedVQMoE, moe_decode,
+                         moe_layer, moe_layer_supported)
 from keep_amd.ops import (
     decode_e8p,
     decode_weight_matrix,
@@ -31,6 +32,6 @@ __all__ = [
     "LimitedSwiGLU", "QuantizedVQSwitchGLU", "QuantizedVQSwitchLinear", "RoutedVQMoE", "decode_e8p",
     "decode_weight_matrix", "e8_1bit_packed", "e8p_m1_per_route", "e8p_m1_token_layout", "e8p_nested_m1_per_route",
     "e8p_nested_m1_token_layout", "e8p_packed_abs_grid", "expert_select", "gather_vqmm", "gather_vqmm_sorted_routes",
-    "gather_vqmm_verify_rows", "half2_pairs", "is_available", "moe_decode", "resident_bias", "route_plan",
+    "gather_vqmm_verify_rows", "half2_pairs", "is_available", "moe_decode", "moe_layer", "moe_layer_supported", "resident_bias", "route_plan",
     "router_dual_topk", "trace_gather_vqmm_calls", "vq_qmm", "vq_qmv",
 ]

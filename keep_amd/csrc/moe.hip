@@ -22,6 +22,7 @@
 // table to LDS and joins the barrier, so the HBM stream is in flight while
 // the table is staged. Lane reductions use DPP row ops plus readlane.
 #include "common.h"
+#include "route_dev.h"
 
 namespace keep {
 
@@ -719,6 +720,194 @@ __global__ __launch_bounds__(512) void k_moe3_down(M3Args a) {
   }
 }
 
+// ------------------------------------------------------------------ v3: router + gate/up in one launch
+//
+// One block per 3 q-tiles (1024 threads; the table takes 128 KiB of LDS, so
+// one block per CU) runs, for one token:
+//   1. the dual top-k router, block-parallel (same selection and weights as
+//      k_router; block 0 publishes the router outputs);
+//   2. the activation-kind table and the token DMA'd into LDS, then the gate/
+//      up scales and codes;
+//   3. gate/up on the matrix cores one tile at a time as its codes arrive,
+//      SwiGLU, h stored to h_work (bf16);
+// and, while gate/up decodes, pulls the down rows that the same-numbered
+// block of the down launch will read through the caches (the 256 MB Infinity
+// Cache holds them), so the down launch streams from cache instead of HBM.
+// A grid-wide barrier inside one launch was measured at 5+ us per use on
+// MI355X (device-scope atomics or flag polls across XCDs), no cheaper than a
+// launch boundary, so down stays a second launch (k_moe3_down).
+// Requires H = 4096 (16 waves x 256-element K slices) and k <= 8.
+
+constexpr int M3L_UNION = 1544;  // uint4: max(token 512, k * (I/8 + 1) h chunks, reduction 2048 floats)
+
+struct M3Layer {
+  const float* logits;
+  const float *bias_s, *bias_d;
+  int func, renorm, same_bias;
+  float route_scale, tau;
+  int32_t E, k;
+  int32_t* idx_out;
+  float* w_out;
+  int32_t* want_out;
+  float* want_score_out;
+  uint8_t* admit_out;
+  const void* x;
+  int32_t H, I;
+  const uint16_t *gc, *uc, *dc;
+  const void *gs, *us, *ds;
+  int sdt;
+  int32_t Gh, gsz_h, Gi, gsz_i;
+  const uint4* xt_x;  // expanded table in the activation pair kind
+  const uint4* xt_h;  // expanded table in bf16
+  float limit;
+  uint16_t* h;  // [k, I] bf16
+  int32_t qtiles;
+  int32_t down_blocks;  // H / 16: blocks of the down launch
+};
+
+// Block barrier for LDS traffic only: unlike __syncthreads it does not wait
+// for this wave's outstanding global loads (the code stream keeps flowing).
+__device__ __forceinline__ void lds_barrier() { rt_lds_barrier(); }
+
+template <int PK, int NT, int KMAX>
+__global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
+  __shared__ uint4 tab4[XT_BYTES / 16];
+  // uni: [0, 512) the token, [512, ...) routing scratch, [1024, ...) gate/up
+  // partials; later the h rows of every route and then the down partials.
+  __shared__ uint4 uni[M3L_UNION];
+  __shared__ int32_t s_idx[KMAX];
+  __shared__ float s_w[KMAX];
+  // 1 KiB that only the cache-warming DMA writes; an object of its own so the
+  // compiler sees that LDS reads of the other arrays never wait for it
+  __shared__ uint4 sink[64];
+  constexpr int QT = NT / 2;
+  const char* tab = (const char*)tab4;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t j = lane & 15, g = lane >> 4;
+  const uint32_t C = (uint32_t)a.H >> 3;  // 512 token chunks
+  const uint32_t Ci = (uint32_t)a.I >> 3;
+  float* gred = (float*)(uni + 1024);  // [16 waves][NT][16]
+
+  // 1. routing (its three inputs are the only loads in flight). Plain loads
+  //    only in this kernel: the compiler counts every wait exactly, which it
+  //    cannot do for a load issued ahead of LDS DMA (it waits for everything).
+  float* rsc = (float*)(uni + 512);
+  RtCand* rcand = (RtCand*)(uni + 512 + 276);
+  RtCand* rres = rcand + 2 * 16 * 8;
+  const RtInput rin = rt_input_load(a.logits, a.bias_s, a.bias_d, a.E);
+  const RouteLane r = rt_route_block(rin, a.bias_s != nullptr, a.bias_d != nullptr, a.E, a.k, a.func, a.renorm,
+                                     a.route_scale, a.tau, a.same_bias != 0, rsc, rcand, rres);
+  if (wv == 0 && r.valid) {
+    s_idx[lane] = r.expert;
+    s_w[lane] = r.value;
+  }
+  if (blockIdx.x == 0 && r.valid) {
+    if (wv == 0) {
+      a.idx_out[lane] = r.expert;
+      a.w_out[lane] = r.value;
+    } else {
+      if (a.want_out) a.want_out[lane] = r.expert;
+      if (a.want_score_out) a.want_score_out[lane] = r.value;
+      if (a.admit_out) a.admit_out[lane] = r.admit;
+    }
+  }
+  lds_barrier();
+  // the activation table and the token, DMA'd straight into LDS ahead of the
+  // code stream: exactly 9 ops per wave (waves 8..15 repeat 0..7's token piece)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dma16(a.xt_x + (i * 16 + wv) * 64 + lane, tab4 + (i * 16 + wv) * 64);
+  dma16((const uint4*)a.x + (wv & 7) * 64 + lane, uni + (wv & 7) * 64);
+  // warm the caches with the down rows of the same-numbered down block: per
+  // route, rows [16 b, 16 b + 16) are 16 * I/8 contiguous codewords = I/32
+  // pieces of 1 KiB (one DMA op each), all into a write-only sink. Every wave
+  // issues exactly KMAX/2 ops (unused slots repeat a valid piece), so the
+  // compiler's waits stay exact. They go ahead of the gate/up scale and code
+  // loads: a plain load is only waited for exactly when no DMA issued after
+  // it is still pending (else the compiler waits for everything).
+  {
+    const uint32_t per_route = Ci / 32u, npieces = (uint32_t)a.k * per_route;
+    const uint32_t db = blockIdx.x % (uint32_t)a.down_blocks;
+#pragma unroll
+    for (int i = 0; i < (KMAX + 1) / 2; ++i) {
+      uint32_t p = (uint32_t)wv + 16u * i;
+      p = p < npieces ? p : p % npieces;
+      const uint32_t route = p / per_route, piece = p - route * per_route;
+      const int32_t e = s_idx[route];
+      const uint32_t ee = e >= 0 && e < a.E ? (uint32_t)e : 0u;
+      dma16((const uint4*)(a.dc + ((size_t)ee * (uint32_t)a.H + db * 16u) * Ci) + piece * 64 + lane, sink);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. the gate/up tiles of this block
+  uint32_t rbase[QT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const uint32_t qt = blockIdx.x * QT + u;
+    const bool valid = qt < (uint32_t)a.qtiles;
+    const uint32_t q0 = (valid ? qt : 0u) * 16u;
+    const uint32_t route = q0 / (uint32_t)a.I;
+    const int32_t e = s_idx[route];
+    const bool ok = valid && e >= 0 && e < a.E;
+    rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
+  }
+  // scales first (they must not queue behind the code stream), then codes
+  const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
+  ScaleRaw sr[NT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
+    sr[2 * u] = scale_raw(a.gs, a.sdt, si);
+    sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
+  }
+  const uint32_t kc0 = wv * 32 + g * 8;
+  uint4 q[NT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const size_t off = (size_t)(rbase[u] + j) * C + kc0;
+    q[2 * u] = *(const uint4*)(a.gc + off);
+    q[2 * u + 1] = *(const uint4*)(a.uc + off);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm<2 * QT + NT>();  // the DMAs, not the scale and code loads behind them
+  lds_barrier();
+
+  // 3. gate/up, one tile at a time as its codes arrive; the token's 8 chunks stay in registers
+  uint4 A[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) A[m] = permuted(uni[kc0 + m]);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    m3f4_t acc = m3f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const uint32_t wd = dword_of(q[t], m >> 1);
+      const uint4 B = (m & 1) ? xt_decode<16>(tab, wd) : xt_decode<0>(tab, wd);
+      acc = mfma16<PK>(A[m], B, acc);
+    }
+    const uint32_t si = (rbase[t >> 1] + j) * (uint32_t)a.Gh + grp;
+    if (lane < 16) gred[(wv * NT + t) * 16 + j] = acc[0] * scale_cvt(sr[t], a.sdt, si);
+  }
+  lds_barrier();  // activation table and token no longer read; partials visible
+  if (wv == 0 && lane < QT * 16) {
+    const uint32_t u = lane >> 4, jj = lane & 15;
+    const uint32_t qt = blockIdx.x * QT + u;
+    float gsum = 0.f, usum = 0.f;
+    for (int w = 0; w < 16; ++w) {
+      gsum += gred[(w * NT + 2 * u) * 16 + jj];
+      usum += gred[(w * NT + 2 * u + 1) * 16 + jj];
+    }
+    if (qt < (uint32_t)a.qtiles) {
+      const uint32_t q0 = qt * 16u;
+      const int32_t e = s_idx[q0 / (uint32_t)a.I];
+      if (e >= 0 && e < a.E) a.h[q0 + jj] = from_float<bf16s>(silu_mul(gsum, usum, a.limit)).bits;
+    }
+  }
+
+  wait_vm<0>();  // no DMA into this block's LDS may outlive it
+}
+
 // ------------------------------------------------------------------ host
 
 struct GuShape {
@@ -879,6 +1068,50 @@ void moe_v3_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t H
   }
 }
 
+
+// ------------------------------------------------------------------ v3 layer host
+
+bool moe_v3_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
+  const int64_t qtiles = k * I / 16;
+  return H == 4096 && k >= 1 && k <= 8 && k <= E && E <= 1024 && (qtiles + 255) / 256 <= 3 &&
+         group_h % 256 == 0 && moe_v3_down_supported(1, H, I, k, group_i);
+}
+
+int moe_v3_layer_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm,
+                        float route_scale, float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H,
+                        int64_t I, const uint16_t* gc, const void* gs, const uint16_t* uc, const void* us,
+                        const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
+                        const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                        uint8_t* admit, void* h, void* out, int odt, hipStream_t s) {
+  M3Layer a{};
+  a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
+  a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
+  a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
+  a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.dc = dc; a.gs = gs; a.us = us; a.ds = ds;
+  a.sdt = sdt; a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h; a.Gi = (int32_t)(I / group_i);
+  a.gsz_i = (int32_t)group_i;
+  a.xt_x = (const uint4*)((const char*)prepared + (x_dtype == KEEP_BF16 ? XT_BYTES : 0));
+  a.xt_h = (const uint4*)((const char*)prepared + XT_BYTES);
+  a.limit = limit; a.h = (uint16_t*)h;
+  a.qtiles = (int32_t)(k * I / 16);
+  a.down_blocks = (int32_t)(H / 16);
+  const int qt = (int)((a.qtiles + 255) / 256);
+  const dim3 grid((unsigned)((a.qtiles + qt - 1) / qt)), blk(1024);
+#define LY(PK, NT, KM) hipLaunchKernelGGL((k_moe3_route_gateup<PK, NT, KM>), grid, blk, 0, s, a)
+#define LY_K(PK, NT) \
+  if (k <= 4) LY(PK, NT, 4); else if (k <= 6) LY(PK, NT, 6); else LY(PK, NT, 8)
+#define LY_NT(PK) \
+  if (qt <= 1) { LY_K(PK, 2); } else if (qt == 2) { LY_K(PK, 4); } else { LY_K(PK, 6); }
+  if (x_dtype == KEEP_BF16) { LY_NT(PAIR_BF16); } else { LY_NT(PAIR_F16); }
+#undef LY_NT
+#undef LY_K
+#undef LY
+  // down + weighted combine, reading the router outputs and h the first launch wrote
+  moe_v3_launch(false, true, x, x_dtype, H, I, idx, w, k, E, gc, gs, uc, us, dc, ds, sdt, group_h, group_i, prepared,
+                limit, h, out, odt, s);
+  return 0;
+}
+
 }  // namespace keep
 
 using namespace keep;
@@ -894,3 +1127,37 @@ extern "C" int keep_e8p_prepare(const uint32_t* table, void* prepared, void* str
 }
 
 extern "C" int keep_e8p_prepared_bytes(void) { return 2 * XT_BYTES; }
+
+extern "C" int keep_moe_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_size_h,
+                                        int64_t group_size_i) {
+  return moe_v3_layer_supported(E, H, I, k, group_size_h, group_size_i) ? 1 : 0;
+}
+
+extern "C" int keep_moe_layer(const float* logits, const float* bias_served, const float* bias_demand, int score_func,
+                              int renormalize, float route_scale, float tau, int64_t E, int64_t k, const void* x,
+                              int x_dtype, int64_t H, int64_t I, const uint16_t* gate_codes, const void* gate_scales,
+                              const uint16_t* up_codes, const void* up_scales, const uint16_t* down_codes,
+                              const void* down_scales, int scale_dtype, int64_t group_size_h, int64_t group_size_i,
+                              const void* prepared, float swiglu_limit, int32_t* idx, float* w, int32_t* want,
+                              float* want_score, uint8_t* admit, void* h_work, void* out, int out_dtype,
+                              void* stream) {
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
+  KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
+  KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);
+  KEEP_REQUIRE(group_size_h > 0 && H % group_size_h == 0 && group_size_i > 0 && I % group_size_i == 0,
+               "bad group sizes");
+  KEEP_REQUIRE(moe_v3_layer_supported(E, H, I, k, group_size_h, group_size_i),
+               "shape not served by the routed decode layer kernels (needs H = 4096, I a multiple of 512 up to "
+               "2048, k <= 8, E <= 1024, scale groups of 256-element multiples)");
+  KEEP_REQUIRE(logits && x && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
+                   prepared && idx && w && h_work && out,
+               "null pointer argument");
+  KEEP_REQUIRE(aligned(x, 16) && aligned(h_work, 16) && aligned(prepared, 16),
+               "x, h_work and prepared must be 16-byte aligned");
+  KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 8), "codes misaligned");
+  moe_v3_layer_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype,
+                      H, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
+                      group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, h_work,
+                      out, out_dtype, (hipStream_t)stream);
+  return launch_status("keep_moe_layer");
+}

@@ -21,7 +21,7 @@ from typing import Callable
 import torch
 
 from keep_amd import _lib, ops
-from keep_amd.router import router_dual_topk
+from keep_amd.router import RouterOutput, router_dual_topk
 
 CODEWORD_DIM = 8
 
@@ -237,6 +237,71 @@ def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, u
     return out
 
 
+def moe_layer_supported(num_experts: int, hidden: int, intermediate: int, k: int, group_size_h: int,
+                        group_size_i: int) -> bool:
+    """Whether ``moe_layer`` (the two-launch routed decode layer) serves this shape."""
+
+    return bool(_lib.load().keep_moe_layer_supported(num_experts, hidden, intermediate, k, group_size_h,
+                                                     group_size_i))
+
+
+def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, bias_served=None, bias_demand=None,
+              score_func: str = "softmax", renormalize: bool = True, route_scale: float = 1.0,
+              tau: float = float("inf"), limit: float = 0.0, codebook: torch.Tensor | None = None,
+              out_dtype: torch.dtype | None = None, h_work: torch.Tensor | None = None):
+    """One token's whole MoE layer in two launches (``keep_moe_layer``): the dual
+    top-k router (as ``router_dual_topk``) fused with gate/up/SwiGLU, then down +
+    weighted combine. ``x [1, H]`` (fp16/bf16), ``logits [1, E]``. Returns
+    ``(out [1, H], RouterOutput)``; the output is float32 by default."""
+
+    device = x.device
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("moe_layer needs float16 or bfloat16 activations")
+    if score_func not in _lib.SCORE_FUNCS:
+        raise ValueError(f"score_func must be one of {sorted(_lib.SCORE_FUNCS)}")
+    (gc, gs), (uc, us), (dc, ds) = gate, up, down
+    E, I, Hc = gc.shape
+    H = Hc * 8
+    if x.ndim != 2 or tuple(x.shape) != (1, H):
+        raise ValueError(f"x must be [1, {H}], found {tuple(x.shape)}")
+    if tuple(uc.shape) != (E, I, Hc) or tuple(dc.shape) != (E, H, I // 8):
+        raise ValueError("gate/up codes must be [E, I, H/8] and down codes [E, H, I/8]")
+    if not (gs.dtype == us.dtype == ds.dtype):
+        raise ValueError("gate/up/down scales must share a dtype")
+    z = logits.to(device=device, dtype=torch.float32).reshape(1, -1).contiguous()
+    if z.shape[1] != E:
+        raise ValueError(f"logits must hold {E} experts, found {z.shape[1]}")
+    gh, gi = H // gs.shape[-1], I // ds.shape[-1]
+    if not moe_layer_supported(E, H, I, k, gh, gi):
+        raise ValueError("shape not served by the routed decode layer; use router_dual_topk + moe_decode")
+    bs = None if bias_served is None else bias_served.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    bd = None if bias_demand is None else bias_demand.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    if bias_demand is bias_served:
+        bd = bs
+    for name, b in (("bias_served", bs), ("bias_demand", bd)):
+        if b is not None and b.numel() != E:
+            raise ValueError(f"{name} must have {E} entries, found {b.numel()}")
+    i32 = dict(dtype=torch.int32, device=device)
+    f32 = dict(dtype=torch.float32, device=device)
+    r = RouterOutput(torch.empty((1, k), **i32), torch.empty((1, k), **f32), torch.empty((1, k), **i32),
+                     torch.empty((1, k), **f32), torch.empty((1, k), dtype=torch.uint8, device=device))
+    od = out_dtype or torch.float32
+    out = torch.empty((1, H), dtype=od, device=device)
+    if h_work is None:
+        h_work = torch.empty((k * I,), dtype=torch.bfloat16, device=device)
+    elif h_work.numel() < k * I or h_work.dtype != torch.bfloat16:
+        raise ValueError("h_work must hold k*I bfloat16 elements")
+    cb = ops._codebook_tensor(codebook, 16, device)
+    prep = ops.prepared_table(cb)
+    _lib.call("keep_moe_layer", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
+              int(bool(renormalize)), float(route_scale), float(tau), E, k, x.data_ptr(), ops._DT[x.dtype], H, I,
+              gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
+              ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(), r.weight.data_ptr(),
+              r.want.data_ptr(), r.want_score.data_ptr(), r.admit.data_ptr(), h_work.data_ptr(), out.data_ptr(),
+              ops._DT[od], ops._stream(device))
+    return out, r
+
+
 class RoutedVQMoE:
     """Router + routed E8P SwiGLU experts + weighted combine (one MoE layer).
 
@@ -266,7 +331,21 @@ class RoutedVQMoE:
         y = self.glu(x, idx)  # [T, k, H]
         return (y.float() * weight[..., None].float()).sum(-2).to(self.out_dtype)
 
+    def _layer_path(self, x: torch.Tensor) -> bool:
+        g, d = self.glu.gate_proj, self.glu.down_proj
+        return (x.shape[0] == 1 and x.dtype in (torch.float16, torch.bfloat16) and self.glu._all_e8p() and
+                self.decode_max_tokens >= 1 and
+                moe_layer_supported(g.num_experts, g.input_dims, g.output_dims, self.top_k,
+                                    g.input_dims // g.scales.shape[-1], d.input_dims // d.scales.shape[-1]))
+
     def __call__(self, x: torch.Tensor, logits: torch.Tensor):
+        if self._layer_path(x):
+            g, u, d = self.glu.gate_proj, self.glu.up_proj, self.glu.down_proj
+            return moe_layer(x, logits, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
+                             k=self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
+                             score_func=self.score_func, renormalize=self.renormalize,
+                             route_scale=self.route_scale, tau=self.tau, limit=self.limit, codebook=g.codebook,
+                             out_dtype=self.out_dtype)
         r = router_dual_topk(logits, self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
                              score_func=self.score_func, renormalize=self.renormalize, route_scale=self.route_scale,
                              tau=self.tau)

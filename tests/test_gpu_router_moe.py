@@ -284,3 +284,75 @@ def test_moe_decode_matrix_core_path(dev, xdt, gh, gi):
     bad[0, 1] = E + 3  # out-of-range expert with nonzero weight: the token's row is NaN, not a fault
     out_bad = keep_amd.moe_decode(x, bad, w, tt(gate), tt(up), tt(down), limit=10.0)
     assert torch.isnan(out_bad).all()
+
+
+def _layer_oracle(x, r_idx, w, gate, up, down, limit=0.0):
+    """C-oracle MoE output for one token over the experts actually used."""
+    idx = r_idx.cpu().numpy()
+    used = np.unique(idx)
+    sub = {e: i for i, e in enumerate(used)}
+    sel = torch.from_numpy(used).to(gate.codes.device).long()
+    pick = lambda p: (p.codes[sel].cpu().numpy().view(np.uint16), p.scales[sel].float().cpu().numpy())  # noqa: E731
+    local = np.vectorize(sub.get)(idx).astype(np.int32)
+    return cpu.moe_decode(x.float().cpu().numpy(), local, w.cpu().numpy(), pick(gate), pick(up), pick(down),
+                          e8p.e8p_packed_abs_grid(), limit=limit)
+
+
+def test_moe_layer_config2(dev):
+    """Config 2 through the routed decode layer: router indices exact, output vs the C oracle and the split path,
+    and a second call with other logits on the same h_work (the down launch must see the new routing)."""
+    E, H, I, k = 384, 4096, 2048, 6
+    gate = synth.projection(E, I, H, seed=1, device=dev)
+    up = synth.projection(E, I, H, seed=2, device=dev)
+    down = synth.projection(E, H, I, seed=3, device=dev)
+    assert keep_amd.moe_layer_supported(E, H, I, k, H, I)
+    x = synth.rht_activations(1, H, seed=4, device=dev)
+    h_work = torch.empty(k * I, dtype=torch.bfloat16, device=dev)
+    for seed in (5, 6):
+        z = synth.router_logits(1, E, seed=seed, device=dev)
+        out, r = keep_amd.moe_layer(x, z, (gate.codes, gate.scales), (up.codes, up.scales),
+                                    (down.codes, down.scales), k=k, h_work=h_work)
+        zi, zw, *_ = ops.router_dual_topk(z.cpu().numpy(), np.zeros(E), np.zeros(E), k)
+        np.testing.assert_array_equal(r.idx.cpu().numpy(), zi)
+        np.testing.assert_allclose(r.weight.cpu().numpy(), zw, rtol=1e-5, atol=1e-7)
+        _check(out, _layer_oracle(x, r.idx, r.weight, gate, up, down))
+        split = keep_amd.moe_decode(x, r.idx, r.weight, (gate.codes, gate.scales), (up.codes, up.scales),
+                                    (down.codes, down.scales))
+        _check(out, split.double().cpu().numpy())
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_moe_layer_config5_residency(dev, xdt):
+    """Config 5 shapes: half the pool absent (served vs demand), tau admission, group scales."""
+    E, H, I, k = 288, 4096, 1536, 8
+    gate = synth.projection(E, I, H, group_size=1024, seed=31, device=dev)
+    up = synth.projection(E, I, H, group_size=1024, seed=32, device=dev)
+    down = synth.projection(E, H, I, group_size=512, seed=33, device=dev)
+    x = synth.rht_activations(1, H, seed=34, device=dev, dtype=xdt)
+    z = synth.router_logits(1, E, seed=35, device=dev)
+    mask = synth.resident_mask(E, frac=0.5, seed=36)
+    bias = keep_amd.resident_bias(torch.from_numpy(mask).to(dev))
+    out, r = keep_amd.moe_layer(x, z, (gate.codes, gate.scales), (up.codes, up.scales), (down.codes, down.scales),
+                                k=k, bias_served=bias, tau=0.3)
+    ref = keep_amd.router_dual_topk(z, k, bias_served=bias, tau=0.3)
+    oi, ow, owant, osc, oadm = ops.router_dual_topk(z.cpu().numpy(), bias.cpu().numpy().astype(np.float64),
+                                                    np.zeros(E), k, tau=0.3)
+    np.testing.assert_array_equal(r.idx.cpu().numpy(), oi)
+    np.testing.assert_array_equal(r.want.cpu().numpy(), owant)
+    np.testing.assert_array_equal(r.admit.cpu().numpy(), oadm.astype(np.uint8))
+    for a, b in zip(r, ref):
+        assert torch.equal(a, b)  # the fused router is the standalone router, bit for bit
+    assert set(r.idx.cpu().numpy().ravel()) <= set(np.flatnonzero(mask))
+    _check(out, _layer_oracle(x, r.idx, r.weight, gate, up, down))
+
+
+def test_moe_layer_rejects_unserved_shapes(dev):
+    E, H, I, k = 16, 512, 256, 4
+    assert not keep_amd.moe_layer_supported(E, H, I, k, H, I)
+    gate = synth.projection(E, I, H, seed=1, device=dev)
+    down = synth.projection(E, H, I, seed=3, device=dev)
+    x = synth.rht_activations(1, H, seed=4, device=dev)
+    z = synth.router_logits(1, E, seed=5, device=dev)
+    with pytest.raises(ValueError, match="routed decode layer"):
+        keep_amd.moe_layer(x, z, (gate.codes, gate.scales), (gate.codes, gate.scales), (down.codes, down.scales),
+                           k=k)
