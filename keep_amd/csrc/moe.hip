@@ -624,93 +624,139 @@ __global__ __launch_bounds__(1024) void k_moe3_gateup(M3Args a) {
 }
 
 // Block: 16 output rows (blockIdx.x * 16 ..) over every route; I / 256 waves.
+// Kernel arguments are fetched through the scalar cache on first use; a
+// field first used deep in a kernel costs a cold miss right there (about a
+// microsecond when the argument block's line is not cached). pinned() copies
+// a field into scalar registers at the point it is called, so every field
+// is fetched in one batch at kernel start.
+template <typename T>
+__device__ __forceinline__ T pinned(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "scalar argument");
+  if constexpr (sizeof(T) == 8) {
+    uint64_t u = __builtin_bit_cast(uint64_t, v);
+    asm volatile("" : "+s"(u));
+    return __builtin_bit_cast(T, u);
+  } else {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    asm volatile("" : "+s"(u));
+    return __builtin_bit_cast(T, u);
+  }
+}
+
+// Block barrier for LDS traffic only: unlike __syncthreads it does not wait
+// for this wave's outstanding global loads (the code stream keeps flowing).
+__device__ __forceinline__ void lds_barrier() { rt_lds_barrier(); }
+
+// Every block copies the same 128 KiB table (128 pieces of 1 KiB) into its
+// LDS. Blocks are dealt round-robin to the 8 XCDs, so blocks b, b + 8, ...
+// share one L2: each starts at its own piece, so that at any moment they
+// request different lines and most requests hit a line another block of the
+// XCD already brought in, instead of all missing on the same line together.
+__device__ __forceinline__ uint32_t xt_rotation() { return ((blockIdx.x >> 3) * 4u) & 127u; }
+
 template <int KMAX>
-__global__ __launch_bounds__(512) void k_moe3_down(M3Args a) {
+__global__ __launch_bounds__(512) void k_moe3_down(M3Args args) {
+  M3Args a{};
+  a.H = pinned(args.H); a.I = pinned(args.I); a.E = pinned(args.E);
+  a.idx = pinned(args.idx); a.w = pinned(args.w); a.dc = pinned(args.dc); a.ds = pinned(args.ds);
+  a.sdt = pinned(args.sdt); a.Gi = pinned(args.Gi); a.gsz_i = pinned(args.gsz_i); a.xt = pinned(args.xt);
+  a.h = pinned(args.h); a.out = pinned(args.out); a.odt = pinned(args.odt);
   __shared__ uint4 tab4[XT_BYTES / 16];
   __shared__ uint4 hsh[M3_HCHUNKS];  // route r's h at r * (I / 8 + 1): the pad spreads routes over banks
   __shared__ float red[8][KMAX][16];
   const char* tab = (const char*)tab4;
   const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = blockDim.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // 8 waves; I / 256 of them decode
+  const int nwd = a.I >> 8;
   const uint32_t j = lane & 15, g = lane >> 4;
   const uint32_t C = (uint32_t)a.I >> 3, S = C + 1;
   const uint32_t n0 = blockIdx.x * 16;
 
-  // 0. routes (scalar)
+  // 1. the routes (scalar loads: KMAX == k, so all in bounds), then the bf16
+  //    table, which does not depend on them (16 DMA ops per wave)
+  int32_t e_r[KMAX];
+  float w_r[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    e_r[r] = a.idx[r];
+    w_r[r] = a.w[r];
+  }
+  const uint32_t rot = xt_rotation();
+#pragma unroll
+  for (int i = 0; i < XT_BYTES / 16 / 512; ++i) {
+    const uint32_t piece = ((uint32_t)(i * 8 + wv) + rot) & 127u;
+    dma16(a.xt + piece * 64 + lane, tab4 + piece * 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   uint32_t dbase[KMAX];
   float wt[KMAX];
   bool bad = false;
 #pragma unroll
   for (int r = 0; r < KMAX; ++r) {
-    dbase[r] = n0;
-    wt[r] = 0.f;
-    if (r < a.k) {
-      const int32_t e = a.idx[r];
-      const float wr = a.w[r];
-      const bool ok = e >= 0 && e < a.E;
-      if (wr != 0.f && !ok) bad = true;
-      if (wr != 0.f && ok) {
-        wt[r] = wr;
-        dbase[r] = (uint32_t)e * (uint32_t)a.H + n0;
-      }
-    }
+    const bool ok = e_r[r] >= 0 && e_r[r] < a.E;
+    bad |= w_r[r] != 0.f && !ok;
+    wt[r] = ok ? w_r[r] : 0.f;
+    dbase[r] = (ok ? (uint32_t)e_r[r] * (uint32_t)a.H : 0u) + n0;
   }
 
-  // 1. LDS DMA: bf16 table and every route's h
-  for (int i = wv * 64; i < XT_BYTES / 16; i += nw * 64) dma16(a.xt + i + lane, tab4 + i);
-  for (int r = 0; r < a.k; ++r)
-    for (uint32_t c0 = wv * 64; c0 < C; c0 += nw * 64)
+  // 3. every route's h (pieces of 64 chunks, (KMAX + 1) / 2 DMA ops per wave;
+  //    unused slots repeat a valid piece), then the scales and the codes
+  {
+    const uint32_t per_route = C / 64u, npieces = (uint32_t)KMAX * per_route;
+#pragma unroll
+    for (int i = 0; i < (KMAX + 1) / 2; ++i) {
+      uint32_t p = (uint32_t)wv + 8u * i;
+      p = p < npieces ? p : p % npieces;
+      const uint32_t r = p / per_route, c0 = (p - r * per_route) * 64u;
       dma16((const uint4*)(a.h + (size_t)r * a.I) + c0 + lane, hsh + r * S + c0);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 2. codes, exactly KMAX loads
-  const uint32_t kc0 = wv * 32 + g * 8;
+    }
+  }
+  const bool dec = wv < nwd;  // wave-uniform
+  const uint32_t kc0 = (dec ? wv : 0) * 32 + g * 8;
+  const uint32_t grp = (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.gsz_i;
+  ScaleRaw sr[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) sr[r] = scale_raw(a.ds, a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
   uint4 q[KMAX];
 #pragma unroll
   for (int r = 0; r < KMAX; ++r) q[r] = *(const uint4*)(a.dc + (size_t)(dbase[r] + j) * C + kc0);
   __builtin_amdgcn_sched_barrier(0);
-  wait_vm<KMAX>();
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-  const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_i;
-  ScaleRaw sr[KMAX];
-#pragma unroll
-  for (int r = 0; r < KMAX; ++r) sr[r] = scale_raw(a.ds, a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
+  wait_vm<2 * KMAX>();  // the table and h DMAs, not the scales and codes behind them
+  lds_barrier();
 
-  // 3. decode; A row i holds route i's h
-  const uint32_t ri = j < (uint32_t)a.k ? j : 0u;
-  m3f4_t acc[KMAX];
+  // 4. decode; A row i holds route i's h
+  if (dec) {
+    const uint32_t ri = j < (uint32_t)KMAX ? j : 0u;
+    m3f4_t acc[KMAX];
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) acc[r] = m3f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < KMAX; ++r) acc[r] = m3f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const uint4 A = permuted(hsh[ri * S + kc0 + m]);
+    for (int m = 0; m < 8; ++m) {
+      const uint4 A = permuted(hsh[ri * S + kc0 + m]);
 #pragma unroll
-    for (int r = 0; r < KMAX; ++r) {  // branch-free: unused or zero-weight routes are dropped in the sum
-      const uint32_t wd = dword_of(q[r], m >> 1);
-      const uint4 B = (m & 1) ? xt_decode<16>(tab, wd) : xt_decode<0>(tab, wd);
-      acc[r] = mfma16<PAIR_BF16>(A, B, acc[r]);
+      for (int r = 0; r < KMAX; ++r) {  // branch-free: zero-weight routes are dropped in the sum
+        const uint32_t wd = dword_of(q[r], m >> 1);
+        const uint4 B = (m & 1) ? xt_decode<16>(tab, wd) : xt_decode<0>(tab, wd);
+        acc[r] = mfma16<PAIR_BF16>(A, B, acc[r]);
+      }
+    }
+    // route r's dot is D row r: lanes 16 * (r / 4) + j, register r % 4
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {
+      if (g == (uint32_t)(r >> 2))
+        red[wv][r][j] = acc[r][r & 3] * scale_cvt(sr[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
     }
   }
-
-  // 4. route r's dot is D row r: lanes 16 * (r / 4) + j, register r % 4
-#pragma unroll
-  for (int r = 0; r < KMAX; ++r) {
-    if (r < a.k && g == (uint32_t)(r >> 2))
-      red[wv][r][j] = acc[r][r & 3] * scale_cvt(sr[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
-  }
-  __syncthreads();
+  lds_barrier();
 
   // 5. weighted sum over routes and waves
   if (threadIdx.x < 16) {
     float o = 0.f;
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
-      if (wt[r] == 0.f) continue;
       float v = 0.f;
-      for (int w = 0; w < nw; ++w) v += red[w][r][threadIdx.x];
-      o = fmaf(wt[r], v, o);
+      for (int w = 0; w < nwd; ++w) v += red[w][r][threadIdx.x];
+      o = wt[r] != 0.f ? fmaf(wt[r], v, o) : o;
     }
     if (bad) o = __builtin_nanf("");
     const size_t oi = n0 + threadIdx.x;
@@ -718,27 +764,27 @@ __global__ __launch_bounds__(512) void k_moe3_down(M3Args a) {
     else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;
     else ((float*)a.out)[oi] = o;
   }
+  wait_vm<0>();  // no DMA into this block's LDS may outlive it
 }
 
 // ------------------------------------------------------------------ v3: router + gate/up in one launch
 //
 // One block per 3 q-tiles (1024 threads; the table takes 128 KiB of LDS, so
 // one block per CU) runs, for one token:
-//   1. the dual top-k router, block-parallel (same selection and weights as
-//      k_router; block 0 publishes the router outputs);
-//   2. the activation-kind table and the token DMA'd into LDS, then the gate/
-//      up scales and codes;
+//   0. the router's logits and biases loaded, then the activation-kind table
+//      and the token DMA'd into LDS while
+//   1. the dual top-k router runs, block-parallel (same selection and weights
+//      as k_router; block 0 publishes the router outputs);
+//   2. the gate/up scales and codes of this block's tiles;
 //   3. gate/up on the matrix cores one tile at a time as its codes arrive,
-//      SwiGLU, h stored to h_work (bf16);
-// and, while gate/up decodes, pulls the down rows that the same-numbered
-// block of the down launch will read through the caches (the 256 MB Infinity
-// Cache holds them), so the down launch streams from cache instead of HBM.
+//      SwiGLU, h stored to h_work (bf16).
 // A grid-wide barrier inside one launch was measured at 5+ us per use on
 // MI355X (device-scope atomics or flag polls across XCDs), no cheaper than a
 // launch boundary, so down stays a second launch (k_moe3_down).
 // Requires H = 4096 (16 waves x 256-element K slices) and k <= 8.
 
-constexpr int M3L_UNION = 1544;  // uint4: max(token 512, k * (I/8 + 1) h chunks, reduction 2048 floats)
+// uint4: the routing scratch of 16 waves, later 16 x NT x 16 floats of gate/up partials
+constexpr int M3L_SCRATCH = rt_scratch_units(16, 8);
 
 struct M3Layer {
   const float* logits;
@@ -753,55 +799,59 @@ struct M3Layer {
   uint8_t* admit_out;
   const void* x;
   int32_t H, I;
-  const uint16_t *gc, *uc, *dc;
-  const void *gs, *us, *ds;
+  const uint16_t *gc, *uc;
+  const void *gs, *us;
   int sdt;
-  int32_t Gh, gsz_h, Gi, gsz_i;
+  int32_t Gh, gsz_h;
   const uint4* xt_x;  // expanded table in the activation pair kind
-  const uint4* xt_h;  // expanded table in bf16
   float limit;
   uint16_t* h;  // [k, I] bf16
   int32_t qtiles;
-  int32_t down_blocks;  // H / 16: blocks of the down launch
 };
 
-// Block barrier for LDS traffic only: unlike __syncthreads it does not wait
-// for this wave's outstanding global loads (the code stream keeps flowing).
-__device__ __forceinline__ void lds_barrier() { rt_lds_barrier(); }
-
 template <int PK, int NT, int KMAX>
-__global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
+__global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer args) {
+  M3Layer a{};
+  a.logits = pinned(args.logits); a.bias_s = pinned(args.bias_s); a.bias_d = pinned(args.bias_d);
+  a.func = pinned(args.func); a.renorm = pinned(args.renorm); a.same_bias = pinned(args.same_bias);
+  a.route_scale = pinned(args.route_scale); a.tau = pinned(args.tau); a.E = pinned(args.E); a.k = pinned(args.k);
+  a.idx_out = pinned(args.idx_out); a.w_out = pinned(args.w_out); a.want_out = pinned(args.want_out);
+  a.want_score_out = pinned(args.want_score_out); a.admit_out = pinned(args.admit_out); a.x = pinned(args.x);
+  a.H = pinned(args.H); a.I = pinned(args.I); a.gc = pinned(args.gc); a.uc = pinned(args.uc);
+  a.gs = pinned(args.gs); a.us = pinned(args.us); a.sdt = pinned(args.sdt); a.Gh = pinned(args.Gh);
+  a.gsz_h = pinned(args.gsz_h); a.xt_x = pinned(args.xt_x); a.limit = pinned(args.limit); a.h = pinned(args.h);
+  a.qtiles = pinned(args.qtiles);
   __shared__ uint4 tab4[XT_BYTES / 16];
-  // uni: [0, 512) the token, [512, ...) routing scratch, [1024, ...) gate/up
-  // partials; later the h rows of every route and then the down partials.
-  __shared__ uint4 uni[M3L_UNION];
+  __shared__ uint4 xsh[512];               // the token (H = 4096)
+  __shared__ uint4 scr[M3L_SCRATCH];       // routing scratch, then the gate/up partials
   __shared__ int32_t s_idx[KMAX];
-  __shared__ float s_w[KMAX];
-  // 1 KiB that only the cache-warming DMA writes; an object of its own so the
-  // compiler sees that LDS reads of the other arrays never wait for it
-  __shared__ uint4 sink[64];
   constexpr int QT = NT / 2;
+  static_assert(16 * NT * 16 <= 4 * M3L_SCRATCH, "gate/up partials exceed the scratch");
   const char* tab = (const char*)tab4;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t j = lane & 15, g = lane >> 4;
   const uint32_t C = (uint32_t)a.H >> 3;  // 512 token chunks
-  const uint32_t Ci = (uint32_t)a.I >> 3;
-  float* gred = (float*)(uni + 1024);  // [16 waves][NT][16]
 
-  // 1. routing (its three inputs are the only loads in flight). Plain loads
-  //    only in this kernel: the compiler counts every wait exactly, which it
-  //    cannot do for a load issued ahead of LDS DMA (it waits for everything).
-  float* rsc = (float*)(uni + 512);
-  RtCand* rcand = (RtCand*)(uni + 512 + 276);
-  RtCand* rres = rcand + 2 * 16 * 8;
+  // 0. the router's inputs (one expert per thread) are the first loads; the
+  //    table (8 ops per wave) and the token (1; waves 8..15 repeat 0..7's
+  //    piece) stream in behind them while routing runs
   const RtInput rin = rt_input_load(a.logits, a.bias_s, a.bias_d, a.E);
-  const RouteLane r = rt_route_block(rin, a.bias_s != nullptr, a.bias_d != nullptr, a.E, a.k, a.func, a.renorm,
-                                     a.route_scale, a.tau, a.same_bias != 0, rsc, rcand, rres);
-  if (wv == 0 && r.valid) {
-    s_idx[lane] = r.expert;
-    s_w[lane] = r.value;
+  const uint32_t rot = xt_rotation();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t piece = ((uint32_t)(i * 16 + wv) + rot) & 127u;
+    dma16(a.xt_x + piece * 64 + lane, tab4 + piece * 64);
   }
+  dma16((const uint4*)a.x + (wv & 7) * 64 + lane, xsh + (wv & 7) * 64);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 1. routing
+  const RouteLane r = rt_route_block<16, KMAX>(rin, a.bias_s != nullptr, a.bias_d != nullptr, a.E, a.k, a.func,
+                                                a.renorm, a.route_scale, a.tau, a.same_bias != 0,
+                                                rt_scratch(scr, 16, KMAX));
+  wait_vm<0>();  // this wave's table and token DMAs (long done: routing waited on its inputs behind them)
+  if (wv == 0 && r.valid) s_idx[lane] = r.expert;
   if (blockIdx.x == 0 && r.valid) {
     if (wv == 0) {
       a.idx_out[lane] = r.expert;
@@ -812,35 +862,10 @@ __global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
       if (a.admit_out) a.admit_out[lane] = r.admit;
     }
   }
-  lds_barrier();
-  // the activation table and the token, DMA'd straight into LDS ahead of the
-  // code stream: exactly 9 ops per wave (waves 8..15 repeat 0..7's token piece)
-#pragma unroll
-  for (int i = 0; i < 8; ++i) dma16(a.xt_x + (i * 16 + wv) * 64 + lane, tab4 + (i * 16 + wv) * 64);
-  dma16((const uint4*)a.x + (wv & 7) * 64 + lane, uni + (wv & 7) * 64);
-  // warm the caches with the down rows of the same-numbered down block: per
-  // route, rows [16 b, 16 b + 16) are 16 * I/8 contiguous codewords = I/32
-  // pieces of 1 KiB (one DMA op each), all into a write-only sink. Every wave
-  // issues exactly KMAX/2 ops (unused slots repeat a valid piece), so the
-  // compiler's waits stay exact. They go ahead of the gate/up scale and code
-  // loads: a plain load is only waited for exactly when no DMA issued after
-  // it is still pending (else the compiler waits for everything).
-  {
-    const uint32_t per_route = Ci / 32u, npieces = (uint32_t)a.k * per_route;
-    const uint32_t db = blockIdx.x % (uint32_t)a.down_blocks;
-#pragma unroll
-    for (int i = 0; i < (KMAX + 1) / 2; ++i) {
-      uint32_t p = (uint32_t)wv + 16u * i;
-      p = p < npieces ? p : p % npieces;
-      const uint32_t route = p / per_route, piece = p - route * per_route;
-      const int32_t e = s_idx[route];
-      const uint32_t ee = e >= 0 && e < a.E ? (uint32_t)e : 0u;
-      dma16((const uint4*)(a.dc + ((size_t)ee * (uint32_t)a.H + db * 16u) * Ci) + piece * 64 + lane, sink);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();  // s_idx, and every wave's table and token pieces, visible to all
 
-  // 2. the gate/up tiles of this block
+  // 2. this block's gate/up tiles: scales first (they must not queue behind
+  //    the code stream), then codes
   uint32_t rbase[QT];
 #pragma unroll
   for (int u = 0; u < QT; ++u) {
@@ -852,7 +877,6 @@ __global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
     const bool ok = valid && e >= 0 && e < a.E;
     rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
   }
-  // scales first (they must not queue behind the code stream), then codes
   const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
   ScaleRaw sr[NT];
 #pragma unroll
@@ -870,13 +894,13 @@ __global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
     q[2 * u + 1] = *(const uint4*)(a.uc + off);
   }
   __builtin_amdgcn_sched_barrier(0);
-  wait_vm<2 * QT + NT>();  // the DMAs, not the scale and code loads behind them
-  lds_barrier();
 
-  // 3. gate/up, one tile at a time as its codes arrive; the token's 8 chunks stay in registers
+  // 3. gate/up, one tile at a time as its codes arrive (no block barrier: each
+  //    wave starts on its own first tile); the token's 8 chunks stay in registers
+  float* gred = (float*)scr;  // [16 waves][NT][16]; the routing scratch is dead
   uint4 A[8];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) A[m] = permuted(uni[kc0 + m]);
+  for (int m = 0; m < 8; ++m) A[m] = permuted(xsh[kc0 + m]);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     m3f4_t acc = m3f4_t{0.f, 0.f, 0.f, 0.f};
@@ -889,7 +913,7 @@ __global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
     const uint32_t si = (rbase[t >> 1] + j) * (uint32_t)a.Gh + grp;
     if (lane < 16) gred[(wv * NT + t) * 16 + j] = acc[0] * scale_cvt(sr[t], a.sdt, si);
   }
-  lds_barrier();  // activation table and token no longer read; partials visible
+  lds_barrier();
   if (wv == 0 && lane < QT * 16) {
     const uint32_t u = lane >> 4, jj = lane & 15;
     const uint32_t qt = blockIdx.x * QT + u;
@@ -904,8 +928,6 @@ __global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
       if (e >= 0 && e < a.E) a.h[q0 + jj] = from_float<bf16s>(silu_mul(gsum, usum, a.limit)).bits;
     }
   }
-
-  wait_vm<0>();  // no DMA into this block's LDS may outlive it
 }
 
 // ------------------------------------------------------------------ host
@@ -1054,7 +1076,7 @@ void moe_v3_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t H
   }
   if (down) {
     a.xt = (const uint4*)((const char*)prepared + XT_BYTES);
-    const dim3 grid((unsigned)(H / 16)), blk((unsigned)(I / 256 * 64));
+    const dim3 grid((unsigned)(H / 16)), blk(512u);
     switch (k) {
       case 1: hipLaunchKernelGGL((k_moe3_down<1>), grid, blk, 0, s, a); break;
       case 2: hipLaunchKernelGGL((k_moe3_down<2>), grid, blk, 0, s, a); break;
@@ -1087,14 +1109,11 @@ int moe_v3_layer_launch(const float* logits, const float* bias_s, const float* b
   a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
   a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
   a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
-  a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.dc = dc; a.gs = gs; a.us = us; a.ds = ds;
-  a.sdt = sdt; a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h; a.Gi = (int32_t)(I / group_i);
-  a.gsz_i = (int32_t)group_i;
+  a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.gs = gs; a.us = us;
+  a.sdt = sdt; a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h;
   a.xt_x = (const uint4*)((const char*)prepared + (x_dtype == KEEP_BF16 ? XT_BYTES : 0));
-  a.xt_h = (const uint4*)((const char*)prepared + XT_BYTES);
   a.limit = limit; a.h = (uint16_t*)h;
   a.qtiles = (int32_t)(k * I / 16);
-  a.down_blocks = (int32_t)(H / 16);
   const int qt = (int)((a.qtiles + 255) / 256);
   const dim3 grid((unsigned)((a.qtiles + qt - 1) / qt)), blk(1024);
 #define LY(PK, NT, KM) hipLaunchKernelGGL((k_moe3_route_gateup<PK, NT, KM>), grid, blk, 0, s, a)

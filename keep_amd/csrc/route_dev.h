@@ -227,13 +227,16 @@ __device__ __forceinline__ void rt_load(const float* lrow, const float* bias_s, 
 // ---------------------------------------------------------------- block-parallel form
 //
 // The same routing with one thread per expert (expert t = threadIdx.x, so
-// E <= blockDim.x): every wave keeps the top-k of its 64 experts, then wave 0
-// merges the waves' lists for the served selection and wave 1 for the demand
-// one. A selection round is a DPP max of an order-preserving 32-bit form of
-// the key plus one ballot: among equal keys the lowest lane holds the lowest
-// expert index, so the tie rule costs nothing in the per-wave step. The
-// softmax sum is accumulated in rt_route's order (per lane over e = lane +
-// 64*i, then the DPP tree), so every output is bit-identical to rt_route's.
+// E <= blockDim.x, k <= 8). A selection ranks instead of repeating arg-max
+// rounds: every thread counts how many experts of its own wave beat it under
+// the total order (a 64-bit key: the order-preserving 32-bit form of the
+// score + bias above the inverted expert index, so "larger key, then lower
+// index" is a plain unsigned compare). Local ranks below k are the wave's
+// candidates, stored at slot wave * k + rank; one wave per selection then
+// ranks the waves' candidates the same way, and rank j < k is slot j. The
+// depth is 64 + nwaves * k compares, with no serial chain of reductions.
+// The softmax sum is accumulated in rt_route's order (per lane over e = lane
+// + 64*i, then the DPP tree), so every output is bit-identical to rt_route's.
 
 // Block barrier for LDS traffic only (does not wait for outstanding global loads).
 __device__ __forceinline__ void rt_lds_barrier() {
@@ -243,41 +246,57 @@ __device__ __forceinline__ void rt_lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Larger key -> larger value; NaN ranks as -inf; 0 means "no candidate".
+// Larger key -> larger value; NaN ranks as -inf; 0 is below every key.
 __device__ __forceinline__ uint32_t rt_sortable(float key) {
   if (key != key) key = -__builtin_inff();
   const uint32_t b = __float_as_uint(key + 0.0f);  // -0 -> +0
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-__device__ __forceinline__ uint32_t rt_wave_max_u32(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
-  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-  return max(max(a, b), max(c, d));
-}
-
-__device__ __forceinline__ uint32_t rt_wave_min_u32(uint32_t v) {
-  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0xB1, 0xF, 0xF, false));
-  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x4E, 0xF, 0xF, false));
-  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x141, 0xF, 0xF, false));
-  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)v, 0x140, 0xF, 0xF, false));
-  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-  return min(min(a, b), min(c, d));
+// Total order of the selection: larger key first, then lower expert index.
+// Threads without an expert get key 0 (below every real key), still distinct.
+__device__ __forceinline__ uint64_t rt_rank_key(uint32_t sortable, int expert) {
+  return ((uint64_t)sortable << 32) | (uint64_t)(0xffffffffu - (uint32_t)expert);
 }
 
 struct RtCand {
-  float key, s, b;  // selection key, score, served bias
-  int idx;          // expert (INT_MAX: padding)
+  uint32_t key;  // sortable selection key (rt_sortable)
+  float s, b;    // score, served bias
+  int idx;       // expert
 };
 
-// Loads thread t's logit and biases unconditionally (a missing bias reads the
-// logits and is ignored), so the number of loads is fixed; issue it before
-// any other vector memory traffic the routing must not wait for.
+// LDS scratch of rt_route_block<NW, KMAX>: five disjoint 16-byte aligned arrays.
+struct RtScratch {
+  float* sc;       // 64 * NW + 16 floats: exp values, then the wave maxima
+  uint64_t* keys;  // 64 * NW rank keys
+  RtCand* cand;    // 2 * NW * KMAX candidates
+  uint64_t* ckey;  // their rank keys
+  RtCand* res;     // 2 * 8 winners
+};
+// Its size in 16-byte units, and the carving of one such buffer.
+constexpr int rt_scratch_units(int nw, int kmax) {
+  return (64 * nw + 16) / 4 + 64 * nw / 2 + 2 * nw * kmax + nw * kmax + 16;
+}
+__device__ __forceinline__ RtScratch rt_scratch(uint4* base, int nw, int kmax) {
+  RtScratch m;
+  m.sc = (float*)base;
+  base += (64 * nw + 16) / 4;
+  m.keys = (uint64_t*)base;
+  base += 64 * nw / 2;
+  m.cand = (RtCand*)base;
+  base += 2 * nw * kmax;
+  m.ckey = (uint64_t*)base;
+  base += nw * kmax;
+  m.res = (RtCand*)base;
+  return m;
+}
+
+__device__ __forceinline__ uint64_t rt_u64_lo(uint4 v) { return ((uint64_t)v.y << 32) | v.x; }
+__device__ __forceinline__ uint64_t rt_u64_hi(uint4 v) { return ((uint64_t)v.w << 32) | v.z; }
+
+// Thread t's logit and biases (expert t), loaded unconditionally (address
+// clamped, a missing bias reads the logits and is ignored) so that the number
+// of loads is fixed and nothing waits for them until the routing starts.
 struct RtInput {
   float z, bs, bd;
 };
@@ -287,87 +306,95 @@ __device__ __forceinline__ RtInput rt_input_load(const float* lrow, const float*
   return RtInput{lrow[i], (bias_s ? bias_s : lrow)[i], (bias_d ? bias_d : lrow)[i]};
 }
 
-// Scratch in LDS: sc[64 * nwaves + 17] floats, cand[2 * nwaves * k] records,
-// res[2 * 8] records (k <= 8).
+// Rank of `mine` among 8 * NB rank keys at p, the first valid_n of them
+// counted (independent counters, so the compares do not form one chain).
+template <int NB>
+__device__ __forceinline__ uint32_t rt_count_greater(const uint64_t* p, uint64_t mine, int valid_n) {
+  uint4 q[4 * NB];
+#pragma unroll
+  for (int h = 0; h < 4 * NB; ++h) q[h] = *(const uint4*)(p + 2 * h);
+  uint32_t c[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int h = 0; h < 4 * NB; ++h) {
+    c[h & 3] += (2 * h < valid_n && rt_u64_lo(q[h]) > mine ? 1u : 0u) +
+                (2 * h + 1 < valid_n && rt_u64_hi(q[h]) > mine ? 1u : 0u);
+  }
+  return (c[0] + c[1]) + (c[2] + c[3]);
+}
+
+template <int NW, int KMAX>
 __device__ __forceinline__ RouteLane rt_route_block(RtInput x, bool has_bs, bool has_bd, int E, int k, int func,
                                                    int renorm, float route_scale, float tau, bool same_bias,
-                                                   float* sc, RtCand* cand, RtCand* res) {
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, nwb = blockDim.x >> 6;
+                                                   RtScratch m) {
+  static_assert(NW % 4 == 0 && NW <= 16 && KMAX <= 8, "block router shape");
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int nwe = (E + 63) >> 6;  // waves that hold experts
-  float* part = sc + 64 * nwb;
   const bool in = t < E;
   const float z = in ? x.z : -__builtin_inff();
-  const float bs = in && has_bs ? x.bs : 0.f;
-  const float bd = in && has_bd ? x.bd : 0.f;
-  float s;
+  const float bsw = in && has_bs ? x.bs : 0.f;
+  const float bdw = in && has_bd ? x.bd : 0.f;
+  float sw;
   if (func == KEEP_SCORE_SOFTMAX) {
+    float* part = m.sc + 64 * NW;
     const float wm = rt_wave_reduce(z, true);
     if (lane == 0) part[w] = wm;
     rt_lds_barrier();
-    float m = part[0];
-    for (int i = 1; i < nwb; ++i) m = fmaxf(m, part[i]);
-    const float e = in ? expf(z - m) : 0.f;
-    sc[t] = e;
-    rt_lds_barrier();
-    if (w == 0) {
-      float p = 0.f;
-      for (int i = 0; i < nwe; ++i) p += sc[lane + 64 * i];
-      const float sum = rt_wave_reduce(p, false);
-      if (lane == 0) part[16] = sum;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < NW; i += 4) {
+      const float4 q = *(const float4*)(part + i);
+      mx = fmaxf(mx, fmaxf(fmaxf(q.x, q.y), fmaxf(q.z, q.w)));
     }
+    const float e = in ? expf(z - mx) : 0.f;
+    m.sc[t] = e;
     rt_lds_barrier();
-    s = e / part[16];
+    // every wave forms the sum itself, in rt_route's order (sc is 0 past E)
+    float v[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) v[i] = m.sc[lane + 64 * i];
+    float p = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) p += v[i];
+    const float sum = rt_wave_reduce(p, false);
+    sw = e / sum;
   } else {
-    s = rt_score_of(z, func);
+    sw = rt_score_of(z, func);
   }
-  // per-wave top-k, served (sel 0) and demand (sel 1)
+  // wave w < nwe ranks its slice, experts 64 w + lane: served (sel 0), then
+  // demand (sel 1); candidates packed at sel * NW * KMAX + w * k + rank
   const int nsel = same_bias ? 1 : 2;
-  const RtCand pad{-__builtin_inff(), 0.f, 0.f, 0x7fffffff};
-  for (int sel = 0; sel < nsel; ++sel) {
-    const float key = s + (sel == 0 ? bs : bd);
-    uint32_t sk = in ? rt_sortable(key) : 0u;
-    for (int j = 0; j < k; ++j) {
-      const uint32_t m = rt_wave_max_u32(sk);
-      RtCand* dst = cand + (sel * nwb + w) * k + j;
-      if (m == 0u) {
-        if (lane == 0) *dst = pad;
-        continue;
+  if (w < nwe) {
+    uint64_t* kw = m.keys + 64 * w;
+    for (int sel = 0; sel < nsel; ++sel) {
+      const uint32_t sk = in ? rt_sortable(sw + (sel == 0 ? bsw : bdw)) : 0u;
+      const uint64_t mine = rt_rank_key(sk, t);
+      kw[lane] = mine;  // read back only by this wave, after the write (in order)
+      uint32_t rank = 0;
+#pragma unroll
+      for (int u = 0; u < 64; u += 16) rank += rt_count_greater<2>(kw + u, mine, 64 - u);
+      if (rank < (uint32_t)k) {
+        const int slot = sel * NW * KMAX + w * k + (int)rank;
+        m.cand[slot] = RtCand{sk, sw, bsw, in ? t : 0x7fffffff};
+        m.ckey[slot] = mine;
       }
-      const uint64_t bal = __ballot(sk == m);
-      if (lane == (int)__builtin_ctzll(bal)) {
-        *dst = RtCand{key, s, bs, t};
-        sk = 0u;
-      }
+      __builtin_amdgcn_wave_barrier();
     }
   }
   rt_lds_barrier();
-  // merge: wave 0 served, wave 1 demand (2 candidates per lane, nwb * k <= 128)
+  // merge: wave 0 served, wave 1 demand; nc = nwe * k candidates, 16 per step
   if (w < nsel) {
-    const int nc = nwb * k;
-    RtCand c0 = lane < nc ? cand[w * nc + lane] : pad;
-    RtCand c1 = lane + 64 < nc ? cand[w * nc + lane + 64] : pad;
-    uint32_t s0 = c0.idx != 0x7fffffff ? rt_sortable(c0.key) : 0u;
-    uint32_t s1 = c1.idx != 0x7fffffff ? rt_sortable(c1.key) : 0u;
-    for (int j = 0; j < k; ++j) {
-      const bool first = s0 > s1 || (s0 == s1 && c0.idx < c1.idx);
-      const uint32_t ls = first ? s0 : s1;
-      const int li = first ? c0.idx : c1.idx;
-      const uint32_t m = rt_wave_max_u32(ls);
-      if (m == 0u) {
-        if (lane == 0) res[w * 8 + j] = pad;
-        continue;
-      }
-      const uint64_t bal = __ballot(ls == m);
-      const uint32_t win = __builtin_popcountll(bal) == 1
-                               ? (uint32_t)__builtin_amdgcn_readlane(li, (int)__builtin_ctzll(bal))
-                               : rt_wave_min_u32(ls == m ? (uint32_t)li : 0xffffffffu);
-      if (ls == m && (uint32_t)li == win) {
-        // field-wise select: a select of whole structs goes through private memory
-        res[w * 8 + j] = RtCand{first ? c0.key : c1.key, first ? c0.s : c1.s, first ? c0.b : c1.b, li};
-        if (first) s0 = 0u;
-        else s1 = 0u;
-      }
+    const int nc = nwe * k;
+    const uint64_t* ck = m.ckey + w * NW * KMAX;
+    const uint64_t mine0 = lane < nc ? ck[lane] : 0u;
+    const uint64_t mine1 = lane + 64 < nc ? ck[lane + 64] : 0u;
+    uint32_t r0 = 0, r1 = 0;
+    for (int u = 0; u < nc; u += 16) {
+      r0 += rt_count_greater<2>(ck + u, mine0, nc - u);
+      if (nc > 64) r1 += rt_count_greater<2>(ck + u, mine1, nc - u);
     }
+    const RtCand* cw = m.cand + w * NW * KMAX;
+    if (lane < nc && r0 < (uint32_t)k) m.res[w * 8 + (int)r0] = cw[lane];
+    if (lane + 64 < nc && r1 < (uint32_t)k) m.res[w * 8 + (int)r1] = cw[lane + 64];
   }
   rt_lds_barrier();
   RouteLane r;
@@ -377,15 +404,20 @@ __device__ __forceinline__ RouteLane rt_route_block(RtInput x, bool has_bs, bool
   r.admit = 0;
   if (w < 2 && lane < k) {
     const int src = (w == 1 && same_bias) ? 0 : w;
-    const RtCand c = res[src * 8 + lane];
+    RtCand o[KMAX];
+#pragma unroll
+    for (int q = 0; q < KMAX; ++q) o[q] = m.res[src * 8 + q];
+    const RtCand c = m.res[src * 8 + lane];
     const bool valid = c.idx >= 0 && c.idx < E;
     const bool absent = valid && c.b <= RT_MASKED;
     float tot = 0.f;  // sequential over slots, as rt_route
-    for (int q = 0; q < k; ++q) {
-      const RtCand o = res[src * 8 + q];
-      const bool ov = o.idx >= 0 && o.idx < E;
-      if (w == 0) tot += (ov && !(o.b <= RT_MASKED)) ? o.s : 0.f;
-      else tot += ov ? o.s : 0.f;
+#pragma unroll
+    for (int q = 0; q < KMAX; ++q) {
+      if (q < k) {
+        const bool ov = o[q].idx >= 0 && o[q].idx < E;
+        if (w == 0) tot += (ov && !(o[q].b <= RT_MASKED)) ? o[q].s : 0.f;
+        else tot += ov ? o[q].s : 0.f;
+      }
     }
     r.valid = valid;
     r.expert = valid ? c.idx : 0;
