@@ -624,23 +624,13 @@ __global__ __launch_bounds__(1024) void k_moe3_gateup(M3Args a) {
 }
 
 // Block: 16 output rows (blockIdx.x * 16 ..) over every route; I / 256 waves.
-// Kernel arguments are fetched through the scalar cache on first use; a
-// field first used deep in a kernel costs a cold miss right there (about a
-// microsecond when the argument block's line is not cached). pinned() copies
-// a field into scalar registers at the point it is called, so every field
-// is fetched in one batch at kernel start.
-template <typename T>
-__device__ __forceinline__ T pinned(T v) {
-  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "scalar argument");
-  if constexpr (sizeof(T) == 8) {
-    uint64_t u = __builtin_bit_cast(uint64_t, v);
-    asm volatile("" : "+s"(u));
-    return __builtin_bit_cast(T, u);
-  } else {
-    uint32_t u = __builtin_bit_cast(uint32_t, v);
-    asm volatile("" : "+s"(u));
-    return __builtin_bit_cast(T, u);
-  }
+// 16-byte load through the global address space (a pointer chosen at run time
+// would otherwise be a flat access, which the compiler must also count as
+// LDS traffic and so waits for far too conservatively).
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  const v4u v = *(const __attribute__((address_space(1))) v4u*)p;
+  return uint4{v.x, v.y, v.z, v.w};
 }
 
 // Block barrier for LDS traffic only: unlike __syncthreads it does not wait
@@ -655,12 +645,7 @@ __device__ __forceinline__ void lds_barrier() { rt_lds_barrier(); }
 __device__ __forceinline__ uint32_t xt_rotation() { return ((blockIdx.x >> 3) * 4u) & 127u; }
 
 template <int KMAX>
-__global__ __launch_bounds__(512) void k_moe3_down(M3Args args) {
-  M3Args a{};
-  a.H = pinned(args.H); a.I = pinned(args.I); a.E = pinned(args.E);
-  a.idx = pinned(args.idx); a.w = pinned(args.w); a.dc = pinned(args.dc); a.ds = pinned(args.ds);
-  a.sdt = pinned(args.sdt); a.Gi = pinned(args.Gi); a.gsz_i = pinned(args.gsz_i); a.xt = pinned(args.xt);
-  a.h = pinned(args.h); a.out = pinned(args.out); a.odt = pinned(args.odt);
+__global__ __launch_bounds__(512) void k_moe3_down(M3Args a) {
   __shared__ uint4 tab4[XT_BYTES / 16];
   __shared__ uint4 hsh[M3_HCHUNKS];  // route r's h at r * (I / 8 + 1): the pad spreads routes over banks
   __shared__ float red[8][KMAX][16];
@@ -717,34 +702,36 @@ __global__ __launch_bounds__(512) void k_moe3_down(M3Args args) {
   ScaleRaw sr[KMAX];
 #pragma unroll
   for (int r = 0; r < KMAX; ++r) sr[r] = scale_raw(a.ds, a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
+  // route r's codes are loaded PD routes ahead of its decode (see the gate/up kernel)
+  constexpr int PD = 3;
   uint4 q[KMAX];
+  auto load_route = [&](int r) { q[r] = ldg16(a.dc + (size_t)(dbase[r] + j) * C + kc0); };
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) q[r] = *(const uint4*)(a.dc + (size_t)(dbase[r] + j) * C + kc0);
+  for (int r = 0; r < PD && r < KMAX; ++r) load_route(r);  // every wave: the wait below counts them
   __builtin_amdgcn_sched_barrier(0);
-  wait_vm<2 * KMAX>();  // the table and h DMAs, not the scales and codes behind them
+  wait_vm<KMAX + (PD < KMAX ? PD : KMAX)>();  // the table and h DMAs, not the scales and codes behind them
   lds_barrier();
 
-  // 4. decode; A row i holds route i's h
+  // 4. decode, route by route; A row i holds route i's h
   if (dec) {
     const uint32_t ri = j < (uint32_t)KMAX ? j : 0u;
-    m3f4_t acc[KMAX];
+    uint4 A[8];
 #pragma unroll
-    for (int r = 0; r < KMAX; ++r) acc[r] = m3f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < 8; ++m) A[m] = permuted(hsh[ri * S + kc0 + m]);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const uint4 A = permuted(hsh[ri * S + kc0 + m]);
+    for (int r = 0; r < KMAX; ++r) {  // branch-free: zero-weight routes are dropped in the sum
+      if (r + PD < KMAX) load_route(r + PD);
+      __builtin_amdgcn_sched_barrier(0);
+      m3f4_t acc = m3f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < KMAX; ++r) {  // branch-free: zero-weight routes are dropped in the sum
+      for (int m = 0; m < 8; ++m) {
         const uint32_t wd = dword_of(q[r], m >> 1);
         const uint4 B = (m & 1) ? xt_decode<16>(tab, wd) : xt_decode<0>(tab, wd);
-        acc[r] = mfma16<PAIR_BF16>(A, B, acc[r]);
+        acc = mfma16<PAIR_BF16>(A[m], B, acc);
       }
-    }
-    // route r's dot is D row r: lanes 16 * (r / 4) + j, register r % 4
-#pragma unroll
-    for (int r = 0; r < KMAX; ++r) {
+      // route r's dot is D row r: lanes 16 * (r / 4) + j, register r % 4
       if (g == (uint32_t)(r >> 2))
-        red[wv][r][j] = acc[r][r & 3] * scale_cvt(sr[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
+        red[wv][r][j] = acc[r & 3] * scale_cvt(sr[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
     }
   }
   lds_barrier();
@@ -810,17 +797,7 @@ struct M3Layer {
 };
 
 template <int PK, int NT, int KMAX>
-__global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer args) {
-  M3Layer a{};
-  a.logits = pinned(args.logits); a.bias_s = pinned(args.bias_s); a.bias_d = pinned(args.bias_d);
-  a.func = pinned(args.func); a.renorm = pinned(args.renorm); a.same_bias = pinned(args.same_bias);
-  a.route_scale = pinned(args.route_scale); a.tau = pinned(args.tau); a.E = pinned(args.E); a.k = pinned(args.k);
-  a.idx_out = pinned(args.idx_out); a.w_out = pinned(args.w_out); a.want_out = pinned(args.want_out);
-  a.want_score_out = pinned(args.want_score_out); a.admit_out = pinned(args.admit_out); a.x = pinned(args.x);
-  a.H = pinned(args.H); a.I = pinned(args.I); a.gc = pinned(args.gc); a.uc = pinned(args.uc);
-  a.gs = pinned(args.gs); a.us = pinned(args.us); a.sdt = pinned(args.sdt); a.Gh = pinned(args.Gh);
-  a.gsz_h = pinned(args.gsz_h); a.xt_x = pinned(args.xt_x); a.limit = pinned(args.limit); a.h = pinned(args.h);
-  a.qtiles = pinned(args.qtiles);
+__global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
   __shared__ uint4 tab4[XT_BYTES / 16];
   __shared__ uint4 xsh[512];               // the token (H = 4096)
   __shared__ uint4 scr[M3L_SCRATCH];       // routing scratch, then the gate/up partials
@@ -885,14 +862,19 @@ __global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer args) {
     sr[2 * u] = scale_raw(a.gs, a.sdt, si);
     sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
   }
+  // codes: tile t's load is issued PD tiles ahead of its decode. A wave
+  // issues in order, so loading every tile up front would hold its decode
+  // back until the memory system had accepted all of them; this way the
+  // decode (LDS-bound) runs while the rest of the stream is in flight.
+  constexpr int PD = 3;
   const uint32_t kc0 = wv * 32 + g * 8;
   uint4 q[NT];
+  auto load_tile = [&](int t) {
+    const size_t off = (size_t)(rbase[t >> 1] + j) * C + kc0;
+    q[t] = ldg16(((t & 1) ? a.uc : a.gc) + off);
+  };
 #pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const size_t off = (size_t)(rbase[u] + j) * C + kc0;
-    q[2 * u] = *(const uint4*)(a.gc + off);
-    q[2 * u + 1] = *(const uint4*)(a.uc + off);
-  }
+  for (int t = 0; t < PD && t < NT; ++t) load_tile(t);
   __builtin_amdgcn_sched_barrier(0);
 
   // 3. gate/up, one tile at a time as its codes arrive (no block barrier: each
@@ -903,6 +885,8 @@ __global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer args) {
   for (int m = 0; m < 8; ++m) A[m] = permuted(xsh[kc0 + m]);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
+    if (t + PD < NT) load_tile(t + PD);
+    __builtin_amdgcn_sched_barrier(0);
     m3f4_t acc = m3f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
