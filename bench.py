@@ -42,7 +42,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-LAYER_KERNELS = ("k_moe3_route_gateup", "k_moe3_down")  # the two launches of one layer
+LAYER_KERNELS = ("k_moeq_route_gateup", "k_moeq_down")  # the two launches of one layer
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_layer_config2_counters.md")
 
 

@@ -125,10 +125,15 @@ int keep_vq_grouped_gemm(const void* x, int x_dtype, int64_t x_rows, const int32
                          int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
                          void* out, int out_dtype, void* stream);
 
-/* Expanded E8P table for the fused MoE decode kernels: 2 x 128 KiB (fp16 then
- * bf16), 16384 entries of four packed values each, addressed by
+/* Decode tables for the fused MoE kernels, built on the device from the
+ * 256-entry packed abs grid: at offset 0, 2 x 128 KiB expanded tables (fp16
+ * then bf16), 16384 entries of four packed values each, addressed by
  * (parity, abs index, 4 sign bits) so one decode is two lookups with the
- * signs, parity and +-1/4 shift already applied (src/keep/vq/e8.py:203-234).
+ * signs, parity and +-1/4 shift already applied (src/keep/vq/e8.py:203-234);
+ * at offset 256 KiB, the 4 KiB fp8 table (512 entries of 8 bytes, one per
+ * parity and abs index) the layer kernels decode straight into e4m3 MFMA
+ * operands, followed by a 256-byte word that is nonzero when the grid holds a
+ * value that table cannot express (the layer then writes NaN).
  * `prepared` must hold keep_e8p_prepared_bytes() bytes. No reference
  * counterpart: it replaces the per-threadgroup half2 pair decode of
  * src/ramp/kernels/e8p_m1.metal:36-45 at a larger scale. */

@@ -125,7 +125,7 @@ static std::array<uint32_t, 256> build_e8_1bit_table() {
 
 extern "C" const char* keep_last_error(void) { return keep::g_err; }
 
-extern "C" int keep_abi_version(void) { return 3; }
+extern "C" int keep_abi_version(void) { return 4; }
 
 extern "C" int keep_e8p_packed_abs_grid(uint32_t* out256) {
   if (!out256) {

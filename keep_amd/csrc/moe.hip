@@ -22,6 +22,7 @@
 // table to LDS and joins the barrier, so the HBM stream is in flight while
 // the table is staged. Lane reductions use DPP row ops plus readlane.
 #include "common.h"
+#include "moe_dev.h"
 #include "route_dev.h"
 
 namespace keep {
@@ -115,14 +116,6 @@ __device__ __forceinline__ float scale_of(const void* p, int dt, int64_t i) {
   return ((const float*)p)[i];
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u, float limit) {
-  if (limit > 0.f) {
-    g = fminf(g, limit);
-    u = fminf(fmaxf(u, -limit), limit);
-  }
-  return g / (1.f + __expf(-g)) * u;
-}
-
 struct MoeV2Args {
   const void* x;  // [T, H] fp16/bf16
   int32_t T, H, I, k, E;
@@ -161,28 +154,6 @@ __device__ __forceinline__ void table_dma(const uint4* g, uint4* tab4, int wv, i
 #pragma unroll
   for (int i = 0; i < XT_BYTES / 16 / MOE_THREADS; ++i)
     dma16(g + i * MOE_THREADS + wv * 64 + lane, tab4 + i * MOE_THREADS + wv * 64);
-}
-
-// Force a value into a vector register (keeps the load it feeds a vector load).
-__device__ __forceinline__ uint32_t vreg(uint32_t v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
-
-// Scales are fetched branch-free as the aligned 32-bit word holding element i
-// (one vector load whatever the dtype; an aligned word never crosses a page)
-// and converted after the LDS barrier.
-typedef uint32_t ScaleRaw;
-__device__ __forceinline__ ScaleRaw scale_raw(const void* p, int dt, uint32_t i) {
-  const uint32_t off = vreg(dt == KEEP_F32 ? i * 4u : i * 2u);
-  return *(const uint32_t*)((const char*)p + (off & ~3u));
-}
-__device__ __forceinline__ float scale_cvt(ScaleRaw word, int dt, uint32_t i) {
-  const uint32_t h = (word >> ((i & 1u) * 16u)) & 0xffffu;
-  const float f16 = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-  const float b16 = __uint_as_float(h << 16);
-  const float f32 = __uint_as_float(word);
-  return dt == KEEP_F32 ? f32 : (dt == KEEP_BF16 ? b16 : f16);
 }
 
 template <int CH>
@@ -1115,6 +1086,17 @@ int moe_v3_layer_launch(const float* logits, const float* bias_s, const float* b
   return 0;
 }
 
+// fp8 matrix-core layer (moe8.hip)
+void tq_build(const uint32_t* table, void* prepared, hipStream_t s);
+bool moe_q_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i);
+int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm,
+                        float route_scale, float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H,
+                        int64_t I, const uint16_t* gc, const void* gs, const uint16_t* uc, const void* us,
+                        const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
+                        const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                        uint8_t* admit, void* h, void* out, int odt, hipStream_t s);
+constexpr int PREPARED_TOTAL = 2 * XT_BYTES + 4096 + 256;  // expanded tables, int8 decode tables, flag word
+
 }  // namespace keep
 
 using namespace keep;
@@ -1126,14 +1108,15 @@ extern "C" int keep_e8p_prepare(const uint32_t* table, void* prepared, void* str
   hipLaunchKernelGGL((k_expand_table<PAIR_F16>), dim3(XT_ENTRIES / 256), dim3(256), 0, s, table, (uint2*)prepared);
   hipLaunchKernelGGL((k_expand_table<PAIR_BF16>), dim3(XT_ENTRIES / 256), dim3(256), 0, s, table,
                      (uint2*)((char*)prepared + XT_BYTES));
+  tq_build(table, prepared, s);
   return launch_status("keep_e8p_prepare");
 }
 
-extern "C" int keep_e8p_prepared_bytes(void) { return 2 * XT_BYTES; }
+extern "C" int keep_e8p_prepared_bytes(void) { return PREPARED_TOTAL; }
 
 extern "C" int keep_moe_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_size_h,
                                         int64_t group_size_i) {
-  return moe_v3_layer_supported(E, H, I, k, group_size_h, group_size_i) ? 1 : 0;
+  return moe_q_layer_supported(E, H, I, k, group_size_h, group_size_i) ? 1 : 0;
 }
 
 extern "C" int keep_moe_layer(const float* logits, const float* bias_served, const float* bias_demand, int score_func,
@@ -1149,7 +1132,7 @@ extern "C" int keep_moe_layer(const float* logits, const float* bias_served, con
   KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);
   KEEP_REQUIRE(group_size_h > 0 && H % group_size_h == 0 && group_size_i > 0 && I % group_size_i == 0,
                "bad group sizes");
-  KEEP_REQUIRE(moe_v3_layer_supported(E, H, I, k, group_size_h, group_size_i),
+  KEEP_REQUIRE(moe_q_layer_supported(E, H, I, k, group_size_h, group_size_i),
                "shape not served by the routed decode layer kernels (needs H = 4096, I a multiple of 512 up to "
                "2048, k <= 8, E <= 1024, scale groups of 256-element multiples)");
   KEEP_REQUIRE(logits && x && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
@@ -1158,7 +1141,7 @@ extern "C" int keep_moe_layer(const float* logits, const float* bias_served, con
   KEEP_REQUIRE(aligned(x, 16) && aligned(h_work, 16) && aligned(prepared, 16),
                "x, h_work and prepared must be 16-byte aligned");
   KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 8), "codes misaligned");
-  moe_v3_layer_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype,
+  moe_q_layer_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype,
                       H, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
                       group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, h_work,
                       out, out_dtype, (hipStream_t)stream);

@@ -1,0 +1,543 @@
+// Routed MoE decode layer for one token on the int8 matrix cores of gfx950
+// (v_mfma_i32_16x16x64_i8: exact int32 sums).
+//
+// Weights. Every decoded E8P weight is w = q / 4 with q an odd integer,
+// |q| <= 15 (src/keep/vq/e8.py:203-234: the value v / 2 of an odd packed
+// nibble v = nib - 8, negated when its effective sign bit is set, then +1/4
+// for even sign parity and -1/4 for odd), so q = 2 (+-v) + sigma is exact in
+// int8. Write v = 2a + 1 (a in -4..3): negating v maps a to ~a, and q = 4a' +
+// 2 + sigma is the byte (a' << 2) | (2 + sigma) in two's complement. With
+// T[idx] the 8 bytes 4a + 3 of the packed nibbles (no sign, even parity), a
+// codeword's 8 int8 weights, in packed-nibble order, are
+//   T[idx] ^ M[signs],  M[signs] byte s = (eff bit s ? 0xFC : 0) ^ (p ? 0x02 : 0),
+// p the parity of the sign byte and eff = signs ^ p (bit 0 flipped when p = 1).
+// That is two 8-byte lookups in 2 KiB tables and a few VALU per codeword
+// (keep_e8p_prepare builds both tables, 4 KiB, which every block stages in LDS).
+//
+// Activations. The A operand of a 16x16x64 int8 MFMA is 16 rows of 64 bytes.
+// A wave's 256-element slice of the token x (fp16 or bf16) is scaled by a
+// power of two s so that max |x| s lies in [32, 64), then split into int8
+// terms t0 + t1 / 128 + t2 / 128^2 (each a round-to-nearest of the scaled
+// remainder, so every |t| <= 64); A rows 0-2 are the three terms and the dot is
+// (D0 + D1 / 128 + D2 / 128^2) / (4 s). The residual is below 2^-21 of max |x|,
+// under the rounding of the fp32 sums. h (bf16) uses two terms (residual below
+// 2^-14 of its slice's max), so the down kernel puts route r's terms in rows
+// 2r and 2r + 1 (up to 8 routes). Each wave builds its terms once, in LDS.
+//
+// K layout. Lane l of an MFMA holds row (A) / column (B) l % 16 and 16 bytes
+// of k-block l / 16. A wave's 256-wide K slice is 32 codewords; lane group g
+// owns codewords 8g .. 8g + 7 (one 16-byte code load) and feeds codewords 2i,
+// 2i + 1 to MFMA i, i = 0..3. A rows use the same assignment, with the eight
+// values of a codeword in packed-nibble order (dims 0,2,4,6,1,3,5,7).
+#include "common.h"
+#include "moe_dev.h"
+#include "route_dev.h"
+
+namespace keep {
+
+constexpr int TQ_BYTES = 4096;  // T (256 x 8 bytes), then M (256 x 8 bytes)
+
+typedef int q8v4 __attribute__((ext_vector_type(4)));
+
+// T and M from the packed E8P table; flag[0] = 1 if a nibble is even (not an
+// E8P half-integer coordinate, so not of this form), else 0.
+__global__ __launch_bounds__(256) void k_build_tq(const uint32_t* packed, uint2* tq, uint32_t* flag) {
+  __shared__ uint32_t s_bad;
+  const int i = threadIdx.x;  // one block of 256 threads: abs index i, sign byte i
+  if (i == 0) s_bad = 0u;
+  __syncthreads();
+  const uint32_t word = packed[i];
+  const uint32_t p = (uint32_t)__builtin_popcount((uint32_t)i) & 1u;
+  const uint32_t eff = (uint32_t)i ^ p;
+  uint32_t t[2] = {0u, 0u}, m[2] = {0u, 0u};
+  bool ok = true;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int v = (int)((word >> (4 * s)) & 15u) - 8;
+    ok = ok && (v & 1) != 0;
+    const int av = (v - 1) >> 1;  // v = 2a + 1
+    const uint32_t tb = ((uint32_t)(av * 4 + 3)) & 0xffu;
+    const uint32_t mb = (((eff >> s) & 1u) ? 0xFCu : 0u) ^ (p ? 0x02u : 0u);
+    t[s >> 2] |= tb << (8 * (s & 3));
+    m[s >> 2] |= mb << (8 * (s & 3));
+  }
+  tq[i] = make_uint2(t[0], t[1]);
+  tq[256 + i] = make_uint2(m[0], m[1]);
+  if (!ok) s_bad = 1u;
+  __syncthreads();
+  if (i == 0) flag[0] = s_bad;
+}
+
+// The 8 int8 weights x 4 (packed-nibble order) of codeword c (low 16 bits).
+__device__ __forceinline__ uint2 q8_decode(const char* tq, uint32_t c) {
+  const uint2 t = *(const uint2*)(tq + ((c >> 5) & 0x7f8u));
+  const uint2 m = *(const uint2*)(tq + 2048 + ((c & 0xffu) << 3));
+  return make_uint2(t.x ^ m.x, t.y ^ m.y);
+}
+
+// B operands of one 16-byte code load (8 codewords): codewords 2i, 2i + 1 -> b[i].
+__device__ __forceinline__ void q8_decode8(const char* tq, uint4 q, q8v4 (&b)[4]) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint2 lo = q8_decode(tq, w[i] & 0xffffu), hi = q8_decode(tq, w[i] >> 16);
+    b[i] = q8v4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+  }
+}
+
+__device__ __forceinline__ q8v4 mfma_i8(q8v4 a, q8v4 b, q8v4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Power-of-two s with max_abs * s in [32, 64) (max_abs > 0), and 1 / (4 s);
+// NaN for a non-finite max_abs, so that it reaches the outputs.
+__device__ __forceinline__ void q8_scale(float max_abs, float& s, float& inv4s) {
+  const int e = max_abs > 0.f ? (int)((__float_as_uint(max_abs) >> 23) & 0xffu) - 126 : 0;  // max_abs < 2^e
+  const int es = min(max(127 + 6 - e, 1), 254), ei = min(max(127 - 8 + e, 1), 254);
+  s = __uint_as_float((uint32_t)es << 23);
+  inv4s = max_abs < __builtin_inff() ? __uint_as_float((uint32_t)ei << 23) : __builtin_nanf("");
+}
+
+__device__ __forceinline__ uint32_t q8_pack4(float a, float b, float c, float d) {
+  return ((uint32_t)(int)a & 0xffu) | (((uint32_t)(int)b & 0xffu) << 8) | (((uint32_t)(int)c & 0xffu) << 16) |
+         ((uint32_t)(int)d << 24);
+}
+
+// The four values of this lane in a 16-byte chunk of 8 fp16 / bf16 values:
+// dims 2t + half, t = 0..3 (packed-nibble positions 4 half + t).
+template <bool BF>
+__device__ __forceinline__ void q8_half4(uint4 c, uint32_t half, float (&v)[4]) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t hb = half ? (w[t] >> 16) : (w[t] & 0xffffu);
+    if constexpr (BF) v[t] = __uint_as_float(hb << 16);
+    else v[t] = (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+  }
+}
+
+// NTERM int8 terms of the four values v x s, packed four to a word.
+template <int NTERM>
+__device__ __forceinline__ void q8_terms(const float (&v)[4], float s, uint32_t (&out)[NTERM]) {
+  float y[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) y[t] = v[t] * s;
+#pragma unroll
+  for (int n = 0; n < NTERM; ++n) {
+    float r[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      r[t] = rintf(y[t]);
+      y[t] = (y[t] - r[t]) * 128.f;
+    }
+    out[n] = q8_pack4(r[0], r[1], r[2], r[3]);
+  }
+}
+
+// Word index in an A-term buffer of 16-byte slots [row][g * 4 + i] for the
+// lane writing chunk c (0..31 of the wave's slice), half `half`.
+__device__ __forceinline__ uint32_t q8_aword(uint32_t row, uint32_t c, uint32_t half) {
+  return (row * 16u + (c >> 3) * 4u + ((c & 7u) >> 1)) * 4u + (c & 1u) * 2u + half;
+}
+
+__device__ __forceinline__ uint4 ldg16_q(const void* p) {
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  const v4u v = *(const __attribute__((address_space(1))) v4u*)p;
+  return uint4{v.x, v.y, v.z, v.w};
+}
+
+__device__ __forceinline__ void dma16_q(const uint4* g, uint4* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0,
+                                   0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm_q() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// ------------------------------------------------------------------ router + gate/up
+
+struct MQLayer {
+  const float* logits;
+  const float *bias_s, *bias_d;
+  int func, renorm, same_bias;
+  float route_scale, tau;
+  int32_t E, k;
+  int32_t* idx_out;
+  float* w_out;
+  int32_t* want_out;
+  float* want_score_out;
+  uint8_t* admit_out;
+  const void* x;
+  int32_t H, I;
+  const uint16_t *gc, *uc;
+  const void *gs, *us;
+  int sdt;
+  int32_t Gh, gsz_h;
+  const uint4* tq;
+  const uint32_t* tq_bad;
+  float limit;
+  uint16_t* h;  // [k, I] bf16
+  int32_t qtiles;
+};
+
+// One block per NT / 2 q-tiles (16 rows of the [k, I] intermediate each), 16
+// waves, H = 4096 (a 256-wide K slice per wave). Waves 0 and 1 route
+// (rt_route_pair) while every wave builds its A terms; then gate/up one tile at
+// a time with its codes loaded three tiles ahead, SwiGLU, h in bf16.
+template <int NT, bool XBF, int PER>
+__global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
+  __shared__ uint4 tqs[TQ_BYTES / 16];
+  __shared__ uint4 ash[16 * 3 * 16];  // [wave][term][g * 4 + i]
+  __shared__ float gred[16 * NT * 16];
+  __shared__ int32_t s_idx[8];
+  constexpr int QT = NT / 2;
+  const char* tq = (const char*)tqs;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t j = lane & 15, g = lane >> 4;
+  const uint32_t C = (uint32_t)a.H >> 3;  // 512 token chunks
+
+  // 0. the router's inputs (waves 0, 1), the table (4 pieces; every wave loads
+  //    one) and this wave's token slice (16 bytes per lane pair)
+  float z[PER], bsv[PER], bdv[PER];
+  if (wv < 2) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
+  dma16_q(a.tq + (wv & 3) * 64 + lane, tqs + (wv & 3) * 64);
+  const uint4 xc = ldg16_q((const uint4*)a.x + wv * 32 + (lane >> 1));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 1. routing
+  RouteLane r;
+  r.valid = false;
+  r.expert = 0;
+  r.value = 0.f;
+  r.admit = 0;
+  if (wv < 2)
+    r = rt_route_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, a.renorm, a.route_scale, a.tau, a.same_bias != 0, wv,
+                           lane);
+  if (wv == 0 && r.valid) s_idx[lane] = r.expert;
+  if (blockIdx.x == 0 && r.valid) {
+    if (wv == 0) {
+      a.idx_out[lane] = r.expert;
+      a.w_out[lane] = r.value;
+    } else {
+      if (a.want_out) a.want_out[lane] = r.expert;
+      if (a.want_score_out) a.want_score_out[lane] = r.value;
+      if (a.admit_out) a.admit_out[lane] = r.admit;
+    }
+  }
+
+  // 2. A terms of this wave's slice: rows 0-2 are the three int8 terms of x s
+  float s, inv4s;
+  {
+    float v[4];
+    q8_half4<XBF>(xc, lane & 1, v);
+    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    q8_scale(rt_wave_reduce(mx, true), s, inv4s);
+    uint32_t tw[3];
+    q8_terms<3>(v, s, tw);
+    uint32_t* aw = (uint32_t*)ash;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) aw[q8_aword((uint32_t)(wv * 3 + n), lane >> 1, lane & 1)] = tw[n];
+  }
+  wait_vm_q<0>();  // this wave's table piece
+  rt_lds_barrier();  // s_idx, the table and every wave's A terms visible
+
+  // 3. this block's tiles: scales, then codes PD tiles ahead of their decode
+  uint32_t rbase[QT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const uint32_t qt = blockIdx.x * QT + u;
+    const bool valid = qt < (uint32_t)a.qtiles;
+    const uint32_t q0 = (valid ? qt : 0u) * 16u;
+    const uint32_t route = q0 / (uint32_t)a.I;
+    const int32_t e = s_idx[route];
+    const bool ok = valid && e >= 0 && e < a.E;
+    rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
+  }
+  const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
+  ScaleRaw sr[NT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
+    sr[2 * u] = scale_raw(a.gs, a.sdt, si);
+    sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
+  }
+  constexpr int PD = 3;
+  const uint32_t kc0 = wv * 32 + g * 8;
+  uint4 q[NT];
+  auto load_tile = [&](int t) {
+    const size_t off = (size_t)(rbase[t >> 1] + j) * C + kc0;
+    q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + off);
+  };
+#pragma unroll
+  for (int t = 0; t < PD && t < NT; ++t) load_tile(t);
+  __builtin_amdgcn_sched_barrier(0);
+
+  q8v4 A[4];
+  {
+    const q8v4* as = (const q8v4*)ash + (wv * 3 + (j < 3 ? j : 0)) * 16 + g * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const q8v4 v = as[i];
+      A[i] = j < 3 ? v : q8v4{0, 0, 0, 0};
+    }
+  }
+
+  // 4. gate/up, tile by tile
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (t + PD < NT) load_tile(t + PD);
+    __builtin_amdgcn_sched_barrier(0);
+    q8v4 B[4];
+    q8_decode8(tq, q[t], B);
+    q8v4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
+    const uint32_t si = (rbase[t >> 1] + j) * (uint32_t)a.Gh + grp;
+    if (lane < 16) {
+      const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
+      gred[(wv * NT + t) * 16 + j] = d * inv4s * scale_cvt(sr[t], a.sdt, si);
+    }
+  }
+  rt_lds_barrier();
+  if (wv == 0 && lane < QT * 16) {
+    const uint32_t u = lane >> 4, jj = lane & 15;
+    const uint32_t qt = blockIdx.x * QT + u;
+    float gsum = 0.f, usum = 0.f;
+    for (int w = 0; w < 16; ++w) {
+      gsum += gred[(w * NT + 2 * u) * 16 + jj];
+      usum += gred[(w * NT + 2 * u + 1) * 16 + jj];
+    }
+    if (qt < (uint32_t)a.qtiles) {
+      const uint32_t q0 = qt * 16u;
+      const int32_t e = s_idx[q0 / (uint32_t)a.I];
+      float hv = silu_mul(gsum, usum, a.limit);
+      if (*a.tq_bad) hv = __builtin_nanf("");
+      if (e >= 0 && e < a.E) a.h[q0 + jj] = from_float<bf16s>(hv).bits;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ down + combine
+
+struct MQDown {
+  int32_t H, I, E;
+  const int32_t* idx;
+  const float* w;
+  const uint16_t* dc;
+  const void* ds;
+  int sdt;
+  int32_t Gi, gsz_i;
+  const uint4* tq;
+  const uint32_t* tq_bad;
+  const uint16_t* h;  // [k, I] bf16
+  void* out;
+  int odt;
+};
+
+// One block per 16 output rows, 8 waves (I / 256 of them decode a 256-wide K
+// slice). A rows 2r and 2r + 1 hold the two int8 terms of route r's h slice
+// (x its own scale); route r's dot is D rows 2r, 2r + 1.
+template <int KMAX>
+__global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
+  static_assert(KMAX <= 8, "two A rows per route");
+  __shared__ uint4 tqs[TQ_BYTES / 16];
+  __shared__ uint4 ash[8 * 2 * KMAX * 16];  // [wave][2 r + term][g * 4 + i]
+  __shared__ float red[8][KMAX][16];
+  const char* tq = (const char*)tqs;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwd = a.I >> 8;
+  const bool dec = wv < nwd;  // wave-uniform
+  const uint32_t j = lane & 15, g = lane >> 4;
+  const uint32_t C = (uint32_t)a.I >> 3;
+  const uint32_t n0 = blockIdx.x * 16;
+
+  // 1. routes (scalar loads; KMAX == k), the table (4 pieces), this wave's h slices
+  typedef const __attribute__((address_space(4))) int32_t* cidx;
+  typedef const __attribute__((address_space(4))) float* cw;
+  int32_t e_r[KMAX];
+  float w_r[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    e_r[r] = ((cidx)a.idx)[r];
+    w_r[r] = ((cw)a.w)[r];
+  }
+  dma16_q(a.tq + (wv & 3) * 64 + lane, tqs + (wv & 3) * 64);
+  const uint32_t wslice = (dec ? wv : 0) * 32 + (lane >> 1);
+  uint4 hq[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) hq[r] = ldg16_q((const uint4*)(a.h + (size_t)r * a.I) + wslice);
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t dbase[KMAX];
+  float wt[KMAX];
+  bool bad = false;
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    const bool ok = e_r[r] >= 0 && e_r[r] < a.E;
+    bad |= w_r[r] != 0.f && !ok;
+    wt[r] = ok ? w_r[r] : 0.f;
+    dbase[r] = (ok ? (uint32_t)e_r[r] * (uint32_t)a.H : 0u) + n0;
+  }
+
+  // 2. scales and codes (route r loaded PD routes ahead of its decode)
+  const uint32_t kc0 = (dec ? wv : 0) * 32 + g * 8;
+  const uint32_t grp = (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.gsz_i;
+  ScaleRaw sr[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) sr[r] = scale_raw(a.ds, a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
+  constexpr int PD = 3;
+  uint4 q[KMAX];
+  auto load_route = [&](int r) { q[r] = ldg16_q(a.dc + (size_t)(dbase[r] + j) * C + kc0); };
+#pragma unroll
+  for (int r = 0; r < PD && r < KMAX; ++r) load_route(r);  // every wave: the wait below counts them
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm_q<KMAX + (PD < KMAX ? PD : KMAX)>();  // the table DMA and h loads, not the scales and codes
+
+  // 3. A terms: rows 2r, 2r + 1 of route r, scaled by the route's own power of two
+  float inv4s[KMAX];
+  {
+    uint32_t* aw = (uint32_t*)ash;
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {
+      float v[4];
+      q8_half4<true>(hq[r], lane & 1, v);
+      const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+      float s;
+      q8_scale(rt_wave_reduce(mx, true), s, inv4s[r]);
+      uint32_t tw[2];
+      q8_terms<2>(v, s, tw);
+      aw[q8_aword((uint32_t)(wv * 2 * KMAX + 2 * r), lane >> 1, lane & 1)] = tw[0];
+      aw[q8_aword((uint32_t)(wv * 2 * KMAX + 2 * r + 1), lane >> 1, lane & 1)] = tw[1];
+    }
+  }
+  rt_lds_barrier();  // the table and A terms visible
+
+  if (dec) {
+    q8v4 A[4];
+    {
+      const bool live = j < 2u * KMAX;
+      const q8v4* as = (const q8v4*)ash + (wv * 2 * KMAX + (live ? j : 0u)) * 16 + g * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const q8v4 v = as[i];
+        A[i] = live ? v : q8v4{0, 0, 0, 0};
+      }
+    }
+
+    // 4. decode route by route
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {  // branch-free: zero-weight routes are dropped in the sum
+      if (r + PD < KMAX) load_route(r + PD);
+      __builtin_amdgcn_sched_barrier(0);
+      q8v4 B[4];
+      q8_decode8(tq, q[r], B);
+      q8v4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
+      // rows 2r, 2r + 1 live in lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
+      if (g == (uint32_t)(r >> 1)) {
+        const float d = (r & 1) ? (float)acc[2] + (float)acc[3] * 0.0078125f
+                                : (float)acc[0] + (float)acc[1] * 0.0078125f;
+        red[wv][r][j] = d * inv4s[r] * scale_cvt(sr[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
+      }
+    }
+  }
+  rt_lds_barrier();
+
+  // 5. weighted sum over routes and waves
+  if (threadIdx.x < 16) {
+    float o = 0.f;
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {
+      float v = 0.f;
+      for (int w = 0; w < nwd; ++w) v += red[w][r][threadIdx.x];
+      o = wt[r] != 0.f ? fmaf(wt[r], v, o) : o;
+    }
+    if (bad || *a.tq_bad) o = __builtin_nanf("");
+    const size_t oi = n0 + threadIdx.x;
+    if (a.odt == KEEP_F16) ((_Float16*)a.out)[oi] = (_Float16)o;
+    else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;
+    else ((float*)a.out)[oi] = o;
+  }
+  wait_vm_q<0>();  // no DMA into this block's LDS may outlive it
+}
+
+// ------------------------------------------------------------------ host
+
+// Offsets in the prepared buffer (keep_e8p_prepare): the two 128 KiB
+// expanded tables, then T and M, then the flag word.
+constexpr size_t TQ_OFFSET = 2u * 131072u;
+constexpr size_t TQ_FLAG_OFFSET = TQ_OFFSET + TQ_BYTES;
+
+void tq_build(const uint32_t* table, void* prepared, hipStream_t s) {
+  hipLaunchKernelGGL(k_build_tq, dim3(1), dim3(256), 0, s, table, (uint2*)((char*)prepared + TQ_OFFSET),
+                     (uint32_t*)((char*)prepared + TQ_FLAG_OFFSET));
+}
+
+bool moe_q_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
+  const int64_t qtiles = k * I / 16;
+  return H == 4096 && I % 512 == 0 && I <= 2048 && k >= 1 && k <= 8 && k <= E && E <= 1024 &&
+         (qtiles + 255) / 256 <= 3 && group_h % 256 == 0 && group_i % 256 == 0;
+}
+
+void moe_q_down_launch(const int32_t* idx, const float* w, int64_t k, int64_t E, int64_t H, int64_t I,
+                       const uint16_t* dc, const void* ds, int sdt, int64_t group_i, const void* prepared,
+                       const void* h, void* out, int odt, hipStream_t s) {
+  MQDown d{};
+  d.H = (int32_t)H; d.I = (int32_t)I; d.E = (int32_t)E; d.idx = idx; d.w = w; d.dc = dc; d.ds = ds; d.sdt = sdt;
+  d.Gi = (int32_t)(I / group_i); d.gsz_i = (int32_t)group_i;
+  d.tq = (const uint4*)((const char*)prepared + TQ_OFFSET);
+  d.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
+  d.h = (const uint16_t*)h; d.out = out; d.odt = odt;
+  const dim3 grid((unsigned)(H / 16)), blk(512u);
+  switch (k) {
+    case 1: hipLaunchKernelGGL((k_moeq_down<1>), grid, blk, 0, s, d); break;
+    case 2: hipLaunchKernelGGL((k_moeq_down<2>), grid, blk, 0, s, d); break;
+    case 3: hipLaunchKernelGGL((k_moeq_down<3>), grid, blk, 0, s, d); break;
+    case 4: hipLaunchKernelGGL((k_moeq_down<4>), grid, blk, 0, s, d); break;
+    case 5: hipLaunchKernelGGL((k_moeq_down<5>), grid, blk, 0, s, d); break;
+    case 6: hipLaunchKernelGGL((k_moeq_down<6>), grid, blk, 0, s, d); break;
+    case 7: hipLaunchKernelGGL((k_moeq_down<7>), grid, blk, 0, s, d); break;
+    default: hipLaunchKernelGGL((k_moeq_down<8>), grid, blk, 0, s, d); break;
+  }
+}
+
+int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm,
+                       float route_scale, float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H,
+                       int64_t I, const uint16_t* gc, const void* gs, const uint16_t* uc, const void* us,
+                       const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
+                       const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                       uint8_t* admit, void* h, void* out, int odt, hipStream_t s) {
+  MQLayer a{};
+  a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
+  a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
+  a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
+  a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.gs = gs; a.us = us;
+  a.sdt = sdt; a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h;
+  a.tq = (const uint4*)((const char*)prepared + TQ_OFFSET);
+  a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
+  a.limit = limit; a.h = (uint16_t*)h;
+  a.qtiles = (int32_t)(k * I / 16);
+  const int qt = (int)((a.qtiles + 255) / 256);
+  const dim3 grid((unsigned)((a.qtiles + qt - 1) / qt)), blk(1024);
+#define LY(NT, BF, PER) hipLaunchKernelGGL((k_moeq_route_gateup<NT, BF, PER>), grid, blk, 0, s, a)
+#define LY_PER(NT, BF)                 \
+  if (E <= 256) LY(NT, BF, 4);         \
+  else if (E <= 384) LY(NT, BF, 6);    \
+  else if (E <= 512) LY(NT, BF, 8);    \
+  else LY(NT, BF, 16)
+#define LY_NT(BF) \
+  if (qt <= 1) { LY_PER(2, BF); } else if (qt == 2) { LY_PER(4, BF); } else { LY_PER(6, BF); }
+  if (x_dtype == KEEP_BF16) { LY_NT(true); } else { LY_NT(false); }
+#undef LY_NT
+#undef LY_PER
+#undef LY
+  moe_q_down_launch(idx, w, k, E, H, I, dc, ds, sdt, group_i, prepared, h, out, odt, s);
+  return 0;
+}
+
+}  // namespace keep

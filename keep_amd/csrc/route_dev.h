@@ -433,4 +433,111 @@ __device__ __forceinline__ RouteLane rt_route_block(RtInput x, bool has_bs, bool
   return r;
 }
 
+// ---------------------------------------------------------------- two-wave form
+//
+// The same routing on two waves of a block, with no LDS and no barrier: wave
+// 0 forms the served selection and wave 1 the demand selection (the served
+// one again when the biases are the same), each over all experts (lane l
+// holds e = l + 64 i, i < PER, as rt_route). A round takes the wave maximum of
+// the order-preserving 32-bit keys (rt_sortable; taken experts and lanes past
+// E hold 0, below every real key), then the lowest expert index holding it
+// from one ballot per slot, so a tie goes to the lower index as in rt_select;
+// the winner's key is cleared. Scores, sums and weights are formed in
+// rt_route's order, so every output is bit-identical to rt_route's. Result:
+// lane j < k of wave 0 holds served slot j, of wave 1 demand slot j.
+
+__device__ __forceinline__ uint32_t rt_wave_max_u32(uint32_t v) {
+#define RT_MAXU(CTRL) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false));
+  RT_MAXU(0xB1) RT_MAXU(0x4E) RT_MAXU(0x141) RT_MAXU(0x140)
+#undef RT_MAXU
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+
+__device__ __forceinline__ float rt_readlane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+template <int PER>
+__device__ __forceinline__ RouteLane rt_route_pair(const float (&z)[PER], const float (&bs)[PER],
+                                                  const float (&bd)[PER], int E, int k, int func, int renorm,
+                                                  float route_scale, float tau, bool same_bias, int wave,
+                                                  int lane) {
+  float s[PER];
+  if (func == KEEP_SCORE_SOFTMAX) {
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < PER; ++i) m = fmaxf(m, z[i]);
+    m = rt_wave_reduce(m, true);
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      s[i] = lane + 64 * i < E ? expf(z[i] - m) : 0.f;
+      part += s[i];
+    }
+    const float sum = rt_wave_reduce(part, false);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) s[i] = s[i] / sum;
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) s[i] = rt_score_of(z[i], func);
+  }
+  const bool served = wave == 0;
+  const bool use_bs = served || same_bias;
+  uint32_t kk[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) kk[i] = lane + 64 * i < E ? rt_sortable(s[i] + (use_bs ? bs[i] : bd[i])) : 0u;
+  RouteLane r;
+  r.expert = 0;
+  r.value = 0.f;
+  r.admit = 0;
+  r.valid = false;
+  bool my_absent = false;
+  float my_s = 0.f, tot = 0.f;  // tot: sequential over slots, as rt_route
+  for (int j = 0; j < k; ++j) {
+    uint32_t lm = kk[0];
+#pragma unroll
+    for (int i = 1; i < PER; ++i) lm = max(lm, kk[i]);
+    const uint32_t top = rt_wave_max_u32(lm);
+    int win = 0x7fffffff;
+#pragma unroll
+    for (int i = PER - 1; i >= 0; --i) {  // the lowest slot holding the maximum wins
+      const unsigned long long b = __ballot(kk[i] == top);
+      if (b != 0ull) win = 64 * i + (int)__builtin_ctzll(b);
+    }
+    const int wl = win & 63, wi = win >> 6;
+    float sw = 0.f, bw = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (i == wi) {
+        sw = rt_readlane_f(s[i], wl);
+        bw = rt_readlane_f(bs[i], wl);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) kk[i] = (i == wi && lane == wl) ? 0u : kk[i];
+    const bool valid = top != 0u && win < E;
+    const bool absent = valid && bw <= RT_MASKED;
+    if (!valid) sw = 0.f;
+    tot += served ? ((valid && !absent) ? sw : 0.f) : sw;
+    if (lane == j) {
+      r.expert = valid ? win : 0;
+      r.valid = valid;
+      my_s = sw;
+      my_absent = absent;
+    }
+  }
+  if (served) {
+    const float wv = (r.valid && !my_absent) ? my_s : 0.f;
+    r.value = (renorm ? wv / (tot + 1e-20f) : wv) * route_scale;
+  } else {
+    r.value = my_s;
+    r.admit = (uint8_t)(my_absent && my_s / (tot + 1e-20f) * route_scale >= tau ? 1 : 0);
+  }
+  return r;
+}
+
 }  // namespace keep
