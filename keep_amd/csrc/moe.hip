@@ -725,166 +725,6 @@ __global__ __launch_bounds__(512) void k_moe3_down(M3Args a) {
   wait_vm<0>();  // no DMA into this block's LDS may outlive it
 }
 
-// ------------------------------------------------------------------ v3: router + gate/up in one launch
-//
-// One block per 3 q-tiles (1024 threads; the table takes 128 KiB of LDS, so
-// one block per CU) runs, for one token:
-//   0. the router's logits and biases loaded, then the activation-kind table
-//      and the token DMA'd into LDS while
-//   1. the dual top-k router runs, block-parallel (same selection and weights
-//      as k_router; block 0 publishes the router outputs);
-//   2. the gate/up scales and codes of this block's tiles;
-//   3. gate/up on the matrix cores one tile at a time as its codes arrive,
-//      SwiGLU, h stored to h_work (bf16).
-// A grid-wide barrier inside one launch was measured at 5+ us per use on
-// MI355X (device-scope atomics or flag polls across XCDs), no cheaper than a
-// launch boundary, so down stays a second launch (k_moe3_down).
-// Requires H = 4096 (16 waves x 256-element K slices) and k <= 8.
-
-// uint4: the routing scratch of 16 waves, later 16 x NT x 16 floats of gate/up partials
-constexpr int M3L_SCRATCH = rt_scratch_units(16, 8);
-
-struct M3Layer {
-  const float* logits;
-  const float *bias_s, *bias_d;
-  int func, renorm, same_bias;
-  float route_scale, tau;
-  int32_t E, k;
-  int32_t* idx_out;
-  float* w_out;
-  int32_t* want_out;
-  float* want_score_out;
-  uint8_t* admit_out;
-  const void* x;
-  int32_t H, I;
-  const uint16_t *gc, *uc;
-  const void *gs, *us;
-  int sdt;
-  int32_t Gh, gsz_h;
-  const uint4* xt_x;  // expanded table in the activation pair kind
-  float limit;
-  uint16_t* h;  // [k, I] bf16
-  int32_t qtiles;
-};
-
-template <int PK, int NT, int KMAX>
-__global__ __launch_bounds__(1024) void k_moe3_route_gateup(M3Layer a) {
-  __shared__ uint4 tab4[XT_BYTES / 16];
-  __shared__ uint4 xsh[512];               // the token (H = 4096)
-  __shared__ uint4 scr[M3L_SCRATCH];       // routing scratch, then the gate/up partials
-  __shared__ int32_t s_idx[KMAX];
-  constexpr int QT = NT / 2;
-  static_assert(16 * NT * 16 <= 4 * M3L_SCRATCH, "gate/up partials exceed the scratch");
-  const char* tab = (const char*)tab4;
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t j = lane & 15, g = lane >> 4;
-  const uint32_t C = (uint32_t)a.H >> 3;  // 512 token chunks
-
-  // 0. the router's inputs (one expert per thread) are the first loads; the
-  //    table (8 ops per wave) and the token (1; waves 8..15 repeat 0..7's
-  //    piece) stream in behind them while routing runs
-  const RtInput rin = rt_input_load(a.logits, a.bias_s, a.bias_d, a.E);
-  const uint32_t rot = xt_rotation();
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t piece = ((uint32_t)(i * 16 + wv) + rot) & 127u;
-    dma16(a.xt_x + piece * 64 + lane, tab4 + piece * 64);
-  }
-  dma16((const uint4*)a.x + (wv & 7) * 64 + lane, xsh + (wv & 7) * 64);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 1. routing
-  const RouteLane r = rt_route_block<16, KMAX>(rin, a.bias_s != nullptr, a.bias_d != nullptr, a.E, a.k, a.func,
-                                                a.renorm, a.route_scale, a.tau, a.same_bias != 0,
-                                                rt_scratch(scr, 16, KMAX));
-  wait_vm<0>();  // this wave's table and token DMAs (long done: routing waited on its inputs behind them)
-  if (wv == 0 && r.valid) s_idx[lane] = r.expert;
-  if (blockIdx.x == 0 && r.valid) {
-    if (wv == 0) {
-      a.idx_out[lane] = r.expert;
-      a.w_out[lane] = r.value;
-    } else {
-      if (a.want_out) a.want_out[lane] = r.expert;
-      if (a.want_score_out) a.want_score_out[lane] = r.value;
-      if (a.admit_out) a.admit_out[lane] = r.admit;
-    }
-  }
-  lds_barrier();  // s_idx, and every wave's table and token pieces, visible to all
-
-  // 2. this block's gate/up tiles: scales first (they must not queue behind
-  //    the code stream), then codes
-  uint32_t rbase[QT];
-#pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const uint32_t qt = blockIdx.x * QT + u;
-    const bool valid = qt < (uint32_t)a.qtiles;
-    const uint32_t q0 = (valid ? qt : 0u) * 16u;
-    const uint32_t route = q0 / (uint32_t)a.I;
-    const int32_t e = s_idx[route];
-    const bool ok = valid && e >= 0 && e < a.E;
-    rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
-  }
-  const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
-  ScaleRaw sr[NT];
-#pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
-    sr[2 * u] = scale_raw(a.gs, a.sdt, si);
-    sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
-  }
-  // codes: tile t's load is issued PD tiles ahead of its decode. A wave
-  // issues in order, so loading every tile up front would hold its decode
-  // back until the memory system had accepted all of them; this way the
-  // decode (LDS-bound) runs while the rest of the stream is in flight.
-  constexpr int PD = 3;
-  const uint32_t kc0 = wv * 32 + g * 8;
-  uint4 q[NT];
-  auto load_tile = [&](int t) {
-    const size_t off = (size_t)(rbase[t >> 1] + j) * C + kc0;
-    q[t] = ldg16(((t & 1) ? a.uc : a.gc) + off);
-  };
-#pragma unroll
-  for (int t = 0; t < PD && t < NT; ++t) load_tile(t);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 3. gate/up, one tile at a time as its codes arrive (no block barrier: each
-  //    wave starts on its own first tile); the token's 8 chunks stay in registers
-  float* gred = (float*)scr;  // [16 waves][NT][16]; the routing scratch is dead
-  uint4 A[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) A[m] = permuted(xsh[kc0 + m]);
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if (t + PD < NT) load_tile(t + PD);
-    __builtin_amdgcn_sched_barrier(0);
-    m3f4_t acc = m3f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const uint32_t wd = dword_of(q[t], m >> 1);
-      const uint4 B = (m & 1) ? xt_decode<16>(tab, wd) : xt_decode<0>(tab, wd);
-      acc = mfma16<PK>(A[m], B, acc);
-    }
-    const uint32_t si = (rbase[t >> 1] + j) * (uint32_t)a.Gh + grp;
-    if (lane < 16) gred[(wv * NT + t) * 16 + j] = acc[0] * scale_cvt(sr[t], a.sdt, si);
-  }
-  lds_barrier();
-  if (wv == 0 && lane < QT * 16) {
-    const uint32_t u = lane >> 4, jj = lane & 15;
-    const uint32_t qt = blockIdx.x * QT + u;
-    float gsum = 0.f, usum = 0.f;
-    for (int w = 0; w < 16; ++w) {
-      gsum += gred[(w * NT + 2 * u) * 16 + jj];
-      usum += gred[(w * NT + 2 * u + 1) * 16 + jj];
-    }
-    if (qt < (uint32_t)a.qtiles) {
-      const uint32_t q0 = qt * 16u;
-      const int32_t e = s_idx[q0 / (uint32_t)a.I];
-      if (e >= 0 && e < a.E) a.h[q0 + jj] = from_float<bf16s>(silu_mul(gsum, usum, a.limit)).bits;
-    }
-  }
-}
-
 // ------------------------------------------------------------------ host
 
 struct GuShape {
@@ -1046,47 +886,7 @@ void moe_v3_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t H
 }
 
 
-// ------------------------------------------------------------------ v3 layer host
-
-bool moe_v3_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
-  const int64_t qtiles = k * I / 16;
-  return H == 4096 && k >= 1 && k <= 8 && k <= E && E <= 1024 && (qtiles + 255) / 256 <= 3 &&
-         group_h % 256 == 0 && moe_v3_down_supported(1, H, I, k, group_i);
-}
-
-int moe_v3_layer_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm,
-                        float route_scale, float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H,
-                        int64_t I, const uint16_t* gc, const void* gs, const uint16_t* uc, const void* us,
-                        const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
-                        const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
-                        uint8_t* admit, void* h, void* out, int odt, hipStream_t s) {
-  M3Layer a{};
-  a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
-  a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
-  a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
-  a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.gs = gs; a.us = us;
-  a.sdt = sdt; a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h;
-  a.xt_x = (const uint4*)((const char*)prepared + (x_dtype == KEEP_BF16 ? XT_BYTES : 0));
-  a.limit = limit; a.h = (uint16_t*)h;
-  a.qtiles = (int32_t)(k * I / 16);
-  const int qt = (int)((a.qtiles + 255) / 256);
-  const dim3 grid((unsigned)((a.qtiles + qt - 1) / qt)), blk(1024);
-#define LY(PK, NT, KM) hipLaunchKernelGGL((k_moe3_route_gateup<PK, NT, KM>), grid, blk, 0, s, a)
-#define LY_K(PK, NT) \
-  if (k <= 4) LY(PK, NT, 4); else if (k <= 6) LY(PK, NT, 6); else LY(PK, NT, 8)
-#define LY_NT(PK) \
-  if (qt <= 1) { LY_K(PK, 2); } else if (qt == 2) { LY_K(PK, 4); } else { LY_K(PK, 6); }
-  if (x_dtype == KEEP_BF16) { LY_NT(PAIR_BF16); } else { LY_NT(PAIR_F16); }
-#undef LY_NT
-#undef LY_K
-#undef LY
-  // down + weighted combine, reading the router outputs and h the first launch wrote
-  moe_v3_launch(false, true, x, x_dtype, H, I, idx, w, k, E, gc, gs, uc, us, dc, ds, sdt, group_h, group_i, prepared,
-                limit, h, out, odt, s);
-  return 0;
-}
-
-// fp8 matrix-core layer (moe8.hip)
+// int8 matrix-core layer (moe_i8.hip)
 void tq_build(const uint32_t* table, void* prepared, hipStream_t s);
 bool moe_q_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i);
 int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm,
@@ -1095,7 +895,7 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
                         const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
                         const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
                         uint8_t* admit, void* h, void* out, int odt, hipStream_t s);
-constexpr int PREPARED_TOTAL = 2 * XT_BYTES + 4096 + 256;  // expanded tables, int8 decode tables, flag word
+constexpr int PREPARED_TOTAL = 2 * XT_BYTES + 4096 + 256 + 65536;  // expanded tables, int8 tables, flag, LDS image
 
 }  // namespace keep
 

@@ -11,8 +11,14 @@
 // codeword's 8 int8 weights, in packed-nibble order, are
 //   T[idx] ^ M[signs],  M[signs] byte s = (eff bit s ? 0xFC : 0) ^ (p ? 0x02 : 0),
 // p the parity of the sign byte and eff = signs ^ p (bit 0 flipped when p = 1).
-// That is two 8-byte lookups in 2 KiB tables and a few VALU per codeword
-// (keep_e8p_prepare builds both tables, 4 KiB, which every block stages in LDS).
+// That is two 8-byte lookups and a few VALU per codeword. The random lookups
+// set the decode rate, so every block stages a 64 KiB image of both tables in
+// LDS (built once by keep_e8p_prepare): row e (256 bytes) holds sixteen copies
+// of the pair (T[e], M[e]), copy r in bytes 16 r .. 16 r + 15, and lane l reads
+// copy l % 16. Sixteen consecutive lanes then touch sixteen disjoint groups of
+// four banks whatever their codewords, so a lookup never waits on a bank
+// conflict inside a 16-lane group. A lookup address is one byte permute:
+// (idx << 8) | 16 r for T, (signs << 8) | 16 r | 8 for M.
 //
 // Activations. The A operand of a 16x16x64 int8 MFMA is 16 rows of 64 bytes.
 // A wave's 256-element slice of the token x (fp16 or bf16) is scaled by a
@@ -35,13 +41,14 @@
 
 namespace keep {
 
-constexpr int TQ_BYTES = 4096;  // T (256 x 8 bytes), then M (256 x 8 bytes)
+constexpr int TQ_BYTES = 4096;     // T (256 x 8 bytes), then M (256 x 8 bytes)
+constexpr int TQR_BYTES = 65536;   // the LDS image: 256 rows x 16 copies x (T, M)
 
 typedef int q8v4 __attribute__((ext_vector_type(4)));
 
 // T and M from the packed E8P table; flag[0] = 1 if a nibble is even (not an
 // E8P half-integer coordinate, so not of this form), else 0.
-__global__ __launch_bounds__(256) void k_build_tq(const uint32_t* packed, uint2* tq, uint32_t* flag) {
+__global__ __launch_bounds__(256) void k_build_tq(const uint32_t* packed, uint2* tq, uint4* tqr, uint32_t* flag) {
   __shared__ uint32_t s_bad;
   const int i = threadIdx.x;  // one block of 256 threads: abs index i, sign byte i
   if (i == 0) s_bad = 0u;
@@ -63,25 +70,52 @@ __global__ __launch_bounds__(256) void k_build_tq(const uint32_t* packed, uint2*
   }
   tq[i] = make_uint2(t[0], t[1]);
   tq[256 + i] = make_uint2(m[0], m[1]);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) tqr[i * 16 + r] = make_uint4(t[0], t[1], m[0], m[1]);
   if (!ok) s_bad = 1u;
   __syncthreads();
   if (i == 0) flag[0] = s_bad;
 }
 
-// The 8 int8 weights x 4 (packed-nibble order) of codeword c (low 16 bits).
-__device__ __forceinline__ uint2 q8_decode(const char* tq, uint32_t c) {
-  const uint2 t = *(const uint2*)(tq + ((c >> 5) & 0x7f8u));
-  const uint2 m = *(const uint2*)(tq + 2048 + ((c & 0xffu) << 3));
-  return make_uint2(t.x ^ m.x, t.y ^ m.y);
+// B operands of one 16-byte code load (8 codewords): codewords 2i, 2i + 1 ->
+// b[i], each the 8 int8 weights x 4 in packed-nibble order, T[idx] ^ M[signs]
+// read from this lane's copy in the LDS image. The permutes place a
+// codeword's abs index (T) or sign byte (M) in address byte 1 beside the
+// lane's copy offset in byte 0 (16 r, | 8 for M). An LDS pass serves 32
+// lanes, and lanes l and l + 16 share copy l % 16, so lanes of odd 16-lane
+// groups look up M first and T second: within a pass one lane of a pair
+// reads the copy's T half while the other reads its M half, and the XOR
+// does not care about the order. lk = lookup_keys(lane) holds the two
+// address bases and the four byte selectors of this lane.
+struct Q8Keys {
+  uint32_t base1, base2;          // copy offset for the first / second lookup
+  uint32_t s1lo, s1hi, s2lo, s2hi;  // v_perm selectors (low / high codeword)
+};
+__device__ __forceinline__ Q8Keys q8_keys(uint32_t lane) {
+  const uint32_t r16 = (lane & 15u) << 4;
+  const bool m_first = (lane >> 4) & 1u;
+  Q8Keys k;
+  k.base1 = m_first ? (r16 | 8u) : r16;
+  k.base2 = m_first ? r16 : (r16 | 8u);
+  // address byte 1 <- codeword byte: T uses the abs index (bits 8-15 / 24-31),
+  // M the sign byte (bits 0-7 / 16-23)
+  k.s1lo = m_first ? 0x0c0c0400u : 0x0c0c0500u;
+  k.s1hi = m_first ? 0x0c0c0600u : 0x0c0c0700u;
+  k.s2lo = m_first ? 0x0c0c0500u : 0x0c0c0400u;
+  k.s2hi = m_first ? 0x0c0c0700u : 0x0c0c0600u;
+  return k;
 }
-
-// B operands of one 16-byte code load (8 codewords): codewords 2i, 2i + 1 -> b[i].
-__device__ __forceinline__ void q8_decode8(const char* tq, uint4 q, q8v4 (&b)[4]) {
+__device__ __forceinline__ void q8_decode8(const char* tqr, const Q8Keys& k, uint4 q, q8v4 (&b)[4]) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint2 lo = q8_decode(tq, w[i] & 0xffffu), hi = q8_decode(tq, w[i] >> 16);
-    b[i] = q8v4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+    const uint32_t a1 = __builtin_amdgcn_perm(w[i], k.base1, k.s1lo);
+    const uint32_t a2 = __builtin_amdgcn_perm(w[i], k.base2, k.s2lo);
+    const uint32_t b1 = __builtin_amdgcn_perm(w[i], k.base1, k.s1hi);
+    const uint32_t b2 = __builtin_amdgcn_perm(w[i], k.base2, k.s2hi);
+    const uint2 x1 = *(const uint2*)(tqr + a1), x2 = *(const uint2*)(tqr + a2);
+    const uint2 y1 = *(const uint2*)(tqr + b1), y2 = *(const uint2*)(tqr + b2);
+    b[i] = q8v4{(int)(x1.x ^ x2.x), (int)(x1.y ^ x2.y), (int)(y1.x ^ y2.x), (int)(y1.y ^ y2.y)};
   }
 }
 
@@ -184,68 +218,65 @@ struct MQLayer {
 };
 
 // One block per NT / 2 q-tiles (16 rows of the [k, I] intermediate each), 16
-// waves, H = 4096 (a 256-wide K slice per wave). Waves 0 and 1 route
-// (rt_route_pair) while every wave builds its A terms; then gate/up one tile at
-// a time with its codes loaded three tiles ahead, SwiGLU, h in bf16.
+// waves, H = 4096 (a 256-wide K slice per wave). Waves 0 and 1 select the
+// experts (rt_select_pair) while waves 2-15 build the A terms of all sixteen
+// slices; after one barrier every wave issues all of its scale and code loads
+// at once, the router waves finish the weights while those are in flight, and
+// gate/up runs tile by tile, then SwiGLU, h in bf16.
 template <int NT, bool XBF, int PER>
 __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
-  __shared__ uint4 tqs[TQ_BYTES / 16];
-  __shared__ uint4 ash[16 * 3 * 16];  // [wave][term][g * 4 + i]
+  __shared__ uint4 tqs[TQR_BYTES / 16];
+  __shared__ uint4 ash[16 * 3 * 16];  // [slice][term][g * 4 + i]
   __shared__ float gred[16 * NT * 16];
+  __shared__ float s_inv4s[16];
   __shared__ int32_t s_idx[8];
   constexpr int QT = NT / 2;
   const char* tq = (const char*)tqs;
+  const Q8Keys lk = q8_keys(threadIdx.x & 63);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t j = lane & 15, g = lane >> 4;
   const uint32_t C = (uint32_t)a.H >> 3;  // 512 token chunks
 
-  // 0. the router's inputs (waves 0, 1), the table (4 pieces; every wave loads
-  //    one) and this wave's token slice (16 bytes per lane pair)
+  // 0. the router's inputs (waves 0, 1), the table image (64 KiB; every wave
+  //    DMAs 4 KiB) and the token slices this wave builds A terms for (16
+  //    bytes per lane pair): wave w >= 2 slice w, waves 2 and 3 also slices 0, 1
   float z[PER], bsv[PER], bdv[PER];
   if (wv < 2) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
-  dma16_q(a.tq + (wv & 3) * 64 + lane, tqs + (wv & 3) * 64);
-  const uint4 xc = ldg16_q((const uint4*)a.x + wv * 32 + (lane >> 1));
+#pragma unroll
+  for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
+  const uint4 xc = ldg16_q((const uint4*)a.x + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
+  const uint4 xc2 = ldg16_q((const uint4*)a.x + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
   __builtin_amdgcn_sched_barrier(0);
 
-  // 1. routing
-  RouteLane r;
-  r.valid = false;
-  r.expert = 0;
-  r.value = 0.f;
-  r.admit = 0;
-  if (wv < 2)
-    r = rt_route_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, a.renorm, a.route_scale, a.tau, a.same_bias != 0, wv,
-                           lane);
-  if (wv == 0 && r.valid) s_idx[lane] = r.expert;
-  if (blockIdx.x == 0 && r.valid) {
-    if (wv == 0) {
-      a.idx_out[lane] = r.expert;
-      a.w_out[lane] = r.value;
-    } else {
-      if (a.want_out) a.want_out[lane] = r.expert;
-      if (a.want_score_out) a.want_score_out[lane] = r.value;
-      if (a.admit_out) a.admit_out[lane] = r.admit;
-    }
-  }
-
-  // 2. A terms of this wave's slice: rows 0-2 are the three int8 terms of x s
-  float s, inv4s;
-  {
+  // 1. routing (waves 0, 1) | A terms: rows 0-2 of slice w are the three int8
+  //    terms of x s, s the slice's power of two (1 / (4 s) kept for the epilogue)
+  float sc[PER];
+  int e_sel = -1;
+  auto build = [&](uint4 c, int slice) {
     float v[4];
-    q8_half4<XBF>(xc, lane & 1, v);
+    q8_half4<XBF>(c, lane & 1, v);
     float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    float s, inv4s;
     q8_scale(rt_wave_reduce(mx, true), s, inv4s);
     uint32_t tw[3];
     q8_terms<3>(v, s, tw);
     uint32_t* aw = (uint32_t*)ash;
 #pragma unroll
-    for (int n = 0; n < 3; ++n) aw[q8_aword((uint32_t)(wv * 3 + n), lane >> 1, lane & 1)] = tw[n];
+    for (int n = 0; n < 3; ++n) aw[q8_aword((uint32_t)(slice * 3 + n), lane >> 1, lane & 1)] = tw[n];
+    if (lane == 0) s_inv4s[slice] = inv4s;
+  };
+  if (wv < 2) {
+    e_sel = rt_select_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, a.same_bias != 0, wv, lane, sc);
+    if (wv == 0 && lane < a.k) s_idx[lane] = e_sel >= 0 && e_sel < a.E ? e_sel : -1;
+  } else {
+    build(xc, wv);
+    if (wv < 4) build(xc2, wv - 2);
   }
-  wait_vm_q<0>();  // this wave's table piece
-  rt_lds_barrier();  // s_idx, the table and every wave's A terms visible
+  wait_vm_q<0>();  // this wave's table pieces
+  rt_lds_barrier();  // s_idx, the table and every slice's A terms visible
 
-  // 3. this block's tiles: scales, then codes PD tiles ahead of their decode
+  // 2. this block's tiles: scales, then every tile's codes
   uint32_t rbase[QT];
 #pragma unroll
   for (int u = 0; u < QT; ++u) {
@@ -265,16 +296,28 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     sr[2 * u] = scale_raw(a.gs, a.sdt, si);
     sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
   }
-  constexpr int PD = 3;
+  constexpr int PD = NT;  // tiles whose codes are loaded before the first decode
   const uint32_t kc0 = wv * 32 + g * 8;
   uint4 q[NT];
-  auto load_tile = [&](int t) {
-    const size_t off = (size_t)(rbase[t >> 1] + j) * C + kc0;
-    q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + off);
-  };
+  auto load_tile = [&](int t) { q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + (size_t)(rbase[t >> 1] + j) * C + kc0); };
 #pragma unroll
-  for (int t = 0; t < PD && t < NT; ++t) load_tile(t);
+  for (int t = 0; t < PD; ++t) load_tile(t);
   __builtin_amdgcn_sched_barrier(0);
+
+  // the router waves' weights and outputs, while the codes are in flight
+  if (wv < 2) {
+    const RouteLane r = rt_finish<PER>(e_sel, wv == 0, sc, bsv, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
+    if (blockIdx.x == 0 && r.valid) {
+      if (wv == 0) {
+        a.idx_out[lane] = r.expert;
+        a.w_out[lane] = r.value;
+      } else {
+        if (a.want_out) a.want_out[lane] = r.expert;
+        if (a.want_score_out) a.want_score_out[lane] = r.value;
+        if (a.admit_out) a.admit_out[lane] = r.admit;
+      }
+    }
+  }
 
   q8v4 A[4];
   {
@@ -285,14 +328,15 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
       A[i] = j < 3 ? v : q8v4{0, 0, 0, 0};
     }
   }
+  const float inv4s = s_inv4s[wv];
 
-  // 4. gate/up, tile by tile
+  // 3. gate/up, tile by tile
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if (t + PD < NT) load_tile(t + PD);
     __builtin_amdgcn_sched_barrier(0);
     q8v4 B[4];
-    q8_decode8(tq, q[t], B);
+    q8_decode8(tq, lk, q[t], B);
     q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
@@ -344,10 +388,11 @@ struct MQDown {
 template <int KMAX>
 __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
   static_assert(KMAX <= 8, "two A rows per route");
-  __shared__ uint4 tqs[TQ_BYTES / 16];
+  __shared__ uint4 tqs[TQR_BYTES / 16];
   __shared__ uint4 ash[8 * 2 * KMAX * 16];  // [wave][2 r + term][g * 4 + i]
   __shared__ float red[8][KMAX][16];
   const char* tq = (const char*)tqs;
+  const Q8Keys lk = q8_keys(threadIdx.x & 63);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwd = a.I >> 8;
@@ -366,7 +411,8 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
     e_r[r] = ((cidx)a.idx)[r];
     w_r[r] = ((cw)a.w)[r];
   }
-  dma16_q(a.tq + (wv & 3) * 64 + lane, tqs + (wv & 3) * 64);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
   const uint32_t wslice = (dec ? wv : 0) * 32 + (lane >> 1);
   uint4 hq[KMAX];
 #pragma unroll
@@ -395,7 +441,7 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
 #pragma unroll
   for (int r = 0; r < PD && r < KMAX; ++r) load_route(r);  // every wave: the wait below counts them
   __builtin_amdgcn_sched_barrier(0);
-  wait_vm_q<KMAX + (PD < KMAX ? PD : KMAX)>();  // the table DMA and h loads, not the scales and codes
+  wait_vm_q<KMAX + (PD < KMAX ? PD : KMAX)>();  // the table DMAs and h loads, not the scales and codes
 
   // 3. A terms: rows 2r, 2r + 1 of route r, scaled by the route's own power of two
   float inv4s[KMAX];
@@ -434,7 +480,7 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
       if (r + PD < KMAX) load_route(r + PD);
       __builtin_amdgcn_sched_barrier(0);
       q8v4 B[4];
-      q8_decode8(tq, q[r], B);
+      q8_decode8(tq, lk, q[r], B);
       q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
@@ -469,13 +515,14 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
 // ------------------------------------------------------------------ host
 
 // Offsets in the prepared buffer (keep_e8p_prepare): the two 128 KiB
-// expanded tables, then T and M, then the flag word.
+// expanded tables, then T and M, then the flag word, then the 64 KiB LDS image.
 constexpr size_t TQ_OFFSET = 2u * 131072u;
 constexpr size_t TQ_FLAG_OFFSET = TQ_OFFSET + TQ_BYTES;
+constexpr size_t TQR_OFFSET = TQ_FLAG_OFFSET + 256u;
 
 void tq_build(const uint32_t* table, void* prepared, hipStream_t s) {
   hipLaunchKernelGGL(k_build_tq, dim3(1), dim3(256), 0, s, table, (uint2*)((char*)prepared + TQ_OFFSET),
-                     (uint32_t*)((char*)prepared + TQ_FLAG_OFFSET));
+                     (uint4*)((char*)prepared + TQR_OFFSET), (uint32_t*)((char*)prepared + TQ_FLAG_OFFSET));
 }
 
 bool moe_q_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
@@ -490,7 +537,7 @@ void moe_q_down_launch(const int32_t* idx, const float* w, int64_t k, int64_t E,
   MQDown d{};
   d.H = (int32_t)H; d.I = (int32_t)I; d.E = (int32_t)E; d.idx = idx; d.w = w; d.dc = dc; d.ds = ds; d.sdt = sdt;
   d.Gi = (int32_t)(I / group_i); d.gsz_i = (int32_t)group_i;
-  d.tq = (const uint4*)((const char*)prepared + TQ_OFFSET);
+  d.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
   d.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
   d.h = (const uint16_t*)h; d.out = out; d.odt = odt;
   const dim3 grid((unsigned)(H / 16)), blk(512u);
@@ -518,7 +565,7 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
   a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
   a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.gs = gs; a.us = us;
   a.sdt = sdt; a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h;
-  a.tq = (const uint4*)((const char*)prepared + TQ_OFFSET);
+  a.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
   a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
   a.limit = limit; a.h = (uint16_t*)h;
   a.qtiles = (int32_t)(k * I / 16);
