@@ -12,8 +12,8 @@ as three launches (router, gate/up, down) is timed alongside for reference.
 
 ``value`` = code-stream bytes of one layer (37,847,040 B: 18 projections of
 2048 x 512 uint16 codes plus fp16 row scales) / time per layer, in GB/s.
-``roofline`` covers the layer's two launches (``k_moe3_route_gateup`` then
-``k_moe3_down``) as one unit, timed with HIP events on the stream they are
+``roofline`` covers the layer's two launches (``k_moeq_route_gateup`` then
+``k_moeq_down``) as one unit, timed with HIP events on the stream they are
 launched on. ``cpu_baseline`` times the C/OpenMP restatement
 of the same layer (``oracle/cpu_ref.c``) on the host.
 

@@ -185,10 +185,8 @@ int keep_moe_down(int h_dtype, int64_t T, int64_t H, int64_t I,
 /* One routed MoE decode layer for one token in two launches on `stream`:
  * first the router (as keep_router_dual_topk with T = 1; outputs written to
  * idx/w/want/want_score/admit, the last three optional) fused with
- * gate/up/SwiGLU into h_work, then down + weighted combine into out[H]. The
- * first launch also pulls the routed experts' down codes into the device's
- * last-level cache so that the second launch reads them from there. No
- * state is kept between calls. `prepared` is keep_e8p_prepare of the E8P
+ * gate/up/SwiGLU into h_work, then down + weighted combine into out[H], both
+ * on the int8 matrix cores. No state is kept between calls. `prepared` is keep_e8p_prepare of the E8P
  * table. Serves H = 4096, I a multiple of 512 up to 2048, k <= 8, E <= 1024
  * and scale groups of 256-element multiples (keep_moe_layer_supported).
  * Replaces the serving decode step of scripts/v41_build/omlx_lattice.py:327-371
