@@ -17,7 +17,19 @@ as three launches (router, gate/up, down) is timed alongside for reference.
 launched on. ``cpu_baseline`` times the C/OpenMP restatement
 of the same layer (``oracle/cpu_ref.c``) on the host.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--config {1,2,3,4,5}]
+
+``--config`` other than 2 measures the BASELINE's other configurations, one
+JSON line per workload, with the same fields (they are parity-test shapes of
+the same path, reported beside the headline, not instead of it):
+1 one E8P projection (M=1, K=4096, N=2048) from a 384 MiB pool of them, with
+the C restatement on the host (all threads and one) and the numpy
+dense-decode oracle; 3 speculative verify, the whole layer for M = 8, 16 and
+64 tokens (router + gate/up + SwiGLU + down), GB/s over the distinct experts
+read; 4 prefill, 2048 tokens with Zipf(1.1) expert popularity (device route
+plan + three MFMA grouped GEMMs + SwiGLU + combine), TFLOP/s and GB/s;
+5 the 288-expert top-8 layer (4096/1536) with a 50% resident mask as -inf
+router bias and tau = 0.3, decode batch 1 and prefill 512 tokens.
 """
 
 from __future__ import annotations
@@ -74,6 +86,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
+                    help="BASELINE configuration to measure (2: the headline decode layer)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy kernel (torch.neg, fp16) 8 times, the known-size "
                          "reference that scales FETCH_SIZE / WRITE_SIZE counter readings to bytes")
@@ -84,6 +98,9 @@ def main() -> int:
                                    "MI355X here (multi-GPU sharding is a design note, not a measured path); "
                                    "run with --gpus 1"}))
         return 2
+
+    if args.config != 2:
+        return other_config(args)
 
     import torch
 
@@ -294,6 +311,220 @@ def cpu_baseline(torch, gate, up, down, x, idx, w, table, seconds):
             "us_per_layer": round(per * 1e6, 1), "tok_per_s": round(1.0 / per, 2),
             "sample": f"{n} config-2 decode layers (4 routings of 6 experts, full 4096/2048 shapes) in {el:.1f} s "
                       f"with oracle/cpu_ref.c (LUT decode, fp32 accumulate, OpenMP {threads} threads)"}
+
+
+def _timed_graph(torch, stream, fn, n_sets, reps, warm=1):
+    """us per call of fn(i): a HIP graph of GRAPH_STEPS calls over n_sets
+    input sets, replayed `reps` times on `stream` between two events."""
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for i in range(min(n_sets, GRAPH_STEPS)):  # eager pass: allocations, checks
+            fn(i)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for j in range(GRAPH_STEPS):
+                fn(j % n_sets)
+        for _ in range(warm):
+            g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        t0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e3 / (reps * GRAPH_STEPS)
+
+
+def _timed_eager(torch, stream, fn, n_sets, iters, warm=2):
+    """us per call of fn(i), launched eagerly on `stream` (for paths that size
+    their work on the host)."""
+
+    with torch.cuda.stream(stream):
+        for i in range(warm):
+            fn(i % n_sets)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(iters):
+            fn(i % n_sets)
+        t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e3 / iters
+
+
+def _line(metric_value, unit, us, workload, extra, dtype, higher=True, roofline=None, cpu=None, data=None):
+    r = {"metric": "routed VQ-GEMM HBM GB/s (% of 8 TB/s) + MoE-layer decode tok/s, 384e top-6",
+         "value": round(metric_value, 3), "unit": unit, "n_gpus": 1, "steps": None, "warmup": None,
+         "ms_per_step": round(us * 1e-3, 6), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
+         "dtype": dtype, "data": data or "synthetic: uniform uint16 codes, fp16 log-normal(0,0.3) row scales, "
+                                        "RHT'd N(0,1) fp16 activations, N(0,1) router logits",
+         "config": dict(workload=workload, **extra), "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(r), flush=True)
+
+
+def other_config(args) -> int:
+    import torch
+
+    from keep_amd import _lib, ops, synth
+    from keep_amd.nn import QuantizedVQSwitchGLU, QuantizedVQSwitchLinear, RoutedVQMoE
+    from keep_amd.router import resident_bias
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(device=dev)
+    cfg = args.config
+    reps = 4
+
+    if cfg == 1:
+        Ep, N, K = 192, 2048, 4096  # 192 distinct projections = 384 MiB, beyond the 256 MB Infinity Cache
+        p = synth.projection(Ep, N, K, seed=11, device=dev)
+        x = synth.rht_activations(1, K, seed=12, device=dev)
+        table = ops._default_codebook(16, dev)
+        outs = [torch.empty((N,), dtype=torch.float16, device=dev) for _ in range(Ep)]
+        code_b = N * (K // 8) * 2
+        tot_b = code_b + N * 2
+
+        def fn(i):
+            outs[i].copy_(ops.vq_qmv(x[0], p.codes[i], p.scales[i], table, in_dim=K, out_dim=N, group_size=K,
+                                     code_bits=16))
+
+        us = _timed_graph(torch, stream, fn, Ep, reps)
+        gbps = tot_b / (us * 1e-6) / 1e9
+        cpu = None
+        if not args.no_cpu_baseline:
+            cpu = _cpu_projection(torch, p, x, table, args.cpu_seconds)
+        _line(gbps, "GB/s", us, "config 1: one E8P projection, M=1, K=4096, N=2048, per-row fp16 scales "
+              "(vq_qmv, 192 distinct projections rotated)", {"tokens": 1, "K": K, "N": N}, "fp16 x E8P, fp32 acc",
+              roofline={"bound": "hbm", "kernel": "k_vq_matvec", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": tot_b,
+                        "us_per_launch": round(us, 3), "traffic": None}, cpu=cpu)
+        return 0
+
+    E, H, I, k = (384, 4096, 2048, 6) if cfg in (3, 4) else (288, 4096, 1536, 8)
+    log(f"bench: config {cfg}: allocating {E} experts x 3 projections")
+    gate = synth.projection(E, I, H, seed=1, device=dev)
+    up = synth.projection(E, I, H, seed=2, device=dev)
+    down = synth.projection(E, H, I, seed=3, device=dev)
+    table = ops._default_codebook(16, dev)
+
+    def lin(pj, K, Nn):
+        return QuantizedVQSwitchLinear(input_dims=K, output_dims=Nn, num_experts=E, codes=pj.codes, scales=pj.scales,
+                                       codebook=table, group_size=K, code_bits=16)
+
+    glu = QuantizedVQSwitchGLU(gate_proj=lin(gate, H, I), up_proj=lin(up, H, I), down_proj=lin(down, I, H))
+    expert_b = 2 * I * (H // 8) * 2 + H * (I // 8) * 2 + (2 * I + H) * 2  # codes + fp16 row scales
+    flops_per_route = 2 * 3 * H * I
+    mask = synth.resident_mask(E, frac=0.5, seed=21) if cfg == 5 else None
+    bias = resident_bias(torch.from_numpy(mask).to(dev)) if cfg == 5 else None
+    moe = RoutedVQMoE(glu, top_k=k, bias_served=bias, bias_demand=None if cfg == 5 else bias,
+                      tau=0.3 if cfg == 5 else float("inf"))
+    sizes = {3: [8, 16, 64], 4: [2048], 5: [1, 512]}[cfg]
+    n_sets = 16
+    for T in sizes:
+        x = synth.rht_activations(T, H, seed=30 + T, device=dev)
+        if cfg == 4:
+            idx_np = [synth.zipf_routes(T, E, k, s=1.1, seed=40 + i) for i in range(4)]
+            idx = [torch.from_numpy(a).to(dev) for a in idx_np]
+            wts = [torch.softmax(torch.randn(T, k, device=dev), -1) for _ in range(4)]
+            distinct = float(np.mean([len(np.unique(a)) for a in idx_np]))
+
+            def fn(i):
+                return moe.experts(x, idx[i % 4], wts[i % 4])
+
+            us = _timed_eager(torch, stream, fn, 4, 8)
+            flops = T * k * flops_per_route
+            tf = flops / (us * 1e-6) / 1e12
+            gbps = distinct * expert_b / (us * 1e-6) / 1e9
+            _line(tf, "TFLOP/s", us, "config 4: prefill, 2048 tokens, Zipf(1.1) routing over 384 experts, top-6 "
+                  "(route plan + 3 MFMA grouped GEMMs + SwiGLU + combine)",
+                  {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I,
+                   "distinct_experts": distinct, "hbm_gbps_distinct": round(gbps, 1),
+                   "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2)},
+                  "fp16 activations x E8P (fp16 MFMA), fp32 accumulate",
+                  roofline={"bound": "mfma", "kernel": "k_vq_grouped_gemm (x3)", "achieved": round(tf, 2),
+                            "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4),
+                            "flops_per_layer": flops, "us_per_layer": round(us, 1), "traffic": None})
+            continue
+        logits = synth.router_logits(n_sets * T, E, seed=50 + T, device=dev).reshape(n_sets, T, E).contiguous()
+        with torch.no_grad():
+            r0 = [moe(x, logits[i])[1] for i in range(n_sets)] if T > 1 else None
+        torch.cuda.synchronize()
+        if r0 is not None:
+            distinct = float(np.mean([len(np.unique(r.idx.cpu().numpy())) for r in r0]))
+        else:
+            distinct = float(k)
+        outs = []
+
+        def fn(i):
+            o = moe(x, logits[i])
+            outs.append(o)  # keep graph outputs alive
+
+        if T <= 64:
+            us = _timed_graph(torch, stream, fn, n_sets, reps)
+        else:
+            us = _timed_eager(torch, stream, fn, n_sets, 8)
+        gbps = distinct * expert_b / (us * 1e-6) / 1e9
+        name = {3: f"config 3: speculative verify, {T} tokens through the 384-expert top-6 layer "
+                   "(router + fused gate/up/SwiGLU + down/combine)",
+                5: f"config 5: 288 experts, top-8, 4096/1536, 50% resident (-inf bias), tau 0.3, "
+                   f"{'decode batch 1' if T == 1 else f'prefill {T} tokens'}"}[cfg]
+        _line(gbps, "GB/s", us, name,
+              {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I, "distinct_experts": distinct,
+               "tok_per_s": round(T / (us * 1e-6), 1), "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2),
+               "tflops": round(T * k * flops_per_route / (us * 1e-6) / 1e12, 2)},
+              "fp16 activations x E8P-2bit codes, fp32 accumulate",
+              roofline={"bound": "hbm", "kernel": "layer", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                        "bytes_per_layer": int(distinct * expert_b), "us_per_layer": round(us, 2), "traffic": None})
+    return 0
+
+
+def _cpu_projection(torch, p, x, table, seconds):
+    """Config 1 on the host: the C restatement (all threads, then one) and the
+    numpy dense-decode oracle (including its 32 MiB materialisation)."""
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import cpu
+    from oracle import ops as oops
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(int(threads), 16))
+    tab = table.cpu().numpy().view(np.uint32)
+    xs = x.float().cpu().numpy()
+    codes = [p.codes[i:i + 1].cpu().numpy().view(np.uint16) for i in range(4)]
+    scales = [p.scales[i:i + 1].float().cpu().numpy() for i in range(4)]
+    rhs = np.zeros((1, 1), dtype=np.int32)
+    res = {}
+    for th in (threads, 1):
+        cpu.routed_matvec(xs, codes[0], scales[0], tab, rhs, group_size=4096, threads=th)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            cpu.routed_matvec(xs, codes[n % 4], scales[n % 4], tab, rhs, group_size=4096, threads=th)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds / 3 or n >= 20000:
+                break
+        res[th] = (el / n, n, el)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oops.qmv(xs[0], codes[n % 4][0], scales[n % 4][0], table=tab)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds / 3 or n >= 200:
+            break
+    npy = el / n
+    b = 2048 * 512 * 2 + 2048 * 2
+    per, n_all, el_all = res[threads]
+    return {"value": round(b / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_projection": round(per * 1e6, 1),
+            "one_thread": {"us_per_projection": round(res[1][0] * 1e6, 1), "GB/s": round(b / res[1][0] / 1e9, 3)},
+            "numpy_dense_decode_oracle": {"us_per_projection": round(npy * 1e6, 1),
+                                          "note": "includes building the 32 MiB dense fp64 matrix"},
+            "sample": f"{n_all} projections in {el_all:.1f} s with oracle/cpu_ref.c (LUT decode, fp32 accumulate, "
+                      f"OpenMP {threads} threads), then {res[1][1]} with 1 thread"}
 
 
 if __name__ == "__main__":

@@ -203,6 +203,29 @@ int keep_moe_layer(const float* logits, const float* bias_served, const float* b
                    float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
                    uint8_t* admit, void* h_work, void* out, int out_dtype, void* stream);
 
+/* Routed SwiGLU MoE for a few tokens (speculative verify) with the routes of
+ * one expert sharing every code load: T tokens x k routes (idx/w [T, k], as
+ * keep_moe_decode takes them), gate/up/SwiGLU into h_work ([T, k, I] bf16),
+ * down per route, then out[t] = sum over the token's routes in route order of
+ * w * y. Five launches on `stream` (activation terms, route plan, gate/up,
+ * down, combine), no host sync. `workspace` is caller-owned device memory of
+ * keep_moe_tiles_workspace_bytes(T, k, num_experts, H) bytes, 256-byte
+ * aligned. The result for each token is byte-identical to keep_moe_layer's
+ * for that token and routing. Replaces the layer-level use of
+ * gather_vqmm_verify_rows(grouping="expert") (src/ramp/ops/vq_switch.py:
+ * 286-377, tile descriptors :186-225) for the three projections and the
+ * combine of deepseek_v4_flash_adapter.py:1776-1784. */
+int64_t keep_moe_tiles_workspace_bytes(int64_t T, int64_t k, int64_t num_experts, int64_t H);
+int keep_moe_tiles_supported(int64_t T, int64_t num_experts, int64_t H, int64_t I, int64_t k,
+                             int64_t group_size_h, int64_t group_size_i);
+int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, const int32_t* idx,
+                   const float* w, int64_t k, int64_t num_experts, const uint16_t* gate_codes,
+                   const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
+                   const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                   int64_t group_size_h, int64_t group_size_i, const void* prepared,
+                   float swiglu_limit, void* h_work, void* workspace, int64_t workspace_bytes,
+                   void* out, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

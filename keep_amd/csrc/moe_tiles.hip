@@ -1,0 +1,484 @@
+// Routed SwiGLU MoE for a few tokens (speculative verify, T <= 256) on the
+// int8 matrix cores, with the routes of one expert sharing every code load.
+//
+// Routes are grouped per expert by the device route plan (keep_route_plan,
+// tiles of <= 16 routes of one expert), as gather_vqmm_verify_rows groups
+// them (src/ramp/ops/vq_switch.py:186-225,286-377): a tile's code rows are
+// read and decoded once and multiply every route of the tile, so a layer
+// reads each hit expert once however many tokens hit it.
+//
+// Launches (no host sync, graph-capturable, all scratch in the caller's
+// workspace):
+//  1. k_q8_xterms: every token's int8 activation terms per 256-wide K slice
+//     (three terms under a per-slice power of two, as the one-token layer
+//     builds them) and the slice scales;
+//  2. keep_route_plan: stable sort of the routes by expert, tile descriptors;
+//  3. k_moeq_gateup_tiles: persistent, one block per CU. A unit is one tile x
+//     16 rows of gate and up; 16 waves each own a K slice. Each code load is
+//     decoded once (LDS image lookups) and then multiplied, with one MFMA
+//     group per route, by the A operand of that route's token (rows 0-2 =
+//     its three terms, kept in registers while the block's units stay in one
+//     tile). The next unit's codes are loaded before this unit's decode.
+//     SwiGLU in fp32, h in bf16 at its route's row;
+//  4. k_moeq_down_tiles: persistent. A unit is one tile x 32 rows of down; a
+//     wave owns a 256-wide K slice of h; the A operand holds two int8 terms
+//     of up to 8 routes (rows 2r, 2r + 1), built once per tile. Output
+//     y[route][row] in fp32;
+//  5. k_moe_combine: out[t] = sum over the token's routes, in route order,
+//     of w * y (a zero weight contributes nothing; an out-of-range expert
+//     with a nonzero weight gives NaN), as the one-token layer combines.
+#include "common.h"
+#include "moe_dev.h"
+#include "q8_dev.h"
+#include "route_dev.h"
+
+namespace keep {
+
+constexpr int MT_TILE = 16;  // routes per tile (one MFMA group each in gate/up, A rows in down)
+constexpr int MT_CHUNK = 2;  // routes whose A operands are held in registers at once (gate/up)
+
+struct MTArgs {
+  const uint4* xt;     // [T][S][3][16] 16-byte slots of int8 terms
+  const float* xinv;   // [T][S] 1 / (4 s)
+  const int32_t *order, *te, *to, *tc, *ntiles;
+  int32_t k, E, H, I, S;
+  const uint16_t *gc, *uc, *dc;
+  const void *gs, *us, *ds;
+  int sdt;
+  int32_t Gh, gsz_h, Gi, gsz_i;
+  const uint4* tq;
+  const uint32_t* tq_bad;
+  float limit;
+  uint16_t* h;  // [R, I] bf16
+  float* y;     // [R, H] fp32
+};
+
+// ------------------------------------------------------------------ x terms
+
+// Block t, wave s: the three int8 terms of x[t] * s_slice over K slice s (256
+// values) in the A-slot layout of q8_aword, and 1 / (4 s_slice).
+template <bool XBF>
+__global__ __launch_bounds__(1024) void k_q8_xterms(const void* x, int H, uint4* xt, float* xinv) {
+  const int lane = threadIdx.x & 63;
+  const int s = threadIdx.x >> 6;
+  const int S = H >> 8;
+  const int t = blockIdx.x;
+  const uint4 c = ldg16_q((const uint4*)x + ((size_t)t * H >> 3) + s * 32 + (lane >> 1));
+  float v[4];
+  q8_half4<XBF>(c, lane & 1, v);
+  const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  float sc, inv4s;
+  q8_scale(rt_wave_reduce(mx, true), sc, inv4s);
+  uint32_t tw[3];
+  q8_terms<3>(v, sc, tw);
+  uint32_t* base = (uint32_t*)(xt + ((size_t)t * S + s) * 3 * 16);
+#pragma unroll
+  for (int n = 0; n < 3; ++n) base[q8_aword((uint32_t)n, lane >> 1, lane & 1)] = tw[n];
+  if (lane == 0) xinv[(size_t)t * S + s] = inv4s;
+}
+
+// ------------------------------------------------------------------ gate/up
+
+// Units [u0, u1) of this block: tile u / rg_n, rows 16 (u % rg_n). Tiles of one
+// block are mostly the same expert's, so consecutive units share A operands.
+template <bool XBF>
+__global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
+  __shared__ uint4 tqs[TQR_BYTES / 16];
+  __shared__ float gred[16][2][MT_TILE][16];  // [wave][gate, up][route][row]
+  const char* tq = (const char*)tqs;
+  const Q8Keys lk = q8_keys(threadIdx.x & 63);
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t j = lane & 15, g = lane >> 4;
+  const bool dec = wv < a.S;  // this wave owns a K slice
+  const int rg_n = a.I >> 4;
+  const int nt = __builtin_amdgcn_readfirstlane(*a.ntiles);
+  const int U = nt * rg_n;
+  const int per = (U + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int u0 = (int)blockIdx.x * per, u1 = min(U, u0 + per);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
+  if (u0 >= u1) {
+    wait_vm_q<0>();
+    return;
+  }
+  const uint32_t C = (uint32_t)a.H >> 3;
+  const uint32_t kc0 = (dec ? wv : 0) * 32 + g * 8;
+  const uint32_t grp = (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.gsz_h;
+  auto unit_rows = [&](int u, uint32_t& rbase, int& ti) {
+    ti = u / rg_n;
+    const int e = a.te[ti];
+    rbase = (uint32_t)e * (uint32_t)a.I + (uint32_t)(u - ti * rg_n) * 16u;
+  };
+  uint4 q[2];
+  ScaleRaw sr[2];
+  auto load_unit = [&](uint32_t rbase) {
+    const uint32_t row = rbase + j;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      q[t] = ldg16_q((t ? a.uc : a.gc) + (size_t)row * C + kc0);
+      sr[t] = scale_raw(t ? a.us : a.gs, a.sdt, row * (uint32_t)a.Gh + grp);
+    }
+  };
+  uint32_t rb;
+  int ti;
+  unit_rows(u0, rb, ti);
+  load_unit(rb);
+  wait_vm_q<4>();  // the table pieces (issued before the 4 unit loads)
+  rt_lds_barrier();
+
+  q8v4 A[MT_CHUNK][4];
+  float inv[MT_CHUNK];
+  auto load_a = [&](int off, int cnt, int c0) {  // A operands of routes c0 .. c0 + MT_CHUNK - 1 of the tile
+#pragma unroll
+    for (int i = 0; i < MT_CHUNK; ++i) {
+      const int ri = c0 + i < cnt ? c0 + i : c0;
+      const int tok = a.order[off + ri] / a.k;
+      const uint4* src = a.xt + (((size_t)tok * a.S + (dec ? wv : 0)) * 3 + (j < 3 ? j : 0)) * 16 + g * 4;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint4 v = ldg16_q(src + m);
+        A[i][m] = j < 3 ? q8v4{(int)v.x, (int)v.y, (int)v.z, (int)v.w} : q8v4{0, 0, 0, 0};
+      }
+      inv[i] = a.xinv[(size_t)tok * a.S + (dec ? wv : 0)];
+    }
+  };
+  int a_tile = -1;  // the tile whose first MT_CHUNK routes' A operands are in A
+  for (int u = u0; u < u1; ++u) {
+    const uint4 qc[2] = {q[0], q[1]};
+    const ScaleRaw sc[2] = {sr[0], sr[1]};
+    const uint32_t rbc = rb;
+    const int tic = ti;
+    const int off = a.to[tic], cnt = a.tc[tic];
+    if (tic != a_tile) {  // before the next unit's loads, so that waiting for it does not wait for them
+      load_a(off, cnt, 0);
+      a_tile = tic;
+    }
+    if (u + 1 < u1) {     // the next unit's codes and scales, in flight during this one
+      unit_rows(u + 1, rb, ti);
+      load_unit(rb);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (dec) {
+      float scl[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) scl[t] = scale_cvt(sc[t], a.sdt, (rbc + j) * (uint32_t)a.Gh + grp);
+      for (int c0 = 0; c0 < cnt; c0 += MT_CHUNK) {
+        if (c0 > 0) {  // more routes than one chunk: reload, and the first chunk again next unit
+          load_a(off, cnt, c0);
+          a_tile = -1;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          q8v4 B[4];
+          q8_decode8(tq, lk, qc[t], B);
+#pragma unroll
+          for (int i = 0; i < MT_CHUNK; ++i) {
+            if (c0 + i < cnt) {
+              q8v4 acc = {0, 0, 0, 0};
+#pragma unroll
+              for (int m = 0; m < 4; ++m) acc = mfma_i8(A[i][m], B[m], acc);
+              if (lane < 16) {
+                const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
+                gred[wv][t][c0 + i][j] = d * inv[i] * scl[t];
+              }
+            }
+          }
+        }
+      }
+    }
+    rt_lds_barrier();
+    // SwiGLU: thread (route i, row jj)
+    if ((int)threadIdx.x < cnt * 16) {
+      const int i = threadIdx.x >> 4, jj = threadIdx.x & 15;
+      float gsum = 0.f, usum = 0.f;
+      for (int w = 0; w < a.S; ++w) {
+        gsum += gred[w][0][i][jj];
+        usum += gred[w][1][i][jj];
+      }
+      float hv = silu_mul(gsum, usum, a.limit);
+      if (*a.tq_bad) hv = __builtin_nanf("");
+      const int route = a.order[off + i];
+      const uint32_t row = (rbc - (uint32_t)a.te[tic] * (uint32_t)a.I) + (uint32_t)jj;
+      a.h[(size_t)route * a.I + row] = from_float<bf16s>(hv).bits;
+    }
+    rt_lds_barrier();
+  }
+  wait_vm_q<0>();
+}
+
+// ------------------------------------------------------------------ down
+
+// Units [u0, u1): tile u / rg_n, rows 32 (u % rg_n) of down. Wave w < I / 256
+// owns K slice w; the A operands of the tile's routes (two int8 terms of h
+// each, rows 2r, 2r + 1 of chunk r / 8) are rebuilt only when the tile changes.
+__global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
+  __shared__ uint4 tqs[TQR_BYTES / 16];
+  __shared__ uint4 ash[8][2][16 * 16];  // [wave][route chunk][row * 16 + slot]
+  __shared__ float s_inv[8][MT_TILE];
+  __shared__ float red[8][2][MT_TILE][16];  // [wave][row-tile][route][row]
+  const char* tq = (const char*)tqs;
+  const Q8Keys lk = q8_keys(threadIdx.x & 63);
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t j = lane & 15, g = lane >> 4;
+  const int nsl = a.I >> 8;
+  const bool dec = wv < nsl;
+  const int rg_n = a.H >> 5;
+  const int nt = __builtin_amdgcn_readfirstlane(*a.ntiles);
+  const int U = nt * rg_n;
+  const int per = (U + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int u0 = (int)blockIdx.x * per, u1 = min(U, u0 + per);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
+  if (u0 >= u1) {
+    wait_vm_q<0>();
+    return;
+  }
+  const uint32_t C = (uint32_t)a.I >> 3;
+  const uint32_t kc0 = (dec ? wv : 0) * 32 + g * 8;
+  const uint32_t grp = (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.gsz_i;
+  uint4 q[2];
+  ScaleRaw sr[2];
+  auto load_unit = [&](int u) {
+    const int t = u / rg_n;
+    const uint32_t rbase = (uint32_t)a.te[t] * (uint32_t)a.H + (uint32_t)(u - t * rg_n) * 32u;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const uint32_t row = rbase + (uint32_t)rt * 16u + j;
+      q[rt] = ldg16_q(a.dc + (size_t)row * C + kc0);
+      sr[rt] = scale_raw(a.ds, a.sdt, row * (uint32_t)a.Gi + grp);
+    }
+  };
+  load_unit(u0);
+  wait_vm_q<4>();  // the table pieces (issued before the 4 unit loads)
+  rt_lds_barrier();
+
+  int cur = -1;
+  for (int u = u0; u < u1; ++u) {
+    const uint4 qc[2] = {q[0], q[1]};
+    const ScaleRaw sc[2] = {sr[0], sr[1]};
+    const int tic = u / rg_n;
+    const uint32_t rb = (uint32_t)a.te[tic] * (uint32_t)a.H + (uint32_t)(u - tic * rg_n) * 32u;
+    const int off = a.to[tic], cnt = a.tc[tic];
+    const bool rebuild = dec && tic != cur;
+    uint4 hq[MT_TILE];
+    if (rebuild) {  // this tile's h slices, before the next unit's loads
+#pragma unroll
+      for (int i = 0; i < MT_TILE; ++i) {
+        const int route = a.order[off + (i < cnt ? i : 0)];
+        hq[i] = ldg16_q((const uint4*)(a.h + (size_t)route * a.I) + wv * 32 + (lane >> 1));
+      }
+    }
+    if (u + 1 < u1) load_unit(u + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (rebuild) {  // A operands of the tile's routes (this wave's own LDS rows)
+      uint32_t* aw = (uint32_t*)ash[wv][0];
+      for (int i = 0; i < 2 * 16 * 16 * 4; i += 64) aw[i + lane] = 0u;
+#pragma unroll
+      for (int i = 0; i < MT_TILE; ++i) {
+        if (i < cnt) {
+          float v[4];
+          q8_half4<true>(hq[i], lane & 1, v);
+          const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+          float s, inv4s;
+          q8_scale(rt_wave_reduce(mx, true), s, inv4s);
+          uint32_t tw[2];
+          q8_terms<2>(v, s, tw);
+          uint32_t* cw = (uint32_t*)ash[wv][i >> 3];
+          cw[q8_aword((uint32_t)(2 * (i & 7)), lane >> 1, lane & 1)] = tw[0];
+          cw[q8_aword((uint32_t)(2 * (i & 7) + 1), lane >> 1, lane & 1)] = tw[1];
+          if (lane == 0) s_inv[wv][i] = inv4s;
+        }
+      }
+    }
+    cur = tic;
+    if (dec) {
+      float scl[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) scl[rt] = scale_cvt(sc[rt], a.sdt, (rb + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
+      for (int ch = 0; ch * 8 < cnt; ++ch) {
+        q8v4 A[4];
+        const q8v4* as = (const q8v4*)ash[wv][ch] + j * 16 + g * 4;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) A[m] = as[m];  // rows past the tile's routes are zero
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          q8v4 B[4];
+          q8_decode8(tq, lk, qc[rt], B);
+          q8v4 acc = {0, 0, 0, 0};
+#pragma unroll
+          for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[m], acc);
+          // route r of the chunk: rows 2r, 2r + 1 = lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int r = ch * 8 + 2 * (int)g + h2;
+            if (r < cnt) {
+              const float d = h2 ? (float)acc[2] + (float)acc[3] * 0.0078125f : (float)acc[0] + (float)acc[1] * 0.0078125f;
+              red[wv][rt][r][j] = d * s_inv[wv][r] * scl[rt];
+            }
+          }
+        }
+      }
+    }
+    rt_lds_barrier();
+    if ((int)threadIdx.x < cnt * 32) {
+      const int i = threadIdx.x >> 5, rt = (threadIdx.x >> 4) & 1, jj = threadIdx.x & 15;
+      float v = 0.f;
+      for (int w = 0; w < nsl; ++w) v += red[w][rt][i][jj];
+      const int route = a.order[off + i];
+      const uint32_t row = (rb - (uint32_t)a.te[tic] * (uint32_t)a.H) + (uint32_t)rt * 16u + (uint32_t)jj;
+      a.y[(size_t)route * a.H + row] = v;
+    }
+    rt_lds_barrier();
+  }
+  wait_vm_q<0>();
+}
+
+// ------------------------------------------------------------------ combine
+
+__global__ __launch_bounds__(256) void k_moe_combine(const float* y, const int32_t* idx, const float* w, int T,
+                                                     int k, int E, int H, const uint32_t* tq_bad, void* out,
+                                                     int odt) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)T * H) return;
+  const int t = (int)(i / H), n = (int)(i - (int64_t)t * H);
+  float o = 0.f;
+  bool bad = false;
+  for (int r = 0; r < k; ++r) {
+    const int e = idx[t * k + r];
+    const float wt = w[t * k + r];
+    const bool ok = e >= 0 && e < E;
+    bad |= wt != 0.f && !ok;
+    if (ok && wt != 0.f) o = fmaf(wt, y[(int64_t)(t * k + r) * H + n], o);
+  }
+  if (bad || *tq_bad) o = __builtin_nanf("");
+  if (odt == KEEP_F16) ((_Float16*)out)[i] = (_Float16)o;
+  else if (odt == KEEP_BF16) ((uint16_t*)out)[i] = from_float<bf16s>(o).bits;
+  else ((float*)out)[i] = o;
+}
+
+// ------------------------------------------------------------------ host
+
+struct MTWorkspace {
+  size_t xt, xinv, order, inverse, counts, offsets, te, to, tc, nt, y, total;
+  int64_t max_tiles;
+};
+
+static size_t mt_align(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static MTWorkspace mt_layout(int64_t T, int64_t k, int64_t E, int64_t H) {
+  MTWorkspace w{};
+  const int64_t R = T * k, S = H / 256;
+  w.max_tiles = (R + MT_TILE - 1) / MT_TILE + E;
+  size_t o = 0;
+  w.xt = o; o = mt_align(o + (size_t)T * S * 3 * 256);
+  w.xinv = o; o = mt_align(o + (size_t)T * S * 4);
+  w.order = o; o = mt_align(o + (size_t)R * 4);
+  w.inverse = o; o = mt_align(o + (size_t)R * 4);
+  w.counts = o; o = mt_align(o + (size_t)E * 4);
+  w.offsets = o; o = mt_align(o + (size_t)E * 4);
+  w.te = o; o = mt_align(o + (size_t)w.max_tiles * 4);
+  w.to = o; o = mt_align(o + (size_t)w.max_tiles * 4);
+  w.tc = o; o = mt_align(o + (size_t)w.max_tiles * 4);
+  w.nt = o; o = mt_align(o + 4);
+  w.y = o; o = mt_align(o + (size_t)R * H * 4);
+  w.total = o;
+  return w;
+}
+
+bool moe_tiles_supported(int64_t T, int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
+  return T >= 1 && T <= 256 && k >= 1 && k <= 16 && k <= E && E >= 1 && E <= 1024 && H % 256 == 0 && H <= 4096 &&
+         I % 256 == 0 && I <= 2048 && group_h % 256 == 0 && group_i % 256 == 0 && (int64_t)E * I <= 0x7fffffffLL &&
+         (int64_t)E * H <= 0x7fffffffLL;
+}
+
+}  // namespace keep
+
+using namespace keep;
+
+// Route-plan launch (plan.hip).
+extern "C" int keep_route_plan(const int32_t* rhs, int64_t R, int64_t E, int64_t tile, int32_t* order,
+                               int32_t* inverse, int32_t* counts, int32_t* offsets, int32_t* tile_expert,
+                               int32_t* tile_offset, int32_t* tile_count, int64_t max_tiles, int32_t* n_tiles_out,
+                               void* stream);
+
+extern "C" int64_t keep_moe_tiles_workspace_bytes(int64_t T, int64_t k, int64_t num_experts, int64_t H) {
+  if (T < 0 || k < 1 || num_experts < 1 || H < 256) return -1;
+  return (int64_t)mt_layout(T, k, num_experts, H).total;
+}
+
+extern "C" int keep_moe_tiles_supported(int64_t T, int64_t num_experts, int64_t H, int64_t I, int64_t k,
+                                        int64_t group_size_h, int64_t group_size_i) {
+  return moe_tiles_supported(T, num_experts, H, I, k, group_size_h, group_size_i) ? 1 : 0;
+}
+
+extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, const int32_t* idx,
+                              const float* w, int64_t k, int64_t num_experts, const uint16_t* gate_codes,
+                              const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
+                              const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                              int64_t group_size_h, int64_t group_size_i, const void* prepared, float swiglu_limit,
+                              void* h_work, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
+                              void* stream) {
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
+  KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
+  KEEP_REQUIRE(group_size_h > 0 && H % group_size_h == 0 && group_size_i > 0 && I % group_size_i == 0,
+               "bad group sizes");
+  KEEP_REQUIRE(moe_tiles_supported(T, num_experts, H, I, k, group_size_h, group_size_i),
+               "shape not served by the tiled MoE kernels (T <= 256, k <= 16, E <= 1024, H a multiple of 256 up "
+               "to 4096, I a multiple of 256 up to 2048, scale groups of 256-element multiples)");
+  KEEP_REQUIRE(x && idx && w && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
+                   prepared && h_work && workspace && out,
+               "null pointer argument");
+  const MTWorkspace L = mt_layout(T, k, num_experts, H);
+  KEEP_REQUIRE(workspace_bytes >= (int64_t)L.total, "workspace needs %lld bytes, got %lld", (long long)L.total,
+               (long long)workspace_bytes);
+  KEEP_REQUIRE(aligned(x, 16) && aligned(h_work, 16) && aligned(prepared, 16) && aligned(workspace, 256),
+               "x, h_work and prepared must be 16-byte aligned and the workspace 256-byte aligned");
+  KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 16), "codes misaligned");
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  MTArgs a{};
+  a.xt = (const uint4*)(ws + L.xt);
+  a.xinv = (const float*)(ws + L.xinv);
+  a.order = (const int32_t*)(ws + L.order);
+  a.te = (const int32_t*)(ws + L.te);
+  a.to = (const int32_t*)(ws + L.to);
+  a.tc = (const int32_t*)(ws + L.tc);
+  a.ntiles = (const int32_t*)(ws + L.nt);
+  a.k = (int32_t)k; a.E = (int32_t)num_experts; a.H = (int32_t)H; a.I = (int32_t)I; a.S = (int32_t)(H / 256);
+  a.gc = gate_codes; a.uc = up_codes; a.dc = down_codes; a.gs = gate_scales; a.us = up_scales; a.ds = down_scales;
+  a.sdt = scale_dtype; a.Gh = (int32_t)(H / group_size_h); a.gsz_h = (int32_t)group_size_h;
+  a.Gi = (int32_t)(I / group_size_i); a.gsz_i = (int32_t)group_size_i;
+  a.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
+  a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
+  a.limit = swiglu_limit;
+  a.h = (uint16_t*)h_work;
+  a.y = (float*)(ws + L.y);
+  const int64_t R = T * k;
+
+  const dim3 xb((unsigned)(64 * (H / 256)));
+  if (x_dtype == KEEP_BF16)
+    hipLaunchKernelGGL((k_q8_xterms<true>), dim3((unsigned)T), xb, 0, s, x, (int)H, (uint4*)(ws + L.xt),
+                       (float*)(ws + L.xinv));
+  else
+    hipLaunchKernelGGL((k_q8_xterms<false>), dim3((unsigned)T), xb, 0, s, x, (int)H, (uint4*)(ws + L.xt),
+                       (float*)(ws + L.xinv));
+  const int rc = keep_route_plan(idx, R, num_experts, MT_TILE, (int32_t*)(ws + L.order), (int32_t*)(ws + L.inverse),
+                                 (int32_t*)(ws + L.counts), (int32_t*)(ws + L.offsets), (int32_t*)(ws + L.te),
+                                 (int32_t*)(ws + L.to), (int32_t*)(ws + L.tc), L.max_tiles, (int32_t*)(ws + L.nt),
+                                 stream);
+  if (rc != KEEP_OK) return rc;
+  const int64_t tiles_ub = std::min<int64_t>(R, L.max_tiles);
+  const unsigned g1 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (I / 16)));
+  const unsigned g2 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (H / 32)));
+  if (x_dtype == KEEP_BF16)
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<true>), dim3(g1), dim3(1024), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<false>), dim3(g1), dim3(1024), 0, s, a);
+  hipLaunchKernelGGL(k_moeq_down_tiles, dim3(g2), dim3(512), 0, s, a);
+  const int64_t n = T * H;
+  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const float*)(ws + L.y), idx,
+                     w, (int)T, (int)k, (int)num_experts, (int)H, a.tq_bad, out, out_dtype);
+  return launch_status("keep_moe_tiles");
+}

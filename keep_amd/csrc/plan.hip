@@ -23,6 +23,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs,
   __shared__ int run[PLAN_MAX_E + 1];
   __shared__ int tbase[PLAN_MAX_E + 1];
   __shared__ int wh[PLAN_WAVES][PLAN_MAX_E + 1];
+  __shared__ int wtot[2][PLAN_WAVES];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int EB = E + 1;  // bucket E collects invalid expert ids
   for (int e = tid; e < EB; e += PLAN_THREADS) cnt[e] = 0;
@@ -33,16 +34,43 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs,
     atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0, tacc = 0;
-    for (int e = 0; e < EB; ++e) {
-      run[e] = acc;
-      acc += cnt[e];
-      tbase[e] = tacc;
-      if (e < E) tacc += (cnt[e] + tile - 1) / tile;
+  // Exclusive prefix sums of the bucket sizes (route bases) and of the tile
+  // counts (first tile of each expert): buckets 2 tid, 2 tid + 1 per thread,
+  // a shuffle scan inside each wave, then the 16 wave totals.
+  {
+    const int b0 = 2 * tid, b1 = 2 * tid + 1;
+    const int c0 = b0 < EB ? cnt[b0] : 0, c1 = b1 < EB ? cnt[b1] : 0;
+    const int t0 = b0 < E ? (c0 + tile - 1) / tile : 0, t1 = b1 < E ? (c1 + tile - 1) / tile : 0;
+    int vc = c0 + c1, vt = t0 + t1;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int oc = __shfl_up(vc, d, 64), ot = __shfl_up(vt, d, 64);
+      if (lane >= d) {
+        vc += oc;
+        vt += ot;
+      }
     }
-    tbase[E] = tacc;
-    n_tiles_out[0] = tacc;
+    if (lane == 63) {
+      wtot[0][wv] = vc;
+      wtot[1][wv] = vt;
+    }
+    __syncthreads();
+    int bc = 0, bt = 0;
+    for (int w = 0; w < wv; ++w) {
+      bc += wtot[0][w];
+      bt += wtot[1][w];
+    }
+    const int ec = bc + vc - (c0 + c1), et = bt + vt - (t0 + t1);  // exclusive
+    if (b0 < EB) {
+      run[b0] = ec;
+      tbase[b0] = et;
+    }
+    if (b1 < EB) {
+      run[b1] = ec + c0;
+      tbase[b1] = et + t0;
+    }
+    if (b0 == E) n_tiles_out[0] = et;
+    if (b1 == E) n_tiles_out[0] = et + t0;
   }
   __syncthreads();
   for (int e = tid; e < E; e += PLAN_THREADS) {

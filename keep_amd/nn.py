@@ -197,7 +197,9 @@ class QuantizedVQSwitchGLU:
 def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, up, down, *, limit: float = 0.0,
                codebook: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
                h_work: torch.Tensor | None = None, prepared: bool = True) -> torch.Tensor:
-    """Fused routed SwiGLU MoE for few tokens (``keep_moe_decode``, two launches).
+    """Fused routed SwiGLU MoE for few tokens: ``keep_moe_tiles`` (routes grouped
+    per expert, each hit expert read once; five launches) for T > 1 where it
+    serves the shape, else ``keep_moe_decode`` (two launches).
 
     ``gate``/``up``/``down`` are ``(codes, scales)``: gate/up ``[E, I, H/8]``,
     down ``[E, H, I/8]``. ``out[t] = sum_j w[t,j] * down_e(swiglu(gate_e x_t, up_e x_t))``
@@ -230,11 +232,28 @@ def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, u
     idx32 = idx.to(torch.int32).contiguous()
     w32 = weight.to(torch.float32).contiguous()
     prep = ops.prepared_table(cb) if prepared else None
+    gh, gi = H // gs.shape[-1], I // ds.shape[-1]
+    if T > 1 and prep is not None and moe_tiles_supported(T, E, H, I, k, gh, gi):
+        ws = torch.empty(int(_lib.load().keep_moe_tiles_workspace_bytes(T, k, E, H)), dtype=torch.uint8,
+                         device=device)
+        _lib.call("keep_moe_tiles", x.data_ptr(), ops._DT[x.dtype], T, H, I, idx32.data_ptr(), w32.data_ptr(), k, E,
+                  gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
+                  ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), h_work.data_ptr(), ws.data_ptr(),
+                  ws.numel(), out.data_ptr(), ops._DT[od], ops._stream(device))
+        return out
     _lib.call("keep_moe_decode", x.data_ptr(), ops._DT[x.dtype], T, H, I, idx32.data_ptr(), w32.data_ptr(), k, E,
               gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
               ops._DT[gs.dtype], H // gs.shape[-1], I // ds.shape[-1], cb.data_ptr(), ops._ptr(prep),
               float(limit), h_work.data_ptr(), out.data_ptr(), ops._DT[od], ops._stream(device))
     return out
+
+
+def moe_tiles_supported(T: int, num_experts: int, hidden: int, intermediate: int, k: int, group_size_h: int,
+                        group_size_i: int) -> bool:
+    """Whether the expert-grouped few-token path (``keep_moe_tiles``) serves this shape."""
+
+    return bool(_lib.load().keep_moe_tiles_supported(T, num_experts, hidden, intermediate, k, group_size_h,
+                                                      group_size_i))
 
 
 def moe_layer_supported(num_experts: int, hidden: int, intermediate: int, k: int, group_size_h: int,

@@ -1,0 +1,113 @@
+"""GPU parity of the expert-grouped few-token MoE (keep_moe_tiles): byte
+identity with the one-token layer token by token (the verify-rows discipline
+of the reference, tests/test_gather_vqmm_verify_rows.py:1-33), the C oracle at
+the verify shapes of config 3, the float64 oracle with many routes per expert
+(several tiles and route chunks per expert), and the combine's edge cases."""
+
+import numpy as np
+import pytest
+import torch
+
+import keep_amd
+from keep_amd import synth
+from oracle import cpu, e8p, ops
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _t(a, dev):
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _check(got, want, tol=TOL):
+    g = got.float().cpu().numpy()
+    err = ops.max_rel_err(g, want)
+    assert err <= tol, f"max rel err {err:.3e}"
+    assert ops.elementwise_ok(g, want, rtol=tol), "elementwise bound violated"
+    return err
+
+
+@pytest.fixture(scope="module")
+def pool(dev):
+    E, H, I = 384, 4096, 2048
+    return (synth.projection(E, I, H, seed=1, device=dev), synth.projection(E, I, H, seed=2, device=dev),
+            synth.projection(E, H, I, seed=3, device=dev))
+
+
+def _pairs(pool):
+    return tuple((p.codes, p.scales) for p in pool)
+
+
+def test_tiles_byte_identical_to_one_token_layer(dev, pool):
+    """Each token's output equals keep_moe_layer's for that token bit for bit."""
+    E, H, I, k, T = 384, 4096, 2048, 6, 8
+    assert keep_amd.nn.moe_tiles_supported(T, E, H, I, k, H, I)
+    x = synth.rht_activations(T, H, seed=21, device=dev)
+    z = synth.router_logits(T, E, seed=22, device=dev)
+    z[1] = z[0]  # two tokens routed to the same experts: their routes share tiles
+    r = keep_amd.router_dual_topk(z, k)
+    out = keep_amd.moe_decode(x, r.idx, r.weight, *_pairs(pool))
+    for t in range(T):
+        one, rt = keep_amd.moe_layer(x[t:t + 1], z[t:t + 1], *_pairs(pool), k=k)
+        assert torch.equal(rt.idx[0], r.idx[t])
+        assert torch.equal(one[0], out[t]), f"token {t} differs from the one-token layer"
+
+
+@pytest.mark.parametrize("T", [16, 64])
+def test_tiles_verify_shapes_vs_c_oracle(dev, pool, T):
+    E, H, I, k = 384, 4096, 2048, 6
+    x = synth.rht_activations(T, H, seed=30 + T, device=dev)
+    z = synth.router_logits(T, E, seed=40 + T, device=dev)
+    r = keep_amd.router_dual_topk(z, k)
+    out = keep_amd.moe_decode(x, r.idx, r.weight, *_pairs(pool))
+    idx = r.idx.cpu().numpy()
+    used = np.unique(idx)
+    sub = {e: i for i, e in enumerate(used)}
+    sel = torch.from_numpy(used).to(dev).long()
+    pick = lambda p: (p.codes[sel].cpu().numpy().view(np.uint16), p.scales[sel].float().cpu().numpy())  # noqa: E731
+    local = np.vectorize(sub.get)(idx).astype(np.int32)
+    want = cpu.moe_decode(x.float().cpu().numpy(), local, r.weight.cpu().numpy(), *(pick(p) for p in pool),
+                          e8p.e8p_packed_abs_grid())
+    _check(out, want)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_tiles_many_routes_per_expert_vs_oracle(dev, xdt):
+    """Four experts, 48 tokens x 3 routes: ~36 routes per expert, so several
+    16-route tiles per expert and several A chunks per tile."""
+    E, H, I, k, T = 4, 512, 512, 3, 48
+    gate = synth.projection_np(E, I, H, group_size=256, seed=51)
+    up = synth.projection_np(E, I, H, group_size=256, seed=52)
+    down = synth.projection_np(E, H, I, seed=53)
+    x = synth.rht_activations(T, H, seed=54, device=dev, dtype=xdt)
+    z = synth.router_logits(T, E, seed=55, device=dev)
+    r = keep_amd.router_dual_topk(z, k)
+    counts = np.bincount(r.idx.cpu().numpy().ravel(), minlength=E)
+    assert counts.max() > 16
+    tt = lambda p: (_t(p[0], dev), _t(p[1], dev))  # noqa: E731
+    out = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=7.0)
+    want = ops.moe_layer(x.float().cpu().numpy(), r.idx.cpu().numpy(), r.weight.cpu().numpy(), gate, up, down,
+                         limit=7.0, h_round="bfloat16")
+    _check(out, want)
+
+
+def test_tiles_zero_weight_and_bad_expert(dev):
+    """A zero-weight route adds nothing; an out-of-range expert with a weight
+    makes its token's row NaN and leaves the others intact."""
+    E, H, I, k, T = 8, 256, 256, 2, 3
+    gate = synth.projection_np(E, I, H, seed=61)
+    up = synth.projection_np(E, I, H, seed=62)
+    down = synth.projection_np(E, H, I, seed=63)
+    x = synth.rht_activations(T, H, seed=64, device=dev)
+    idx = torch.tensor([[1, 2], [3, 99], [5, -4]], dtype=torch.int32, device=dev)
+    w = torch.tensor([[0.7, 0.0], [0.4, 0.6], [1.0, 0.0]], dtype=torch.float32, device=dev)
+    tt = lambda p: (_t(p[0], dev), _t(p[1], dev))  # noqa: E731
+    out = keep_amd.moe_decode(x, idx, w, tt(gate), tt(up), tt(down)).cpu()
+    assert torch.isnan(out[1]).all()
+    good = np.array([[1, 2], [5, 0]], dtype=np.int32)
+    gw = np.array([[0.7, 0.0], [1.0, 0.0]], dtype=np.float32)
+    want = ops.moe_layer(x[[0, 2]].float().cpu().numpy(), good, gw, gate, up, down, h_round="bfloat16")
+    _check(out[[0, 2]], want)
