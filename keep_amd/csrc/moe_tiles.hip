@@ -17,10 +17,10 @@
 //     16 rows of gate and up; 16 waves each own a K slice. Each code load is
 //     decoded once (LDS image lookups) and then multiplied, with one MFMA
 //     group per route, by the A operand of that route's token (rows 0-2 =
-//     its three terms, kept in registers while the block's units stay in one
-//     tile). The next unit's codes are loaded before this unit's decode.
+//     its three terms, DMA'd into LDS when the block enters a tile). The next
+//     two units' codes are in flight while one is decoded.
 //     SwiGLU in fp32, h in bf16 at its route's row;
-//  4. k_moeq_down_tiles: persistent. A unit is one tile x 32 rows of down; a
+//  4. k_moeq_down_tiles: persistent. A unit is one tile x 64 rows of down; a
 //     wave owns a 256-wide K slice of h; the A operand holds two int8 terms
 //     of up to 8 routes (rows 2r, 2r + 1), built once per tile. Output
 //     y[route][row] in fp32;
@@ -35,7 +35,6 @@
 namespace keep {
 
 constexpr int MT_TILE = 16;  // routes per tile (one MFMA group each in gate/up, A rows in down)
-constexpr int MT_CHUNK = 2;  // routes whose A operands are held in registers at once (gate/up)
 
 struct MTArgs {
   const uint4* xt;     // [T][S][3][16] 16-byte slots of int8 terms
@@ -79,18 +78,38 @@ __global__ __launch_bounds__(1024) void k_q8_xterms(const void* x, int H, uint4*
 
 // ------------------------------------------------------------------ gate/up
 
-// Units [u0, u1) of this block: tile u / rg_n, rows 16 (u % rg_n). Tiles of one
-// block are mostly the same expert's, so consecutive units share A operands.
+// The two persistent kernels share one schedule. A block's units form runs
+// of one tile, cut into segments of at most SEG units. Per segment and per
+// pass over the tile's routes (RA at a time): the routes' A operands, then
+// the segment's units with two units' codes (and their scale words, DMA'd to
+// LDS ahead of them) in flight while one is decoded, unrolled by two over
+// two register buffers. Inside a segment every load is unconditional (past
+// its end the last unit is loaded again and stores nothing) and no global
+// store is issued -- outputs are staged in LDS and written when the segment
+// ends -- so each wait the compiler inserts counts exactly the loads before
+// it (a store among them would make it wait for everything).
+
+// Gate/up: a unit is 16 rows of gate and of up (two code loads per wave, 32
+// KiB per block); a route's A operand for this wave's slice (3 term rows x
+// 256 B) is one 768-byte DMA into the wave's LDS slot.
 template <bool XBF>
 __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
+  constexpr int RA = 4;    // routes per pass
+  constexpr int SEG = 32;  // units per segment
   __shared__ uint4 tqs[TQR_BYTES / 16];
-  __shared__ float gred[16][2][MT_TILE][16];  // [wave][gate, up][route][row]
+  __shared__ uint4 asl[16][RA][3 * 16];    // [wave][route][term row * 16 + slot]
+  __shared__ float s_inv[16][RA];
+  __shared__ float gred[16][2][RA][16];    // [wave][gate, up][route][row]
+  __shared__ uint16_t hst[RA][SEG * 16];   // the segment's h rows
+  __shared__ int32_t s_route[RA];
   const char* tq = (const char*)tqs;
+  const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
   const Q8Keys lk = q8_keys(threadIdx.x & 63);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t j = lane & 15, g = lane >> 4;
   const bool dec = wv < a.S;  // this wave owns a K slice
+  const int sl = dec ? wv : 0;
   const int rg_n = a.I >> 4;
   const int nt = __builtin_amdgcn_readfirstlane(*a.ntiles);
   const int U = nt * rg_n;
@@ -103,120 +122,122 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
     return;
   }
   const uint32_t C = (uint32_t)a.H >> 3;
-  const uint32_t kc0 = (dec ? wv : 0) * 32 + g * 8;
-  const uint32_t grp = (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.gsz_h;
-  auto unit_rows = [&](int u, uint32_t& rbase, int& ti) {
-    ti = u / rg_n;
-    const int e = a.te[ti];
-    rbase = (uint32_t)e * (uint32_t)a.I + (uint32_t)(u - ti * rg_n) * 16u;
+  const uint32_t kc0 = (uint32_t)sl * 32 + g * 8;
+  const uint32_t grp = (uint32_t)(sl * 256) / (uint32_t)a.gsz_h;
+  const uint32_t sbytes = a.sdt == KEEP_F32 ? 4u : 2u;
+  struct Buf {
+    uint4 q[2];
+    uint32_t s[2];
   };
-  uint4 q[2];
-  ScaleRaw sr[2];
-  auto load_unit = [&](uint32_t rbase) {
-    const uint32_t row = rbase + j;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      q[t] = ldg16_q((t ? a.uc : a.gc) + (size_t)row * C + kc0);
-      sr[t] = scale_raw(t ? a.us : a.gs, a.sdt, row * (uint32_t)a.Gh + grp);
-    }
-  };
-  uint32_t rb;
-  int ti;
-  unit_rows(u0, rb, ti);
-  load_unit(rb);
-  wait_vm_q<4>();  // the table pieces (issued before the 4 unit loads)
-  rt_lds_barrier();
-
-  q8v4 A[MT_CHUNK][4];
-  float inv[MT_CHUNK];
-  auto load_a = [&](int off, int cnt, int c0) {  // A operands of routes c0 .. c0 + MT_CHUNK - 1 of the tile
-#pragma unroll
-    for (int i = 0; i < MT_CHUNK; ++i) {
-      const int ri = c0 + i < cnt ? c0 + i : c0;
-      const int tok = a.order[off + ri] / a.k;
-      const uint4* src = a.xt + (((size_t)tok * a.S + (dec ? wv : 0)) * 3 + (j < 3 ? j : 0)) * 16 + g * 4;
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const uint4 v = ldg16_q(src + m);
-        A[i][m] = j < 3 ? q8v4{(int)v.x, (int)v.y, (int)v.z, (int)v.w} : q8v4{0, 0, 0, 0};
-      }
-      inv[i] = a.xinv[(size_t)tok * a.S + (dec ? wv : 0)];
-    }
-  };
-  int a_tile = -1;  // the tile whose first MT_CHUNK routes' A operands are in A
-  for (int u = u0; u < u1; ++u) {
-    const uint4 qc[2] = {q[0], q[1]};
-    const ScaleRaw sc[2] = {sr[0], sr[1]};
-    const uint32_t rbc = rb;
-    const int tic = ti;
+  for (int us = u0; us < u1;) {
+    const int tic = us / rg_n;
+    const int ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
+    const uint32_t ebase = (uint32_t)a.te[tic] * (uint32_t)a.I;
+    const uint32_t row0 = (uint32_t)(us - tic * rg_n) * 16u;
     const int off = a.to[tic], cnt = a.tc[tic];
-    if (tic != a_tile) {  // before the next unit's loads, so that waiting for it does not wait for them
-      load_a(off, cnt, 0);
-      a_tile = tic;
-    }
-    if (u + 1 < u1) {     // the next unit's codes and scales, in flight during this one
-      unit_rows(u + 1, rb, ti);
-      load_unit(rb);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (dec) {
-      float scl[2];
+    // a unit's codes and its rows' scale words (the aligned word holding each)
+    auto load_unit = [&](int u, Buf& b) {
+      const uint32_t row = ebase + (uint32_t)(min(u, ue - 1) - tic * rg_n) * 16u + j;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) scl[t] = scale_cvt(sc[t], a.sdt, (rbc + j) * (uint32_t)a.Gh + grp);
-      for (int c0 = 0; c0 < cnt; c0 += MT_CHUNK) {
-        if (c0 > 0) {  // more routes than one chunk: reload, and the first chunk again next unit
-          load_a(off, cnt, c0);
-          a_tile = -1;
-        }
+      for (int t = 0; t < 2; ++t) {
+        b.q[t] = ldg16_q((t ? a.uc : a.gc) + (size_t)row * C + kc0);
+        b.s[t] = ldg4_q((const char*)(t ? a.us : a.gs) + ((row * (uint32_t)a.Gh + grp) * sbytes & ~3u));
+      }
+    };
+    for (int r0 = 0; r0 < cnt; r0 += RA) {
+      const int nr = min(RA, cnt - r0);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          q8v4 B[4];
-          q8_decode8(tq, lk, qc[t], B);
+      for (int i = 0; i < RA; ++i) {  // the routes' A operands (lanes 0-47) and slice scales
+        const int tok = a.order[off + r0 + min(i, nr - 1)] / a.k;
+        if (lane < 48) dma16_q(a.xt + ((size_t)tok * a.S + sl) * 48 + lane, asl[wv][i]);
+        if (lane == 0) s_inv[wv][i] = a.xinv[(size_t)tok * a.S + sl];
+      }
+      if ((int)threadIdx.x < RA) s_route[threadIdx.x] = a.order[off + r0 + min((int)threadIdx.x, nr - 1)];
+      Buf b0, b1;
+      load_unit(us, b0);
+      load_unit(us + 1, b1);
+      wait_vm_q<0>();
+      rt_lds_barrier();  // every wave's table pieces, A operands, the routes
+      auto unit = [&](int u, Buf& b) {
+        const uint32_t rowc = (uint32_t)(min(u, ue - 1) - tic * rg_n) * 16u;
+        q8v4 B[2][4];
 #pragma unroll
-          for (int i = 0; i < MT_CHUNK; ++i) {
-            if (c0 + i < cnt) {
+        for (int t = 0; t < 2; ++t) q8_decode8(tq, lk, b.q[t], B[t]);
+        float scl[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          scl[t] = scale_cvt(b.s[t], a.sdt, (ebase + rowc + j) * (uint32_t)a.Gh + grp);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(scl[t]));  // converted before b.s is reloaded
+        load_unit(u + 2, b);
+        __builtin_amdgcn_sched_barrier(0);
+        if (dec) {
+#pragma unroll 1
+          for (int i = 0; i < nr; ++i) {
+            const q8v4* as = (const q8v4*)asl[wv][i] + (j < 3 ? j : 0) * 16 + g * 4;
+            q8v4 A[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const q8v4 av = as[m];
+              A[m] = j < 3 ? av : q8v4{0, 0, 0, 0};
+            }
+            const float inv = s_inv[wv][i];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
               q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
-              for (int m = 0; m < 4; ++m) acc = mfma_i8(A[i][m], B[m], acc);
+              for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[t][m], acc);
               if (lane < 16) {
                 const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
-                gred[wv][t][c0 + i][j] = d * inv[i] * scl[t];
+                gred[wv][t][i][j] = d * inv * scl[t];
               }
             }
           }
         }
+        rt_lds_barrier();
+        // SwiGLU: thread (route i, row jj) -> the staged h rows
+        if ((int)threadIdx.x < nr * 16 && u < ue) {
+          const int i = threadIdx.x >> 4, jj = threadIdx.x & 15;
+          float gsum = 0.f, usum = 0.f;
+          for (int w = 0; w < a.S; ++w) {
+            gsum += gred[w][0][i][jj];
+            usum += gred[w][1][i][jj];
+          }
+          float hv = silu_mul(gsum, usum, a.limit);
+          if (tq_bad) hv = __builtin_nanf("");
+          hst[i][(u - us) * 16 + jj] = from_float<bf16s>(hv).bits;
+        }
+      };
+      for (int u = us; u < ue; u += 2) {  // both calls unconditional: a unit past the end stores nothing
+        unit(u, b0);
+        unit(u + 1, b1);
+      }
+      rt_lds_barrier();
+      const int rows = (ue - us) * 16;
+      for (int x = threadIdx.x; x < nr * rows; x += 1024) {
+        const int i = x / rows, r = x - i * rows;
+        a.h[(size_t)s_route[i] * a.I + row0 + (uint32_t)r] = hst[i][r];
       }
     }
-    rt_lds_barrier();
-    // SwiGLU: thread (route i, row jj)
-    if ((int)threadIdx.x < cnt * 16) {
-      const int i = threadIdx.x >> 4, jj = threadIdx.x & 15;
-      float gsum = 0.f, usum = 0.f;
-      for (int w = 0; w < a.S; ++w) {
-        gsum += gred[w][0][i][jj];
-        usum += gred[w][1][i][jj];
-      }
-      float hv = silu_mul(gsum, usum, a.limit);
-      if (*a.tq_bad) hv = __builtin_nanf("");
-      const int route = a.order[off + i];
-      const uint32_t row = (rbc - (uint32_t)a.te[tic] * (uint32_t)a.I) + (uint32_t)jj;
-      a.h[(size_t)route * a.I + row] = from_float<bf16s>(hv).bits;
-    }
-    rt_lds_barrier();
+    us = ue;
   }
   wait_vm_q<0>();
 }
 
-// ------------------------------------------------------------------ down
-
-// Units [u0, u1): tile u / rg_n, rows 32 (u % rg_n) of down. Wave w < I / 256
-// owns K slice w; the A operands of the tile's routes (two int8 terms of h
-// each, rows 2r, 2r + 1 of chunk r / 8) are rebuilt only when the tile changes.
+// Down: a unit is 64 rows (four 16-row tiles, 32 KiB of codes per block);
+// wave w < I / 256 owns K slice w. The A operand holds two int8 terms of h
+// for each of up to 8 routes (rows 2r, 2r + 1), built from h at each pass;
+// route r's dot is D rows 2r, 2r + 1.
 __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
+  constexpr int RT = 4;
+  constexpr int RP = 8;   // routes per pass
+  constexpr int SEG = 8;  // units per segment
   __shared__ uint4 tqs[TQR_BYTES / 16];
-  __shared__ uint4 ash[8][2][16 * 16];  // [wave][route chunk][row * 16 + slot]
-  __shared__ float s_inv[8][MT_TILE];
-  __shared__ float red[8][2][MT_TILE][16];  // [wave][row-tile][route][row]
+  __shared__ uint4 ash[8][16 * 16];         // [wave][row * 16 + slot]
+  __shared__ float s_inv[8][RP];
+  __shared__ float red[8][RT][RP][16];      // [wave][row-tile][route][row]
+  __shared__ float yst[RP][SEG * 16 * RT];  // the segment's y rows
+  __shared__ int32_t s_route[RP];
   const char* tq = (const char*)tqs;
   const Q8Keys lk = q8_keys(threadIdx.x & 63);
   const int lane = threadIdx.x & 63;
@@ -224,7 +245,7 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
   const uint32_t j = lane & 15, g = lane >> 4;
   const int nsl = a.I >> 8;
   const bool dec = wv < nsl;
-  const int rg_n = a.H >> 5;
+  const int rg_n = a.H / (16 * RT);
   const int nt = __builtin_amdgcn_readfirstlane(*a.ntiles);
   const int U = nt * rg_n;
   const int per = (U + (int)gridDim.x - 1) / (int)gridDim.x;
@@ -238,99 +259,116 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
   const uint32_t C = (uint32_t)a.I >> 3;
   const uint32_t kc0 = (dec ? wv : 0) * 32 + g * 8;
   const uint32_t grp = (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.gsz_i;
-  uint4 q[2];
-  ScaleRaw sr[2];
-  auto load_unit = [&](int u) {
-    const int t = u / rg_n;
-    const uint32_t rbase = (uint32_t)a.te[t] * (uint32_t)a.H + (uint32_t)(u - t * rg_n) * 32u;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const uint32_t row = rbase + (uint32_t)rt * 16u + j;
-      q[rt] = ldg16_q(a.dc + (size_t)row * C + kc0);
-      sr[rt] = scale_raw(a.ds, a.sdt, row * (uint32_t)a.Gi + grp);
-    }
+  const uint32_t sbytes = a.sdt == KEEP_F32 ? 4u : 2u;
+  struct Buf {
+    uint4 q[RT];
+    uint32_t s[RT];
   };
-  load_unit(u0);
-  wait_vm_q<4>();  // the table pieces (issued before the 4 unit loads)
-  rt_lds_barrier();
-
-  int cur = -1;
-  for (int u = u0; u < u1; ++u) {
-    const uint4 qc[2] = {q[0], q[1]};
-    const ScaleRaw sc[2] = {sr[0], sr[1]};
-    const int tic = u / rg_n;
-    const uint32_t rb = (uint32_t)a.te[tic] * (uint32_t)a.H + (uint32_t)(u - tic * rg_n) * 32u;
+  for (int us = u0; us < u1;) {
+    const int tic = us / rg_n;
+    const int ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
+    const uint32_t ebase = (uint32_t)a.te[tic] * (uint32_t)a.H;
+    const uint32_t row0 = (uint32_t)(us - tic * rg_n) * (16u * RT);
     const int off = a.to[tic], cnt = a.tc[tic];
-    const bool rebuild = dec && tic != cur;
-    uint4 hq[MT_TILE];
-    if (rebuild) {  // this tile's h slices, before the next unit's loads
+    // a unit's codes and its rows' scale words (the aligned word holding each)
+    auto load_unit = [&](int u, Buf& b) {
+      const uint32_t rbase = ebase + (uint32_t)(min(u, ue - 1) - tic * rg_n) * (16u * RT) + j;
 #pragma unroll
-      for (int i = 0; i < MT_TILE; ++i) {
-        const int route = a.order[off + (i < cnt ? i : 0)];
-        hq[i] = ldg16_q((const uint4*)(a.h + (size_t)route * a.I) + wv * 32 + (lane >> 1));
+      for (int rt = 0; rt < RT; ++rt) {
+        b.q[rt] = ldg16_q(a.dc + (size_t)(rbase + (uint32_t)rt * 16u) * C + kc0);
+        b.s[rt] = ldg4_q((const char*)a.ds + (((rbase + (uint32_t)rt * 16u) * (uint32_t)a.Gi + grp) * sbytes & ~3u));
       }
-    }
-    if (u + 1 < u1) load_unit(u + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    if (rebuild) {  // A operands of the tile's routes (this wave's own LDS rows)
-      uint32_t* aw = (uint32_t*)ash[wv][0];
-      for (int i = 0; i < 2 * 16 * 16 * 4; i += 64) aw[i + lane] = 0u;
+    };
+    for (int r0 = 0; r0 < cnt; r0 += RP) {
+      const int nr = min(RP, cnt - r0);
+      if ((int)threadIdx.x < RP) s_route[threadIdx.x] = a.order[off + r0 + min((int)threadIdx.x, nr - 1)];
+      if (dec) {  // the pass's h slices -> A operands (this wave's own LDS rows)
+        uint4 hq[RP];
 #pragma unroll
-      for (int i = 0; i < MT_TILE; ++i) {
-        if (i < cnt) {
-          float v[4];
-          q8_half4<true>(hq[i], lane & 1, v);
-          const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-          float s, inv4s;
-          q8_scale(rt_wave_reduce(mx, true), s, inv4s);
-          uint32_t tw[2];
-          q8_terms<2>(v, s, tw);
-          uint32_t* cw = (uint32_t*)ash[wv][i >> 3];
-          cw[q8_aword((uint32_t)(2 * (i & 7)), lane >> 1, lane & 1)] = tw[0];
-          cw[q8_aword((uint32_t)(2 * (i & 7) + 1), lane >> 1, lane & 1)] = tw[1];
-          if (lane == 0) s_inv[wv][i] = inv4s;
+        for (int i = 0; i < RP; ++i) {
+          const int route = a.order[off + r0 + min(i, nr - 1)];
+          hq[i] = ldg16_q((const uint4*)(a.h + (size_t)route * a.I) + wv * 32 + (lane >> 1));
         }
-      }
-    }
-    cur = tic;
-    if (dec) {
-      float scl[2];
+        uint32_t* aw = (uint32_t*)ash[wv];
+        for (int i = 0; i < 16 * 16 * 4; i += 64) aw[i + lane] = 0u;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) scl[rt] = scale_cvt(sc[rt], a.sdt, (rb + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
-      for (int ch = 0; ch * 8 < cnt; ++ch) {
-        q8v4 A[4];
-        const q8v4* as = (const q8v4*)ash[wv][ch] + j * 16 + g * 4;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) A[m] = as[m];  // rows past the tile's routes are zero
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          q8v4 B[4];
-          q8_decode8(tq, lk, qc[rt], B);
-          q8v4 acc = {0, 0, 0, 0};
-#pragma unroll
-          for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[m], acc);
-          // route r of the chunk: rows 2r, 2r + 1 = lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
-#pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2) {
-            const int r = ch * 8 + 2 * (int)g + h2;
-            if (r < cnt) {
-              const float d = h2 ? (float)acc[2] + (float)acc[3] * 0.0078125f : (float)acc[0] + (float)acc[1] * 0.0078125f;
-              red[wv][rt][r][j] = d * s_inv[wv][r] * scl[rt];
-            }
+        for (int i = 0; i < RP; ++i) {
+          if (i < nr) {
+            float v[4];
+            q8_half4<true>(hq[i], lane & 1, v);
+            const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+            float sc, inv4s;
+            q8_scale(rt_wave_reduce(mx, true), sc, inv4s);
+            uint32_t tw[2];
+            q8_terms<2>(v, sc, tw);
+            aw[q8_aword((uint32_t)(2 * i), lane >> 1, lane & 1)] = tw[0];
+            aw[q8_aword((uint32_t)(2 * i + 1), lane >> 1, lane & 1)] = tw[1];
+            if (lane == 0) s_inv[wv][i] = inv4s;
           }
         }
       }
+      Buf b0, b1;
+      load_unit(us, b0);
+      load_unit(us + 1, b1);
+      wait_vm_q<0>();
+      rt_lds_barrier();  // every wave's table pieces, the routes
+      q8v4 A[4];
+      {
+        const q8v4* as = (const q8v4*)ash[wv] + j * 16 + g * 4;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) A[m] = as[m];  // rows past the pass's routes are zero
+      }
+      auto unit = [&](int u, Buf& b) {
+        const uint32_t rowc = (uint32_t)(min(u, ue - 1) - tic * rg_n) * (16u * RT);
+        q8v4 B[RT][4];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) q8_decode8(tq, lk, b.q[rt], B[rt]);
+        float scl[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          scl[rt] = scale_cvt(b.s[rt], a.sdt, (ebase + rowc + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(scl[rt]));  // converted before b.s is reloaded
+        load_unit(u + 2, b);
+        __builtin_amdgcn_sched_barrier(0);
+        if (dec) {
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            q8v4 acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[rt][m], acc);
+            // route r: rows 2r, 2r + 1 = lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int r = 2 * (int)g + h2;
+              if (r < nr) {
+                const float d = h2 ? (float)acc[2] + (float)acc[3] * 0.0078125f : (float)acc[0] + (float)acc[1] * 0.0078125f;
+                red[wv][rt][r][j] = d * s_inv[wv][r] * scl[rt];
+              }
+            }
+          }
+        }
+        rt_lds_barrier();
+        if ((int)threadIdx.x < nr * 16 * RT && u < ue) {
+          const int i = threadIdx.x / (16 * RT), rt = (threadIdx.x >> 4) % RT, jj = threadIdx.x & 15;
+          float v = 0.f;
+          for (int w = 0; w < nsl; ++w) v += red[w][rt][i][jj];
+          yst[i][(u - us) * 16 * RT + rt * 16 + jj] = v;
+        }
+      };
+      for (int u = us; u < ue; u += 2) {  // both calls unconditional: a unit past the end stores nothing
+        unit(u, b0);
+        unit(u + 1, b1);
+      }
+      rt_lds_barrier();
+      const int rows = (ue - us) * 16 * RT;
+      for (int x = threadIdx.x; x < nr * rows; x += 512) {
+        const int i = x / rows, r = x - i * rows;
+        a.y[(size_t)s_route[i] * a.H + row0 + (uint32_t)r] = yst[i][r];
+      }
+      rt_lds_barrier();  // the flush has read yst and s_route
     }
-    rt_lds_barrier();
-    if ((int)threadIdx.x < cnt * 32) {
-      const int i = threadIdx.x >> 5, rt = (threadIdx.x >> 4) & 1, jj = threadIdx.x & 15;
-      float v = 0.f;
-      for (int w = 0; w < nsl; ++w) v += red[w][rt][i][jj];
-      const int route = a.order[off + i];
-      const uint32_t row = (rb - (uint32_t)a.te[tic] * (uint32_t)a.H) + (uint32_t)rt * 16u + (uint32_t)jj;
-      a.y[(size_t)route * a.H + row] = v;
-    }
-    rt_lds_barrier();
+    us = ue;
   }
   wait_vm_q<0>();
 }
@@ -471,7 +509,7 @@ extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, 
   if (rc != KEEP_OK) return rc;
   const int64_t tiles_ub = std::min<int64_t>(R, L.max_tiles);
   const unsigned g1 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (I / 16)));
-  const unsigned g2 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (H / 32)));
+  const unsigned g2 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (H / 64)));
   if (x_dtype == KEEP_BF16)
     hipLaunchKernelGGL((k_moeq_gateup_tiles<true>), dim3(g1), dim3(1024), 0, s, a);
   else

@@ -73,10 +73,12 @@ __device__ __forceinline__ Q8Keys q8_keys(uint32_t lane) {
   k.s2hi = m_first ? 0x0c0c0700u : 0x0c0c0600u;
   return k;
 }
+template <bool HALVES = false>
 __device__ __forceinline__ void q8_decode8(const char* tqr, const Q8Keys& k, uint4 q, q8v4 (&b)[4]) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    if (HALVES && i == 2) __builtin_amdgcn_sched_barrier(0);  // at most 8 lookups in flight (register pressure)
     const uint32_t a1 = __builtin_amdgcn_perm(w[i], k.base1, k.s1lo);
     const uint32_t a2 = __builtin_amdgcn_perm(w[i], k.base2, k.s2lo);
     const uint32_t b1 = __builtin_amdgcn_perm(w[i], k.base1, k.s1hi);
@@ -147,6 +149,8 @@ __device__ __forceinline__ uint4 ldg16_q(const void* p) {
   const v4u v = *(const __attribute__((address_space(1))) v4u*)p;
   return uint4{v.x, v.y, v.z, v.w};
 }
+
+__device__ __forceinline__ uint32_t ldg4_q(const void* p) { return *(const __attribute__((address_space(1))) uint32_t*)p; }
 
 __device__ __forceinline__ void dma16_q(const uint4* g, uint4* lds_wave_base) {
   __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0,
