@@ -34,7 +34,7 @@
 
 namespace keep {
 
-constexpr int MT_TILE = 16;  // routes per tile (one MFMA group each in gate/up, A rows in down)
+constexpr int MT_TILE = 4;  // routes per tile: one MFMA chain serves them all in either kernel
 
 struct MTArgs {
   const uint4* xt;     // [T][S][3][16] 16-byte slots of int8 terms
@@ -78,30 +78,31 @@ __global__ __launch_bounds__(1024) void k_q8_xterms(const void* x, int H, uint4*
 
 // ------------------------------------------------------------------ gate/up
 
-// The two persistent kernels share one schedule. A block's units form runs
-// of one tile, cut into segments of at most SEG units. Per segment and per
-// pass over the tile's routes (RA at a time): the routes' A operands, then
-// the segment's units with two units' codes (and their scale words, DMA'd to
-// LDS ahead of them) in flight while one is decoded, unrolled by two over
-// two register buffers. Inside a segment every load is unconditional (past
-// its end the last unit is loaded again and stores nothing) and no global
-// store is issued -- outputs are staged in LDS and written when the segment
-// ends -- so each wait the compiler inserts counts exactly the loads before
-// it (a store among them would make it wait for everything).
+// The two persistent kernels share one schedule. Tiles hold at most
+// MT_TILE routes, so every unit of every tile is one pass over its codes and
+// costs about the same: an even split of the units balances the blocks. A
+// block's units form segments (the units of one tile, at most SEG of them):
+// per segment the tile's A operands go to registers, then the units run
+// with the next two units' codes and scale words in flight while one is
+// decoded, unrolled by two over two register buffers. Inside a segment every
+// load is unconditional (past its end the last unit is loaded again and
+// stores nothing) and no global store is issued -- outputs are staged in LDS
+// and written when the segment ends -- so each wait the compiler inserts
+// counts exactly the loads before it. The cross-wave partial sums are
+// double-buffered by unit parity: a wave writes a unit's partials only after
+// the barrier that the previous reader of that buffer has passed.
 
 // Gate/up: a unit is 16 rows of gate and of up (two code loads per wave, 32
-// KiB per block); a route's A operand for this wave's slice (3 term rows x
-// 256 B) is one 768-byte DMA into the wave's LDS slot.
+// KiB per block). One MFMA chain per projection serves all the tile's
+// routes: A row 4i + t is term t of route i's token (t < 3; row 4i + 3 is
+// zero), so D rows 4i .. 4i + 2 of column j, in lane 16 i + j, are route i's
+// three partial dots with weight row j.
 template <bool XBF>
 __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
-  constexpr int RA = 4;    // routes per pass
-  constexpr int SEG = 32;  // units per segment
+  constexpr int SEG = 128;  // units per segment (h staging capacity)
   __shared__ uint4 tqs[TQR_BYTES / 16];
-  __shared__ uint4 asl[16][RA][3 * 16];    // [wave][route][term row * 16 + slot]
-  __shared__ float s_inv[16][RA];
-  __shared__ float gred[16][2][RA][16];    // [wave][gate, up][route][row]
-  __shared__ uint16_t hst[RA][SEG * 16];   // the segment's h rows
-  __shared__ int32_t s_route[RA];
+  __shared__ float gred[2][16][2][MT_TILE][16];  // [parity][wave][gate, up][route][row]
+  __shared__ uint16_t hst[MT_TILE][SEG * 16];    // the segment's h rows
   const char* tq = (const char*)tqs;
   const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
   const Q8Keys lk = q8_keys(threadIdx.x & 63);
@@ -134,7 +135,7 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
     const int ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
     const uint32_t ebase = (uint32_t)a.te[tic] * (uint32_t)a.I;
     const uint32_t row0 = (uint32_t)(us - tic * rg_n) * 16u;
-    const int off = a.to[tic], cnt = a.tc[tic];
+    const int off = a.to[tic], nr = a.tc[tic];  // 1 <= nr <= MT_TILE
     // a unit's codes and its rows' scale words (the aligned word holding each)
     auto load_unit = [&](int u, Buf& b) {
       const uint32_t row = ebase + (uint32_t)(min(u, ue - 1) - tic * rg_n) * 16u + j;
@@ -144,80 +145,70 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
         b.s[t] = ldg4_q((const char*)(t ? a.us : a.gs) + ((row * (uint32_t)a.Gh + grp) * sbytes & ~3u));
       }
     };
-    for (int r0 = 0; r0 < cnt; r0 += RA) {
-      const int nr = min(RA, cnt - r0);
+    // A row j = 4i + t: term t of route i (routes past nr repeat the last one; their D rows are unused)
+    const int tok_a = a.order[off + min((int)(j >> 2), nr - 1)] / a.k;
+    const int tok_d = a.order[off + min((int)g, nr - 1)] / a.k;  // the route of this lane's D rows
+    const uint4* asrc = a.xt + ((size_t)tok_a * a.S + sl) * 48 + min(j & 3u, 2u) * 16 + g * 4;
+    uint4 araw[4];
 #pragma unroll
-      for (int i = 0; i < RA; ++i) {  // the routes' A operands (lanes 0-47) and slice scales
-        const int tok = a.order[off + r0 + min(i, nr - 1)] / a.k;
-        if (lane < 48) dma16_q(a.xt + ((size_t)tok * a.S + sl) * 48 + lane, asl[wv][i]);
-        if (lane == 0) s_inv[wv][i] = a.xinv[(size_t)tok * a.S + sl];
-      }
-      if ((int)threadIdx.x < RA) s_route[threadIdx.x] = a.order[off + r0 + min((int)threadIdx.x, nr - 1)];
-      Buf b0, b1;
-      load_unit(us, b0);
-      load_unit(us + 1, b1);
-      wait_vm_q<0>();
-      rt_lds_barrier();  // every wave's table pieces, A operands, the routes
-      auto unit = [&](int u, Buf& b) {
-        const uint32_t rowc = (uint32_t)(min(u, ue - 1) - tic * rg_n) * 16u;
-        q8v4 B[2][4];
+    for (int m = 0; m < 4; ++m) araw[m] = ldg16_q(asrc + m);
+    const float inv = a.xinv[(size_t)tok_d * a.S + sl];
+    Buf b0, b1;
+    load_unit(us, b0);
+    load_unit(us + 1, b1);
+    wait_vm_q<0>();
+    rt_lds_barrier();  // the table image (first segment); the previous flush has read hst
+    q8v4 A[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) q8_decode8(tq, lk, b.q[t], B[t]);
-        float scl[2];
+    for (int m = 0; m < 4; ++m) {
+      const bool z = (j & 3u) == 3u;
+      A[m] = q8v4{z ? 0 : (int)araw[m].x, z ? 0 : (int)araw[m].y, z ? 0 : (int)araw[m].z, z ? 0 : (int)araw[m].w};
+    }
+    auto unit = [&](int u, Buf& b, int par) {
+      const uint32_t rowc = (uint32_t)(min(u, ue - 1) - tic * rg_n) * 16u;
+      q8v4 B[2][4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          scl[t] = scale_cvt(b.s[t], a.sdt, (ebase + rowc + j) * (uint32_t)a.Gh + grp);
+      for (int t = 0; t < 2; ++t) q8_decode8(tq, lk, b.q[t], B[t]);
+      float scl[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(scl[t]));  // converted before b.s is reloaded
-        load_unit(u + 2, b);
-        __builtin_amdgcn_sched_barrier(0);
-        if (dec) {
-#pragma unroll 1
-          for (int i = 0; i < nr; ++i) {
-            const q8v4* as = (const q8v4*)asl[wv][i] + (j < 3 ? j : 0) * 16 + g * 4;
-            q8v4 A[4];
+      for (int t = 0; t < 2; ++t) scl[t] = scale_cvt(b.s[t], a.sdt, (ebase + rowc + j) * (uint32_t)a.Gh + grp);
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-              const q8v4 av = as[m];
-              A[m] = j < 3 ? av : q8v4{0, 0, 0, 0};
-            }
-            const float inv = s_inv[wv][i];
+      for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(scl[t]));  // converted before b.s is reloaded
+      load_unit(u + 2, b);
+      __builtin_amdgcn_sched_barrier(0);
+      if (dec) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              q8v4 acc = {0, 0, 0, 0};
+        for (int t = 0; t < 2; ++t) {
+          q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
-              for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[t][m], acc);
-              if (lane < 16) {
-                const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
-                gred[wv][t][i][j] = d * inv * scl[t];
-              }
-            }
-          }
+          for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[t][m], acc);
+          const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
+          if ((int)g < nr) gred[par][wv][t][g][j] = d * inv * scl[t];
         }
-        rt_lds_barrier();
-        // SwiGLU: thread (route i, row jj) -> the staged h rows
-        if ((int)threadIdx.x < nr * 16 && u < ue) {
-          const int i = threadIdx.x >> 4, jj = threadIdx.x & 15;
-          float gsum = 0.f, usum = 0.f;
-          for (int w = 0; w < a.S; ++w) {
-            gsum += gred[w][0][i][jj];
-            usum += gred[w][1][i][jj];
-          }
-          float hv = silu_mul(gsum, usum, a.limit);
-          if (tq_bad) hv = __builtin_nanf("");
-          hst[i][(u - us) * 16 + jj] = from_float<bf16s>(hv).bits;
-        }
-      };
-      for (int u = us; u < ue; u += 2) {  // both calls unconditional: a unit past the end stores nothing
-        unit(u, b0);
-        unit(u + 1, b1);
       }
       rt_lds_barrier();
-      const int rows = (ue - us) * 16;
-      for (int x = threadIdx.x; x < nr * rows; x += 1024) {
-        const int i = x / rows, r = x - i * rows;
-        a.h[(size_t)s_route[i] * a.I + row0 + (uint32_t)r] = hst[i][r];
+      // SwiGLU: thread (route i, row jj) -> the staged h rows
+      if ((int)threadIdx.x < nr * 16 && u < ue) {
+        const int i = threadIdx.x >> 4, jj = threadIdx.x & 15;
+        float gsum = 0.f, usum = 0.f;
+        for (int w = 0; w < a.S; ++w) {
+          gsum += gred[par][w][0][i][jj];
+          usum += gred[par][w][1][i][jj];
+        }
+        float hv = silu_mul(gsum, usum, a.limit);
+        if (tq_bad) hv = __builtin_nanf("");
+        hst[i][(u - us) * 16 + jj] = from_float<bf16s>(hv).bits;
       }
+    };
+    for (int u = us; u < ue; u += 2) {  // both calls unconditional: a unit past the end stores nothing
+      unit(u, b0, 0);
+      unit(u + 1, b1, 1);
+    }
+    rt_lds_barrier();
+    const int rows = (ue - us) * 16;
+    for (int x = threadIdx.x; x < nr * rows; x += 1024) {
+      const int i = x / rows, r = x - i * rows;
+      a.h[(size_t)a.order[off + i] * a.I + row0 + (uint32_t)r] = hst[i][r];
     }
     us = ue;
   }
@@ -226,18 +217,17 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
 
 // Down: a unit is 64 rows (four 16-row tiles, 32 KiB of codes per block);
 // wave w < I / 256 owns K slice w. The A operand holds two int8 terms of h
-// for each of up to 8 routes (rows 2r, 2r + 1), built from h at each pass;
-// route r's dot is D rows 2r, 2r + 1.
+// for each of the tile's routes (rows 2r, 2r + 1; rows past them zero),
+// built from h when the block enters a segment; route r's dot is D rows 2r,
+// 2r + 1.
 __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
   constexpr int RT = 4;
-  constexpr int RP = 8;   // routes per pass
-  constexpr int SEG = 8;  // units per segment
+  constexpr int SEG = 48;  // units per segment (y staging capacity)
   __shared__ uint4 tqs[TQR_BYTES / 16];
-  __shared__ uint4 ash[8][16 * 16];         // [wave][row * 16 + slot]
-  __shared__ float s_inv[8][RP];
-  __shared__ float red[8][RT][RP][16];      // [wave][row-tile][route][row]
-  __shared__ float yst[RP][SEG * 16 * RT];  // the segment's y rows
-  __shared__ int32_t s_route[RP];
+  __shared__ uint4 ash[8][2 * MT_TILE * 16];         // [wave][row * 16 + slot]
+  __shared__ float s_inv[8][MT_TILE];
+  __shared__ float red[2][8][RT][MT_TILE][16];       // [parity][wave][row-tile][route][row]
+  __shared__ float yst[MT_TILE][SEG * 16 * RT];      // the segment's y rows
   const char* tq = (const char*)tqs;
   const Q8Keys lk = q8_keys(threadIdx.x & 63);
   const int lane = threadIdx.x & 63;
@@ -269,7 +259,7 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
     const int ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
     const uint32_t ebase = (uint32_t)a.te[tic] * (uint32_t)a.H;
     const uint32_t row0 = (uint32_t)(us - tic * rg_n) * (16u * RT);
-    const int off = a.to[tic], cnt = a.tc[tic];
+    const int off = a.to[tic], nr = a.tc[tic];  // 1 <= nr <= MT_TILE
     // a unit's codes and its rows' scale words (the aligned word holding each)
     auto load_unit = [&](int u, Buf& b) {
       const uint32_t rbase = ebase + (uint32_t)(min(u, ue - 1) - tic * rg_n) * (16u * RT) + j;
@@ -279,94 +269,93 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
         b.s[rt] = ldg4_q((const char*)a.ds + (((rbase + (uint32_t)rt * 16u) * (uint32_t)a.Gi + grp) * sbytes & ~3u));
       }
     };
-    for (int r0 = 0; r0 < cnt; r0 += RP) {
-      const int nr = min(RP, cnt - r0);
-      if ((int)threadIdx.x < RP) s_route[threadIdx.x] = a.order[off + r0 + min((int)threadIdx.x, nr - 1)];
-      if (dec) {  // the pass's h slices -> A operands (this wave's own LDS rows)
-        uint4 hq[RP];
+    if (dec) {  // the tile's h slices -> A operands (this wave's own LDS rows)
+      uint4 hq[MT_TILE];
 #pragma unroll
-        for (int i = 0; i < RP; ++i) {
-          const int route = a.order[off + r0 + min(i, nr - 1)];
-          hq[i] = ldg16_q((const uint4*)(a.h + (size_t)route * a.I) + wv * 32 + (lane >> 1));
-        }
-        uint32_t* aw = (uint32_t*)ash[wv];
-        for (int i = 0; i < 16 * 16 * 4; i += 64) aw[i + lane] = 0u;
-#pragma unroll
-        for (int i = 0; i < RP; ++i) {
-          if (i < nr) {
-            float v[4];
-            q8_half4<true>(hq[i], lane & 1, v);
-            const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-            float sc, inv4s;
-            q8_scale(rt_wave_reduce(mx, true), sc, inv4s);
-            uint32_t tw[2];
-            q8_terms<2>(v, sc, tw);
-            aw[q8_aword((uint32_t)(2 * i), lane >> 1, lane & 1)] = tw[0];
-            aw[q8_aword((uint32_t)(2 * i + 1), lane >> 1, lane & 1)] = tw[1];
-            if (lane == 0) s_inv[wv][i] = inv4s;
-          }
-        }
+      for (int i = 0; i < MT_TILE; ++i) {
+        const int route = a.order[off + min(i, nr - 1)];
+        hq[i] = ldg16_q((const uint4*)(a.h + (size_t)route * a.I) + wv * 32 + (lane >> 1));
       }
-      Buf b0, b1;
-      load_unit(us, b0);
-      load_unit(us + 1, b1);
-      wait_vm_q<0>();
-      rt_lds_barrier();  // every wave's table pieces, the routes
-      q8v4 A[4];
-      {
-        const q8v4* as = (const q8v4*)ash[wv] + j * 16 + g * 4;
+      uint32_t* aw = (uint32_t*)ash[wv];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) A[m] = as[m];  // rows past the pass's routes are zero
+      for (int i = 0; i < MT_TILE; ++i) {
+        float v[4];
+        q8_half4<true>(hq[i], lane & 1, v);
+        const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        float sc, inv4s;
+        q8_scale(rt_wave_reduce(mx, true), sc, inv4s);
+        uint32_t tw[2];
+        q8_terms<2>(v, sc, tw);
+        aw[q8_aword((uint32_t)(2 * i), lane >> 1, lane & 1)] = tw[0];
+        aw[q8_aword((uint32_t)(2 * i + 1), lane >> 1, lane & 1)] = tw[1];
+        if (lane == 0) s_inv[wv][i] = inv4s;
       }
-      auto unit = [&](int u, Buf& b) {
-        const uint32_t rowc = (uint32_t)(min(u, ue - 1) - tic * rg_n) * (16u * RT);
-        q8v4 B[RT][4];
+    }
+    Buf b0, b1;
+    load_unit(us, b0);
+    load_unit(us + 1, b1);
+    wait_vm_q<0>();
+    rt_lds_barrier();  // the table image (first segment); the previous flush has read yst
+    q8v4 A[4];
+    {
+      const q8v4* as = (const q8v4*)ash[wv] + (j & (2 * MT_TILE - 1)) * 16 + g * 4;
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) q8_decode8(tq, lk, b.q[rt], B[rt]);
-        float scl[RT];
+      for (int m = 0; m < 4; ++m) {
+        const q8v4 v = as[m];
+        const bool z = (int)j >= 2 * nr;  // rows past the tile's routes
+        A[m] = q8v4{z ? 0 : v[0], z ? 0 : v[1], z ? 0 : v[2], z ? 0 : v[3]};
+      }
+    }
+    float inv[2];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-          scl[rt] = scale_cvt(b.s[rt], a.sdt, (ebase + rowc + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
+    for (int h2 = 0; h2 < 2; ++h2) inv[h2] = s_inv[dec ? wv : 0][min(2 * (int)g + h2, MT_TILE - 1)];
+    auto unit = [&](int u, Buf& b, int par) {
+      const uint32_t rowc = (uint32_t)(min(u, ue - 1) - tic * rg_n) * (16u * RT);
+      q8v4 B[RT][4];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(scl[rt]));  // converted before b.s is reloaded
-        load_unit(u + 2, b);
-        __builtin_amdgcn_sched_barrier(0);
-        if (dec) {
+      for (int rt = 0; rt < RT; ++rt) q8_decode8(tq, lk, b.q[rt], B[rt]);
+      float scl[RT];
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            q8v4 acc = {0, 0, 0, 0};
+      for (int rt = 0; rt < RT; ++rt)
+        scl[rt] = scale_cvt(b.s[rt], a.sdt, (ebase + rowc + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
 #pragma unroll
-            for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[rt][m], acc);
-            // route r: rows 2r, 2r + 1 = lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
+      for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(scl[rt]));  // converted before b.s is reloaded
+      load_unit(u + 2, b);
+      __builtin_amdgcn_sched_barrier(0);
+      if (dec) {
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-              const int r = 2 * (int)g + h2;
-              if (r < nr) {
-                const float d = h2 ? (float)acc[2] + (float)acc[3] * 0.0078125f : (float)acc[0] + (float)acc[1] * 0.0078125f;
-                red[wv][rt][r][j] = d * s_inv[wv][r] * scl[rt];
-              }
+        for (int rt = 0; rt < RT; ++rt) {
+          q8v4 acc = {0, 0, 0, 0};
+#pragma unroll
+          for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[rt][m], acc);
+          // route r: rows 2r, 2r + 1 = lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int r = 2 * (int)g + h2;
+            if (r < nr) {
+              const float d = h2 ? (float)acc[2] + (float)acc[3] * 0.0078125f : (float)acc[0] + (float)acc[1] * 0.0078125f;
+              red[par][wv][rt][r][j] = d * inv[h2] * scl[rt];
             }
           }
         }
-        rt_lds_barrier();
-        if ((int)threadIdx.x < nr * 16 * RT && u < ue) {
-          const int i = threadIdx.x / (16 * RT), rt = (threadIdx.x >> 4) % RT, jj = threadIdx.x & 15;
-          float v = 0.f;
-          for (int w = 0; w < nsl; ++w) v += red[w][rt][i][jj];
-          yst[i][(u - us) * 16 * RT + rt * 16 + jj] = v;
-        }
-      };
-      for (int u = us; u < ue; u += 2) {  // both calls unconditional: a unit past the end stores nothing
-        unit(u, b0);
-        unit(u + 1, b1);
       }
       rt_lds_barrier();
-      const int rows = (ue - us) * 16 * RT;
-      for (int x = threadIdx.x; x < nr * rows; x += 512) {
-        const int i = x / rows, r = x - i * rows;
-        a.y[(size_t)s_route[i] * a.H + row0 + (uint32_t)r] = yst[i][r];
+      if ((int)threadIdx.x < nr * 16 * RT && u < ue) {
+        const int i = threadIdx.x / (16 * RT), rt = (threadIdx.x >> 4) % RT, jj = threadIdx.x & 15;
+        float v = 0.f;
+        for (int w = 0; w < nsl; ++w) v += red[par][w][rt][i][jj];
+        yst[i][(u - us) * 16 * RT + rt * 16 + jj] = v;
       }
-      rt_lds_barrier();  // the flush has read yst and s_route
+    };
+    for (int u = us; u < ue; u += 2) {  // both calls unconditional: a unit past the end stores nothing
+      unit(u, b0, 0);
+      unit(u + 1, b1, 1);
+    }
+    rt_lds_barrier();
+    const int rows = (ue - us) * 16 * RT;
+    for (int x = threadIdx.x; x < nr * rows; x += 512) {
+      const int i = x / rows, r = x - i * rows;
+      a.y[(size_t)a.order[off + i] * a.H + row0 + (uint32_t)r] = yst[i][r];
     }
     us = ue;
   }
