@@ -104,20 +104,21 @@ __device__ __forceinline__ float pair_hi(uint32_t w) {
 // CB = 16: E8P abs table, pair k = nibbles (k, k+4). CB = 8: E8 table,
 // pair k = nibbles (2k, 2k+1) (dim d = nibble d).
 template <int CB, int PK>
-__device__ __forceinline__ void build_codebook(uint4* tab, const uint32_t* packed) {
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) {
-    const uint32_t p = packed[i];
-    uint32_t w[4];
+__device__ __forceinline__ void codebook_entry(uint4* tab, int i, uint32_t p) {
+  uint32_t w[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int lo_n = CB == 16 ? k : 2 * k;
-      const int hi_n = CB == 16 ? k + 4 : 2 * k + 1;
-      const int lo = (int)((p >> (4 * lo_n)) & 15u) - 8;
-      const int hi = (int)((p >> (4 * hi_n)) & 15u) - 8;
-      w[k] = encode_half_units<PK>(lo) | (encode_half_units<PK>(hi) << 16);
-    }
-    tab[i] = make_uint4(w[0], w[1], w[2], w[3]);
+  for (int k = 0; k < 4; ++k) {
+    const int lo_n = CB == 16 ? k : 2 * k;
+    const int hi_n = CB == 16 ? k + 4 : 2 * k + 1;
+    const int lo = (int)((p >> (4 * lo_n)) & 15u) - 8;
+    const int hi = (int)((p >> (4 * hi_n)) & 15u) - 8;
+    w[k] = encode_half_units<PK>(lo) | (encode_half_units<PK>(hi) << 16);
   }
+  tab[i] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+template <int CB, int PK>
+__device__ __forceinline__ void build_codebook(uint4* tab, const uint32_t* packed) {
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) codebook_entry<CB, PK>(tab, i, packed[i]);
 }
 
 // Residual table given as fp16 half2 pairs uint32[256*4]; converted to PK.

@@ -15,13 +15,26 @@
 namespace keep {
 
 constexpr int MV_WAVES = 4;
-constexpr int MV_ROWS = 4;
+constexpr int MV_ROWS = 2;
 constexpr uint32_t NO_RESIDUAL = 0xffffffffu;
 
 __device__ __forceinline__ float scale_at(const void* p, int dt, int64_t i) {
   if (dt == KEEP_F16) return (float)((const _Float16*)p)[i];
   if (dt == KEEP_BF16) return __uint_as_float((uint32_t)((const uint16_t*)p)[i] << 16);
   return ((const float*)p)[i];
+}
+
+// The raw bits of scale i (loaded in one place whatever the dtype, so the
+// load can stay in flight) and their value; scale_of_bits(scale_bits(..))
+// equals scale_at(..).
+__device__ __forceinline__ uint32_t scale_bits(const void* p, int dt, int64_t i) {
+  if (dt == KEEP_F32) return ((const uint32_t*)p)[i];
+  return ((const uint16_t*)p)[i];
+}
+__device__ __forceinline__ float scale_of_bits(uint32_t b, int dt) {
+  if (dt == KEEP_F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+  if (dt == KEEP_BF16) return __uint_as_float(b << 16);
+  return __uint_as_float(b);
 }
 
 __device__ __forceinline__ void store_at(void* p, int dt, int64_t i, float v) {
@@ -101,16 +114,14 @@ __global__ __launch_bounds__(256) void k_vq_matvec(MatvecArgs a) {
   constexpr int RNW = (CH + 3) / 4;
   __shared__ uint4 tab[256];
   __shared__ uint4 rtab[NESTED ? 256 : 1];
-  build_codebook<CB, PK>(tab, a.table);
-  if constexpr (NESTED) load_pair_table<PK>(rtab, a.rtable);
-  __syncthreads();
-
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int64_t route = blockIdx.x / a.row_blocks;
   const int64_t rb = blockIdx.x - route * a.row_blocks;
   const int64_t row0 = (rb * MV_WAVES + wv) * MV_ROWS;
-  if (row0 >= a.N) return;
+  const bool live = row0 < a.N;
+  // The route's expert and activation row, then the first chunk's codes,
+  // scales and activations are in flight while the codebook is built.
   const int64_t e = a.rhs[route];
   const int64_t xr = a.lhs ? (int64_t)a.lhs[route] : route / a.x_div;
   uint32_t hot = NO_RESIDUAL;
@@ -121,36 +132,42 @@ __global__ __launch_bounds__(256) void k_vq_matvec(MatvecArgs a) {
       bad = hot != NO_RESIDUAL && (int64_t)hot >= a.nhot;
     }
   }
+  const int64_t C = a.K >> 3;
+  const XT* xrow = (const XT*)a.x + xr * a.K;
+  const char* cbase = (const char*)a.codes + (e * a.N) * C * (CB / 8);
+  uint32_t words[MV_ROWS][NW], sb[MV_ROWS];
+  XChunk<XT, CH> xc;
+  auto load_chunk = [&](int64_t cw) {  // rows past N load row N - 1 and are never used
+    const int64_t g = cw / a.cpg;
+#pragma unroll
+    for (int r = 0; r < MV_ROWS; ++r) {
+      const int64_t row = row0 + r < a.N ? row0 + r : a.N - 1;
+      load_codes<CB, CH>(cbase + row * C * (CB / 8), cw, words[r]);
+      sb[r] = scale_bits(a.scales, a.sdt, (e * a.N + row) * a.G + g);
+    }
+    xc.load(xrow, cw);
+  };
+  const uint32_t tpk = a.table[threadIdx.x];  // blockDim.x == 256: one codebook entry per thread
+  int64_t cw = (int64_t)lane * CH;
+  if (live && !bad && cw < C) load_chunk(cw);
+  codebook_entry<CB, PK>(tab, threadIdx.x, tpk);
+  if constexpr (NESTED) load_pair_table<PK>(rtab, a.rtable);
+  __syncthreads();
+  if (!live) return;
   if (bad) {
     if (lane < MV_ROWS && row0 + lane < a.N) store_at(a.out, a.odt, route * a.N + row0 + lane, __builtin_nanf(""));
     return;
   }
-  const int64_t C = a.K >> 3;
-  const XT* xrow = (const XT*)a.x + xr * a.K;
-  const char* cbase = (const char*)a.codes + (e * a.N) * C * (CB / 8);
   float acc[MV_ROWS], racc[MV_ROWS];
 #pragma unroll
   for (int r = 0; r < MV_ROWS; ++r) acc[r] = racc[r] = 0.f;
 
-  for (int64_t cw = (int64_t)lane * CH; cw < C; cw += 64 * CH) {
-    uint32_t words[MV_ROWS][NW];
+  for (; cw < C; cw += 64 * CH) {
 #pragma unroll
     for (int r = 0; r < MV_ROWS; ++r) {
-      const int64_t row = row0 + r;
-      if (row < a.N) load_codes<CB, CH>(cbase + row * C * (CB / 8), cw, words[r]);
-      else
-#pragma unroll
-        for (int q = 0; q < NW; ++q) words[r][q] = 0u;
-    }
-    XChunk<XT, CH> xc;
-    xc.load(xrow, cw);
-    const int64_t g = cw / a.cpg;
-#pragma unroll
-    for (int r = 0; r < MV_ROWS; ++r) {
-      const int64_t row = row0 + r;
-      if (row < a.N) {
+      if (row0 + r < a.N) {
         const float part = chunk_dot<CB, XT, CH>(words[r], tab, xc);
-        acc[r] += part * scale_at(a.scales, a.sdt, (e * a.N + row) * a.G + g);
+        acc[r] += part * scale_of_bits(sb[r], a.sdt);
       }
     }
     if constexpr (NESTED) {
@@ -169,6 +186,7 @@ __global__ __launch_bounds__(256) void k_vq_matvec(MatvecArgs a) {
         }
       }
     }
+    if (cw + 64 * CH < C) load_chunk(cw + 64 * CH);
   }
 #pragma unroll
   for (int r = 0; r < MV_ROWS; ++r) {
@@ -210,26 +228,42 @@ __global__ __launch_bounds__(256) void k_vq_matvec_tiles(TileArgs a) {
   constexpr int NW = (CH * 2 + 3) / 4;
   constexpr int MMAX = 8;
   __shared__ uint4 tab[256];
-  build_codebook<16, PK>(tab, a.table);
-  __syncthreads();
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int64_t tile = blockIdx.x / a.row_blocks;
   const int64_t rb = blockIdx.x - tile * a.row_blocks;
   const int64_t row0 = (rb * MV_WAVES + wv) * MV_ROWS;
-  if (row0 >= a.N) return;
+  // The tile, then its first chunk's codes and scales are in flight while
+  // the codebook is built.
   const int cnt = a.tc[tile];
-  if (cnt <= 0) return;
   const int64_t off = a.to[tile];
   const int64_t e = a.te[tile];
   const int m = cnt < (int)a.m_rows ? cnt : (int)a.m_rows;
-  if (e < 0 || e >= a.E || off < 0 || off + m > a.routes) {
+  const bool live = row0 < a.N && cnt > 0;
+  const bool bad = e < 0 || e >= a.E || off < 0 || off + m > a.routes;
+  const int64_t C = a.K >> 3;
+  const char* cbase = (const char*)a.codes + (e * a.N) * C * 2;
+  uint32_t words[MV_ROWS][NW], sb[MV_ROWS];
+  auto load_chunk = [&](int64_t cw) {  // rows past N load row N - 1 and are never used
+    const int64_t g = cw / a.cpg;
+#pragma unroll
+    for (int r = 0; r < MV_ROWS; ++r) {
+      const int64_t row = row0 + r < a.N ? row0 + r : a.N - 1;
+      load_codes<16, CH>(cbase + row * C * 2, cw, words[r]);
+      sb[r] = scale_bits(a.scales, a.sdt, (e * a.N + row) * a.G + g);
+    }
+  };
+  const uint32_t tpk = a.table[threadIdx.x];  // blockDim.x == 256: one codebook entry per thread
+  int64_t cw = (int64_t)lane * CH;
+  if (live && !bad && cw < C) load_chunk(cw);
+  codebook_entry<16, PK>(tab, threadIdx.x, tpk);
+  __syncthreads();
+  if (!live) return;
+  if (bad) {
     for (int i = 0; i < m && off + i < a.routes && off + i >= 0; ++i)
       if (lane < MV_ROWS && row0 + lane < a.N) store_at(a.out, a.odt, (off + i) * a.N + row0 + lane, __builtin_nanf(""));
     return;
   }
-  const int64_t C = a.K >> 3;
-  const char* cbase = (const char*)a.codes + (e * a.N) * C * 2;
   int64_t xr[MMAX];
 #pragma unroll
   for (int i = 0; i < MMAX; ++i) {
@@ -242,22 +276,7 @@ __global__ __launch_bounds__(256) void k_vq_matvec_tiles(TileArgs a) {
 #pragma unroll
     for (int r = 0; r < MV_ROWS; ++r) acc[i][r] = 0.f;
 
-  for (int64_t cw = (int64_t)lane * CH; cw < C; cw += 64 * CH) {
-    uint32_t words[MV_ROWS][NW];
-    float sc[MV_ROWS];
-    const int64_t g = cw / a.cpg;
-#pragma unroll
-    for (int r = 0; r < MV_ROWS; ++r) {
-      const int64_t row = row0 + r;
-      if (row < a.N) {
-        load_codes<16, CH>(cbase + row * C * 2, cw, words[r]);
-        sc[r] = scale_at(a.scales, a.sdt, (e * a.N + row) * a.G + g);
-      } else {
-#pragma unroll
-        for (int q = 0; q < NW; ++q) words[r][q] = 0u;
-        sc[r] = 0.f;
-      }
-    }
+  for (; cw < C; cw += 64 * CH) {
 #pragma unroll
     for (int i = 0; i < MMAX; ++i) {
       if (i < m && xr[i] >= 0) {
@@ -265,10 +284,11 @@ __global__ __launch_bounds__(256) void k_vq_matvec_tiles(TileArgs a) {
         xc.load((const XT*)a.x + xr[i] * a.K, cw);
 #pragma unroll
         for (int r = 0; r < MV_ROWS; ++r) {
-          if (row0 + r < a.N) acc[i][r] += chunk_dot<16, XT, CH>(words[r], tab, xc) * sc[r];
+          if (row0 + r < a.N) acc[i][r] += chunk_dot<16, XT, CH>(words[r], tab, xc) * scale_of_bits(sb[r], a.sdt);
         }
       }
     }
+    if (cw + 64 * CH < C) load_chunk(cw + 64 * CH);
   }
 #pragma unroll
   for (int i = 0; i < MMAX; ++i) {

@@ -373,6 +373,21 @@ def decode_weight_matrix(codes, scales=None, *, code_bits: int = 16, codebook=No
 # --------------------------------------------------------------------------- vq_qmv / vq_qmm
 
 
+_ZERO_ROUTES: dict = {}
+
+
+def _zero_routes(n: int, device: torch.device) -> torch.Tensor:
+    """A cached int32 zeros vector of length >= n on `device` (every route on
+    expert 0), so a single-matrix call launches no fill kernel."""
+
+    key = (device.type, device.index)
+    z = _ZERO_ROUTES.get(key)
+    if z is None or z.numel() < n:
+        z = torch.zeros(max(n, 64), dtype=torch.int32, device=device)
+        _ZERO_ROUTES[key] = z
+    return z[:n]
+
+
 def vq_qmv(x, codes, scales, codebook=None, *, in_dim: int, out_dim: int, group_size: int = 512,
            code_bits: Literal[8, 16] = 8, implementation: str = "hip",
            codebook_duplication: Literal[1, 4, 8] = 1) -> torch.Tensor:
@@ -392,7 +407,7 @@ def vq_qmv(x, codes, scales, codebook=None, *, in_dim: int, out_dim: int, group_
     if tuple(s.shape) != (out_dim, in_dim // group_size):
         raise ValueError(f"scales must have shape ({out_dim}, {in_dim // group_size}), found {tuple(s.shape)}")
     cb = _codebook_tensor(codebook, code_bits, device)
-    rhs = torch.zeros(1, dtype=torch.int32, device=device)
+    rhs = _zero_routes(1, device)
     y = routed_matvec(xt.reshape(1, in_dim), c.reshape(1, out_dim, -1), s.reshape(1, out_dim, -1), cb, rhs,
                       input_dims=in_dim, output_dims=out_dim, group_size=group_size, code_bits=code_bits)
     return y.reshape(out_dim)
@@ -418,7 +433,7 @@ def vq_qmm(x, codes, scales, codebook=None, *, in_dim: int, out_dim: int, group_
         raise ValueError(f"scales must have shape ({out_dim}, {in_dim // group_size}), found {tuple(s.shape)}")
     cb = _codebook_tensor(codebook, code_bits, device)
     M = xt.shape[0]
-    rhs = torch.zeros(M, dtype=torch.int32, device=device)
+    rhs = _zero_routes(M, device)
     return routed_matvec(xt, c.reshape(1, out_dim, -1), s.reshape(1, out_dim, -1), cb, rhs, input_dims=in_dim,
                          output_dims=out_dim, group_size=group_size, code_bits=code_bits)
 
