@@ -226,6 +226,42 @@ int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, 
                    float swiglu_limit, void* h_work, void* workspace, int64_t workspace_bytes,
                    void* out, int out_dtype, void* stream);
 
+/* Prefill grouped GEMM on the int8 matrix cores over expert-sorted routes
+ * (tiles of <= 64 routes of one expert from keep_route_plan): for every tile
+ * t and route i < tile_count[t], with p = tile_offset[t] + i,
+ *   out[out_index[p], :] = W[tile_expert[t]] . x[lhs[p], :]
+ * (lhs / out_index NULL: p itself). x is fp16, bf16 or fp32 [x_rows, K]; each
+ * row is split into two int8 terms under a power-of-two row scale (residual
+ * at most 2^-13 of the row's max), weights are E8P decoded exactly (x 4) from
+ * the `prepared` image (keep_e8p_prepare), int32 sums per term, scales per
+ * group in fp32. `workspace` (caller-owned, 256-byte aligned) holds the terms:
+ * keep_vq_grouped_gemm_q8_workspace_bytes(x_rows, K) bytes. Replaces
+ * gather_vqmm_sorted_routes' NAX E8P GEMM (src/ramp/ops/vq_switch.py:620-913;
+ * native/vq_nax_ext/kernels/nax_fp16_matmul.metal:904-1062); out_index
+ * folds in the scatter back to route order of
+ * src/ramp/models/glm4_moe_adapter.py:274-353. */
+int64_t keep_vq_grouped_gemm_q8_workspace_bytes(int64_t x_rows, int64_t K);
+int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
+                            const int32_t* out_index, const uint16_t* codes, const void* scales,
+                            int scale_dtype, const void* prepared, const int32_t* tile_expert,
+                            const int32_t* tile_offset, const int32_t* tile_count, int64_t n_tiles,
+                            int64_t routes, int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
+                            void* workspace, int64_t workspace_bytes, void* out, int out_dtype, void* stream);
+
+/* The gate and up projections of the same tiles in one pass, with SwiGLU
+ * (silu(min(g, L)) * clip(u, -L, L), plain for L <= 0) in fp32 and h stored
+ * in bf16 at the route's sorted position: h_out[p, :] for p < routes, I
+ * columns. Workspace as keep_vq_grouped_gemm_q8 with K = H. Replaces the
+ * gate/up GEMM pair and the activation of QuantizedVQSwitchGLU's shared
+ * sorted-route prefill (src/ramp/models/glm4_moe_adapter.py:274-353,355-365). */
+int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
+                              const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
+                              const void* up_scales, int scale_dtype, const void* prepared,
+                              const int32_t* tile_expert, const int32_t* tile_offset,
+                              const int32_t* tile_count, int64_t n_tiles, int64_t routes, int64_t num_experts,
+                              int64_t I, int64_t H, int64_t group_size, float swiglu_limit, void* workspace,
+                              int64_t workspace_bytes, void* h_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,11 @@ _SIGS = {
     "keep_moe_tiles": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int,
                        c_int64, c_int64, _P, c_float, _P, _P, c_int64, _P, c_int, _P],
     "keep_moe_tiles_workspace_bytes": [c_int64, c_int64, c_int64, c_int64],
+    "keep_vq_grouped_gemm_q8_workspace_bytes": [c_int64, c_int64],
+    "keep_vq_grouped_gemm_q8": [_P, c_int, c_int64, _P, _P, _P, _P, c_int, _P, _P, _P, _P, c_int64, c_int64, c_int64,
+                                c_int64, c_int64, c_int64, _P, c_int64, _P, c_int, _P],
+    "keep_vq_grouped_swiglu_q8": [_P, c_int, c_int64, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, c_int64, c_int64,
+                                  c_int64, c_int64, c_int64, c_int64, c_float, _P, c_int64, _P, _P],
     "keep_moe_tiles_supported": [c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64],
     "keep_moe_gateup": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, c_int,
                         c_int64, _P, _P, c_float, _P, _P],
@@ -52,7 +57,8 @@ _SIGS = {
     "keep_e8p_prepare": [_P, _P, _P],
     "keep_e8p_prepared_bytes": [],
 }
-_RESTYPE = {"keep_last_error": c_char_p, "keep_moe_tiles_workspace_bytes": c_int64}
+_RESTYPE = {"keep_last_error": c_char_p, "keep_moe_tiles_workspace_bytes": c_int64,
+            "keep_vq_grouped_gemm_q8_workspace_bytes": c_int64}
 EXPORTED = tuple(_SIGS)
 
 _lib = None

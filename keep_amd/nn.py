@@ -160,31 +160,49 @@ class QuantizedVQSwitchGLU:
                                           group_size=p.group_size)
                         for p in (self.gate_proj, self.up_proj, self.down_proj)))
 
+    def _fused_swiglu_limit(self) -> float | None:
+        """The SwiGLU limit when the activation is one the gate/up kernel
+        applies itself (plain or limited SwiGLU in fp32), else None."""
+
+        if self.activation is None:
+            return 0.0
+        if isinstance(self.activation, LimitedSwiGLU):
+            return self.activation.limit
+        return None
+
     def _shared_sorted_route_prefill(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-        """One device route plan shared by the gate, up and down MFMA GEMMs
-        (``glm4_moe_adapter.py:274-353``); per-route outputs are float32."""
+        """One device route plan shared by gate, up and down
+        (``glm4_moe_adapter.py:274-353``): gate and up in one int8 grouped GEMM
+        with SwiGLU in its epilogue (h in bf16), down scattered straight back
+        to route order; per-route outputs are float32."""
         lead, k = tuple(x.shape[:-1]), indices.shape[-1]
         flat_x = x.reshape(-1, self.input_dims).contiguous()
         flat_rhs = indices.reshape(-1).to(torch.int32).contiguous()
         R = flat_rhs.numel()
         flat_lhs = torch.arange(R, dtype=torch.int32, device=x.device) // k
-        order, inverse, _, _, te, to, tc, _ = ops.route_plan(flat_rhs, self.num_experts, ops.GEMM_ROUTE_TILE)
+        order, _, _, _, te, to, tc, _ = ops.route_plan(flat_rhs, self.num_experts, ops.GEMM_ROUTE_TILE)
         sorted_lhs = flat_lhs[order.long()].contiguous()
         tiles = (te, to, tc)
         g, u, d = self.gate_proj, self.up_proj, self.down_proj
         f32 = torch.float32
-        gate = ops.grouped_gemm(flat_x, g.codes, g.scales, g.codebook, tiles, lhs=sorted_lhs, routes=R,
-                                input_dims=g.input_dims, output_dims=g.output_dims, group_size=g.group_size,
-                                out_dtype=f32)
-        up = ops.grouped_gemm(flat_x, u.codes, u.scales, u.codebook, tiles, lhs=sorted_lhs, routes=R,
-                              input_dims=u.input_dims, output_dims=u.output_dims, group_size=u.group_size,
-                              out_dtype=f32)
-        # activation in fp32, hidden held in bf16 (fp16 would overflow the SwiGLU product)
-        hidden = self._apply_activation(up, gate).to(torch.bfloat16).contiguous()
+        limit = self._fused_swiglu_limit()
+        if limit is not None and g.group_size == u.group_size and g.scales.dtype == u.scales.dtype:
+            hidden = ops.grouped_swiglu(flat_x, g.codes, g.scales, u.codes, u.scales, g.codebook, tiles,
+                                        lhs=sorted_lhs, routes=R, input_dims=g.input_dims,
+                                        hidden_dims=g.output_dims, group_size=g.group_size, limit=limit)
+        else:
+            gate = ops.grouped_gemm(flat_x, g.codes, g.scales, g.codebook, tiles, lhs=sorted_lhs, routes=R,
+                                    input_dims=g.input_dims, output_dims=g.output_dims, group_size=g.group_size,
+                                    out_dtype=f32)
+            up = ops.grouped_gemm(flat_x, u.codes, u.scales, u.codebook, tiles, lhs=sorted_lhs, routes=R,
+                                  input_dims=u.input_dims, output_dims=u.output_dims, group_size=u.group_size,
+                                  out_dtype=f32)
+            # activation in fp32, hidden held in bf16 (fp16 would overflow the SwiGLU product)
+            hidden = self._apply_activation(up, gate).to(torch.bfloat16).contiguous()
         y = ops.grouped_gemm(hidden, d.codes, d.scales, d.codebook, tiles, lhs=None, routes=R,
                              input_dims=d.input_dims, output_dims=d.output_dims, group_size=d.group_size,
-                             out_dtype=f32)
-        return y[inverse.long()].reshape(lead + (k, d.output_dims))
+                             out_dtype=f32, out_index=order)
+        return y.reshape(lead + (k, d.output_dims))
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         if self._can_use_shared_sorted_route_prefill(x, indices):

@@ -303,10 +303,18 @@ def route_plan(rhs: torch.Tensor, num_experts: int, tile: int):
     return order, inverse, counts, offsets, te, to, tc, nt
 
 
+def _q8_workspace(rows: int, K: int, device: torch.device) -> torch.Tensor:
+    n = int(_lib.load().keep_vq_grouped_gemm_q8_workspace_bytes(rows, K))
+    return torch.empty((n,), dtype=torch.uint8, device=device)
+
+
 def grouped_gemm(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor, codebook: torch.Tensor,
                  tile_descriptors, *, lhs: torch.Tensor | None, routes: int, input_dims: int, output_dims: int,
-                 group_size: int, out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """``keep_vq_grouped_gemm``: sorted-route MFMA GEMM -> ``[routes, N]`` in sorted order."""
+                 group_size: int, out_dtype: torch.dtype | None = None,
+                 out_index: torch.Tensor | None = None) -> torch.Tensor:
+    """``keep_vq_grouped_gemm_q8``: sorted-route GEMM on the int8 matrix cores ->
+    ``[routes, N]``, row ``p`` in sorted order, or row ``out_index[p]`` when
+    ``out_index`` is given (the scatter back to route order folded in)."""
 
     device = x.device
     od = out_dtype or output_dtype(x.dtype)
@@ -314,18 +322,46 @@ def grouped_gemm(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor, cod
     if routes == 0:
         return out
     te, to, tc = tile_descriptors
-    _lib.call("keep_vq_grouped_gemm", x.data_ptr(), _dtype_code(x, "x"), x.shape[0], _ptr(lhs), codes.data_ptr(),
-              scales.data_ptr(), _dtype_code(scales, "scales"), codebook.data_ptr(), te.data_ptr(), to.data_ptr(),
-              tc.data_ptr(), te.numel(), routes, codes.shape[0], output_dims, input_dims, group_size, out.data_ptr(),
-              _DT[od], _stream(device))
+    xc = x.contiguous()
+    ws = _q8_workspace(xc.shape[0], input_dims, device)
+    prep = prepared_table(codebook)
+    _lib.call("keep_vq_grouped_gemm_q8", xc.data_ptr(), _dtype_code(xc, "x"), xc.shape[0], _ptr(lhs),
+              _ptr(out_index), codes.data_ptr(), scales.data_ptr(), _dtype_code(scales, "scales"), prep.data_ptr(),
+              te.data_ptr(), to.data_ptr(), tc.data_ptr(), te.numel(), routes, codes.shape[0], output_dims,
+              input_dims, group_size, ws.data_ptr(), ws.numel(), out.data_ptr(), _DT[od], _stream(device))
     return out
 
 
-def gemm_eligible(*, code_bits: int, x_dtype: torch.dtype, input_dims: int, group_size: int) -> bool:
-    """Whether the MFMA grouped GEMM serves this call (E8P, 16-bit activations,
-    K and the scale group multiples of 128)."""
+def grouped_swiglu(x: torch.Tensor, gate_codes: torch.Tensor, gate_scales: torch.Tensor, up_codes: torch.Tensor,
+                   up_scales: torch.Tensor, codebook: torch.Tensor, tile_descriptors, *, lhs: torch.Tensor | None,
+                   routes: int, input_dims: int, hidden_dims: int, group_size: int,
+                   limit: float = 0.0) -> torch.Tensor:
+    """``keep_vq_grouped_swiglu_q8``: gate and up of the same sorted-route tiles
+    in one pass, SwiGLU in fp32 -> bf16 ``h [routes, I]`` in sorted order."""
 
-    return (code_bits == 16 and x_dtype in (torch.float16, torch.bfloat16) and input_dims % 128 == 0
+    device = x.device
+    h = torch.empty((routes, hidden_dims), dtype=torch.bfloat16, device=device)
+    if routes == 0:
+        return h
+    if gate_scales.dtype != up_scales.dtype:
+        raise ValueError("gate and up scales must share a dtype")
+    te, to, tc = tile_descriptors
+    xc = x.contiguous()
+    ws = _q8_workspace(xc.shape[0], input_dims, device)
+    prep = prepared_table(codebook)
+    _lib.call("keep_vq_grouped_swiglu_q8", xc.data_ptr(), _dtype_code(xc, "x"), xc.shape[0], _ptr(lhs),
+              gate_codes.data_ptr(), gate_scales.data_ptr(), up_codes.data_ptr(), up_scales.data_ptr(),
+              _dtype_code(gate_scales, "scales"), prep.data_ptr(), te.data_ptr(), to.data_ptr(), tc.data_ptr(),
+              te.numel(), routes, gate_codes.shape[0], hidden_dims, input_dims, group_size, float(limit),
+              ws.data_ptr(), ws.numel(), h.data_ptr(), _stream(device))
+    return h
+
+
+def gemm_eligible(*, code_bits: int, x_dtype: torch.dtype, input_dims: int, group_size: int) -> bool:
+    """Whether the int8 grouped GEMM serves this call (E8P, fp16/bf16/fp32
+    activations, K and the scale group multiples of 128)."""
+
+    return (code_bits == 16 and x_dtype in (torch.float16, torch.bfloat16, torch.float32) and input_dims % 128 == 0
             and group_size % 128 == 0)
 
 
@@ -539,9 +575,10 @@ def gather_vqmm(x, codes, scales, codebook, rhs_indices, *, lhs_indices=None, in
     full_lhs = lhs if lhs is not None else torch.arange(R, dtype=torch.int32, device=device) // x_div
     order, inverse, _, _, te, to, tc, _ = route_plan(flat_rhs, E, GEMM_ROUTE_TILE)
     sorted_lhs = full_lhs[order.long()].contiguous()
-    if eligible:
-        routed = grouped_gemm(xt, c, s, cb, (te, to, tc), lhs=sorted_lhs, routes=R, input_dims=input_dims,
-                              output_dims=output_dims, group_size=group_size)
+    if eligible:  # rows land in route order directly
+        y = grouped_gemm(xt, c, s, cb, (te, to, tc), lhs=sorted_lhs, routes=R, input_dims=input_dims,
+                         output_dims=output_dims, group_size=group_size, out_index=order)
+        return y.reshape(out_shape)
     else:
         sorted_rhs = flat_rhs[order.long()].contiguous()
         routed = routed_matvec(xt, c, s, cb, sorted_rhs, lhs=sorted_lhs, input_dims=input_dims,

@@ -1,0 +1,110 @@
+"""GPU parity of the int8 prefill grouped GEMM (keep_vq_grouped_gemm_q8) and
+its fused gate/up + SwiGLU form (keep_vq_grouped_swiglu_q8) against the
+float64 oracle: partial column blocks, tiles of one and two 32-route
+m-tiles, per-row and grouped scales, fp16 / bf16 / fp32 activations, the
+scatter back to route order, and NaN rows / out-of-range experts (the
+sorted-route prefill of src/ramp/ops/vq_switch.py:620-913 and
+src/ramp/models/glm4_moe_adapter.py:274-353)."""
+
+import numpy as np
+import pytest
+import torch
+
+import keep_amd
+from keep_amd import ops as kops
+from keep_amd import synth
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _t(a, dev):
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _check(got, want, tol=TOL):
+    g = got.float().cpu().numpy()
+    err = ops.max_rel_err(g, want)
+    assert err <= tol, f"max rel err {err:.3e}"
+    assert ops.elementwise_ok(g, want, rtol=tol), "elementwise bound violated"
+    return err
+
+
+def _plan(rhs, E, k, dev):
+    flat = _t(rhs.reshape(-1).astype(np.int32), dev)
+    order, inverse, counts, _, te, to, tc, _ = keep_amd.route_plan(flat, E, 64)
+    lhs = (torch.arange(flat.numel(), device=dev, dtype=torch.int32) // k)[order.long()].contiguous()
+    return flat, order, inverse, counts, (te, to, tc), lhs
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("G", [1, 4])
+def test_grouped_gemm_q8_vs_oracle(dev, xdt, G):
+    """N = 320: a full and a partial 256-column block; Zipf routing gives
+    experts with > 64, 33..64 and <= 32 routes."""
+    E, N, K, T, k = 12, 320, 512, 100, 4
+    codes, scales = synth.projection_np(E, N, K, group_size=K // G, seed=G)
+    rhs = synth.zipf_routes(T, E, k, seed=3)
+    x = synth.rht_activations(T, K, seed=4, device=dev, dtype=xdt)
+    flat, order, inverse, counts, tiles, lhs = _plan(rhs, E, k, dev)
+    c = counts.cpu().numpy()
+    assert c.max() > 64 and ((c > 32) & (c <= 64)).any() and ((c > 0) & (c <= 32)).any()
+    cb = kops._default_codebook(16, dev)
+    want = ops.gather_token(x.float().cpu().numpy(), codes, scales, rhs)
+    y = kops.grouped_gemm(x, _t(codes, dev), _t(scales, dev), cb, tiles, lhs=lhs, routes=flat.numel(),
+                          input_dims=K, output_dims=N, group_size=K // G, out_dtype=torch.float32)
+    _check(y[inverse.long()].reshape(T, k, N), want)
+    # the same rows scattered straight to route order
+    y2 = kops.grouped_gemm(x, _t(codes, dev), _t(scales, dev), cb, tiles, lhs=lhs, routes=flat.numel(),
+                           input_dims=K, output_dims=N, group_size=K // G, out_dtype=torch.float32, out_index=order)
+    assert torch.equal(y2, y[inverse.long()])
+
+
+@pytest.mark.parametrize("limit", [0.0, 7.0])
+def test_grouped_swiglu_q8_vs_oracle(dev, limit):
+    """I = 320: two full 128-row blocks and a partial one."""
+    E, H, I, T, k = 10, 512, 320, 60, 3
+    gate = synth.projection_np(E, I, H, seed=31)
+    up = synth.projection_np(E, I, H, seed=32)
+    rhs = synth.zipf_routes(T, E, k, seed=33)
+    x = synth.rht_activations(T, H, seed=34, device=dev)
+    flat, order, inverse, _, tiles, lhs = _plan(rhs, E, k, dev)
+    cb = kops._default_codebook(16, dev)
+    h = kops.grouped_swiglu(x, _t(gate[0], dev), _t(gate[1], dev), _t(up[0], dev), _t(up[1], dev), cb, tiles,
+                            lhs=lhs, routes=flat.numel(), input_dims=H, hidden_dims=I, group_size=H, limit=limit)
+    xf = x.float().cpu().numpy()
+    g = ops.gather_token(xf, gate[0], gate[1], rhs)
+    u = ops.gather_token(xf, up[0], up[1], rhs)
+    want = ops.round_bf16(ops.swiglu(g, u, limit))
+    # bf16-stored h on both sides: two nearly equal values can round one bf16
+    # ulp apart, 2**-7 of the smaller where they straddle a power of two
+    _check(h[inverse.long()].reshape(T, k, I), want, TOL + 2.0 ** -7)
+
+
+def test_grouped_gemm_q8_nan_row_and_bad_expert(dev):
+    E, N, K, T, k = 4, 256, 256, 40, 2
+    codes, scales = synth.projection_np(E, N, K, seed=41)
+    rng = np.random.default_rng(42)
+    rhs = rng.integers(0, E, size=(T, k)).astype(np.int32)
+    rhs[5, 1] = 7  # out of range: its route's row is NaN
+    x = synth.rht_activations(T, K, seed=43, device=dev)
+    x[9, 17] = float("nan")  # token 9's routes are NaN
+    flat = _t(rhs.reshape(-1), dev)
+    order, inverse, _, _, te, to, tc, _ = keep_amd.route_plan(flat, 8, 64)  # 8 buckets: expert 7 gets a tile
+    lhs = (torch.arange(flat.numel(), device=dev, dtype=torch.int32) // k)[order.long()].contiguous()
+    cb = kops._default_codebook(16, dev)
+    y = kops.grouped_gemm(x, _t(codes, dev), _t(scales, dev), cb, (te, to, tc), lhs=lhs, routes=flat.numel(),
+                          input_dims=K, output_dims=N, group_size=K, out_dtype=torch.float32,
+                          out_index=order).reshape(T, k, N).cpu()
+    bad = np.zeros((T, k), dtype=bool)
+    bad[5, 1] = True
+    bad[9, :] = True
+    assert torch.isnan(y[torch.from_numpy(bad)]).all()
+    good = ~bad
+    assert not torch.isnan(y[torch.from_numpy(good)]).any()
+    rr = np.where(rhs < E, rhs, 0)
+    want = ops.gather_token(np.nan_to_num(x.float().cpu().numpy()), codes, scales, rr)
+    _check(y[torch.from_numpy(good)], want[good])
