@@ -264,15 +264,21 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
         for (int t = 0; t < NTERM; ++t) acc[mt][t] = i32x16{};
       }
     };
-    // NT live m-tiles; A operands of k-step s + 1 are read while step s multiplies
+    // NT live m-tiles. Unit u multiplies with the B operands of block u
+    // (decoded during unit u - 1) while it decodes block u + 1 one dword per
+    // k-step, stages the A terms of block u + 1 and issues the loads of
+    // block u + D: the matrix cores run under the decode and the staging.
+    q8v4 Bx[2][4];
+    {
+      const uint32_t w4[4] = {bb[0].q.x, bb[0].q.y, bb[0].q.z, bb[0].q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Bx[0][i] = q8_decode2(tq, lk, w4[i]);
+    }
     auto run = [&](auto nt_c) {
       constexpr int NT = decltype(nt_c)::value;
-      auto unit = [&](int u, Buf& b) {
-        q8v4 B[4];
-        q8_decode8(tq, lk, b.q, B);
+      auto unit = [&](int u, Buf& b, const Buf& bn, const q8v4 (&Bc)[4], q8v4 (&Bn)[4]) {
         stage((u + 1) & 1, b.at);
-        issue(u + D, b);
-        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t wn[4] = {bn.q.x, bn.q.y, bn.q.z, bn.q.w};
         if (u < nkb) {
           const uint8_t* abase = &ash[u & 1][c * ROW + 64 * h];
 #pragma unroll
@@ -285,17 +291,20 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
-              for (int t = 0; t < NTERM; ++t) acc[mt][t] = mfma32_i8(A[mt][t], B[s], acc[mt][t]);
+              for (int t = 0; t < NTERM; ++t) acc[mt][t] = mfma32_i8(A[mt][t], Bc[s], acc[mt][t]);
+            Bn[s] = q8_decode2(tq, lk, wn[s]);
           }
           if constexpr (GROUPED) {
             if ((u + 1) % a.kpg == 0) fold(u / (int)a.kpg);
           }
         }
+        issue(u + D, b);
         __syncthreads();
       };
-      for (int u = 0; u < nkb; u += D) {  // every call unconditional: blocks past the end only reload
+      constexpr int UN = D % 2 == 0 ? D : 2 * D;  // a multiple of D (buffers) and of 2 (B operands)
+      for (int u = 0; u < nkb; u += UN) {  // every call unconditional: blocks past the end only reload
 #pragma unroll
-        for (int i = 0; i < D; ++i) unit(u + i, bb[i]);
+        for (int i = 0; i < UN; ++i) unit(u + i, bb[i % D], bb[(i + 1) % D], Bx[i & 1], Bx[(i + 1) & 1]);
       }
     };
     if (two) run(std::integral_constant<int, 2>{});

@@ -73,19 +73,23 @@ __device__ __forceinline__ Q8Keys q8_keys(uint32_t lane) {
   k.s2hi = m_first ? 0x0c0c0700u : 0x0c0c0600u;
   return k;
 }
+// One code dword (codewords 2i, 2i + 1) -> one B operand.
+__device__ __forceinline__ q8v4 q8_decode2(const char* tqr, const Q8Keys& k, uint32_t w) {
+  const uint32_t a1 = __builtin_amdgcn_perm(w, k.base1, k.s1lo);
+  const uint32_t a2 = __builtin_amdgcn_perm(w, k.base2, k.s2lo);
+  const uint32_t b1 = __builtin_amdgcn_perm(w, k.base1, k.s1hi);
+  const uint32_t b2 = __builtin_amdgcn_perm(w, k.base2, k.s2hi);
+  const uint2 x1 = *(const uint2*)(tqr + a1), x2 = *(const uint2*)(tqr + a2);
+  const uint2 y1 = *(const uint2*)(tqr + b1), y2 = *(const uint2*)(tqr + b2);
+  return q8v4{(int)(x1.x ^ x2.x), (int)(x1.y ^ x2.y), (int)(y1.x ^ y2.x), (int)(y1.y ^ y2.y)};
+}
 template <bool HALVES = false>
 __device__ __forceinline__ void q8_decode8(const char* tqr, const Q8Keys& k, uint4 q, q8v4 (&b)[4]) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (HALVES && i == 2) __builtin_amdgcn_sched_barrier(0);  // at most 8 lookups in flight (register pressure)
-    const uint32_t a1 = __builtin_amdgcn_perm(w[i], k.base1, k.s1lo);
-    const uint32_t a2 = __builtin_amdgcn_perm(w[i], k.base2, k.s2lo);
-    const uint32_t b1 = __builtin_amdgcn_perm(w[i], k.base1, k.s1hi);
-    const uint32_t b2 = __builtin_amdgcn_perm(w[i], k.base2, k.s2hi);
-    const uint2 x1 = *(const uint2*)(tqr + a1), x2 = *(const uint2*)(tqr + a2);
-    const uint2 y1 = *(const uint2*)(tqr + b1), y2 = *(const uint2*)(tqr + b2);
-    b[i] = q8v4{(int)(x1.x ^ x2.x), (int)(x1.y ^ x2.y), (int)(y1.x ^ y2.x), (int)(y1.y ^ y2.y)};
+    b[i] = q8_decode2(tqr, k, w[i]);
   }
 }
 
