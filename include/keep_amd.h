@@ -262,6 +262,14 @@ int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_rows, const 
                               int64_t I, int64_t H, int64_t group_size, float swiglu_limit, void* workspace,
                               int64_t workspace_bytes, void* h_out, void* stream);
 
+/* Weighted combine of per-route outputs: out[t, :] = sum over j < k, in
+ * order, of w[t, j] * y[t k + j, :] with fp32 multiply-adds (a NaN route row
+ * stays NaN whatever its weight). y fp32 [T k, H], w fp32 [T, k]. Replaces the
+ * MoE block's (y * scores[..., None]).sum(axis=-2)
+ * (src/ramp/models/glm4_moe_adapter.py:367-372). */
+int keep_route_combine(const float* y, const float* w, int64_t T, int64_t k, int64_t H, void* out, int out_dtype,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -346,6 +346,39 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ route combine
+
+// out[t, :] = sum over j < k, in order, of w[t, j] * y[t k + j, :] (fp32
+// multiply-adds: a NaN row stays NaN whatever its weight, as the reference's
+// (y * scores[..., None]).sum(-2) keeps it). Four columns per thread.
+__global__ __launch_bounds__(256) void k_route_combine(const float* y, const float* w, int64_t T, int k, int64_t H,
+                                                       void* out, int odt) {
+  const int64_t H4 = H >> 2;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= T * H4) return;
+  const int64_t t = i / H4, c = i - t * H4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j = 0; j < k; ++j) {
+    const float wt = w[t * k + j];
+    const float4 v = ((const float4*)(y + (t * k + j) * H))[c];
+    acc.x = fmaf(wt, v.x, acc.x);
+    acc.y = fmaf(wt, v.y, acc.y);
+    acc.z = fmaf(wt, v.z, acc.z);
+    acc.w = fmaf(wt, v.w, acc.w);
+  }
+  const int64_t o = t * H + 4 * c;
+  if (odt == KEEP_F32) {
+    ((float4*)((float*)out + o))[0] = acc;
+  } else if (odt == KEEP_BF16) {
+    uint16_t* p = (uint16_t*)out + o;
+    p[0] = from_float<bf16s>(acc.x).bits; p[1] = from_float<bf16s>(acc.y).bits;
+    p[2] = from_float<bf16s>(acc.z).bits; p[3] = from_float<bf16s>(acc.w).bits;
+  } else {
+    _Float16* p = (_Float16*)out + o;
+    p[0] = (_Float16)acc.x; p[1] = (_Float16)acc.y; p[2] = (_Float16)acc.z; p[3] = (_Float16)acc.w;
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 int gq_nterm(int x_dtype) { return x_dtype == KEEP_BF16 ? 2 : 3; }
@@ -476,4 +509,17 @@ extern "C" int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_r
   a.out = h_out; a.odt = KEEP_BF16;
   gq_launch(a, true, gq_nterm(x_dtype), s);
   return launch_status("keep_vq_grouped_swiglu_q8");
+}
+
+extern "C" int keep_route_combine(const float* y, const float* w, int64_t T, int64_t k, int64_t H, void* out,
+                                  int out_dtype, void* stream) {
+  KEEP_REQUIRE(dtype_ok(out_dtype), "bad dtype enum");
+  KEEP_REQUIRE(T >= 0 && k >= 1 && H >= 4 && H % 4 == 0, "need k >= 1 and H a multiple of 4");
+  if (T == 0) return KEEP_OK;
+  KEEP_REQUIRE(y && w && out, "null pointer argument");
+  KEEP_REQUIRE(aligned(y, 16) && aligned(out, 16), "y and out must be 16-byte aligned");
+  const int64_t n = T * (H / 4);
+  hipLaunchKernelGGL(k_route_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, y, w, T,
+                     (int)k, H, out, out_dtype);
+  return launch_status("keep_route_combine");
 }

@@ -366,7 +366,7 @@ class RoutedVQMoE:
             return moe_decode(x, idx, weight, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
                               limit=self.limit, codebook=g.codebook, out_dtype=self.out_dtype)
         y = self.glu(x, idx)  # [T, k, H]
-        return (y.float() * weight[..., None].float()).sum(-2).to(self.out_dtype)
+        return ops.route_combine(y, weight, self.out_dtype)
 
     def _layer_path(self, x: torch.Tensor) -> bool:
         g, d = self.glu.gate_proj, self.glu.down_proj

@@ -357,6 +357,21 @@ def grouped_swiglu(x: torch.Tensor, gate_codes: torch.Tensor, gate_scales: torch
     return h
 
 
+def route_combine(y: torch.Tensor, weight: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """``keep_route_combine``: ``sum_j w[t, j] * y[t, j, :]`` in fp32 for
+    ``y [T, k, H]`` (``glm4_moe_adapter.py:367-372``)."""
+
+    T, k, H = y.shape
+    od = out_dtype or torch.float32
+    yf = y.float().contiguous()
+    wf = weight.reshape(T, k).float().contiguous()
+    if H % 4:
+        raise ValueError(f"route_combine needs H a multiple of 4, found {H}")
+    out = torch.empty((T, H), dtype=od, device=y.device)
+    _lib.call("keep_route_combine", yf.data_ptr(), wf.data_ptr(), T, k, H, out.data_ptr(), _DT[od], _stream(y.device))
+    return out
+
+
 def gemm_eligible(*, code_bits: int, x_dtype: torch.dtype, input_dims: int, group_size: int) -> bool:
     """Whether the int8 grouped GEMM serves this call (E8P, fp16/bf16/fp32
     activations, K and the scale group multiples of 128)."""
