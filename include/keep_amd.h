@@ -67,6 +67,17 @@ int keep_vq_matvec(const void* x, int x_dtype, int64_t x_rows,
                    const uint32_t* res_table, const uint32_t* hot_of_slot, int64_t num_hot,
                    void* out, int out_dtype, void* stream);
 
+/* The residual tier alone: out[r, :] = W[rhs[r]] . x[r / x_div, :] for 8-bit E8
+ * codes [E, N, K/8] with scales [E, N, K/group_size] and the packed E8 table
+ * (nibble d = dim d); a route whose index is 0xFFFFFFFF writes zeros (any other
+ * out-of-range index: NaN). fp32 accumulate. Replaces
+ * ramp.kernels.e8_1bit_m1.e8_1bit_m1_token_layout / e8_1bit_m1_per_route
+ * (src/ramp/kernels/e8_1bit_m1.py:48-97, e8_1bit_m1.metal:1-90). */
+int keep_e8_1bit_matvec(const void* x, int x_dtype, int64_t x_rows, const uint8_t* codes, const void* scales,
+                        int scale_dtype, const uint32_t* table, const uint32_t* rhs, int64_t routes,
+                        int64_t x_div, int64_t num_experts, int64_t N, int64_t K, int64_t group_size, void* out,
+                        int out_dtype, void* stream);
+
 /* Expert-grouped verify rows: each tile holds up to m_rows routes of one
  * expert (tile_offset/tile_count index the sorted routes; tile_expert is
  * the expert). Routes of a tile share every code load and decode. Output row

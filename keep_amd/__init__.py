@@ -11,6 +11,8 @@ from keep_amd.nn import (LimitedSwiGLU, QuantizedVQSwitchGLU, QuantizedVQSwitchL
 from keep_amd.ops import (
     decode_e8p,
     decode_weight_matrix,
+    e8_1bit_m1_per_route,
+    e8_1bit_m1_token_layout,
     e8_1bit_packed,
     e8p_m1_per_route,
     e8p_m1_token_layout,
@@ -21,6 +23,7 @@ from keep_amd.ops import (
     gather_vqmm_sorted_routes,
     gather_vqmm_verify_rows,
     half2_pairs,
+    pair_packed,
     route_plan,
     trace_gather_vqmm_calls,
     vq_qmm,
@@ -30,8 +33,9 @@ from keep_amd.router import expert_select, resident_bias, router_dual_topk
 
 __all__ = [
     "LimitedSwiGLU", "QuantizedVQSwitchGLU", "QuantizedVQSwitchLinear", "RoutedVQMoE", "decode_e8p",
-    "decode_weight_matrix", "e8_1bit_packed", "e8p_m1_per_route", "e8p_m1_token_layout", "e8p_nested_m1_per_route",
-    "e8p_nested_m1_token_layout", "e8p_packed_abs_grid", "expert_select", "gather_vqmm", "gather_vqmm_sorted_routes",
-    "gather_vqmm_verify_rows", "half2_pairs", "is_available", "moe_decode", "moe_layer", "moe_layer_supported", "resident_bias", "route_plan",
+    "decode_weight_matrix", "e8_1bit_m1_per_route", "e8_1bit_m1_token_layout", "e8_1bit_packed", "e8p_m1_per_route",
+    "e8p_m1_token_layout", "e8p_nested_m1_per_route", "e8p_nested_m1_token_layout", "e8p_packed_abs_grid",
+    "expert_select", "gather_vqmm", "gather_vqmm_sorted_routes", "gather_vqmm_verify_rows", "half2_pairs",
+    "is_available", "moe_decode", "moe_layer", "moe_layer_supported", "pair_packed", "resident_bias", "route_plan",
     "router_dual_topk", "trace_gather_vqmm_calls", "vq_qmm", "vq_qmv",
 ]

@@ -105,6 +105,7 @@ struct MatvecArgs {
   void* out;
   int odt;
   int64_t row_blocks;
+  int zero_none;  // a route whose index is 0xFFFFFFFF writes zeros (the residual-only form)
 };
 
 template <int CB, typename XT, int CH, bool NESTED>
@@ -155,7 +156,8 @@ __global__ __launch_bounds__(256) void k_vq_matvec(MatvecArgs a) {
   __syncthreads();
   if (!live) return;
   if (bad) {
-    if (lane < MV_ROWS && row0 + lane < a.N) store_at(a.out, a.odt, route * a.N + row0 + lane, __builtin_nanf(""));
+    const float fill = a.zero_none && e == -1 ? 0.f : __builtin_nanf("");
+    if (lane < MV_ROWS && row0 + lane < a.N) store_at(a.out, a.odt, route * a.N + row0 + lane, fill);
     return;
   }
   float acc[MV_ROWS], racc[MV_ROWS];
@@ -752,4 +754,36 @@ extern "C" int keep_moe_down(int h_dtype, int64_t T, int64_t H, int64_t I, const
   return moe_common(false, true, "keep_moe_down", nullptr, h_dtype, T, H, I, idx, w, k, num_experts, nullptr,
                     nullptr, nullptr, nullptr, down_codes, down_scales, scale_dtype, H, group_size_i, table,
                     prepared, 0.f, const_cast<void*>(h_work), out, out_dtype, stream);
+}
+
+extern "C" int keep_e8_1bit_matvec(const void* x, int x_dtype, int64_t x_rows, const uint8_t* codes,
+                                   const void* scales, int scale_dtype, const uint32_t* table, const uint32_t* rhs,
+                                   int64_t routes, int64_t x_div, int64_t num_experts, int64_t N, int64_t K,
+                                   int64_t group_size, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE(dtype_ok(x_dtype) && dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
+  KEEP_REQUIRE(N > 0 && K > 0 && K % 8 == 0, "need N > 0 and K > 0 divisible by 8 (N=%lld K=%lld)", (long long)N,
+               (long long)K);
+  KEEP_REQUIRE(group_size > 0 && group_size % 8 == 0 && K % group_size == 0,
+               "group_size must be a positive multiple of 8 dividing K (group_size=%lld)", (long long)group_size);
+  KEEP_REQUIRE(routes >= 0 && num_experts > 0 && x_div > 0, "need routes >= 0, num_experts > 0 and x_div > 0");
+  if (routes == 0) return KEEP_OK;
+  KEEP_REQUIRE(x && codes && scales && table && rhs && out, "null pointer argument");
+  KEEP_REQUIRE(x_rows > 0 && aligned(x, 16), "x must be non-empty and 16-byte aligned");
+  const int64_t C = K / 8, cpg = group_size / 8;
+  const int ch = pick_chunk(C, cpg, 0);
+  KEEP_REQUIRE(aligned(codes, (uintptr_t)ch), "codes pointer misaligned for %d-codeword loads", ch);
+  MatvecArgs a{};
+  a.x = x; a.x_rows = x_rows; a.codes = codes; a.scales = scales; a.sdt = scale_dtype; a.table = table;
+  a.rhs = (const int32_t*)rhs; a.lhs = nullptr; a.routes = routes; a.x_div = x_div;
+  a.E = num_experts; a.N = N; a.K = K; a.G = K / group_size; a.cpg = cpg; a.rG = 1; a.rcpg = 1;
+  a.out = out; a.odt = out_dtype; a.zero_none = 1;
+  a.row_blocks = (N + MV_WAVES * MV_ROWS - 1) / (MV_WAVES * MV_ROWS);
+  const int64_t blocks = a.row_blocks * routes;
+  KEEP_REQUIRE(blocks <= 0x7fffffffLL, "too many blocks");
+  dim3 grid((unsigned)blocks);
+  hipStream_t s = (hipStream_t)stream;
+  if (x_dtype == KEEP_F16) launch_matvec_x<_Float16>(8, false, ch, grid, s, a);
+  else if (x_dtype == KEEP_BF16) launch_matvec_x<bf16s>(8, false, ch, grid, s, a);
+  else launch_matvec_x<float>(8, false, ch, grid, s, a);
+  return launch_status("keep_e8_1bit_matvec");
 }

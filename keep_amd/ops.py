@@ -840,3 +840,111 @@ def e8p_nested_m1_per_route(x, base, rhs_indices, residual, hot_of_slot, *, outp
         raise ValueError(f"per-route nested E8P needs x [{R}, in], got {tuple(xt.shape)}")
     return routed_matvec(xt, c, s, cb, rhs.reshape(-1), x_div=1, input_dims=K, output_dims=output_dims,
                          group_size=gs, residual=res, hot_of_slot=hot)
+
+
+# --------------------------------------------------------------------------- e8_1bit_m1 (residual tier alone)
+
+
+def pair_packed(packed) -> np.ndarray:
+    """The packed 8-bit E8 table (nibble d = dim d) with dims 2k and 2k + 1 in
+    nibbles k and k + 4 (reference ``e8_1bit_m1.py:25-33``)."""
+
+    p = np.asarray(packed, dtype=np.uint32)
+    out = np.zeros(p.shape, np.uint32)
+    for k in range(4):
+        out |= ((p >> np.uint32(8 * k)) & np.uint32(0xF)) << np.uint32(4 * k)
+        out |= ((p >> np.uint32(8 * k + 4)) & np.uint32(0xF)) << np.uint32(16 + 4 * k)
+    return out
+
+
+_UNPAIRED: dict = {}
+
+
+def _unpaired_table(codebook: torch.Tensor) -> torch.Tensor:
+    """The inverse of ``pair_packed`` on a device table (nibble d = dim d), cached
+    per table tensor."""
+
+    key = (codebook.data_ptr(), str(codebook.device))
+    hit = _UNPAIRED.get(key)
+    if hit is not None and hit[0] is codebook:
+        return hit[1]
+    p = codebook.to(torch.int64) & 0xFFFFFFFF
+    out = torch.zeros_like(p)
+    for k in range(4):
+        out |= ((p >> (4 * k)) & 0xF) << (8 * k)
+        out |= ((p >> (16 + 4 * k)) & 0xF) << (8 * k + 4)
+    t = (out - ((out >> 31) << 32)).to(torch.int32).contiguous()  # the same bits as int32
+    _UNPAIRED[key] = (codebook, t)
+    return t
+
+
+def _route_bits(rhs_indices, device) -> torch.Tensor:
+    """Route indices as int32 holding the uint32 bits (``NO_RESIDUAL`` -> -1), flat."""
+
+    if isinstance(rhs_indices, torch.Tensor) and rhs_indices.dtype == torch.int32:
+        return rhs_indices.to(device).reshape(-1).contiguous()
+    if isinstance(rhs_indices, torch.Tensor) and rhs_indices.dtype == torch.int64:
+        r = rhs_indices.to(device) & 0xFFFFFFFF
+        return (r - ((r >> 31) << 32)).to(torch.int32).reshape(-1).contiguous()
+    a = rhs_indices.cpu().numpy() if isinstance(rhs_indices, torch.Tensor) else np.asarray(rhs_indices)
+    a = a.astype(np.int64) & 0xFFFFFFFF
+    return torch.from_numpy(a.astype(np.uint32).view(np.int32).reshape(-1).copy()).to(device)
+
+
+def _e8_1bit_launch(x, codes, scales, codebook, rhs_indices, output_dims: int, x_div: int,
+                    rows_per_simdgroup: int, simdgroups: int) -> torch.Tensor:
+    _m1_args(rows_per_simdgroup, simdgroups)
+    device = _device_of(x, codes, scales, rhs_indices)
+    xt = _to_dev(x, device).contiguous()
+    c = _codes_tensor(codes, 8, device)
+    s = _to_dev(scales, device)
+    if c.ndim != 3 or c.shape[1] != output_dims:
+        raise ValueError(f"codes must be [experts, {output_dims}, in/8], found {tuple(c.shape)}")
+    K = c.shape[2] * 8
+    if xt.ndim != 2 or xt.shape[1] != K:
+        raise ValueError(f"x must be [rows, {K}], found {tuple(xt.shape)}")
+    if s.ndim != 3 or s.shape[:2] != c.shape[:2] or c.shape[2] % s.shape[2]:
+        raise ValueError(f"scales must be [experts, {output_dims}, groups] dividing {c.shape[2]} codewords")
+    if codebook is None:
+        cb = _to_dev(e8_1bit_packed().view(np.int32), device)
+    else:
+        t = _to_dev(codebook, device)
+        if t.numel() != 256 or str(t.dtype).rsplit(".", 1)[-1] not in ("uint32", "int32"):
+            raise ValueError("the 8-bit E8 table must be 256 uint32 entries in pair_packed layout")
+        cb = _unpaired_table(t.reshape(256))
+    rhs = _route_bits(rhs_indices, device)
+    R = rhs.numel()
+    out = torch.empty((R, output_dims), dtype=output_dtype(xt.dtype), device=device)
+    if R == 0:
+        return out
+    _lib.call("keep_e8_1bit_matvec", xt.data_ptr(), _dtype_code(xt, "x"), xt.shape[0], c.data_ptr(), s.data_ptr(),
+              _dtype_code(s, "scales"), cb.data_ptr(), rhs.data_ptr(), R, x_div, c.shape[0], output_dims, K,
+              K // s.shape[2], out.data_ptr(), _DT[out.dtype], _stream(device))
+    return out
+
+
+def e8_1bit_m1_token_layout(x, codes, scales, codebook, rhs_indices, *, output_dims: int,
+                            rows_per_simdgroup: int = 4, simdgroups: int = 1) -> torch.Tensor:
+    """8-bit E8 residual alone, token layout -> ``[T, k, N]``; a route index of
+    ``NO_RESIDUAL`` writes zeros (reference ``e8_1bit_m1.py:76-85``).
+    ``codebook`` is the ``pair_packed`` table (``None``: the default one)."""
+
+    shape = tuple(rhs_indices.shape)
+    if x.ndim != 2 or len(shape) != 2 or shape[0] != x.shape[0]:
+        raise ValueError("token-layout E8 needs x [tokens, in] and rhs_indices [tokens, top_k]")
+    T, k = shape
+    rhs = rhs_indices
+    y = _e8_1bit_launch(x, codes, scales, codebook, rhs, output_dims, k, rows_per_simdgroup, simdgroups)
+    return y.reshape(T, k, output_dims)
+
+
+def e8_1bit_m1_per_route(x, codes, scales, codebook, rhs_indices, *, output_dims: int,
+                         rows_per_simdgroup: int = 4, simdgroups: int = 1) -> torch.Tensor:
+    """8-bit E8 residual alone, per-route layout -> ``[R, N]``; ``NO_RESIDUAL``
+    routes write zeros (reference ``e8_1bit_m1.py:88-97``)."""
+
+    R = int(np.prod(tuple(rhs_indices.shape)))
+    if x.ndim != 2 or x.shape[0] != R:
+        raise ValueError(f"per-route E8 needs x [{R}, in], got {tuple(x.shape)}")
+    return _e8_1bit_launch(x, codes, scales, codebook, rhs_indices, output_dims, 1, rows_per_simdgroup,
+                           simdgroups)

@@ -99,3 +99,20 @@ def test_byte_accounting_literal():
 def test_decode_rejects_bad_table_shape(bad):
     with pytest.raises((IndexError, ValueError)):
         e8p.decode_e8p(np.array([0xFFFF], dtype=np.uint16), bad)
+
+
+def test_pair_packed_keeps_every_value_and_inverts():
+    """The residual kernels' table layout (reference e8_1bit_m1.py:25-33 and the
+    reference's tests/test_e8_1bit_m1.py:32-36): nibbles k and k + 4 hold dims
+    2k and 2k + 1; the device-side inverse restores the packed table."""
+    import torch
+
+    from keep_amd import ops as kops
+
+    grid = e8p.decode_e8_1bit(np.arange(256))
+    pairs = kops.pair_packed(e8p.e8_1bit_packed())
+    nib = lambda p, n: ((p >> (4 * n)) & 0xF).astype(np.float64)  # noqa: E731
+    back = np.stack([(nib(pairs, d // 2 if d % 2 == 0 else d // 2 + 4) - 8) / 2 for d in range(8)], axis=1)
+    np.testing.assert_array_equal(back, grid)
+    t = torch.from_numpy(pairs.view(np.int32).copy())
+    np.testing.assert_array_equal(kops._unpaired_table(t).numpy().view(np.uint32), e8p.e8_1bit_packed())
