@@ -242,8 +242,9 @@ int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, 
  * t and route i < tile_count[t], with p = tile_offset[t] + i,
  *   out[out_index[p], :] = W[tile_expert[t]] . x[lhs[p], :]
  * (lhs / out_index NULL: p itself). x is fp16, bf16 or fp32 [x_rows, K]; each
- * row is split into two int8 terms under a power-of-two row scale (residual
- * at most 2^-13 of the row's max), weights are E8P decoded exactly (x 4) from
+ * row is split into int8 terms under a power-of-two row scale (three for
+ * fp16/fp32 rows, residual at most 2^-20 of the row's max; two for bf16 rows,
+ * 2^-13), weights are E8P decoded exactly (x 4) from
  * the `prepared` image (keep_e8p_prepare), int32 sums per term, scales per
  * group in fp32. `workspace` (caller-owned, 256-byte aligned) holds the terms:
  * keep_vq_grouped_gemm_q8_workspace_bytes(x_rows, K) bytes. Replaces

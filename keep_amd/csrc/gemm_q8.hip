@@ -13,11 +13,12 @@
 //  * A = activations as NTERM int8 terms under a per-row power of two s
 //    (max |x| s in [32, 64)): x s = t0 + t1 / 128 (+ t2 / 128^2) + r. Three
 //    terms for fp16 / fp32 rows (residual at most 2^-20 of the row's max, as
-//    the decode layer's activations), two for bf16 rows (2^-13 of the max,
-//    below a bf16 ulp of every value within 2^-5 of the max; h of the down
-//    projection). Three matter for gate/up: their outputs are rounded to bf16
-//    in h, and a 2^-13 error flips that rounding often enough to cost ~1e-3 at
-//    the layer output. k_q8_rows writes the terms once per row ([row][term][K],
+//    the decode layer's activations): gate/up outputs are rounded to bf16 in
+//    h, and two terms (2^-13) flip that rounding often enough to cost ~1e-3
+//    at the layer output. Two for bf16 rows (h of the down projection): a
+//    third changed the layer's error by < 1e-4, while the bf16 rounding of h
+//    itself sets the noise floor, and it costs the down GEMM half again as
+//    many MFMAs. k_q8_rows writes the terms once per row ([row][term][K],
 //    each codeword's 8 values in packed-nibble order), so the A bytes of lane
 //    (m, h) at k-step s are row m's bytes 64h + 16s .. + 15 of the K block of
 //    each term: the same k as B.

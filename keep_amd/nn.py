@@ -18,6 +18,7 @@ from __future__ import annotations
 
 from typing import Callable
 
+import numpy as np
 import torch
 
 from keep_amd import _lib, ops
@@ -121,12 +122,66 @@ class QuantizedVQSwitchLinear:
         return y
 
 
+class HotTier:
+    """The nested 3-bit tier of a routed SwiGLU block: for the experts with a
+    row in ``hot_of_slot`` (``uint32 [E]``, ``0xFFFFFFFF`` = none), an 8-bit E8
+    residual per projection, ``residual[name] = (codes uint8 [H, N, K/8],
+    scales [H, N, G])`` for ``name`` in gate / up / down, added to the E8P base
+    (``e8p_nested_m1.py:90-112``; the serving step ``omlx_lattice.py:172-186,
+    358-370``)."""
+
+    def __init__(self, hot_of_slot, residual: dict):
+        if set(residual) != {"gate", "up", "down"}:
+            raise ValueError("the hot tier needs residual codes and scales for gate, up and down")
+        dev = residual["gate"][0].device
+        if not isinstance(hot_of_slot, torch.Tensor):
+            hot_of_slot = torch.from_numpy(np.asarray(hot_of_slot, dtype=np.uint32).view(np.int32).copy())
+        self.hot_of_slot = hot_of_slot.to(dev)
+        self.residual_arrays = {n: (ops._codes_tensor(c, 8, dev), ops._to_dev(sc, dev)) for n, (c, sc) in residual.items()}
+        self._table = None
+        self._pairs = None
+
+    def check(self, glu) -> None:
+        hot = self.hot_of_slot
+        if str(hot.dtype).rsplit(".", 1)[-1] not in ("uint32", "int32") or hot.numel() != glu.num_experts:
+            raise ValueError(f"hot_of_slot must be uint32 [{glu.num_experts}]")
+        for name, proj in (("gate", glu.gate_proj), ("up", glu.up_proj), ("down", glu.down_proj)):
+            c, sc = self.residual_arrays[name]
+            if c.ndim != 3 or tuple(c.shape[1:]) != (proj.output_dims, proj.input_dims // CODEWORD_DIM):
+                raise ValueError(f"{name} residual codes must be [H, {proj.output_dims}, {proj.input_dims // 8}]")
+            if sc.ndim != 3 or tuple(sc.shape[:2]) != tuple(c.shape[:2]):
+                raise ValueError(f"{name} residual scales must be [H, {proj.output_dims}, groups]")
+
+    def nested(self, name: str):
+        """``(codes, scales, half2 table)`` for the one-pass nested mat-vec."""
+        if self._pairs is None:
+            c = self.residual_arrays["gate"][0]
+            self._pairs = ops._to_dev(ops.e8_1bit_half2_table().view(np.int32), c.device)
+        c, sc = self.residual_arrays[name]
+        return c, sc, self._pairs
+
+    def route_rows(self, rhs: torch.Tensor) -> torch.Tensor:
+        """The residual row of every route (int32 bits; ``0xFFFFFFFF`` = none)."""
+        hot = self.hot_of_slot.to(torch.int64) & 0xFFFFFFFF
+        rows = hot[rhs.long().clamp(0, hot.numel() - 1)]
+        rows = torch.where((rhs < 0) | (rhs >= hot.numel()), torch.full_like(rows, 0xFFFFFFFF), rows)
+        return (rows - ((rows >> 31) << 32)).to(torch.int32)
+
+    def residual(self, name: str, rows: torch.Tensor, route_rows: torch.Tensor) -> torch.Tensor:
+        """Per-route residual ``[R, N]`` of routes ``rows[r]`` at residual rows
+        ``route_rows[r]`` (zeros off the tier)."""
+        c, sc = self.residual_arrays[name]
+        if self._table is None:
+            self._table = ops._to_dev(ops.pair_packed(ops.e8_1bit_packed()).view(np.int32), c.device)
+        return ops.e8_1bit_m1_per_route(rows, c, sc, self._table, route_rows, output_dims=c.shape[1])
+
+
 class QuantizedVQSwitchGLU:
     """Routed SwiGLU experts: ``down(act(up(x), gate(x)))`` per route -> ``[..., k, H]``."""
 
     def __init__(self, *, gate_proj: QuantizedVQSwitchLinear, up_proj: QuantizedVQSwitchLinear,
                  down_proj: QuantizedVQSwitchLinear, prefill_engine: str = "auto",
-                 activation: Callable | None = None):
+                 activation: Callable | None = None, hot_tier: HotTier | None = None):
         if gate_proj.input_dims != up_proj.input_dims:
             raise ValueError("gate_proj and up_proj input dimensions must match")
         if gate_proj.output_dims != up_proj.output_dims:
@@ -143,6 +198,9 @@ class QuantizedVQSwitchGLU:
         self.input_dims = gate_proj.input_dims
         self.hidden_dims = gate_proj.output_dims
         self.num_experts = gate_proj.num_experts
+        if hot_tier is not None:
+            hot_tier.check(self)
+        self.hot_tier = hot_tier
 
     def _apply_activation(self, up: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
         if self.activation is None:
@@ -180,12 +238,30 @@ class QuantizedVQSwitchGLU:
         flat_rhs = indices.reshape(-1).to(torch.int32).contiguous()
         R = flat_rhs.numel()
         flat_lhs = torch.arange(R, dtype=torch.int32, device=x.device) // k
-        order, _, _, _, te, to, tc, _ = ops.route_plan(flat_rhs, self.num_experts, ops.GEMM_ROUTE_TILE)
+        order, inverse, _, _, te, to, tc, _ = ops.route_plan(flat_rhs, self.num_experts, ops.GEMM_ROUTE_TILE)
         sorted_lhs = flat_lhs[order.long()].contiguous()
         tiles = (te, to, tc)
         g, u, d = self.gate_proj, self.up_proj, self.down_proj
         f32 = torch.float32
         limit = self._fused_swiglu_limit()
+        ht = self.hot_tier
+        if ht is not None:  # base GEMMs plus each route's residual (zero off the hot tier), in fp32
+            hot_sorted = ht.route_rows(flat_rhs)[order.long()].contiguous()
+            gate = ops.grouped_gemm(flat_x, g.codes, g.scales, g.codebook, tiles, lhs=sorted_lhs, routes=R,
+                                    input_dims=g.input_dims, output_dims=g.output_dims, group_size=g.group_size,
+                                    out_dtype=f32)
+            up = ops.grouped_gemm(flat_x, u.codes, u.scales, u.codebook, tiles, lhs=sorted_lhs, routes=R,
+                                  input_dims=u.input_dims, output_dims=u.output_dims, group_size=u.group_size,
+                                  out_dtype=f32)
+            xs = flat_x[sorted_lhs.long()].float().contiguous()  # fp32 rows: the residual comes back in fp32
+            gate = gate + ht.residual("gate", xs, hot_sorted)
+            up = up + ht.residual("up", xs, hot_sorted)
+            hidden = self._apply_activation(up, gate).to(torch.bfloat16).contiguous()
+            y = ops.grouped_gemm(hidden, d.codes, d.scales, d.codebook, tiles, lhs=None, routes=R,
+                                 input_dims=d.input_dims, output_dims=d.output_dims, group_size=d.group_size,
+                                 out_dtype=f32)
+            y = y + ht.residual("down", hidden.float(), hot_sorted)
+            return y[inverse.long()].reshape(lead + (k, d.output_dims))
         if limit is not None and g.group_size == u.group_size and g.scales.dtype == u.scales.dtype:
             hidden = ops.grouped_swiglu(flat_x, g.codes, g.scales, u.codes, u.scales, g.codebook, tiles,
                                         lhs=sorted_lhs, routes=R, input_dims=g.input_dims,
@@ -204,9 +280,28 @@ class QuantizedVQSwitchGLU:
                              out_dtype=f32, out_index=order)
         return y.reshape(lead + (k, d.output_dims))
 
+    def _nested_decode(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """Few routes with a hot tier: one pass over base and residual per
+        projection (``omlx_lattice.py:358-370``): gate/up in the token layout,
+        down per route on the bf16 hidden."""
+        ht, g, u, d = self.hot_tier, self.gate_proj, self.up_proj, self.down_proj
+        lead, k = tuple(x.shape[:-1]), indices.shape[-1]
+        rows = x.reshape(-1, self.input_dims).float().contiguous()  # fp32 rows: gate / up come back in fp32
+        idx = indices.reshape(-1, k).to(torch.int32).contiguous()
+        gate = ops.e8p_nested_m1_token_layout(rows, (g.codes, g.scales, g.codebook), idx, ht.nested("gate"),
+                                              ht.hot_of_slot, output_dims=g.output_dims)
+        up = ops.e8p_nested_m1_token_layout(rows, (u.codes, u.scales, u.codebook), idx, ht.nested("up"),
+                                            ht.hot_of_slot, output_dims=u.output_dims)
+        h = self._apply_activation(up.float(), gate.float()).to(torch.bfloat16).reshape(-1, self.hidden_dims)
+        y = ops.e8p_nested_m1_per_route(h.float().contiguous(), (d.codes, d.scales, d.codebook), idx.reshape(-1),
+                                        ht.nested("down"), ht.hot_of_slot, output_dims=d.output_dims)
+        return y.float().reshape(lead + (k, d.output_dims))
+
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         if self._can_use_shared_sorted_route_prefill(x, indices):
             return self._shared_sorted_route_prefill(x, indices)
+        if self.hot_tier is not None:
+            return self._nested_decode(x, indices)
         gate = self.gate_proj(x, indices)
         up = self.up_proj(x, indices)
         return self.down_proj(self._apply_activation(up, gate), indices)
@@ -362,7 +457,8 @@ class RoutedVQMoE:
     def experts(self, x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         g, u, d = self.glu.gate_proj, self.glu.up_proj, self.glu.down_proj
         T = x.shape[0]
-        if T <= self.decode_max_tokens and self.glu._all_e8p() and x.dtype in (torch.float16, torch.bfloat16):
+        if (T <= self.decode_max_tokens and self.glu._all_e8p() and self.glu.hot_tier is None
+                and x.dtype in (torch.float16, torch.bfloat16)):
             return moe_decode(x, idx, weight, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
                               limit=self.limit, codebook=g.codebook, out_dtype=self.out_dtype)
         y = self.glu(x, idx)  # [T, k, H]
@@ -371,7 +467,7 @@ class RoutedVQMoE:
     def _layer_path(self, x: torch.Tensor) -> bool:
         g, d = self.glu.gate_proj, self.glu.down_proj
         return (x.shape[0] == 1 and x.dtype in (torch.float16, torch.bfloat16) and self.glu._all_e8p() and
-                self.decode_max_tokens >= 1 and
+                self.glu.hot_tier is None and self.decode_max_tokens >= 1 and
                 moe_layer_supported(g.num_experts, g.input_dims, g.output_dims, self.top_k,
                                     g.input_dims // g.scales.shape[-1], d.input_dims // d.scales.shape[-1]))
 
