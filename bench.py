@@ -422,7 +422,26 @@ def other_config(args) -> int:
         return QuantizedVQSwitchLinear(input_dims=K, output_dims=Nn, num_experts=E, codes=pj.codes, scales=pj.scales,
                                        codebook=table, group_size=K, code_bits=16)
 
-    glu = QuantizedVQSwitchGLU(gate_proj=lin(gate, H, I), up_proj=lin(up, H, I), down_proj=lin(down, I, H))
+    tier, hot_rows = None, None
+    res_b = 2 * I * (H // 8) + H * (I // 8) + (2 * I + H) * 2  # 8-bit residual codes + fp16 row scales
+    if cfg == 5:  # the 3-bit tier: 8-bit E8 residuals on 10% of the experts (29), all of them resident
+        from keep_amd.nn import HotTier
+        rng = np.random.default_rng(23)
+        resident = np.nonzero(synth.resident_mask(E, frac=0.5, seed=21))[0]
+        n_hot = E // 10
+        hot = rng.choice(resident, n_hot, replace=False)
+        hot_rows = np.full(E, 0xFFFFFFFF, np.uint32)
+        hot_rows[hot] = np.arange(n_hot, dtype=np.uint32)
+
+        def res(N, K):
+            c = torch.randint(0, 256, (n_hot, N, K // 8), dtype=torch.uint8, device=dev)
+            sc = (torch.exp(torch.randn((n_hot, N, 1), device=dev) * 0.3) * 0.1).half()
+            return c, sc
+
+        tier = HotTier(hot_rows, {"gate": res(I, H), "up": res(I, H), "down": res(H, I)})
+        log(f"bench: config 5: hot tier on {n_hot} resident experts")
+    glu = QuantizedVQSwitchGLU(gate_proj=lin(gate, H, I), up_proj=lin(up, H, I), down_proj=lin(down, I, H),
+                               hot_tier=tier)
     expert_b = 2 * I * (H // 8) * 2 + H * (I // 8) * 2 + (2 * I + H) * 2  # codes + fp16 row scales
     flops_per_route = 2 * 3 * H * I
     mask = synth.resident_mask(E, frac=0.5, seed=21) if cfg == 5 else None
@@ -461,9 +480,13 @@ def other_config(args) -> int:
             r0 = [moe(x, logits[i])[1] for i in range(n_sets)] if T > 1 else None
         torch.cuda.synchronize()
         if r0 is not None:
-            distinct = float(np.mean([len(np.unique(r.idx.cpu().numpy())) for r in r0]))
+            sets = [np.unique(r.idx.cpu().numpy()) for r in r0]
         else:
-            distinct = float(k)
+            with torch.no_grad():
+                sets = [np.unique(moe(x, logits[i])[1].idx.cpu().numpy()) for i in range(n_sets)]
+        distinct = float(np.mean([len(u) for u in sets]))
+        distinct_hot = float(np.mean([int((hot_rows[u] != 0xFFFFFFFF).sum()) for u in sets])) if tier else 0.0
+        layer_b = distinct * expert_b + distinct_hot * res_b
         outs = []
 
         def fn(i):
@@ -474,19 +497,22 @@ def other_config(args) -> int:
             us = _timed_graph(torch, stream, fn, n_sets, reps)
         else:
             us = _timed_eager(torch, stream, fn, n_sets, 8)
-        gbps = distinct * expert_b / (us * 1e-6) / 1e9
+        gbps = layer_b / (us * 1e-6) / 1e9
         name = {3: f"config 3: speculative verify, {T} tokens through the 384-expert top-6 layer "
                    "(router + fused gate/up/SwiGLU + down/combine)",
-                5: f"config 5: 288 experts, top-8, 4096/1536, 50% resident (-inf bias), tau 0.3, "
-                   f"{'decode batch 1' if T == 1 else f'prefill {T} tokens'}"}[cfg]
+                5: f"config 5: 288 experts, top-8, 4096/1536, 50% resident (-inf bias), tau 0.3, 3-bit tier "
+                   f"(E8P + 8-bit E8 residual) on 29 experts, {'decode batch 1' if T == 1 else f'prefill {T} tokens'}"
+                }[cfg]
+        extra = {"distinct_hot_experts": distinct_hot} if tier else {}
         _line(gbps, "GB/s", us, name,
               {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I, "distinct_experts": distinct,
+               **extra,
                "tok_per_s": round(T / (us * 1e-6), 1), "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2),
                "tflops": round(T * k * flops_per_route / (us * 1e-6) / 1e12, 2)},
               "fp16 activations x E8P-2bit codes, fp32 accumulate",
               roofline={"bound": "hbm", "kernel": "layer", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                        "bytes_per_layer": int(distinct * expert_b), "us_per_layer": round(us, 2), "traffic": None})
+                        "bytes_per_layer": int(layer_b), "us_per_layer": round(us, 2), "traffic": None})
     return 0
 
 

@@ -247,14 +247,18 @@ int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, 
  * 2^-13), weights are E8P decoded exactly (x 4) from
  * the `prepared` image (keep_e8p_prepare), int32 sums per term, scales per
  * group in fp32. `workspace` (caller-owned, 256-byte aligned) holds the terms:
- * keep_vq_grouped_gemm_q8_workspace_bytes(x_rows, K) bytes. Replaces
+ * keep_vq_grouped_gemm_q8_workspace_bytes(x_rows, K) bytes. code_bits = 8
+ * runs the nested tier's 8-bit E8 residual instead ([H, N, K/8] uint8 codes,
+ * `prepared` = the packed 8-bit E8 table uint32[256]) and adds it to `out`,
+ * which must then be fp32 (the base projection's output, e8p_nested_m1.py:
+ * 90-112 run per expert tile). Replaces
  * gather_vqmm_sorted_routes' NAX E8P GEMM (src/ramp/ops/vq_switch.py:620-913;
  * native/vq_nax_ext/kernels/nax_fp16_matmul.metal:904-1062); out_index
  * folds in the scatter back to route order of
  * src/ramp/models/glm4_moe_adapter.py:274-353. */
 int64_t keep_vq_grouped_gemm_q8_workspace_bytes(int64_t x_rows, int64_t K);
 int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
-                            const int32_t* out_index, const uint16_t* codes, const void* scales,
+                            const int32_t* out_index, const void* codes, int code_bits, const void* scales,
                             int scale_dtype, const void* prepared, const int32_t* tile_expert,
                             const int32_t* tile_offset, const int32_t* tile_count, int64_t n_tiles,
                             int64_t routes, int64_t num_experts, int64_t N, int64_t K, int64_t group_size,

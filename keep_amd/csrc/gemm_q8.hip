@@ -147,7 +147,13 @@ struct GQArgs {
   int64_t ncb, total, per_xcd;  // column blocks, work items, items per XCD
 };
 
-template <bool GATEUP, bool GROUPED, int NTERM>
+// RES: the nested tier's 8-bit E8 residual instead of E8P base codes. A code
+// byte n indexes the packed E8 table (nibble d = dim d, value (nib - 8) / 2),
+// so the weight x 4 is 2 (nib - 8), exact in int8; the block builds a 32 KiB
+// LDS image (row n = sixteen copies of the 8 bytes, packed-nibble order, lane
+// l reading copy l % 16: conflict-free as the E8P image) and the result is
+// added to the fp32 output (the base projection's).
+template <bool GATEUP, bool GROUPED, int NTERM, bool RES = false>
 __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
   constexpr int D = NTERM == 3 ? 3 : 4;  // K blocks in flight
   constexpr int ROW = gq_row<NTERM>();
@@ -161,8 +167,22 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
   const int c = lane & 31, h = lane >> 5;
   const Q8Keys lk = q8_keys(lane);
   const uint32_t tq_bad = GATEUP ? ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0] : 0u;
+  if constexpr (RES) {
+    const uint32_t p = ((const uint32_t*)a.tq)[tid >> 1];  // entry tid / 2, copies 8 (tid & 1) .. + 7
+    uint32_t b[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
+    for (int i = 0; i < 8; ++i) {
+      const int d = i < 4 ? 2 * i : 2 * (i - 4) + 1;  // packed-nibble order: dims 0 2 4 6 1 3 5 7
+      b[i] = (uint32_t)(2 * ((int)((p >> (4 * d)) & 15u) - 8)) & 0xffu;
+    }
+    const uint2 v = make_uint2(b[0] | b[1] << 8 | b[2] << 16 | b[3] << 24, b[4] | b[5] << 8 | b[6] << 16 | b[7] << 24);
+    uint2* row = (uint2*)((char*)tqs + (tid >> 1) * 128 + (tid & 1) * 64);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) row[i] = v;
+  } else {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
+  }
   wait_vm_q<0>();
   __syncthreads();
 
@@ -171,6 +191,24 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
   const int xcd = blockIdx.x % GQ_XCDS;
   const int nb = gridDim.x / GQ_XCDS;
   const int sr = tid >> 3, sp = tid & 7;  // A staging: row sr, 16-byte chunk sp of each term
+  const uint32_t r8 = (uint32_t)(lane & 15) * 8u;  // this lane's copy in the residual image
+  // B operands of k-step s from a code word: E8P dword (two codewords) or two residual bytes
+  auto decode = [&](uint32_t w) -> q8v4 {
+    if constexpr (RES) {
+      const uint2 x0 = *(const uint2*)(tq + (w & 0xffu) * 128u + r8);
+      const uint2 x1 = *(const uint2*)(tq + ((w >> 8) & 0xffu) * 128u + r8);
+      return q8v4{(int)x0.x, (int)x0.y, (int)x1.x, (int)x1.y};
+    } else {
+      return q8_decode2(tq, lk, w);
+    }
+  };
+  auto words = [&](const uint4& q, uint32_t (&w)[4]) {
+    if constexpr (RES) {
+      w[0] = q.x & 0xffffu; w[1] = q.x >> 16; w[2] = q.y & 0xffffu; w[3] = q.y >> 16;
+    } else {
+      w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+    }
+  };
   const uint32_t sbytes = a.sdt == KEEP_F32 ? 4u : 2u;
 
   for (int64_t j = blockIdx.x / GQ_XCDS; j < a.per_xcd; j += nb) {
@@ -200,7 +238,8 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
     }
     const bool nv = n < a.N;
     const int64_t crow = (bad || !nv) ? 0 : e * a.N + n;
-    const uint16_t* cp = cbase + crow * C + 8 * h;
+    const uint16_t* cp = cbase + crow * C + 8 * h;  // E8P: 16 bytes per K block
+    const uint8_t* cp8 = (const uint8_t*)cbase + crow * C + 8 * h;  // residual: 8 bytes per K block
     // A staging row of this thread
     int64_t xs = off + min(sr, cnt - 1);
     xs = a.lhs ? (int64_t)a.lhs[xs] : xs;
@@ -218,7 +257,12 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
     };
     auto issue = [&](int u, Buf& b) {
       const int kq = min(u, nkb - 1), ka = min(u + 1, nkb - 1);
-      b.q = ldg16_q(cp + kq * 16);
+      if constexpr (RES) {
+        const uint2 v = ldg8_q(cp8 + kq * 16);
+        b.q = make_uint4(v.x, v.y, 0u, 0u);
+      } else {
+        b.q = ldg16_q(cp + kq * 16);
+      }
 #pragma unroll
       for (int t = 0; t < NTERM; ++t) b.at[t] = ldg16_q(ap + t * a.K + ka * GQ_KB);
     };
@@ -271,15 +315,17 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
     // block u + D: the matrix cores run under the decode and the staging.
     q8v4 Bx[2][4];
     {
-      const uint32_t w4[4] = {bb[0].q.x, bb[0].q.y, bb[0].q.z, bb[0].q.w};
+      uint32_t w4[4];
+      words(bb[0].q, w4);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Bx[0][i] = q8_decode2(tq, lk, w4[i]);
+      for (int i = 0; i < 4; ++i) Bx[0][i] = decode(w4[i]);
     }
     auto run = [&](auto nt_c) {
       constexpr int NT = decltype(nt_c)::value;
       auto unit = [&](int u, Buf& b, const Buf& bn, const q8v4 (&Bc)[4], q8v4 (&Bn)[4]) {
         stage((u + 1) & 1, b.at);
-        const uint32_t wn[4] = {bn.q.x, bn.q.y, bn.q.z, bn.q.w};
+        uint32_t wn[4];
+        words(bn.q, wn);
         if (u < nkb) {
           const uint8_t* abase = &ash[u & 1][c * ROW + 64 * h];
 #pragma unroll
@@ -293,7 +339,7 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
             for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
               for (int t = 0; t < NTERM; ++t) acc[mt][t] = mfma32_i8(A[mt][t], Bc[s], acc[mt][t]);
-            Bn[s] = q8_decode2(tq, lk, wn[s]);
+            Bn[s] = decode(wn[s]);
           }
           if constexpr (GROUPED) {
             if ((u + 1) % a.kpg == 0) fold(u / (int)a.kpg);
@@ -337,7 +383,8 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
         } else {
           if (m < cnt && nv) {
             const int64_t o = (int64_t)s_orow[m] * a.N + n;
-            if (a.odt == KEEP_F32) ((float*)a.out)[o] = val;
+            if constexpr (RES) ((float*)a.out)[o] += val;
+            else if (a.odt == KEEP_F32) ((float*)a.out)[o] = val;
             else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[o] = from_float<bf16s>(val).bits;
             else ((_Float16*)a.out)[o] = (_Float16)val;
           }
@@ -404,7 +451,13 @@ void gq_launch_t(const GQArgs& a, dim3 grid, hipStream_t s) {
   else hipLaunchKernelGGL((k_gemm_q8<GATEUP, false, NTERM>), grid, dim3(512), 0, s, a);
 }
 
-void gq_launch(GQArgs& a, bool gateup, int nterm, hipStream_t s) {
+template <int NTERM>
+void gq_launch_res(const GQArgs& a, dim3 grid, hipStream_t s) {
+  if (a.G > 1) hipLaunchKernelGGL((k_gemm_q8<false, true, NTERM, true>), grid, dim3(512), 0, s, a);
+  else hipLaunchKernelGGL((k_gemm_q8<false, false, NTERM, true>), grid, dim3(512), 0, s, a);
+}
+
+void gq_launch(GQArgs& a, bool gateup, int nterm, hipStream_t s, bool res = false) {
   a.ncb = gateup ? (a.N + 127) / 128 : (a.N + 255) / 256;
   a.total = a.ncb * a.n_tiles;
   a.per_xcd = (a.total + GQ_XCDS - 1) / GQ_XCDS;
@@ -412,7 +465,10 @@ void gq_launch(GQArgs& a, bool gateup, int nterm, hipStream_t s) {
   if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   const int64_t per = std::max<int64_t>(1, std::min<int64_t>(a.per_xcd, cus / GQ_XCDS));
   const dim3 grid((unsigned)(per * GQ_XCDS));
-  if (gateup) {
+  if (res) {
+    if (nterm == 3) gq_launch_res<3>(a, grid, s);
+    else gq_launch_res<2>(a, grid, s);
+  } else if (gateup) {
     if (nterm == 3) gq_launch_t<true, 3>(a, grid, s);
     else gq_launch_t<true, 2>(a, grid, s);
   } else {
@@ -436,7 +492,7 @@ extern "C" int64_t keep_vq_grouped_gemm_q8_workspace_bytes(int64_t x_rows, int64
 }
 
 extern "C" int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
-                                       const int32_t* out_index, const uint16_t* codes, const void* scales,
+                                       const int32_t* out_index, const void* codes, int code_bits, const void* scales,
                                        int scale_dtype, const void* prepared, const int32_t* tile_expert,
                                        const int32_t* tile_offset, const int32_t* tile_count, int64_t n_tiles,
                                        int64_t routes, int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
@@ -444,6 +500,8 @@ extern "C" int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_row
                                        void* stream) {
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
+  KEEP_REQUIRE(code_bits == 16 || code_bits == 8, "code_bits must be 16 (E8P) or 8 (residual E8)");
+  KEEP_REQUIRE(code_bits == 16 || out_dtype == KEEP_F32, "the residual form adds into an fp32 output");
   KEEP_REQUIRE(gq_shape_ok(K, group_size),
                "int8 grouped GEMM needs K and the scale group multiples of %d, the group dividing K (K=%lld, "
                "group_size=%lld)",
@@ -455,20 +513,26 @@ extern "C" int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_row
                "null pointer argument");
   KEEP_REQUIRE(workspace_bytes >= gq_ws_bytes(x_rows, K), "workspace needs %lld bytes, got %lld",
                (long long)gq_ws_bytes(x_rows, K), (long long)workspace_bytes);
-  KEEP_REQUIRE(aligned(x, 16) && aligned(codes, 16) && aligned(prepared, 16) && aligned(workspace, 256),
-               "x, codes and prepared must be 16-byte aligned, the workspace 256-byte aligned");
+  KEEP_REQUIRE(aligned(x, 16) && aligned(codes, code_bits == 16 ? 16 : 8) && aligned(prepared, 16) &&
+                   aligned(workspace, 256),
+               "x and prepared must be 16-byte aligned, codes 16 (E8P) or 8 (residual) bytes, the workspace 256");
   hipStream_t s = (hipStream_t)stream;
   uint8_t* ws = (uint8_t*)workspace;
   gq_rows(x, x_dtype, x_rows, K, ws, s);
   GQArgs a{};
   a.xt = ws; a.xinv = (const float*)(ws + gq_ws_terms(x_rows, K)); a.x_rows = x_rows; a.lhs = lhs;
-  a.oidx = out_index; a.c0 = a.c1 = codes; a.s0 = a.s1 = scales; a.sdt = scale_dtype;
-  a.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
-  a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
+  a.oidx = out_index; a.c0 = a.c1 = (const uint16_t*)codes; a.s0 = a.s1 = scales; a.sdt = scale_dtype;
+  if (code_bits == 8) {  // `prepared` is the packed 8-bit E8 table, uint32[256]
+    a.tq = (const uint4*)prepared;
+    a.tq_bad = nullptr;
+  } else {
+    a.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
+    a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
+  }
   a.te = tile_expert; a.to = tile_offset; a.tc = tile_count; a.n_tiles = n_tiles; a.routes = routes;
   a.E = num_experts; a.N = N; a.K = K; a.G = K / group_size; a.kpg = group_size / GQ_KB; a.limit = 0.f;
   a.out = out; a.odt = out_dtype;
-  gq_launch(a, false, gq_nterm(x_dtype), s);
+  gq_launch(a, false, gq_nterm(x_dtype), s, code_bits == 8);
   return launch_status("keep_vq_grouped_gemm_q8");
 }
 

@@ -156,6 +156,12 @@ __device__ __forceinline__ uint4 ldg16_q(const void* p) {
 
 __device__ __forceinline__ uint32_t ldg4_q(const void* p) { return *(const __attribute__((address_space(1))) uint32_t*)p; }
 
+__device__ __forceinline__ uint2 ldg8_q(const void* p) {
+  typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+  const v2u v = *(const __attribute__((address_space(1))) v2u*)p;
+  return make_uint2(v.x, v.y);
+}
+
 __device__ __forceinline__ void dma16_q(const uint4* g, uint4* lds_wave_base) {
   __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0,
                                    0);

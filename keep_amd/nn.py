@@ -138,8 +138,14 @@ class HotTier:
             hot_of_slot = torch.from_numpy(np.asarray(hot_of_slot, dtype=np.uint32).view(np.int32).copy())
         self.hot_of_slot = hot_of_slot.to(dev)
         self.residual_arrays = {n: (ops._codes_tensor(c, 8, dev), ops._to_dev(sc, dev)) for n, (c, sc) in residual.items()}
-        self._table = None
-        self._pairs = None
+        self.rows = int(self.residual_arrays["gate"][0].shape[0])
+        # every table form made here, so that no call copies from the host (graph capture)
+        self._pairs = ops._to_dev(ops.e8_1bit_half2_table().view(np.int32), dev)
+        self._table = ops._to_dev(ops.pair_packed(ops.e8_1bit_packed()).view(np.int32), dev)
+        self._table_packed = ops._to_dev(ops.e8_1bit_packed().view(np.int32), dev)
+        ops._unpaired_table(self._table)
+        hot = self.hot_of_slot.to(torch.int64) & 0xFFFFFFFF
+        self._hot32 = torch.where(hot == ops.NO_RESIDUAL, torch.full_like(hot, -1), hot).to(torch.int32)
 
     def check(self, glu) -> None:
         hot = self.hot_of_slot
@@ -154,9 +160,6 @@ class HotTier:
 
     def nested(self, name: str):
         """``(codes, scales, half2 table)`` for the one-pass nested mat-vec."""
-        if self._pairs is None:
-            c = self.residual_arrays["gate"][0]
-            self._pairs = ops._to_dev(ops.e8_1bit_half2_table().view(np.int32), c.device)
         c, sc = self.residual_arrays[name]
         return c, sc, self._pairs
 
@@ -171,8 +174,6 @@ class HotTier:
         """Per-route residual ``[R, N]`` of routes ``rows[r]`` at residual rows
         ``route_rows[r]`` (zeros off the tier)."""
         c, sc = self.residual_arrays[name]
-        if self._table is None:
-            self._table = ops._to_dev(ops.pair_packed(ops.e8_1bit_packed()).view(np.int32), c.device)
         return ops.e8_1bit_m1_per_route(rows, c, sc, self._table, route_rows, output_dims=c.shape[1])
 
 
@@ -245,23 +246,33 @@ class QuantizedVQSwitchGLU:
         f32 = torch.float32
         limit = self._fused_swiglu_limit()
         ht = self.hot_tier
-        if ht is not None:  # base GEMMs plus each route's residual (zero off the hot tier), in fp32
-            hot_sorted = ht.route_rows(flat_rhs)[order.long()].contiguous()
+        if ht is not None:  # base GEMMs, then the residual GEMMs over tiles of routes grouped by residual row
+            rrows = ht.route_rows(flat_rhs)
+            r_order, _, _, _, rte, rto, rtc, _ = ops.route_plan(rrows, ht.rows, ops.GEMM_ROUTE_TILE)
+            ro = r_order.long()
+            r_tiles = (rte, rto, rtc)
+            at_base = inverse[ro].to(torch.int32).contiguous()  # each residual position's base output row
             gate = ops.grouped_gemm(flat_x, g.codes, g.scales, g.codebook, tiles, lhs=sorted_lhs, routes=R,
                                     input_dims=g.input_dims, output_dims=g.output_dims, group_size=g.group_size,
                                     out_dtype=f32)
             up = ops.grouped_gemm(flat_x, u.codes, u.scales, u.codebook, tiles, lhs=sorted_lhs, routes=R,
                                   input_dims=u.input_dims, output_dims=u.output_dims, group_size=u.group_size,
                                   out_dtype=f32)
-            xs = flat_x[sorted_lhs.long()].float().contiguous()  # fp32 rows: the residual comes back in fp32
-            gate = gate + ht.residual("gate", xs, hot_sorted)
-            up = up + ht.residual("up", xs, hot_sorted)
+            x_lhs = flat_lhs[ro].contiguous()
+            for out_t, name, proj in ((gate, "gate", g), (up, "up", u)):
+                rc, rs = ht.residual_arrays[name]
+                ops.grouped_residual_add(out_t, flat_x, rc, rs, r_tiles, lhs=x_lhs, out_index=at_base, routes=R,
+                                         input_dims=proj.input_dims, output_dims=proj.output_dims,
+                                         group_size=proj.input_dims // rs.shape[-1], table=ht._table_packed)
             hidden = self._apply_activation(up, gate).to(torch.bfloat16).contiguous()
             y = ops.grouped_gemm(hidden, d.codes, d.scales, d.codebook, tiles, lhs=None, routes=R,
                                  input_dims=d.input_dims, output_dims=d.output_dims, group_size=d.group_size,
-                                 out_dtype=f32)
-            y = y + ht.residual("down", hidden.float(), hot_sorted)
-            return y[inverse.long()].reshape(lead + (k, d.output_dims))
+                                 out_dtype=f32, out_index=order)
+            rc, rs = ht.residual_arrays["down"]
+            ops.grouped_residual_add(y, hidden, rc, rs, r_tiles, lhs=at_base, out_index=r_order, routes=R,
+                                     input_dims=d.input_dims, output_dims=d.output_dims,
+                                     group_size=d.input_dims // rs.shape[-1], table=ht._table_packed)
+            return y.reshape(lead + (k, d.output_dims))
         if limit is not None and g.group_size == u.group_size and g.scales.dtype == u.scales.dtype:
             hidden = ops.grouped_swiglu(flat_x, g.codes, g.scales, u.codes, u.scales, g.codebook, tiles,
                                         lhs=sorted_lhs, routes=R, input_dims=g.input_dims,
@@ -283,19 +294,25 @@ class QuantizedVQSwitchGLU:
     def _nested_decode(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """Few routes with a hot tier: one pass over base and residual per
         projection (``omlx_lattice.py:358-370``): gate/up in the token layout,
-        down per route on the bf16 hidden."""
+        down per route on the bf16 hidden, every output in fp32."""
         ht, g, u, d = self.hot_tier, self.gate_proj, self.up_proj, self.down_proj
         lead, k = tuple(x.shape[:-1]), indices.shape[-1]
-        rows = x.reshape(-1, self.input_dims).float().contiguous()  # fp32 rows: gate / up come back in fp32
-        idx = indices.reshape(-1, k).to(torch.int32).contiguous()
-        gate = ops.e8p_nested_m1_token_layout(rows, (g.codes, g.scales, g.codebook), idx, ht.nested("gate"),
-                                              ht.hot_of_slot, output_dims=g.output_dims)
-        up = ops.e8p_nested_m1_token_layout(rows, (u.codes, u.scales, u.codebook), idx, ht.nested("up"),
-                                            ht.hot_of_slot, output_dims=u.output_dims)
-        h = self._apply_activation(up.float(), gate.float()).to(torch.bfloat16).reshape(-1, self.hidden_dims)
-        y = ops.e8p_nested_m1_per_route(h.float().contiguous(), (d.codes, d.scales, d.codebook), idx.reshape(-1),
-                                        ht.nested("down"), ht.hot_of_slot, output_dims=d.output_dims)
-        return y.float().reshape(lead + (k, d.output_dims))
+        rows = x.reshape(-1, self.input_dims).contiguous()
+        idx = indices.reshape(-1).to(torch.int32).contiguous()
+        f32 = torch.float32
+
+        def nested(rows_, proj, name, x_div):
+            rc, rs, rt = ht.nested(name)
+            return ops.routed_matvec(rows_, proj.codes, proj.scales, proj.codebook, idx, x_div=x_div,
+                                     input_dims=proj.input_dims, output_dims=proj.output_dims,
+                                     group_size=proj.group_size, residual=(rc, rs, rt), hot_of_slot=ht._hot32,
+                                     out_dtype=f32)
+
+        gate = nested(rows, g, "gate", k)
+        up = nested(rows, u, "up", k)
+        h = self._apply_activation(up, gate).to(torch.bfloat16).contiguous()
+        y = nested(h, d, "down", 1)
+        return y.reshape(lead + (k, d.output_dims))
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         if self._can_use_shared_sorted_route_prefill(x, indices):

@@ -326,9 +326,35 @@ def grouped_gemm(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor, cod
     ws = _q8_workspace(xc.shape[0], input_dims, device)
     prep = prepared_table(codebook)
     _lib.call("keep_vq_grouped_gemm_q8", xc.data_ptr(), _dtype_code(xc, "x"), xc.shape[0], _ptr(lhs),
-              _ptr(out_index), codes.data_ptr(), scales.data_ptr(), _dtype_code(scales, "scales"), prep.data_ptr(),
+              _ptr(out_index), codes.data_ptr(), 16, scales.data_ptr(), _dtype_code(scales, "scales"), prep.data_ptr(),
               te.data_ptr(), to.data_ptr(), tc.data_ptr(), te.numel(), routes, codes.shape[0], output_dims,
               input_dims, group_size, ws.data_ptr(), ws.numel(), out.data_ptr(), _DT[od], _stream(device))
+    return out
+
+
+def grouped_residual_add(out: torch.Tensor, x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
+                         tile_descriptors, *, lhs: torch.Tensor | None, out_index: torch.Tensor | None, routes: int,
+                         input_dims: int, output_dims: int, group_size: int,
+                         table: torch.Tensor | None = None) -> torch.Tensor:
+    """``keep_vq_grouped_gemm_q8`` on the nested tier's 8-bit E8 residual:
+    ``out[out_index[p]] += R[hot row of tile] . x[lhs[p]]`` over tiles of routes
+    grouped by residual row (``route_plan`` over the routes' hot rows). ``out``
+    is fp32 ``[*, N]``; ``table`` is the packed 8-bit E8 table (default one)."""
+
+    if out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("the residual is added into a contiguous float32 output")
+    if routes == 0:
+        return out
+    device = x.device
+    te, to, tc = tile_descriptors
+    xc = x.contiguous()
+    ws = _q8_workspace(xc.shape[0], input_dims, device)
+    tab = _to_dev(e8_1bit_packed().view(np.int32), device) if table is None else table
+    _lib.call("keep_vq_grouped_gemm_q8", xc.data_ptr(), _dtype_code(xc, "x"), xc.shape[0], _ptr(lhs),
+              _ptr(out_index), codes.data_ptr(), 8, scales.data_ptr(), _dtype_code(scales, "scales"), tab.data_ptr(),
+              te.data_ptr(), to.data_ptr(), tc.data_ptr(), te.numel(), routes, codes.shape[0], output_dims,
+              input_dims, group_size, ws.data_ptr(), ws.numel(), out.data_ptr(), _DT[torch.float32],
+              _stream(device))
     return out
 
 

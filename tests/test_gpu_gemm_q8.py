@@ -108,3 +108,32 @@ def test_grouped_gemm_q8_nan_row_and_bad_expert(dev):
     rr = np.where(rhs < E, rhs, 0)
     want = ops.gather_token(np.nan_to_num(x.float().cpu().numpy()), codes, scales, rr)
     _check(y[torch.from_numpy(good)], want[good])
+
+
+@pytest.mark.parametrize("G", [1, 2])
+def test_grouped_residual_add_vs_oracle(dev, G):
+    """The 8-bit E8 residual form: tiles of routes grouped by residual row
+    (route_plan over the routes' rows, -1 = none, sorted past every tile) add
+    R[row] . x into an fp32 output at out_index; routes off the tier keep
+    their value."""
+    from oracle import e8p
+
+    Hh, N, K, T, k = 5, 320, 512, 60, 3
+    rng = np.random.default_rng(101)
+    rc = rng.integers(0, 256, (Hh, N, K // 8), dtype=np.uint8)
+    rs = (np.exp(rng.normal(0, 0.3, (Hh, N, G))) * 0.1).astype(np.float16)
+    dense = e8p.decode_e8_1bit(rc).astype(np.float64).reshape(Hh, N, K) * np.repeat(rs.astype(np.float64), K // G, -1)
+    rows = rng.integers(-1, Hh, size=T * k).astype(np.int32)
+    x = synth.rht_activations(T, K, seed=102, device=dev)
+    flat = _t(rows, dev)
+    order, _, _, _, te, to, tc, _ = keep_amd.route_plan(flat, Hh, 64)
+    lhs = (torch.arange(T * k, device=dev, dtype=torch.int32) // k)[order.long()].contiguous()
+    base = torch.randn(T * k, N, device=dev)
+    out = base.clone()
+    kops.grouped_residual_add(out, x, _t(rc, dev), _t(rs, dev), (te, to, tc), lhs=lhs, out_index=order,
+                              routes=T * k, input_dims=K, output_dims=N, group_size=K // G)
+    xf = x.float().cpu().numpy().astype(np.float64)
+    want = np.stack([dense[r] @ xf[i // k] if r >= 0 else np.zeros(N) for i, r in enumerate(rows)])
+    got = (out - base).cpu().numpy()
+    assert (got[rows < 0] == 0).all()
+    assert ops.max_rel_err(got, want) <= TOL
