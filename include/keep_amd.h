@@ -214,6 +214,35 @@ int keep_moe_layer(const float* logits, const float* bias_served, const float* b
                    float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
                    uint8_t* admit, void* h_work, void* out, int out_dtype, void* stream);
 
+/* keep_moe_layer with the nested 3-bit tier: an expert e with a residual row
+ * (hot_of_slot[e] < num_hot; 0xFFFFFFFF = none; any other value makes that
+ * route's output NaN) adds R[row] . x to gate, up and down, R the 8-bit E8
+ * residual (codes uint8 [num_hot, N, K/8] indexing the packed E8 table,
+ * value (nibble - 8) / 2 per dimension, times scales [num_hot, N, K/group]
+ * of res_scale_dtype; residual groups of 256-element multiples). res_image
+ * is the residual table's LDS image (keep_e8_1bit_image, once per table);
+ * hot_route is device scratch of k int32 handed from the first launch to the
+ * second. Same two launches as keep_moe_layer, which stays as it is.
+ * Replaces the decode step of scripts/v41_build/omlx_lattice.py:358-370
+ * (nested mat-vecs, e8p_nested_m1.py:90-112) inside the layer of :327-371. */
+int keep_e8_1bit_image_bytes(void);
+int keep_e8_1bit_image(const uint32_t* packed_table, void* image, void* stream);
+int keep_moe_layer_nested(const float* logits, const float* bias_served, const float* bias_demand,
+                          int score_func, int renormalize, float route_scale, float tau,
+                          int64_t num_experts, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
+                          const uint16_t* gate_codes, const void* gate_scales,
+                          const uint16_t* up_codes, const void* up_scales,
+                          const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                          int64_t group_size_h, int64_t group_size_i, const void* prepared,
+                          float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                          uint8_t* admit, void* h_work, void* out, int out_dtype,
+                          const uint32_t* hot_of_slot, int64_t num_hot,
+                          const uint8_t* res_gate_codes, const void* res_gate_scales,
+                          const uint8_t* res_up_codes, const void* res_up_scales,
+                          const uint8_t* res_down_codes, const void* res_down_scales,
+                          int res_scale_dtype, int64_t res_group_size_h, int64_t res_group_size_i,
+                          const void* res_image, int32_t* hot_route, void* stream);
+
 /* Routed SwiGLU MoE for a few tokens (speculative verify) with the routes of
  * one expert sharing every code load: T tokens x k routes (idx/w [T, k], as
  * keep_moe_decode takes them), gate/up/SwiGLU into h_work ([T, k, I] bf16),

@@ -55,6 +55,12 @@ _SIGS = {
     "keep_moe_layer": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64, c_int64,
                        _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P, _P,
                        c_int, _P],
+    "keep_moe_layer_nested": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64,
+                              c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P,
+                              _P, _P, _P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, _P,
+                              _P],
+    "keep_e8_1bit_image": [_P, _P, _P],
+    "keep_e8_1bit_image_bytes": [],
     "keep_moe_down": [c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, c_int, c_int64, _P, _P, _P,
                       _P, c_int, _P],
     "keep_e8p_prepare": [_P, _P, _P],

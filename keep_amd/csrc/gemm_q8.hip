@@ -147,12 +147,10 @@ struct GQArgs {
   int64_t ncb, total, per_xcd;  // column blocks, work items, items per XCD
 };
 
-// RES: the nested tier's 8-bit E8 residual instead of E8P base codes. A code
-// byte n indexes the packed E8 table (nibble d = dim d, value (nib - 8) / 2),
-// so the weight x 4 is 2 (nib - 8), exact in int8; the block builds a 32 KiB
-// LDS image (row n = sixteen copies of the 8 bytes, packed-nibble order, lane
-// l reading copy l % 16: conflict-free as the E8P image) and the result is
-// added to the fp32 output (the base projection's).
+// RES: the nested tier's 8-bit E8 residual instead of E8P base codes (t8_entry
+// and t8_decode2 in q8_dev.h); the block builds the 32 KiB residual image from
+// the packed table and the result is added to the fp32 output (the base
+// projection's).
 template <bool GATEUP, bool GROUPED, int NTERM, bool RES = false>
 __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
   constexpr int D = NTERM == 3 ? 3 : 4;  // K blocks in flight
@@ -168,14 +166,7 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
   const Q8Keys lk = q8_keys(lane);
   const uint32_t tq_bad = GATEUP ? ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0] : 0u;
   if constexpr (RES) {
-    const uint32_t p = ((const uint32_t*)a.tq)[tid >> 1];  // entry tid / 2, copies 8 (tid & 1) .. + 7
-    uint32_t b[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int d = i < 4 ? 2 * i : 2 * (i - 4) + 1;  // packed-nibble order: dims 0 2 4 6 1 3 5 7
-      b[i] = (uint32_t)(2 * ((int)((p >> (4 * d)) & 15u) - 8)) & 0xffu;
-    }
-    const uint2 v = make_uint2(b[0] | b[1] << 8 | b[2] << 16 | b[3] << 24, b[4] | b[5] << 8 | b[6] << 16 | b[7] << 24);
+    const uint2 v = t8_entry(((const uint32_t*)a.tq)[tid >> 1]);  // entry tid / 2, copies 8 (tid & 1) .. + 7
     uint2* row = (uint2*)((char*)tqs + (tid >> 1) * 128 + (tid & 1) * 64);
 #pragma unroll
     for (int i = 0; i < 8; ++i) row[i] = v;
@@ -191,13 +182,10 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
   const int xcd = blockIdx.x % GQ_XCDS;
   const int nb = gridDim.x / GQ_XCDS;
   const int sr = tid >> 3, sp = tid & 7;  // A staging: row sr, 16-byte chunk sp of each term
-  const uint32_t r8 = (uint32_t)(lane & 15) * 8u;  // this lane's copy in the residual image
   // B operands of k-step s from a code word: E8P dword (two codewords) or two residual bytes
   auto decode = [&](uint32_t w) -> q8v4 {
     if constexpr (RES) {
-      const uint2 x0 = *(const uint2*)(tq + (w & 0xffu) * 128u + r8);
-      const uint2 x1 = *(const uint2*)(tq + ((w >> 8) & 0xffu) * 128u + r8);
-      return q8v4{(int)x0.x, (int)x0.y, (int)x1.x, (int)x1.y};
+      return t8_decode2(tq, (uint32_t)lane, w);
     } else {
       return q8_decode2(tq, lk, w);
     }

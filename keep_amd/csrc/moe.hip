@@ -894,7 +894,7 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
                         int64_t I, const uint16_t* gc, const void* gs, const uint16_t* uc, const void* us,
                         const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
                         const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
-                        uint8_t* admit, void* h, void* out, int odt, hipStream_t s);
+                        uint8_t* admit, void* h, void* out, int odt, hipStream_t s, const struct MQNest* nest = nullptr);
 constexpr int PREPARED_TOTAL = 2 * XT_BYTES + 4096 + 256 + 65536;  // expanded tables, int8 tables, flag, LDS image
 
 }  // namespace keep

@@ -40,6 +40,37 @@ __global__ __launch_bounds__(256) void k_build_tq(const uint32_t* packed, uint2*
   if (i == 0) flag[0] = s_bad;
 }
 
+// The nested 3-bit tier: experts with a residual row (hot[e] in [0, nhot);
+// -1 = none, anything else is invalid and gives NaN) add an 8-bit E8
+// residual projection (codes uint8 [nhot, N, K/8], scales [nhot, N, G]) to
+// the E8P base. A cold tile's residual codes come from a buffer load with no
+// records, which returns zeros without touching memory, so every tile issues
+// the same loads and the wait counts stay exact.
+struct MQNest {
+  const int32_t* hot;  // [E]
+  int32_t nhot;
+  const uint8_t *gc, *uc, *dc;
+  const void *gs, *us, *ds;
+  int sdt;
+  int32_t Gh, gsz_h, Gi, gsz_i;
+  const uint4* t8;    // T8R_BYTES residual image (keep_e8_1bit_image)
+  int32_t* hot_route;  // [k] the routes' residual rows, written by the gate/up launch for the down launch
+};
+
+__device__ __forceinline__ uint2 res_load8(const uint8_t* row0, uint32_t bytes, uint32_t off) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)row0, (short)0, (int)bytes, 0x00020000);
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2(v[0], v[1]);
+}
+
+// Residual B operands of 8 codewords (one code byte each) -> the layout of q8_decode8.
+__device__ __forceinline__ void t8_decode8(const char* img, uint32_t lane, uint2 w, q8v4 B[4]) {
+  B[0] = t8_decode2(img, lane, w.x);
+  B[1] = t8_decode2(img, lane, w.x >> 16);
+  B[2] = t8_decode2(img, lane, w.y);
+  B[3] = t8_decode2(img, lane, w.y >> 16);
+}
+
 // ------------------------------------------------------------------ router + gate/up
 
 struct MQLayer {
@@ -64,6 +95,7 @@ struct MQLayer {
   float limit;
   uint16_t* h;  // [k, I] bf16
   int32_t qtiles;
+  MQNest n;  // RES only
 };
 
 // One block per NT / 2 q-tiles (16 rows of the [k, I] intermediate each), 16
@@ -71,10 +103,14 @@ struct MQLayer {
 // experts (rt_select_pair) while waves 2-15 build the A terms of all sixteen
 // slices; after one barrier every wave issues all of its scale and code loads
 // at once, the router waves finish the weights while those are in flight, and
-// gate/up runs tile by tile, then SwiGLU, h in bf16.
-template <int NT, bool XBF, int PER>
+// gate/up runs tile by tile, then SwiGLU, h in bf16. RES: the nested tier's
+// residual image and hot[] come into LDS with the table, and a tile of a hot
+// expert adds its residual dot (same A terms) before the SwiGLU.
+template <int NT, bool XBF, int PER, bool RES>
 __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   __shared__ uint4 tqs[TQR_BYTES / 16];
+  __shared__ uint4 t8s[RES ? T8R_BYTES / 16 : 1];
+  __shared__ int32_t s_hot[RES ? 1024 : 1];
   __shared__ uint4 ash[16 * 3 * 16];  // [slice][term][g * 4 + i]
   __shared__ float gred[16 * NT * 16];
   __shared__ float s_inv4s[16];
@@ -94,6 +130,15 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   if (wv < 2) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
 #pragma unroll
   for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
+  if constexpr (RES) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) dma16_q(a.n.t8 + (wv * 2 + u) * 64 + lane, t8s + (wv * 2 + u) * 64);
+    if (wv >= 2) {  // hot[0 .. E): 64 entries per wave, waves 2 and 3 also 896 ..
+      const int i0 = (wv - 2) * 64;
+      dma4_q(a.n.hot + min(i0 + lane, a.E - 1), (uint32_t*)s_hot + i0);
+      if (wv < 4 && a.E > 896) dma4_q(a.n.hot + min(896 + i0 + lane, a.E - 1), (uint32_t*)s_hot + 896 + i0);
+    }
+  }
   const uint4 xc = ldg16_q((const uint4*)a.x + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
   const uint4 xc2 = ldg16_q((const uint4*)a.x + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
   __builtin_amdgcn_sched_barrier(0);
@@ -126,7 +171,8 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   rt_lds_barrier();  // s_idx, the table and every slice's A terms visible
 
   // 2. this block's tiles: scales, then every tile's codes
-  uint32_t rbase[QT];
+  uint32_t rbase[QT], rres[QT];
+  bool hot_t[QT];
 #pragma unroll
   for (int u = 0; u < QT; ++u) {
     const uint32_t qt = blockIdx.x * QT + u;
@@ -136,6 +182,11 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     const int32_t e = s_idx[route];
     const bool ok = valid && e >= 0 && e < a.E;
     rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
+    if constexpr (RES) {
+      const int32_t hr = __builtin_amdgcn_readfirstlane(ok ? s_hot[e] : -1);
+      hot_t[u] = hr >= 0 && hr < a.n.nhot;
+      rres[u] = (hot_t[u] ? (uint32_t)hr * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
+    }
   }
   const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
   ScaleRaw sr[NT];
@@ -151,6 +202,22 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   auto load_tile = [&](int t) { q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + (size_t)(rbase[t >> 1] + j) * C + kc0); };
 #pragma unroll
   for (int t = 0; t < PD; ++t) load_tile(t);
+  // residual scales and codes (C bytes per row: one byte per codeword)
+  const uint32_t rgrp = RES ? (uint32_t)(wv * 256) / (uint32_t)a.n.gsz_h : 0u;
+  ScaleRaw srr[NT];
+  uint2 qr[NT];
+  if constexpr (RES) {
+#pragma unroll
+    for (int u = 0; u < QT; ++u) {
+      const uint32_t si = (rres[u] + j) * (uint32_t)a.n.Gh + rgrp;
+      srr[2 * u] = scale_raw(a.n.gs, a.n.sdt, si);
+      srr[2 * u + 1] = scale_raw(a.n.us, a.n.sdt, si);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      qr[t] = res_load8(((t & 1) ? a.n.uc : a.n.gc) + (size_t)rres[t >> 1] * C, hot_t[t >> 1] ? 16u * C : 0u,
+                        j * C + kc0);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // the router waves' weights and outputs, while the codes are in flight
@@ -189,10 +256,22 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
+    float vr = 0.f;
+    if constexpr (RES) {
+      if (hot_t[t >> 1]) {  // block-uniform
+        q8v4 R[4];
+        t8_decode8((const char*)t8s, (uint32_t)lane, qr[t], R);
+        q8v4 accr = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) accr = mfma_i8(A[i], R[i], accr);
+        const float dr = ((float)accr[0] + (float)accr[1] * 0.0078125f) + (float)accr[2] * 0.00006103515625f;
+        vr = dr * inv4s * scale_cvt(srr[t], a.n.sdt, (rres[t >> 1] + j) * (uint32_t)a.n.Gh + rgrp);
+      }
+    }
     const uint32_t si = (rbase[t >> 1] + j) * (uint32_t)a.Gh + grp;
     if (lane < 16) {
       const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
-      gred[(wv * NT + t) * 16 + j] = d * inv4s * scale_cvt(sr[t], a.sdt, si);
+      gred[(wv * NT + t) * 16 + j] = d * inv4s * scale_cvt(sr[t], a.sdt, si) + vr;
     }
   }
   rt_lds_barrier();
@@ -209,7 +288,17 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
       const int32_t e = s_idx[q0 / (uint32_t)a.I];
       float hv = silu_mul(gsum, usum, a.limit);
       if (*a.tq_bad) hv = __builtin_nanf("");
+      if constexpr (RES) {
+        const int32_t hr = e >= 0 && e < a.E ? s_hot[e] : -1;
+        if (hr < -1 || hr >= a.n.nhot) hv = __builtin_nanf("");
+      }
       if (e >= 0 && e < a.E) a.h[q0 + jj] = from_float<bf16s>(hv).bits;
+    }
+  }
+  if constexpr (RES) {
+    if (blockIdx.x == 0 && wv == 0 && lane < a.k) {
+      const int32_t e = s_idx[lane];
+      a.n.hot_route[lane] = e >= 0 && e < a.E ? s_hot[e] : -1;
     }
   }
 }
@@ -229,15 +318,18 @@ struct MQDown {
   const uint16_t* h;  // [k, I] bf16
   void* out;
   int odt;
+  MQNest n;  // RES only
 };
 
 // One block per 16 output rows, 8 waves (I / 256 of them decode a 256-wide K
 // slice). A rows 2r and 2r + 1 hold the two int8 terms of route r's h slice
-// (x its own scale); route r's dot is D rows 2r, 2r + 1.
-template <int KMAX>
+// (x its own scale); route r's dot is D rows 2r, 2r + 1. RES: a route with a
+// residual row (hot_route, from the gate/up launch) adds its residual dot.
+template <int KMAX, bool RES>
 __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
   static_assert(KMAX <= 8, "two A rows per route");
   __shared__ uint4 tqs[TQR_BYTES / 16];
+  __shared__ uint4 t8s[RES ? T8R_BYTES / 16 : 1];
   __shared__ uint4 ash[8 * 2 * KMAX * 16];  // [wave][2 r + term][g * 4 + i]
   __shared__ float red[8][KMAX][16];
   const char* tq = (const char*)tqs;
@@ -253,21 +345,27 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
   // 1. routes (scalar loads; KMAX == k), the table (4 pieces), this wave's h slices
   typedef const __attribute__((address_space(4))) int32_t* cidx;
   typedef const __attribute__((address_space(4))) float* cw;
-  int32_t e_r[KMAX];
+  int32_t e_r[KMAX], h_r[KMAX];
   float w_r[KMAX];
 #pragma unroll
   for (int r = 0; r < KMAX; ++r) {
     e_r[r] = ((cidx)a.idx)[r];
     w_r[r] = ((cw)a.w)[r];
+    if constexpr (RES) h_r[r] = ((cidx)a.n.hot_route)[r];
   }
 #pragma unroll
   for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
+  if constexpr (RES) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dma16_q(a.n.t8 + (wv * 4 + u) * 64 + lane, t8s + (wv * 4 + u) * 64);
+  }
   const uint32_t wslice = (dec ? wv : 0) * 32 + (lane >> 1);
   uint4 hq[KMAX];
 #pragma unroll
   for (int r = 0; r < KMAX; ++r) hq[r] = ldg16_q((const uint4*)(a.h + (size_t)r * a.I) + wslice);
   __builtin_amdgcn_sched_barrier(0);
-  uint32_t dbase[KMAX];
+  uint32_t dbase[KMAX], rres[KMAX];
+  bool hot[KMAX];
   float wt[KMAX];
   bool bad = false;
 #pragma unroll
@@ -276,9 +374,14 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
     bad |= w_r[r] != 0.f && !ok;
     wt[r] = ok ? w_r[r] : 0.f;
     dbase[r] = (ok ? (uint32_t)e_r[r] * (uint32_t)a.H : 0u) + n0;
+    if constexpr (RES) {
+      hot[r] = ok && h_r[r] >= 0 && h_r[r] < a.n.nhot;
+      bad |= w_r[r] != 0.f && ok && (h_r[r] < -1 || h_r[r] >= a.n.nhot);
+      rres[r] = (hot[r] ? (uint32_t)h_r[r] * (uint32_t)a.H : 0u) + n0;
+    }
   }
 
-  // 2. scales and codes (route r loaded PD routes ahead of its decode)
+  // 2. scales and codes (route r loaded PD routes ahead of its decode; RES: every residual up front)
   const uint32_t kc0 = (dec ? wv : 0) * 32 + g * 8;
   const uint32_t grp = (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.gsz_i;
   ScaleRaw sr[KMAX];
@@ -288,9 +391,23 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
   uint4 q[KMAX];
   auto load_route = [&](int r) { q[r] = ldg16_q(a.dc + (size_t)(dbase[r] + j) * C + kc0); };
 #pragma unroll
-  for (int r = 0; r < PD && r < KMAX; ++r) load_route(r);  // every wave: the wait below counts them
+  for (int r = 0; r < PD && r < KMAX; ++r) load_route(r);
+  const uint32_t rgrp = RES ? (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.n.gsz_i : 0u;
+  ScaleRaw srr[KMAX];
+  uint2 qr[KMAX];
+  if constexpr (RES) {  // residual scales and codes (C bytes per row), 2 KMAX more loads
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) srr[r] = scale_raw(a.n.ds, a.n.sdt, (rres[r] + j) * (uint32_t)a.n.Gi + rgrp);
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r)
+      qr[r] = res_load8(a.n.dc + (size_t)rres[r] * C, hot[r] && dec ? 16u * C : 0u, j * C + kc0);
+  }
   __builtin_amdgcn_sched_barrier(0);
-  wait_vm_q<KMAX + (PD < KMAX ? PD : KMAX)>();  // the table DMAs and h loads, not the scales and codes
+  // the table DMAs and h loads, not the scales and codes. (The compiler hoists
+  // the A-term maxima and, with LDS DMAs in flight beside register loads, can
+  // only wait for all of them; issuing every code load before that wait
+  // measured slower, so it is left there.)
+  wait_vm_q<KMAX + (PD < KMAX ? PD : KMAX) + (RES ? 2 * KMAX : 0)>();
 
   // 3. A terms: rows 2r, 2r + 1 of route r, scaled by the route's own power of two
   float inv4s[KMAX];
@@ -333,11 +450,24 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
       q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
+      float vr = 0.f;
+      if constexpr (RES) {
+        if (hot[r]) {  // block-uniform
+          q8v4 R[4];
+          t8_decode8((const char*)t8s, (uint32_t)lane, qr[r], R);
+          q8v4 accr = {0, 0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) accr = mfma_i8(A[i], R[i], accr);
+          const float dr = (r & 1) ? (float)accr[2] + (float)accr[3] * 0.0078125f
+                                   : (float)accr[0] + (float)accr[1] * 0.0078125f;
+          vr = dr * inv4s[r] * scale_cvt(srr[r], a.n.sdt, (rres[r] + j) * (uint32_t)a.n.Gi + rgrp);
+        }
+      }
       // rows 2r, 2r + 1 live in lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
       if (g == (uint32_t)(r >> 1)) {
         const float d = (r & 1) ? (float)acc[2] + (float)acc[3] * 0.0078125f
                                 : (float)acc[0] + (float)acc[1] * 0.0078125f;
-        red[wv][r][j] = d * inv4s[r] * scale_cvt(sr[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp);
+        red[wv][r][j] = d * inv4s[r] * scale_cvt(sr[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + grp) + vr;
       }
     }
   }
@@ -377,24 +507,29 @@ bool moe_q_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t g
 
 void moe_q_down_launch(const int32_t* idx, const float* w, int64_t k, int64_t E, int64_t H, int64_t I,
                        const uint16_t* dc, const void* ds, int sdt, int64_t group_i, const void* prepared,
-                       const void* h, void* out, int odt, hipStream_t s) {
+                       const void* h, void* out, int odt, hipStream_t s, const MQNest* nest) {
   MQDown d{};
   d.H = (int32_t)H; d.I = (int32_t)I; d.E = (int32_t)E; d.idx = idx; d.w = w; d.dc = dc; d.ds = ds; d.sdt = sdt;
   d.Gi = (int32_t)(I / group_i); d.gsz_i = (int32_t)group_i;
   d.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
   d.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
   d.h = (const uint16_t*)h; d.out = out; d.odt = odt;
+  if (nest) d.n = *nest;
   const dim3 grid((unsigned)(H / 16)), blk(512u);
+#define DN(K)                                                                        \
+  if (nest) hipLaunchKernelGGL((k_moeq_down<K, true>), grid, blk, 0, s, d);          \
+  else hipLaunchKernelGGL((k_moeq_down<K, false>), grid, blk, 0, s, d)
   switch (k) {
-    case 1: hipLaunchKernelGGL((k_moeq_down<1>), grid, blk, 0, s, d); break;
-    case 2: hipLaunchKernelGGL((k_moeq_down<2>), grid, blk, 0, s, d); break;
-    case 3: hipLaunchKernelGGL((k_moeq_down<3>), grid, blk, 0, s, d); break;
-    case 4: hipLaunchKernelGGL((k_moeq_down<4>), grid, blk, 0, s, d); break;
-    case 5: hipLaunchKernelGGL((k_moeq_down<5>), grid, blk, 0, s, d); break;
-    case 6: hipLaunchKernelGGL((k_moeq_down<6>), grid, blk, 0, s, d); break;
-    case 7: hipLaunchKernelGGL((k_moeq_down<7>), grid, blk, 0, s, d); break;
-    default: hipLaunchKernelGGL((k_moeq_down<8>), grid, blk, 0, s, d); break;
+    case 1: DN(1); break;
+    case 2: DN(2); break;
+    case 3: DN(3); break;
+    case 4: DN(4); break;
+    case 5: DN(5); break;
+    case 6: DN(6); break;
+    case 7: DN(7); break;
+    default: DN(8); break;
   }
+#undef DN
 }
 
 int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm,
@@ -402,7 +537,7 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
                        int64_t I, const uint16_t* gc, const void* gs, const uint16_t* uc, const void* us,
                        const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
                        const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
-                       uint8_t* admit, void* h, void* out, int odt, hipStream_t s) {
+                       uint8_t* admit, void* h, void* out, int odt, hipStream_t s, const MQNest* nest) {
   MQLayer a{};
   a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
   a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
@@ -413,9 +548,12 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
   a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
   a.limit = limit; a.h = (uint16_t*)h;
   a.qtiles = (int32_t)(k * I / 16);
+  if (nest) a.n = *nest;
   const int qt = (int)((a.qtiles + 255) / 256);
   const dim3 grid((unsigned)((a.qtiles + qt - 1) / qt)), blk(1024);
-#define LY(NT, BF, PER) hipLaunchKernelGGL((k_moeq_route_gateup<NT, BF, PER>), grid, blk, 0, s, a)
+#define LY(NT, BF, PER)                                                                    \
+  if (nest) hipLaunchKernelGGL((k_moeq_route_gateup<NT, BF, PER, true>), grid, blk, 0, s, a); \
+  else hipLaunchKernelGGL((k_moeq_route_gateup<NT, BF, PER, false>), grid, blk, 0, s, a)
 #define LY_PER(NT, BF)                 \
   if (E <= 256) LY(NT, BF, 4);         \
   else if (E <= 384) LY(NT, BF, 6);    \
@@ -427,8 +565,74 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
 #undef LY_NT
 #undef LY_PER
 #undef LY
-  moe_q_down_launch(idx, w, k, E, H, I, dc, ds, sdt, group_i, prepared, h, out, odt, s);
+  moe_q_down_launch(idx, w, k, E, H, I, dc, ds, sdt, group_i, prepared, h, out, odt, s, nest);
   return 0;
 }
 
+// The residual LDS image (t8_entry per packed E8 entry, sixteen copies).
+__global__ __launch_bounds__(256) void k_build_t8(const uint32_t* packed, uint2* image) {
+  const uint32_t i = threadIdx.x;
+  const uint2 v = t8_entry(packed[i]);
+#pragma unroll
+  for (int c = 0; c < 16; ++c) image[i * 16 + c] = v;
+}
+
 }  // namespace keep
+
+using namespace keep;
+
+extern "C" int keep_e8_1bit_image(const uint32_t* packed_table, void* image, void* stream) {
+  KEEP_REQUIRE(packed_table && image, "table and image must be non-null");
+  KEEP_REQUIRE(aligned(image, 16), "image must be 16-byte aligned");
+  hipLaunchKernelGGL(k_build_t8, dim3(1), dim3(256), 0, (hipStream_t)stream, packed_table, (uint2*)image);
+  return launch_status("keep_e8_1bit_image");
+}
+
+extern "C" int keep_e8_1bit_image_bytes(void) { return T8R_BYTES; }
+
+extern "C" int keep_moe_layer_nested(
+    const float* logits, const float* bias_served, const float* bias_demand, int score_func, int renormalize,
+    float route_scale, float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
+    const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
+    const uint16_t* down_codes, const void* down_scales, int scale_dtype, int64_t group_size_h, int64_t group_size_i,
+    const void* prepared, float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+    uint8_t* admit, void* h_work, void* out, int out_dtype, const uint32_t* hot_of_slot, int64_t num_hot,
+    const uint8_t* res_gate_codes, const void* res_gate_scales, const uint8_t* res_up_codes,
+    const void* res_up_scales, const uint8_t* res_down_codes, const void* res_down_scales, int res_scale_dtype,
+    int64_t res_group_size_h, int64_t res_group_size_i, const void* res_image, int32_t* hot_route, void* stream) {
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
+  KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype) && dtype_ok(res_scale_dtype), "bad dtype enum");
+  KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);
+  KEEP_REQUIRE(group_size_h > 0 && H % group_size_h == 0 && group_size_i > 0 && I % group_size_i == 0,
+               "bad group sizes");
+  KEEP_REQUIRE(moe_q_layer_supported(E, H, I, k, group_size_h, group_size_i),
+               "shape not served by the routed decode layer kernels (needs H = 4096, I a multiple of 512 up to "
+               "2048, k <= 8, E <= 1024, scale groups of 256-element multiples)");
+  KEEP_REQUIRE(res_group_size_h > 0 && H % res_group_size_h == 0 && res_group_size_h % 256 == 0 &&
+                   res_group_size_i > 0 && I % res_group_size_i == 0 && res_group_size_i % 256 == 0,
+               "residual scale groups must divide H and I and be multiples of 256");
+  KEEP_REQUIRE(num_hot >= 1 && num_hot * I * H < (int64_t(1) << 31), "bad residual row count %lld",
+               (long long)num_hot);
+  KEEP_REQUIRE(logits && x && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
+                   prepared && idx && w && h_work && out && hot_of_slot && res_gate_codes && res_gate_scales &&
+                   res_up_codes && res_up_scales && res_down_codes && res_down_scales && res_image && hot_route,
+               "null pointer argument");
+  KEEP_REQUIRE(aligned(x, 16) && aligned(h_work, 16) && aligned(prepared, 16) && aligned(res_image, 16),
+               "x, h_work, prepared and res_image must be 16-byte aligned");
+  KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 8), "codes misaligned");
+  KEEP_REQUIRE(aligned(res_gate_codes, 8) && aligned(res_up_codes, 8) && aligned(res_down_codes, 8) &&
+                   aligned(hot_of_slot, 4) && aligned(hot_route, 4),
+               "residual codes must be 8-byte aligned");
+  MQNest n{};
+  n.hot = (const int32_t*)hot_of_slot; n.nhot = (int32_t)num_hot;
+  n.gc = res_gate_codes; n.uc = res_up_codes; n.dc = res_down_codes;
+  n.gs = res_gate_scales; n.us = res_up_scales; n.ds = res_down_scales; n.sdt = res_scale_dtype;
+  n.Gh = (int32_t)(H / res_group_size_h); n.gsz_h = (int32_t)res_group_size_h;
+  n.Gi = (int32_t)(I / res_group_size_i); n.gsz_i = (int32_t)res_group_size_i;
+  n.t8 = (const uint4*)res_image; n.hot_route = hot_route;
+  moe_q_layer_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype,
+                     H, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
+                     group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, h_work,
+                     out, out_dtype, (hipStream_t)stream, &n);
+  return launch_status("keep_moe_layer_nested");
+}

@@ -93,6 +93,29 @@ __device__ __forceinline__ void q8_decode8(const char* tqr, const Q8Keys& k, uin
   }
 }
 
+// The nested tier's 8-bit E8 residual: a code byte n indexes the packed E8
+// table (nibble d = dim d, value (nib - 8) / 2), so a weight x 4 is
+// 2 (nib - 8), exact in int8. Its LDS image (keep_e8_1bit_prepare) holds row n
+// as sixteen copies of the 8 bytes in packed-nibble order, lane l reading
+// copy l % 16 (16 lanes touch disjoint bank pairs whatever their codes).
+constexpr int T8R_BYTES = 32768;
+__device__ __forceinline__ uint2 t8_entry(uint32_t p) {
+  uint32_t b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int d = i < 4 ? 2 * i : 2 * (i - 4) + 1;  // packed-nibble order: dims 0 2 4 6 1 3 5 7
+    b[i] = (uint32_t)(2 * ((int)((p >> (4 * d)) & 15u) - 8)) & 0xffu;
+  }
+  return make_uint2(b[0] | b[1] << 8 | b[2] << 16 | b[3] << 24, b[4] | b[5] << 8 | b[6] << 16 | b[7] << 24);
+}
+// Residual code bytes w & 0xff, (w >> 8) & 0xff (codewords 2i, 2i + 1) -> one B operand.
+__device__ __forceinline__ q8v4 t8_decode2(const char* img, uint32_t lane, uint32_t w) {
+  const uint32_t r8 = (lane & 15u) * 8u;
+  const uint2 x0 = *(const uint2*)(img + (w & 0xffu) * 128u + r8);
+  const uint2 x1 = *(const uint2*)(img + ((w >> 8) & 0xffu) * 128u + r8);
+  return q8v4{(int)x0.x, (int)x0.y, (int)x1.x, (int)x1.y};
+}
+
 __device__ __forceinline__ q8v4 mfma_i8(q8v4 a, q8v4 b, q8v4 c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
@@ -160,6 +183,11 @@ __device__ __forceinline__ uint2 ldg8_q(const void* p) {
   typedef unsigned int v2u __attribute__((ext_vector_type(2)));
   const v2u v = *(const __attribute__((address_space(1))) v2u*)p;
   return make_uint2(v.x, v.y);
+}
+
+// 4-byte LDS DMA: the active lanes' words land at lds_wave_base + 4 * lane.
+__device__ __forceinline__ void dma4_q(const void* g, uint32_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 4, 0, 0);
 }
 
 __device__ __forceinline__ void dma16_q(const uint4* g, uint4* lds_wave_base) {

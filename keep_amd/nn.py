@@ -146,6 +146,29 @@ class HotTier:
         ops._unpaired_table(self._table)
         hot = self.hot_of_slot.to(torch.int64) & 0xFFFFFFFF
         self._hot32 = torch.where(hot == ops.NO_RESIDUAL, torch.full_like(hot, -1), hot).to(torch.int32)
+        self._image = None
+
+    def image(self) -> torch.Tensor:
+        """The residual table's LDS image for the fused decode layer (built once, on the tier's device)."""
+        if self._image is None:
+            lib = _lib.load()
+            img = torch.empty(lib.keep_e8_1bit_image_bytes(), dtype=torch.uint8, device=self._table_packed.device)
+            _lib.call("keep_e8_1bit_image", self._table_packed.data_ptr(), img.data_ptr(),
+                      ops._stream(img.device))
+            self._image = img
+        return self._image
+
+    def layer_groups(self, hidden: int, intermediate: int):
+        """``(group_size_h, group_size_i)`` of the residual scales, or None when
+        the fused decode layer cannot take them (groups of 256-multiples)."""
+        gh = hidden // self.residual_arrays["gate"][1].shape[-1]
+        gi = intermediate // self.residual_arrays["down"][1].shape[-1]
+        dts = {sc.dtype for _, sc in self.residual_arrays.values()}
+        if self.residual_arrays["up"][1].shape[-1] != self.residual_arrays["gate"][1].shape[-1] or len(dts) != 1:
+            return None
+        if gh % 256 or gi % 256 or hidden % gh or intermediate % gi:
+            return None
+        return gh, gi
 
     def check(self, glu) -> None:
         hot = self.hot_of_slot
@@ -397,10 +420,13 @@ def moe_layer_supported(num_experts: int, hidden: int, intermediate: int, k: int
 def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, bias_served=None, bias_demand=None,
               score_func: str = "softmax", renormalize: bool = True, route_scale: float = 1.0,
               tau: float = float("inf"), limit: float = 0.0, codebook: torch.Tensor | None = None,
-              out_dtype: torch.dtype | None = None, h_work: torch.Tensor | None = None):
+              out_dtype: torch.dtype | None = None, h_work: torch.Tensor | None = None,
+              hot_tier: HotTier | None = None):
     """One token's whole MoE layer in two launches (``keep_moe_layer``): the dual
     top-k router (as ``router_dual_topk``) fused with gate/up/SwiGLU, then down +
-    weighted combine. ``x [1, H]`` (fp16/bf16), ``logits [1, E]``. Returns
+    weighted combine. ``x [1, H]`` (fp16/bf16), ``logits [1, E]``. With
+    ``hot_tier`` (``keep_moe_layer_nested``) the routes of experts on the
+    nested tier add their 8-bit E8 residual to all three projections. Returns
     ``(out [1, H], RouterOutput)``; the output is float32 by default."""
 
     device = x.device
@@ -442,6 +468,23 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
         raise ValueError("h_work must hold k*I bfloat16 elements")
     cb = ops._codebook_tensor(codebook, 16, device)
     prep = ops.prepared_table(cb)
+    if hot_tier is not None:
+        if hot_tier.hot_of_slot.numel() != E:
+            raise ValueError(f"hot_of_slot must have {E} entries")
+        groups = hot_tier.layer_groups(H, I)
+        if groups is None:
+            raise ValueError("residual scale groups must be 256-element multiples (one dtype) for the decode layer")
+        (rgc, rgs), (ruc, rus), (rdc, rds) = (hot_tier.residual_arrays[n] for n in ("gate", "up", "down"))
+        hot_route = torch.empty((k,), **i32)
+        _lib.call("keep_moe_layer_nested", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
+                  int(bool(renormalize)), float(route_scale), float(tau), E, k, x.data_ptr(), ops._DT[x.dtype], H,
+                  I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
+                  ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(), r.weight.data_ptr(),
+                  r.want.data_ptr(), r.want_score.data_ptr(), r.admit.data_ptr(), h_work.data_ptr(), out.data_ptr(),
+                  ops._DT[od], hot_tier._hot32.data_ptr(), hot_tier.rows, rgc.data_ptr(), rgs.data_ptr(),
+                  ruc.data_ptr(), rus.data_ptr(), rdc.data_ptr(), rds.data_ptr(), ops._DT[rgs.dtype], groups[0],
+                  groups[1], hot_tier.image().data_ptr(), hot_route.data_ptr(), ops._stream(device))
+        return out, r
     _lib.call("keep_moe_layer", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
               int(bool(renormalize)), float(route_scale), float(tau), E, k, x.data_ptr(), ops._DT[x.dtype], H, I,
               gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
@@ -483,8 +526,10 @@ class RoutedVQMoE:
 
     def _layer_path(self, x: torch.Tensor) -> bool:
         g, d = self.glu.gate_proj, self.glu.down_proj
+        ht = self.glu.hot_tier
         return (x.shape[0] == 1 and x.dtype in (torch.float16, torch.bfloat16) and self.glu._all_e8p() and
-                self.glu.hot_tier is None and self.decode_max_tokens >= 1 and
+                (ht is None or ht.layer_groups(g.input_dims, g.output_dims) is not None) and
+                self.decode_max_tokens >= 1 and
                 moe_layer_supported(g.num_experts, g.input_dims, g.output_dims, self.top_k,
                                     g.input_dims // g.scales.shape[-1], d.input_dims // d.scales.shape[-1]))
 
@@ -495,7 +540,7 @@ class RoutedVQMoE:
                              k=self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
                              score_func=self.score_func, renormalize=self.renormalize,
                              route_scale=self.route_scale, tau=self.tau, limit=self.limit, codebook=g.codebook,
-                             out_dtype=self.out_dtype)
+                             out_dtype=self.out_dtype, hot_tier=self.glu.hot_tier)
         r = router_dual_topk(logits, self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
                              score_func=self.score_func, renormalize=self.renormalize, route_scale=self.route_scale,
                              tau=self.tau)

@@ -80,3 +80,76 @@ def test_hot_tier_block_vs_oracle(dev, T, k, hot, limit):
                          h_round="bfloat16", hot_of_slot=hot_of_slot if hot else None,
                          residual=residual if hot else None)
     _check(out, want, elementwise=limit > 0)
+
+
+def _layer_block(dev, E, I, n_hot, gh, gi, rgh, rgi, seed):
+    H = 4096
+    gate = synth.projection_np(E, I, H, group_size=gh, seed=seed)
+    up = synth.projection_np(E, I, H, group_size=gh, seed=seed + 1)
+    down = synth.projection_np(E, H, I, group_size=gi, seed=seed + 2)
+    rng = np.random.default_rng(seed + 3)
+    hot_of_slot = np.full(E, keep_amd.ops.NO_RESIDUAL, np.uint32)
+    hot_of_slot[rng.choice(E, n_hot, replace=False)] = rng.permutation(n_hot).astype(np.uint32)
+
+    def res(N, K, g):
+        c = rng.integers(0, 256, (n_hot, N, K // 8), dtype=np.uint8)
+        s = (np.exp(rng.normal(0, 0.3, (n_hot, N, K // g))) * 0.1).astype(np.float16)
+        return c, s
+
+    residual = {"gate": res(I, H, rgh), "up": res(I, H, rgh), "down": res(H, I, rgi)}
+    mk = lambda p, i, o, g: keep_amd.QuantizedVQSwitchLinear(  # noqa: E731
+        input_dims=i, output_dims=o, num_experts=E, codes=_t(p[0], dev), scales=_t(p[1], dev), group_size=g,
+        code_bits=16)
+    tier = keep_amd.HotTier(hot_of_slot, {n: (_t(c, dev), _t(s, dev)) for n, (c, s) in residual.items()})
+    glu = keep_amd.QuantizedVQSwitchGLU(gate_proj=mk(gate, H, I, gh), up_proj=mk(up, H, I, gh),
+                                        down_proj=mk(down, I, H, gi), hot_tier=tier)
+    return glu, (gate, up, down), hot_of_slot, residual
+
+
+@pytest.mark.parametrize("k,I,gh,gi,rgh,rgi,xdt", [(8, 512, 4096, 512, 4096, 512, torch.float16),
+                                                    (6, 1024, 1024, 256, 256, 512, torch.bfloat16)])
+def test_hot_tier_fused_decode_layer_vs_oracle(dev, k, I, gh, gi, rgh, rgi, xdt):
+    """One token through the fused two-launch layer with the tier
+    (keep_moe_layer_nested): half the pool on the tier, per-row and grouped
+    base and residual scales, fp16 and bf16 activations; the clamped SwiGLU
+    keeps h small enough for the elementwise bound. Also against the nested
+    mat-vec path of the same block on the same routing."""
+    E, H = 32, 4096
+    glu, (gate, up, down), hot_of_slot, residual = _layer_block(dev, E, I, 16, gh, gi, rgh, rgi, seed=200 + k)
+    glu.activation = keep_amd.LimitedSwiGLU(7.0, fp32=True)
+    moe = keep_amd.RoutedVQMoE(glu, top_k=k, swiglu_limit=7.0)
+    x = synth.rht_activations(1, H, seed=210 + k, device=dev, dtype=xdt)
+    z = synth.router_logits(1, E, seed=220 + k, device=dev)
+    assert moe._layer_path(x)
+    out, r = moe(x, z)
+    idx = r.idx.cpu().numpy()
+    on = hot_of_slot[idx] != keep_amd.ops.NO_RESIDUAL
+    assert on.any() and (~on).any(), "want routes on and off the tier"
+    want = ops.moe_layer(x.float().cpu().numpy(), idx, r.weight.cpu().numpy(), gate, up, down, limit=7.0,
+                         h_round="bfloat16", hot_of_slot=hot_of_slot, residual=residual)
+    _check(out, want)
+    split = keep_amd.nn.RoutedVQMoE.experts(moe, x, r.idx, r.weight)  # nested mat-vecs + combine
+    _check(out, split.double().cpu().numpy())
+
+
+def test_hot_tier_fused_layer_off_tier_and_bad_row(dev):
+    """Routes all off the tier: byte-identical to keep_moe_layer. A selected
+    expert whose hot_of_slot row is out of range: NaN output."""
+    E, I, k = 32, 512, 4
+    glu, (gate, up, down), hot_of_slot, residual = _layer_block(dev, E, I, 8, 4096, 512, 4096, 512, seed=300)
+    x = synth.rht_activations(1, 4096, seed=301, device=dev)
+    z = synth.router_logits(1, E, seed=302, device=dev)
+    g, u, d = glu.gate_proj, glu.up_proj, glu.down_proj
+    args = ((g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales))
+    plain, r = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0)
+    sel = r.idx.cpu().numpy().ravel()
+    hot = hot_of_slot.copy()
+    hot[sel] = keep_amd.ops.NO_RESIDUAL
+    tier = keep_amd.HotTier(hot, glu.hot_tier.residual_arrays)
+    nested, r2 = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0, hot_tier=tier)
+    assert torch.equal(r.idx, r2.idx)
+    assert torch.equal(plain, nested)
+    hot[sel[1]] = 8  # rows 0..7 exist
+    bad = keep_amd.HotTier(hot, glu.hot_tier.residual_arrays)
+    out, _ = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0, hot_tier=bad)
+    assert torch.isnan(out).all()
