@@ -315,6 +315,17 @@ int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_rows, const 
 int keep_route_combine(const float* y, const float* w, int64_t T, int64_t k, int64_t H, void* out, int out_dtype,
                        void* stream);
 
+/* Random-sign Walsh-Hadamard transform of T rows of n activations (16 <= n <= 8192,
+ * a power of two): forward y = FWHT(x * signs) / sqrt(n), inverse (inverse != 0)
+ * y = (FWHT(x) / sqrt(n)) * signs; signs = NULL applies the plain orthonormal FWHT.
+ * float32 butterflies in the reference's stage order, so float32 output is
+ * bit-identical to apply_rht_np / apply_inverse_rht_np. x and signs 16-byte
+ * aligned, out a separate buffer. n outside the served range -> KEEP_EUNSUPPORTED.
+ * Replaces apply_rht_np src/keep/quant/rht.py:51-57, apply_inverse_rht_np :60-66,
+ * apply_rht_mx :84-91 (as applied in src/ramp/nn/switch_linear.py:320-322). */
+int keep_rht(const void* x, int x_dtype, const float* signs, int inverse, int64_t T, int64_t n, void* out,
+             int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

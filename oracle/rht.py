@@ -63,3 +63,38 @@ def apply_inverse_rht(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
     """``FWHT(x) * signs`` (``rht.py:60-66``), float64."""
 
     return fwht(x) * np.asarray(signs, dtype=np.float64)
+
+
+def hadamard_f32(x: np.ndarray) -> np.ndarray:
+    """The reference's float32 FWHT, ``_hadamard_np`` (``rht.py:34-48``): float32
+    butterflies, width 1, 2, ..., n/2, then ``* float32(1 / sqrt(n))``. Every
+    butterfly is one float32 add or subtract of the same two inputs in any
+    schedule, so a GPU transform with this stage order matches it bit for bit.
+    Pinned against the float64 ``fwht`` (Sylvester matrix) to float32 rounding."""
+
+    v = np.array(x, dtype=np.float32, copy=True)
+    n = v.shape[-1]
+    _check_pow2(n)
+    lead = v.shape[:-1]
+    w = 1
+    while w < n:
+        v = v.reshape(lead + (n // (2 * w), 2, w))
+        a = v[..., 0, :].copy()
+        b = v[..., 1, :].copy()
+        v[..., 0, :] = a + b
+        v[..., 1, :] = a - b
+        v = v.reshape(lead + (n,))
+        w *= 2
+    return v * np.float32(1.0 / math.sqrt(n))
+
+
+def apply_rht_f32(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """``apply_rht_np`` (``rht.py:51-57``): float32 ``hadamard(x * signs)``."""
+
+    return hadamard_f32(np.asarray(x, dtype=np.float32) * np.asarray(signs, dtype=np.float32))
+
+
+def apply_inverse_rht_f32(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """``apply_inverse_rht_np`` (``rht.py:60-66``): float32 ``hadamard(x) * signs``."""
+
+    return hadamard_f32(x) * np.asarray(signs, dtype=np.float32)

@@ -168,6 +168,24 @@ def test_fwht_matches_sylvester_hadamard_and_round_trips():
     assert set(np.unique(s).tolist()) <= {-1, 1}
 
 
+def test_f32_hadamard_restatement_pins():
+    # float32 restatement of _hadamard_np against the float64 Sylvester FWHT
+    rng = np.random.default_rng(11)
+    for n in (16, 128, 4096):
+        x = rng.standard_normal((3, n)).astype(np.float32)
+        y32 = rht.hadamard_f32(x)
+        assert y32.dtype == np.float32
+        np.testing.assert_allclose(y32, rht.fwht(x), rtol=0, atol=4e-6 * np.log2(n))
+        s = rht.deterministic_rht_signs(n, seed=n)
+        np.testing.assert_allclose(rht.apply_rht_f32(x, s), rht.apply_rht(x, s), rtol=0, atol=4e-6 * np.log2(n))
+        np.testing.assert_allclose(rht.apply_inverse_rht_f32(rht.apply_rht_f32(x, s), s), x, rtol=0, atol=1e-5)
+    # small integers: every butterfly and the power-of-two scale are exact in float32
+    n = 256
+    xi = rng.integers(-8, 8, size=(2, n)).astype(np.float32)
+    H = scipy.linalg.hadamard(n).astype(np.float64) / 16.0
+    np.testing.assert_array_equal(rht.hadamard_f32(xi).astype(np.float64), xi.astype(np.float64) @ H.T)
+
+
 def test_rht_signs_closed_form():
     import hashlib
     raw = hashlib.shake_256(b"13").digest(2)
