@@ -91,6 +91,9 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy kernel (torch.neg, fp16) 8 times, the known-size "
                          "reference that scales FETCH_SIZE / WRITE_SIZE counter readings to bytes")
+    ap.add_argument("--measure", choices=("rht", "install"), default=None,
+                    help="time a component beside the path instead: the activation RHT kernel (keep_rht) or "
+                         "expert installs from a layer-NN.npz into device slot rows")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -99,6 +102,8 @@ def main() -> int:
                                    "run with --gpus 1"}))
         return 2
 
+    if args.measure:
+        return measure_component(args)
     if args.config != 2:
         return other_config(args)
 
@@ -271,6 +276,78 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, gate, up, down, x, idx, w, table, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+    return 0
+
+
+def measure_component(args) -> int:
+    """One JSON line per workload: keep_rht over fp16 rows of 4096 (T = 1 and the 2048-token
+    prefill), HIP events on the launch stream; or expert installs (the config-2 expert size,
+    6.3 MB each) from a layer-NN.npz written to a temporary file, timed from the first submit
+    to the last copy event (the file is in the page cache: host memory -> pinned -> HBM)."""
+
+    import tempfile
+
+    import torch
+
+    from keep_amd import loaders, rht, synth
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    s = torch.cuda.current_stream(dev)
+    if args.measure == "rht":
+        signs = torch.from_numpy(np.where(np.random.default_rng(0).integers(0, 2, H) == 0, -1.0, 1.0)
+                                 .astype(np.float32)).to(dev)
+        side = torch.cuda.Stream(device=dev)  # capture needs a non-default stream (default priority)
+        for T in (1, 2048):
+            x = torch.randn(T, H, device=dev).half()
+            rht.apply_rht(x, signs)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(64):
+                    rht.apply_rht(x, signs)
+            for _ in range(3):
+                graph.replay()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 20
+            a.record(s)
+            for _ in range(reps):
+                graph.replay()
+            b.record(s)
+            b.synchronize()
+            us = a.elapsed_time(b) * 1000.0 / (reps * 64)
+            nbytes = T * H * 2 * 2
+            print(json.dumps({"metric": "activation RHT (keep_rht) HBM GB/s", "value": round(nbytes / us / 1e3, 2),
+                              "unit": "GB/s", "us_per_launch": round(us, 3), "rows": T, "n": H,
+                              "bytes_per_launch": nbytes, "dtype": "fp16 in/out, fp32 butterflies",
+                              "note": "64 launches per HIP graph, graph replays timed with HIP events"}), flush=True)
+        return 0
+    n_exp = 16
+    arrays = {}
+    for proj, (rows, k), seed in (("w1", (I, H), 1), ("w3", (I, H), 2), ("w2", (H, I), 3)):
+        arrays[f"{proj}_codes"], arrays[f"{proj}_scales"] = synth.projection_np(n_exp, rows, k, seed=seed)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "layer-00.npz")
+        np.savez(path, code_bits=np.asarray(16), **arrays)
+        lf = loaders.LayerFile(path)
+        pools = {proj: (torch.zeros((n_exp, *arrays[f"{proj}_codes"].shape[1:]), dtype=torch.int16, device=dev),
+                        torch.zeros((n_exp, *arrays[f"{proj}_scales"].shape[1:]), dtype=torch.float16, device=dev))
+                 for proj in ("w1", "w3", "w2")}
+        inst = loaders.ExpertInstaller(lf, pools, dev)
+        inst.submit(0, 0).synchronize()  # warm the pinned allocator
+        t0 = time.perf_counter()
+        evs = [inst.submit(e, e) for e in range(n_exp)]
+        for ev in evs:
+            ev.synchronize()
+        el = time.perf_counter() - t0
+        per = sum(a[0].nbytes for a in arrays.values() if a.ndim == 3)
+        ok = all(np.array_equal(pools[p][0].cpu().numpy().view(np.uint16), arrays[f"{p}_codes"]) for p in pools)
+        lf.close()
+    print(json.dumps({"metric": "expert install GB/s (layer-NN.npz -> pinned -> slot rows)",
+                      "value": round(per * n_exp / el / 1e9, 3), "unit": "GB/s", "experts": n_exp,
+                      "bytes_per_expert": per, "ms_per_expert": round(el * 1e3 / n_exp, 3), "bytes_match": ok,
+                      "note": "file in the page cache; one reader thread"}), flush=True)
     return 0
 
 
@@ -470,7 +547,7 @@ def other_config(args) -> int:
                   {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I,
                    "distinct_experts": distinct, "hbm_gbps_distinct": round(gbps, 1),
                    "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2)},
-                  "fp16 activations x E8P (fp16 MFMA), fp32 accumulate",
+                  "fp16 activations x E8P-2bit codes on the int8 matrix cores (exact int8 terms), fp32 accumulate",
                   roofline={"bound": "mfma", "kernel": "k_vq_grouped_gemm (x3)", "achieved": round(tf, 2),
                             "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4),
                             "flops_per_layer": flops, "us_per_layer": round(us, 1), "traffic": None})

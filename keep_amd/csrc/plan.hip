@@ -14,6 +14,7 @@ namespace keep {
 constexpr int PLAN_THREADS = 1024;
 constexpr int PLAN_WAVES = PLAN_THREADS / 64;
 constexpr int PLAN_MAX_E = 1024;
+constexpr int PLAN_PER = 16;  // routes per thread held in registers (R <= 16384)
 
 __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs, int R, int E, int tile,
                                                              int32_t* order, int32_t* inverse, int32_t* counts,
@@ -28,10 +29,29 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs,
   const int EB = E + 1;  // bucket E collects invalid expert ids
   for (int e = tid; e < EB; e += PLAN_THREADS) cnt[e] = 0;
   __syncthreads();
-  for (int r = tid; r < R; r += PLAN_THREADS) {
-    int e = rhs[r];
-    if (e < 0 || e >= E) e = E;
-    atomicAdd(&cnt[e], 1);
+  // up to PLAN_PER routes per thread stay in registers from here to the scatter
+  const bool held = R <= PLAN_THREADS * PLAN_PER;
+  int ev[PLAN_PER];
+  if (held) {
+#pragma unroll
+    for (int i = 0; i < PLAN_PER; ++i) {
+      const int r = i * PLAN_THREADS + tid;
+      int e = -1;
+      if (r < R) {
+        e = rhs[r];
+        if (e < 0 || e >= E) e = E;
+      }
+      ev[i] = e;
+    }
+#pragma unroll
+    for (int i = 0; i < PLAN_PER; ++i)
+      if (ev[i] >= 0) atomicAdd(&cnt[ev[i]], 1);
+  } else {
+    for (int r = tid; r < R; r += PLAN_THREADS) {
+      int e = rhs[r];
+      if (e < 0 || e >= E) e = E;
+      atomicAdd(&cnt[e], 1);
+    }
   }
   __syncthreads();
   // Exclusive prefix sums of the bucket sizes (route bases) and of the tile
@@ -91,20 +111,21 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs,
     to[ti] = 0;
     tc[ti] = 0;
   }
-  for (int base = 0; base < R; base += PLAN_THREADS) {
+  // stable scatter, PLAN_THREADS routes per pass: a route's position is its
+  // bucket's running offset + the routes of that bucket in earlier waves of
+  // the pass + the lanes of its own wave below it with the same bucket
+  const int nbits = 32 - __builtin_clz((unsigned)E);  // bucket ids 0..E
+  auto pass = [&](int base, int e) {
     for (int i = tid; i < PLAN_WAVES * EB; i += PLAN_THREADS) wh[i / EB][i % EB] = 0;
     __syncthreads();
     const int r = base + tid;
-    int e = -1;
-    if (r < R) {
-      e = rhs[r];
-      if (e < 0 || e >= E) e = E;
+    uint64_t peers = __ballot(e >= 0);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
     }
-    int rank = 0;
-    for (int l = 0; l < 64; ++l) {
-      const int el = __shfl(e, l, 64);
-      if (l < lane && el == e) ++rank;
-    }
+    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
     if (e >= 0) atomicAdd(&wh[wv][e], 1);
     __syncthreads();
     for (int q = tid; q < EB; q += PLAN_THREADS) {
@@ -123,6 +144,23 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs,
       inverse[r] = pos;
     }
     __syncthreads();
+  };
+  if (held) {
+#pragma unroll
+    for (int i = 0; i < PLAN_PER; ++i) {
+      if (i * PLAN_THREADS >= R) break;
+      pass(i * PLAN_THREADS, ev[i]);
+    }
+  } else {
+    for (int base = 0; base < R; base += PLAN_THREADS) {
+      const int r = base + tid;
+      int e = -1;
+      if (r < R) {
+        e = rhs[r];
+        if (e < 0 || e >= E) e = E;
+      }
+      pass(base, e);
+    }
   }
 }
 

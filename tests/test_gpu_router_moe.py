@@ -71,10 +71,16 @@ def test_router_fewer_resident_than_k(dev):
     np.testing.assert_allclose(wg, w, rtol=2e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("R,E,tile", [(6, 384, 64), (384, 384, 4), (12288, 384, 64), (1000, 7, 16), (0, 5, 8)])
-def test_route_plan_exact(dev, R, E, tile):
+@pytest.mark.parametrize("R,E,tile,skew", [(6, 384, 64, False), (384, 384, 4, False), (12288, 384, 64, False),
+                                           (1000, 7, 16, False), (0, 5, 8, False), (16384, 384, 64, False),
+                                           (20000, 384, 64, False), (5000, 1024, 32, False), (1025, 1, 4, False),
+                                           (12288, 384, 64, True)])
+def test_route_plan_exact(dev, R, E, tile, skew):
+    # R <= 16384 keeps the routes in registers, beyond that they are re-read per pass
     rng = np.random.default_rng(R + E)
     rhs = rng.integers(0, E, size=R).astype(np.int32)
+    if skew:  # a few hot experts: long same-expert runs inside each wave
+        rhs = ((rng.zipf(1.3, size=R) - 1) % E).astype(np.int32)
     order, inv, counts, offsets, te, to, tc, nt = keep_amd.route_plan(_t(rhs, dev), E, tile)
     o_order, o_inv, o_counts, o_offsets, o_te, o_to, o_tc = ops.route_plan(rhs, E, tile)
     np.testing.assert_array_equal(order.cpu().numpy(), o_order)
