@@ -32,6 +32,7 @@ import json
 import os
 import struct
 import zipfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 import numpy as np
@@ -333,6 +334,7 @@ class ExpertInstaller:
         self.layer, self.pools = layer, pools
         self.device = torch.device(device)
         self.stream = torch.cuda.Stream(device=self.device)
+        self._pool = ThreadPoolExecutor(max_workers=8, thread_name_prefix="keep-install")
         self._held: list[tuple[torch.cuda.Event, list]] = []
         for proj, (codes, scales) in pools.items():
             for name, dst in ((f"{proj}_codes", codes), (f"{proj}_scales", scales)):
@@ -341,20 +343,28 @@ class ExpertInstaller:
                     raise ValueError(f"pool for {name} must be [S, {', '.join(map(str, shape[1:]))}] "
                                      f"of {dtype.itemsize}-byte elements, found {tuple(dst.shape)}")
 
+    CHUNK = 1 << 20  # bytes per positional read; the pieces of one expert are read in parallel
+
     def submit(self, expert: int, slot: int) -> torch.cuda.Event:
-        staged = []
+        staged, reads = [], []
+        for proj, (codes, scales) in self.pools.items():
+            for name, dst in ((f"{proj}_codes", codes), (f"{proj}_scales", scales)):
+                if not 0 <= slot < dst.shape[0]:
+                    raise IndexError(f"slot {slot} out of range for a pool of {dst.shape[0]}")
+                off, size = self.layer.slab(name, int(expert))
+                host = torch.empty(dst.shape[1:], dtype=dst.dtype, pin_memory=True)
+                raw = host.numpy().reshape(-1).view(np.uint8)
+                for c in range(0, size, self.CHUNK):
+                    reads.append(self._pool.submit(_pread_into, self.layer.fd, off + c, raw[c:c + self.CHUNK]))
+                staged.append((dst, host))
+        for r in reads:
+            r.result()
         with torch.cuda.stream(self.stream):
-            for proj, (codes, scales) in self.pools.items():
-                for name, dst in ((f"{proj}_codes", codes), (f"{proj}_scales", scales)):
-                    if not 0 <= slot < dst.shape[0]:
-                        raise IndexError(f"slot {slot} out of range for a pool of {dst.shape[0]}")
-                    _, shape, dtype = self.layer.info(name)
-                    host = torch.empty(dst.shape[1:], dtype=dst.dtype, pin_memory=True)
-                    self.layer.read(name, [expert], host.numpy().view(dtype)[None])
-                    dst[slot].copy_(host, non_blocking=True)
-                    staged.append(host)
+            for dst, host in staged:
+                dst[slot].copy_(host, non_blocking=True)
             ev = torch.cuda.Event()
             ev.record(self.stream)
+        staged = [host for _, host in staged]
         self._held.append((ev, staged))
         return ev
 
