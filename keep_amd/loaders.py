@@ -95,7 +95,7 @@ class _Members:
         self.fd = os.open(path, os.O_RDONLY)
 
     def close(self) -> None:
-        if self.fd >= 0:
+        if getattr(self, "fd", -1) >= 0:  # a constructor that raised early opened nothing
             os.close(self.fd)
             self.fd = -1
 
