@@ -10,8 +10,11 @@ sets), so the 2.42 GB resident code pool streams from HBM, not from the
 replayed; inputs are resident in HBM before the timed region. The same layer
 as three launches (router, gate/up, down) is timed alongside for reference.
 
-``value`` = code-stream bytes of one layer (37,847,040 B: 18 projections of
-2048 x 512 uint16 codes plus fp16 row scales) / time per layer, in GB/s.
+``value`` = code-stream bytes of one layer (37,748,736 B: 18 projections of
+2048 x 512 uint16 codes; 37,847,040 B with the fp16 row scales, reported as
+``layer_bytes_with_scales``) / time per layer, in GB/s, over exactly K timed
+steps; 32 more replays of the 64-step graph are each timed on their own,
+and the median and minimum per layer over those samples are reported beside it.
 ``roofline`` covers the layer's two launches (``k_moeq_route_gateup`` then
 ``k_moeq_down``) as one unit, timed with HIP events on the stream they are
 launched on. ``cpu_baseline`` times the C/OpenMP restatement
@@ -45,9 +48,15 @@ import time
 import numpy as np
 
 HBM_PEAK_GBPS = 8000.0
+# the arithmetic of every int8 matrix-core path: decoded E8P weights x 4 are exact int8; activations are split
+# exactly into int8 terms under a power-of-two scale (residual below the fp32 rounding of the sums)
+DTYPE_Q8 = ("fp16 activations x E8P-2bit (uint16) codes on the int8 matrix cores: x as 3 int8 terms per "
+            "256-wide slice (residual < 2^-21 of the slice max), SwiGLU output h in bf16 as 2 int8 terms "
+            "(residual < 2^-14), exact int32 MFMA sums, fp32 scaling, SwiGLU and route combine")
 E, H, I, K_TOP = 384, 4096, 2048, 6
 GRAPH_STEPS = 64
 N_SETS = 64
+N_SAMPLES = 32  # timed graph replays behind the median / min
 
 
 def log(*a):
@@ -202,6 +211,18 @@ def main() -> int:
         torch.cuda.synchronize()
         return t0.elapsed_time(t1)  # ms
 
+    def timed_samples(graphs):
+        """Total ms over the graphs, and ms of each replay (events between replays on the launch stream)."""
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(graphs) + 1)]
+        with torch.cuda.stream(stream):
+            ev[0].record(stream)
+            for i, g in enumerate(graphs):
+                g.replay()
+                ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[-1]), [ev[i].elapsed_time(ev[i + 1]) for i in range(len(graphs))]
+
     # capture graphs inside the torch stream context so our raw calls use the capture stream
     with torch.cuda.stream(stream):
         full = capture(layer1, GRAPH_STEPS)
@@ -221,10 +242,13 @@ def main() -> int:
     graphs = [full] * n_full + ([tail] if tail is not None else [])
     ms = timed_replay(graphs)
     ms_per_step = ms / args.steps
+    # beside the K timed steps: N_SAMPLES replays of the 64-step graph, each timed on its own
+    _, per_graph = timed_samples([full] * N_SAMPLES)
+    samples_us = sorted(t * 1e3 / GRAPH_STEPS for t in per_graph)
 
     layer_bytes = K_TOP * (2 * projection_bytes(I, H) + projection_bytes(H, I))
     code_bytes = K_TOP * 3 * I * (H // 8) * 2
-    value = layer_bytes / (ms_per_step * 1e-3) / 1e9
+    value = code_bytes / (ms_per_step * 1e-3) / 1e9
 
     # per-kernel averages (HIP events over graph replays on the launch stream)
     reps = max(2, min(16, args.steps // GRAPH_STEPS))
@@ -251,7 +275,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 activations x E8P-2bit (uint16) codes, fp32 accumulate",
+        "dtype": DTYPE_Q8,
         "data": "synthetic: uniform uint16 codes, fp16 log-normal(0,0.3) row scales, RHT'd N(0,1) fp16 "
                 "activations, N(0,1) router logits (64 routing sets)",
         "config": {"workload": "config 2: routed decode MoE layer, batch 1, 384 experts, hidden 4096, "
@@ -261,13 +285,18 @@ def main() -> int:
         "pct_of_8TBps": round(100.0 * value / HBM_PEAK_GBPS, 2),
         "us_per_layer": round(ms_per_step * 1e3, 3),
         "tok_per_s": round(1.0 / (ms_per_step * 1e-3), 1),
-        "layer_bytes": layer_bytes,
         "layer_code_bytes": code_bytes,
+        "layer_bytes_with_scales": layer_bytes,
+        "gbps_with_scales": round(layer_bytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "samples": {"n": len(samples_us), "steps_each": GRAPH_STEPS,
+                    "median_us_per_layer": round(float(np.median(samples_us)), 3) if samples_us else None,
+                    "min_us_per_layer": round(samples_us[0], 3) if samples_us else None,
+                    "max_us_per_layer": round(samples_us[-1], 3) if samples_us else None},
         "kernels_us": {"moe_layer (route_gateup + down)": round(layer_us, 3), "split_path_total": round(split_us, 3),
                        "router": round(rt_us, 3), "moe_gateup": round(gu_us, 3), "moe_down": round(dn_us, 3)},
         "roofline": {"bound": "hbm", "kernel": " + ".join(LAYER_KERNELS), "achieved": round(value, 2),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(value / HBM_PEAK_GBPS, 4),
-                     "bytes_per_launch": layer_bytes, "us_per_launch": round(layer_us, 3),
+                     "bytes_per_launch": code_bytes, "us_per_launch": round(layer_us, 3),
                      "traffic": measured_traffic(LAYER_KERNELS),
                      "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
                                        "profiles/moe_layer_config2_counters.md"},
@@ -358,8 +387,7 @@ def cpu_baseline(torch, gate, up, down, x, idx, w, table, seconds):
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import cpu
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(int(threads), 16))
+    nproc, threads = host_threads()
     tab = table.cpu().numpy().view(np.uint32)
     xs = x.float().cpu().numpy()
     sets = []
@@ -368,21 +396,39 @@ def cpu_baseline(torch, gate, up, down, x, idx, w, table, seconds):
         pick = lambda p: (p.codes[ids].cpu().numpy().view(np.uint16), p.scales[ids].float().cpu().numpy())  # noqa
         sets.append((pick(gate), pick(up), pick(down), np.arange(K_TOP, dtype=np.int32)[None, :],
                      w[i].cpu().numpy()))
-    cpu.moe_decode(xs, sets[0][3], sets[0][4], *sets[0][:3], tab, threads=threads)  # warm (LUT build)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        s = sets[n % len(sets)]
-        cpu.moe_decode(xs, s[3], s[4], s[0], s[1], s[2], tab, threads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 2000:
-            break
-    per = el / n
-    layer_bytes = K_TOP * (2 * projection_bytes(I, H) + projection_bytes(H, I))
-    return {"value": round(layer_bytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_layer": round(per * 1e6, 1), "tok_per_s": round(1.0 / per, 2),
-            "sample": f"{n} config-2 decode layers (4 routings of 6 experts, full 4096/2048 shapes) in {el:.1f} s "
-                      f"with oracle/cpu_ref.c (LUT decode, fp32 accumulate, OpenMP {threads} threads)"}
+    code_bytes = K_TOP * 3 * I * (H // 8) * 2
+    res = {}
+    for th, budget in ((threads, seconds), (1, seconds)):
+        cpu.moe_decode(xs, sets[0][3], sets[0][4], *sets[0][:3], tab, threads=th)  # warm (LUT build)
+        times = []
+        t0 = time.perf_counter()
+        while True:
+            s = sets[len(times) % len(sets)]
+            a = time.perf_counter()
+            cpu.moe_decode(xs, s[3], s[4], s[0], s[1], s[2], tab, threads=th)
+            times.append(time.perf_counter() - a)
+            el = time.perf_counter() - t0
+            if (el >= budget and len(times) >= 20) or len(times) >= 4000 or el >= 3 * budget:
+                break
+        res[th] = (float(np.median(times)), float(np.min(times)), len(times), el)
+    med, mn, n, el = res[threads]
+    med1, mn1, n1, el1 = res[1]
+    return {"value": round(code_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "nproc": nproc,
+            "kind": "port", "us_per_layer_median": round(med * 1e6, 1), "us_per_layer_min": round(mn * 1e6, 1),
+            "tok_per_s": round(1.0 / med, 2),
+            "one_thread": {"us_per_layer_median": round(med1 * 1e6, 1), "us_per_layer_min": round(mn1 * 1e6, 1),
+                           "GB/s": round(code_bytes / med1 / 1e9, 3), "samples": n1},
+            "sample": f"config-2 decode layers (4 routings of 6 experts, full 4096/2048 shapes) with "
+                      f"oracle/cpu_ref.c (LUT decode, fp32 accumulate): {n} layers in {el:.1f} s on {threads} "
+                      f"OpenMP threads (host nproc {nproc}, capped at the box's 16-core share), then {n1} layers "
+                      f"in {el1:.1f} s on 1 thread; median per layer, GB/s of the code stream"}
+
+
+def host_threads():
+    """(nproc, threads used): the host's usable cores, capped at the GPU box's 16-core CPU share."""
+
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return int(nproc), max(1, min(int(nproc), 16))
 
 
 def _timed_graph(torch, stream, fn, n_sets, reps, warm=1):
@@ -547,8 +593,9 @@ def other_config(args) -> int:
                   {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I,
                    "distinct_experts": distinct, "hbm_gbps_distinct": round(gbps, 1),
                    "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2)},
-                  "fp16 activations x E8P-2bit codes on the int8 matrix cores (exact int8 terms), fp32 accumulate",
-                  roofline={"bound": "mfma", "kernel": "k_vq_grouped_gemm (x3)", "achieved": round(tf, 2),
+                  DTYPE_Q8,
+                  roofline={"bound": "mfma", "kernel": "k_gemm_q8 (gate/up + SwiGLU, then down) with k_q8_rows, "
+                                                       "k_route_plan, k_route_combine", "achieved": round(tf, 2),
                             "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4),
                             "flops_per_layer": flops, "us_per_layer": round(us, 1), "traffic": None})
             continue
@@ -586,7 +633,7 @@ def other_config(args) -> int:
                **extra,
                "tok_per_s": round(T / (us * 1e-6), 1), "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2),
                "tflops": round(T * k * flops_per_route / (us * 1e-6) / 1e12, 2)},
-              "fp16 activations x E8P-2bit codes, fp32 accumulate",
+              DTYPE_Q8,
               roofline={"bound": "hbm", "kernel": "layer", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                         "bytes_per_layer": int(layer_b), "us_per_layer": round(us, 2), "traffic": None})
@@ -601,8 +648,7 @@ def _cpu_projection(torch, p, x, table, seconds):
     from oracle import cpu
     from oracle import ops as oops
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(int(threads), 16))
+    nproc, threads = host_threads()
     tab = table.cpu().numpy().view(np.uint32)
     xs = x.float().cpu().numpy()
     codes = [p.codes[i:i + 1].cpu().numpy().view(np.uint16) for i in range(4)]
@@ -629,7 +675,7 @@ def _cpu_projection(torch, p, x, table, seconds):
     npy = el / n
     b = 2048 * 512 * 2 + 2048 * 2
     per, n_all, el_all = res[threads]
-    return {"value": round(b / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(b / per / 1e9, 3), "unit": "GB/s", "cores": threads, "nproc": nproc, "kind": "port",
             "us_per_projection": round(per * 1e6, 1),
             "one_thread": {"us_per_projection": round(res[1][0] * 1e6, 1), "GB/s": round(b / res[1][0] / 1e9, 3)},
             "numpy_dense_decode_oracle": {"us_per_projection": round(npy * 1e6, 1),

@@ -141,11 +141,13 @@ int keep_vq_grouped_gemm(const void* x, int x_dtype, int64_t x_rows, const int32
  * then bf16), 16384 entries of four packed values each, addressed by
  * (parity, abs index, 4 sign bits) so one decode is two lookups with the
  * signs, parity and +-1/4 shift already applied (src/keep/vq/e8.py:203-234);
- * at offset 256 KiB, the 4 KiB fp8 table (512 entries of 8 bytes, one per
- * parity and abs index) the layer kernels decode straight into e4m3 MFMA
- * operands, followed by a 256-byte word that is nonzero when the grid holds a
- * value that table cannot express (the layer then writes NaN).
- * `prepared` must hold keep_e8p_prepared_bytes() bytes. No reference
+ * at offset 256 KiB, the 4 KiB int8 T / M tables (T[idx]: the 8 bytes 4 x the
+ * unsigned even-parity codeword; M[signs]: its sign and parity mask, so a
+ * codeword's int8 weights x 4 are T[idx] ^ M[signs]), then a 256-byte word
+ * that is nonzero when the grid holds a value those tables cannot express
+ * (the int8 kernels then write NaN), then the 64 KiB LDS image of T and M
+ * (256 rows of sixteen copies) that the int8 kernels stage per block:
+ * 332,032 bytes in all. `prepared` must hold keep_e8p_prepared_bytes() bytes. No reference
  * counterpart: it replaces the per-threadgroup half2 pair decode of
  * src/ramp/kernels/e8p_m1.metal:36-45 at a larger scale. */
 int keep_e8p_prepare(const uint32_t* table, void* prepared, void* stream);

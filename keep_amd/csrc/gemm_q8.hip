@@ -15,10 +15,10 @@
 //    terms for fp16 / fp32 rows (residual at most 2^-20 of the row's max, as
 //    the decode layer's activations): gate/up outputs are rounded to bf16 in
 //    h, and two terms (2^-13) flip that rounding often enough to cost ~1e-3
-//    at the layer output. Two for bf16 rows (h of the down projection): a
-//    third changed the layer's error by < 1e-4, while the bf16 rounding of h
-//    itself sets the noise floor, and it costs the down GEMM half again as
-//    many MFMAs. k_q8_rows writes the terms once per row ([row][term][K],
+//    at the layer output. Three for bf16 rows (h of the down projection)
+//    too: h is heavy tailed and two terms under the row's scale left 5.8e-3
+//    of the output rms at single outputs of the 2048-token layer.
+//    k_q8_rows writes the terms once per row ([row][term][K],
 //    each codeword's 8 values in packed-nibble order), so the A bytes of lane
 //    (m, h) at k-step s are row m's bytes 64h + 16s .. + 15 of the K block of
 //    each term: the same k as B.
@@ -208,6 +208,7 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
     const int cnt = min(cnt_raw, GQ_M);
     if (cnt_raw <= 0 || off < 0 || off + cnt > a.routes) continue;  // nothing can be written safely
     const int64_t e = a.te[tile];
+    if (RES && e < 0) continue;  // routes off the residual tier (row -1): nothing to add
     const bool bad = e < 0 || e >= a.E || cnt_raw > GQ_M;  // rows written as NaN
     const bool two = cnt > 32;
 
@@ -233,6 +234,10 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
     xs = a.lhs ? (int64_t)a.lhs[xs] : xs;
     if (xs < 0 || xs >= a.x_rows) xs = 0;
     const uint8_t* ap = a.xt + xs * NTERM * a.K + 16 * sp;
+    // every wave has left the previous item's epilogue, which reads s_inv and
+    // s_orow after the run loop's last barrier (block-uniform: every skip
+    // above is taken by the whole block)
+    __syncthreads();
     if (tid < GQ_M) {
       const int64_t pos = off + min(tid, cnt - 1);
       const int64_t xr = a.lhs ? (int64_t)a.lhs[pos] : pos;
@@ -417,7 +422,12 @@ __global__ __launch_bounds__(256) void k_route_combine(const float* y, const flo
 
 // ------------------------------------------------------------------ host side
 
-int gq_nterm(int x_dtype) { return x_dtype == KEEP_BF16 ? 2 : 3; }
+// Three terms for every row dtype. Two terms for bf16 rows (h of the down
+// projection) leave a residual of 2^-13 of the row's maximum; h is heavy
+// tailed (a row's maximum is ~12x its rms at config 4), and that residual
+// measured 5.8e-3 of the output rms at single outputs of a 2048-token layer,
+// where three terms leave 2^-20.
+int gq_nterm(int) { return 3; }
 int64_t gq_ws_terms(int64_t rows, int64_t K) { return (rows * 3 * K + 255) / 256 * 256; }
 int64_t gq_ws_bytes(int64_t rows, int64_t K) { return gq_ws_terms(rows, K) + (rows * 4 + 255) / 256 * 256; }
 
@@ -428,7 +438,7 @@ void gq_rows(const void* x, int x_dtype, int64_t rows, int64_t K, uint8_t* ws, h
   if (x_dtype == KEEP_F16)
     hipLaunchKernelGGL((k_q8_rows<_Float16, 3>), grid, dim3(256), 0, s, (const _Float16*)x, rows, (int)K, terms, inv);
   else if (x_dtype == KEEP_BF16)
-    hipLaunchKernelGGL((k_q8_rows<bf16s, 2>), grid, dim3(256), 0, s, (const bf16s*)x, rows, (int)K, terms, inv);
+    hipLaunchKernelGGL((k_q8_rows<bf16s, 3>), grid, dim3(256), 0, s, (const bf16s*)x, rows, (int)K, terms, inv);
   else
     hipLaunchKernelGGL((k_q8_rows<float, 3>), grid, dim3(256), 0, s, (const float*)x, rows, (int)K, terms, inv);
 }
@@ -453,16 +463,10 @@ void gq_launch(GQArgs& a, bool gateup, int nterm, hipStream_t s, bool res = fals
   if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   const int64_t per = std::max<int64_t>(1, std::min<int64_t>(a.per_xcd, cus / GQ_XCDS));
   const dim3 grid((unsigned)(per * GQ_XCDS));
-  if (res) {
-    if (nterm == 3) gq_launch_res<3>(a, grid, s);
-    else gq_launch_res<2>(a, grid, s);
-  } else if (gateup) {
-    if (nterm == 3) gq_launch_t<true, 3>(a, grid, s);
-    else gq_launch_t<true, 2>(a, grid, s);
-  } else {
-    if (nterm == 3) gq_launch_t<false, 3>(a, grid, s);
-    else gq_launch_t<false, 2>(a, grid, s);
-  }
+  (void)nterm;  // always 3 (gq_nterm)
+  if (res) gq_launch_res<3>(a, grid, s);
+  else if (gateup) gq_launch_t<true, 3>(a, grid, s);
+  else gq_launch_t<false, 3>(a, grid, s);
 }
 
 bool gq_shape_ok(int64_t K, int64_t group_size) {

@@ -1,7 +1,11 @@
 // Device route plan: stable counting sort of routes by expert plus tile
 // descriptors, in one workgroup of 1024 threads (no host sync, no device
 // allocation). Routes with an expert outside [0, E) sort after every valid
-// route and belong to no tile.
+// route; their tiles follow the valid ones with tile_expert -1, so a GEMM
+// over every descriptor writes their rows (as NaN) instead of leaving them
+// unset. n_tiles_out counts the valid tiles only. With B <= E + 1 non-empty
+// buckets the descriptors fit in ceil(R / tile) + E entries, since
+// ceil(a / t) + ceil(b / t) <= ceil((a + b) / t) + 1.
 //
 // Stability: routes are taken in chunks of 1024 in route order. Inside a
 // chunk, a route's rank among same-expert routes is (routes of its expert in
@@ -106,10 +110,15 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs,
       }
     }
   }
-  for (int ti = tbase[E] + tid; ti < max_tiles; ti += PLAN_THREADS) {
-    te[ti] = 0;
-    to[ti] = 0;
-    tc[ti] = 0;
+  {
+    const int nbad = (cnt[E] + tile - 1) / tile;  // the invalid routes' tiles, expert -1
+    for (int ti = tbase[E] + tid; ti < max_tiles; ti += PLAN_THREADS) {
+      const int i = ti - tbase[E];
+      const bool b = i < nbad;
+      te[ti] = b ? -1 : 0;
+      to[ti] = b ? run[E] + i * tile : 0;
+      tc[ti] = b ? min(tile, cnt[E] - i * tile) : 0;
+    }
   }
   // stable scatter, PLAN_THREADS routes per pass: a route's position is its
   // bucket's running offset + the routes of that bucket in earlier waves of

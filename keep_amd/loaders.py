@@ -317,14 +317,23 @@ def load_switch_linear_safetensors(path, prefix: str, *, device):
                                    group_size=g, code_bits=bits)
 
 
+# torch dtypes that hold a file array's bits unchanged (codes are copied as
+# raw bits; the scales keep their floating-point type)
+_POOL_DTYPES = {"u2": (torch.int16, torch.uint16), "i2": (torch.int16, torch.uint16),
+                "u1": (torch.uint8, torch.int8), "i1": (torch.uint8, torch.int8),
+                "f2": (torch.float16,), "f4": (torch.float32,)}
+
+
 class ExpertInstaller:
     """Installs experts from a ``LayerFile`` into slot rows of device pools.
 
     ``pools`` maps a projection (``w1`` / ``w3`` / ``w2``) to its device
     ``(codes [S, N, K/8], scales [S, N, K/g])`` slot arrays. ``submit`` reads
     the expert's six slabs into pinned memory and queues their copies on the
-    installer's own stream (default priority); it returns the event that
-    completes with the copies. Only once ``ready(event)`` holds may the caller
+    installer's own stream (default priority), after the work already queued
+    on the caller's current stream; it returns the event that completes with
+    the copies. Pool dtypes must hold the file's bits unchanged (uint16 /
+    int16 codes for uint16 files, float16 scales for float16 ones). Only once ``ready(event)`` holds may the caller
     route the expert (clear its router bias), and a slot may only be
     overwritten once no call that can still route to it is in flight, as the
     reference's cooling rule requires (``omlx_routed.py:218-236``).
@@ -339,9 +348,13 @@ class ExpertInstaller:
         for proj, (codes, scales) in pools.items():
             for name, dst in ((f"{proj}_codes", codes), (f"{proj}_scales", scales)):
                 _, shape, dtype = layer.info(name)
-                if tuple(dst.shape[1:]) != tuple(shape[1:]) or dst.element_size() != dtype.itemsize:
-                    raise ValueError(f"pool for {name} must be [S, {', '.join(map(str, shape[1:]))}] "
-                                     f"of {dtype.itemsize}-byte elements, found {tuple(dst.shape)}")
+                if tuple(dst.shape[1:]) != tuple(shape[1:]):
+                    raise ValueError(f"pool for {name} must be [S, {', '.join(map(str, shape[1:]))}], "
+                                     f"found {tuple(dst.shape)}")
+                ok = _POOL_DTYPES.get(np.dtype(dtype).str.lstrip("<>|="), ())
+                if dst.dtype not in ok:
+                    raise ValueError(f"pool for {name} must hold the file's {np.dtype(dtype).name} bits "
+                                     f"({' or '.join(str(d) for d in ok) or 'no torch dtype'}), found {dst.dtype}")
 
     CHUNK = 1 << 20  # bytes per positional read; the pieces of one expert are read in parallel
 
@@ -359,6 +372,8 @@ class ExpertInstaller:
                 staged.append((dst, host))
         for r in reads:
             r.result()
+        # pool writes already queued on the caller's stream land before the install copies
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(self.stream):
             for dst, host in staged:
                 dst[slot].copy_(host, non_blocking=True)

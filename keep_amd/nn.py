@@ -88,6 +88,9 @@ class QuantizedVQSwitchLinear:
         self.codebook = ops._codebook_tensor(codebook, code_bits, device)
         self.bias = None if bias is None else ops._to_dev(bias, device)
         self.rht_signs = None if rht_signs is None else ops._to_dev(rht_signs, device, torch.float32)
+        if self.rht_signs is not None:
+            from keep_amd.rht import check_signs
+            check_signs(self.rht_signs)
 
     def effective_scales(self) -> torch.Tensor:
         return self.scales
@@ -96,7 +99,7 @@ class QuantizedVQSwitchLinear:
         if self.rht_signs is None:
             return x
         from keep_amd.rht import apply_rht
-        return apply_rht(x, self.rht_signs)
+        return apply_rht(x, self.rht_signs, validate_signs=False)  # checked once, at construction
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor, *, sorted_indices: bool = False) -> torch.Tensor:
         x = self._rht(x)

@@ -35,6 +35,12 @@ def load():
                                           c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
                                           c_int64, c_void_p, c_float, c_int, c_void_p, c_int]
         lib.oracle_moe_decode.restype = None
+        lib.oracle_moe_decode_nested.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                                 c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                                                 c_int64, c_void_p, c_float, c_int, c_void_p, c_void_p, c_void_p,
+                                                 c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
+                                                 c_void_p, c_int]
+        lib.oracle_moe_decode_nested.restype = None
         lib.oracle_max_threads.restype = c_int
         _lib = lib
     return _lib
@@ -84,4 +90,33 @@ def moe_decode(x, idx, w, gate, up, down, table, *, limit=0.0, h_bf16=True, thre
     load().oracle_moe_decode(_p(x), T, H, I, _p(idx), _p(w), k, _p(gc), _p(gs), _p(uc), _p(us), _p(dc), _p(ds),
                              H // gs.shape[-1], I // ds.shape[-1], _p(t), float(limit), int(bool(h_bf16)), _p(out),
                              int(threads))
+    return out
+
+
+def moe_decode_nested(x, idx, w, gate, up, down, table, hot_of_slot, residual, table8, *, limit=0.0, h_bf16=True,
+                      threads=0) -> np.ndarray:
+    """``moe_decode`` with the nested tier: ``hot_of_slot[e]`` is expert e's row in
+    ``residual[name] = (uint8 codes [nhot, N, K/8], scales [nhot, N, G])`` or
+    ``0xFFFFFFFF`` (none); ``table8`` is the packed 8-bit E8 table."""
+
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    (gc, gs), (uc, us), (dc, ds) = [(np.ascontiguousarray(c, dtype=np.uint16), np.ascontiguousarray(s, np.float32))
+                                    for c, s in (gate, up, down)]
+    (rgc, rgs), (ruc, rus), (rdc, rds) = [(np.ascontiguousarray(residual[n][0], dtype=np.uint8),
+                                           np.ascontiguousarray(residual[n][1], dtype=np.float32))
+                                          for n in ("gate", "up", "down")]
+    hot = np.asarray(hot_of_slot, dtype=np.uint32).astype(np.int64)
+    hot = np.ascontiguousarray(np.where(hot == 0xFFFFFFFF, -1, hot), dtype=np.int32)
+    t = np.ascontiguousarray(table, dtype=np.uint32)
+    t8 = np.ascontiguousarray(table8, dtype=np.uint32)
+    T, H = x.shape
+    k = idx.shape[1]
+    I = gc.shape[1]
+    out = np.empty((T, H), dtype=np.float32)
+    load().oracle_moe_decode_nested(_p(x), T, H, I, _p(idx), _p(w), k, _p(gc), _p(gs), _p(uc), _p(us), _p(dc),
+                                    _p(ds), H // gs.shape[-1], I // ds.shape[-1], _p(t), float(limit),
+                                    int(bool(h_bf16)), _p(hot), _p(rgc), _p(rgs), _p(ruc), _p(rus), _p(rdc), _p(rds),
+                                    H // rgs.shape[-1], I // rds.shape[-1], _p(t8), _p(out), int(threads))
     return out

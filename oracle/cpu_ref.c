@@ -14,7 +14,7 @@
  * src/ramp/models/deepseek_v4_flash_adapter.py:962-967,1776-1784).
  *
  * Pins: oracle_e8p_decode is compared with the numpy oracle over all 65,536
- * codewords (tests/test_oracle_cpu.py), which is itself pinned by the
+ * codewords (tests/test_oracle_ops.py, test_c_oracle_decode_matches_numpy_oracle_everywhere), which is itself pinned by the
  * reference's golden vectors; the mat-vec and MoE layer against the float64
  * dense oracle.
  */
@@ -91,15 +91,50 @@ void oracle_routed_matvec(const float* x, const uint16_t* codes, const float* sc
   }
 }
 
+/* 256 x 8 decoded values of a packed 8-bit E8 table (nibble d = dim d,
+ * value (nibble - 8) / 2; src/keep/vq/e8.py:192-200). */
+static void e8_lut(const uint32_t* table8, float* lut8) {
+  for (int i = 0; i < 256; ++i)
+    for (int d = 0; d < 8; ++d) lut8[i * 8 + d] = (float)((int)((table8[i] >> (4 * d)) & 15u) - 8) * 0.5f;
+}
+
+/* Dot of one 8-bit E8 code row (C codewords, G groups) with x (fp32). */
+static inline float row_dot8(const uint8_t* crow, const float* srow, int64_t C, int64_t cpg, const float* x,
+                             const float* lut8) {
+  float total = 0.f;
+  for (int64_t g0 = 0; g0 < C; g0 += cpg) {
+    float acc = 0.f;
+    for (int64_t c = g0; c < g0 + cpg; ++c) {
+      const float* w = lut8 + (size_t)crow[c] * 8;
+      const float* xv = x + c * 8;
+      acc += w[0] * xv[0] + w[1] * xv[1] + w[2] * xv[2] + w[3] * xv[3] + w[4] * xv[4] + w[5] * xv[5] +
+             w[6] * xv[6] + w[7] * xv[7];
+    }
+    total += acc * srow[g0 / cpg];
+  }
+  return total;
+}
+
 /* Routed SwiGLU MoE for T tokens; x [T, H] fp32, scales fp32, out [T, H].
- * h_bf16 != 0 rounds the SwiGLU output to bf16 before the down projection. */
-void oracle_moe_decode(const float* x, int64_t T, int64_t H, int64_t I, const int32_t* idx, const float* w,
-                       int64_t k, const uint16_t* gc, const float* gs, const uint16_t* uc, const float* us,
-                       const uint16_t* dc, const float* ds, int64_t group_h, int64_t group_i,
-                       const uint32_t* table, float limit, int h_bf16, float* out, int threads) {
+ * h_bf16 != 0 rounds the SwiGLU output to bf16 before the down projection.
+ * With hot != NULL, the nested 3-bit tier: an expert e with hot[e] = r >= 0
+ * adds the 8-bit E8 residual row r of each projection (codes uint8
+ * [nhot, N, K/8], fp32 scales [nhot, N, K/rgroup]) to its E8P base before the
+ * SwiGLU (gate, up) and before the weighted sum (down), as the nested mat-vec
+ * src/ramp/kernels/e8p_nested_m1.metal:99-115 sums base and residual. */
+void oracle_moe_decode_nested(const float* x, int64_t T, int64_t H, int64_t I, const int32_t* idx, const float* w,
+                              int64_t k, const uint16_t* gc, const float* gs, const uint16_t* uc, const float* us,
+                              const uint16_t* dc, const float* ds, int64_t group_h, int64_t group_i,
+                              const uint32_t* table, float limit, int h_bf16, const int32_t* hot,
+                              const uint8_t* rgc, const float* rgs, const uint8_t* ruc, const float* rus,
+                              const uint8_t* rdc, const float* rds, int64_t rgroup_h, int64_t rgroup_i,
+                              const uint32_t* table8, float* out, int threads) {
   const float* lut = get_lut(table);
+  float lut8[256 * 8];
+  if (hot) e8_lut(table8, lut8);
   float* h = (float*)malloc(sizeof(float) * T * k * I);
   const int64_t Ch = H / 8, Ci = I / 8, Gh = H / group_h, Gi = I / group_i;
+  const int64_t RGh = hot ? H / rgroup_h : 1, RGi = hot ? I / rgroup_i : 1;
   if (threads > 0) omp_set_num_threads(threads);
 #pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < T * k * I; ++i) {
@@ -107,6 +142,11 @@ void oracle_moe_decode(const float* x, int64_t T, int64_t H, int64_t I, const in
     const int64_t e = idx[route];
     float g = row_dot(gc + (e * I + n) * Ch, gs + (e * I + n) * Gh, Ch, group_h / 8, x + t * H, lut);
     float u = row_dot(uc + (e * I + n) * Ch, us + (e * I + n) * Gh, Ch, group_h / 8, x + t * H, lut);
+    const int64_t r = hot ? hot[e] : -1;
+    if (r >= 0) {
+      g += row_dot8(rgc + (r * I + n) * Ch, rgs + (r * I + n) * RGh, Ch, rgroup_h / 8, x + t * H, lut8);
+      u += row_dot8(ruc + (r * I + n) * Ch, rus + (r * I + n) * RGh, Ch, rgroup_h / 8, x + t * H, lut8);
+    }
     if (limit > 0.f) {
       g = fminf(g, limit);
       u = fminf(fmaxf(u, -limit), limit);
@@ -127,11 +167,22 @@ void oracle_moe_decode(const float* x, int64_t T, int64_t H, int64_t I, const in
     for (int64_t j = 0; j < k; ++j) {
       const int64_t route = t * k + j;
       const int64_t e = idx[route];
-      acc += w[route] * row_dot(dc + (e * H + n) * Ci, ds + (e * H + n) * Gi, Ci, group_i / 8, h + route * I, lut);
+      float y = row_dot(dc + (e * H + n) * Ci, ds + (e * H + n) * Gi, Ci, group_i / 8, h + route * I, lut);
+      const int64_t r = hot ? hot[e] : -1;
+      if (r >= 0) y += row_dot8(rdc + (r * H + n) * Ci, rds + (r * H + n) * RGi, Ci, rgroup_i / 8, h + route * I, lut8);
+      acc += w[route] * y;
     }
     out[i] = acc;
   }
   free(h);
+}
+
+void oracle_moe_decode(const float* x, int64_t T, int64_t H, int64_t I, const int32_t* idx, const float* w,
+                       int64_t k, const uint16_t* gc, const float* gs, const uint16_t* uc, const float* us,
+                       const uint16_t* dc, const float* ds, int64_t group_h, int64_t group_i,
+                       const uint32_t* table, float limit, int h_bf16, float* out, int threads) {
+  oracle_moe_decode_nested(x, T, H, I, idx, w, k, gc, gs, uc, us, dc, ds, group_h, group_i, table, limit, h_bf16,
+                           NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1, 1, NULL, out, threads);
 }
 
 int oracle_max_threads(void) { return omp_get_max_threads(); }

@@ -248,21 +248,26 @@ def route_plan(rhs, num_experts: int, tile: int):
     Returns ``order`` (stable sort of routes by expert), ``inverse`` (its
     inverse permutation), per-expert ``counts``/``offsets`` into the sorted
     routes and the tile descriptors ``(tile_expert, tile_offset, tile_count)``
-    with at most ``tile`` routes per tile, tiles in expert order.
+    with at most ``tile`` routes per tile, tiles in expert order. Routes whose
+    expert is outside ``[0, num_experts)`` sort after all others and their
+    tiles come last, with expert ``-1``.
     """
 
     rhs = np.asarray(rhs).reshape(-1).astype(np.int64)
-    order = np.argsort(rhs, kind="stable")
+    key = np.where((rhs < 0) | (rhs >= num_experts), num_experts, rhs)  # invalid ids sort last
+    order = np.argsort(key, kind="stable")
     inverse = np.empty_like(order)
     inverse[order] = np.arange(order.shape[0])
-    counts = np.bincount(rhs, minlength=num_experts)
+    allc = np.bincount(key, minlength=num_experts + 1)
+    counts = allc[:num_experts]
     offsets = np.concatenate([[0], np.cumsum(counts)[:-1]])
     te, to, tc = [], [], []
-    for e in range(num_experts):
-        for start in range(0, int(counts[e]), tile):
-            te.append(e)
-            to.append(int(offsets[e]) + start)
-            tc.append(min(tile, int(counts[e]) - start))
+    for e in range(num_experts + 1):  # the invalid routes' tiles last, with expert -1
+        base = int(np.sum(allc[:e]))
+        for start in range(0, int(allc[e]), tile):
+            te.append(e if e < num_experts else -1)
+            to.append(base + start)
+            tc.append(min(tile, int(allc[e]) - start))
     return (order, inverse, counts, offsets,
             np.array(te, dtype=np.int64), np.array(to, dtype=np.int64), np.array(tc, dtype=np.int64))
 

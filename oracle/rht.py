@@ -4,11 +4,11 @@ Restated from the reference's ``src/keep/quant/rht.py:24-66``.
 
 Pins: the FWHT is checked against ``scipy.linalg.hadamard`` (Sylvester order)
 and by round-trip / norm preservation (``tests/test_glm45_air_rht.py:14-28``).
-``deterministic_rht_signs`` is pinned only by its closed form
-(``shake_256(str(seed))``, little-endian bit unpack, 0 -> -1): no golden sign
-vector exists in the reference, so its exact bit stream is "parity unpinned"
-beyond that closed form (the synthetic inputs use their own seeded signs, so
-no hot-path parity claim depends on it).
+``deterministic_rht_signs`` is pinned by the FIPS 202 SHAKE256 known answer for
+the empty message: the digest bytes, and the sign vector of ``seed=""`` derived
+by hand from them (little-endian bit order, 0 -> -1), which a big-endian
+unpack, a swapped sign map or another hash would each fail
+(``tests/test_oracle_ops.py``).
 """
 
 from __future__ import annotations

@@ -1,0 +1,187 @@
+"""GPU parity of the prefill and tiered paths at the BASELINE configurations'
+full shapes, against the C oracle (oracle/cpu_ref.c: LUT decode, fp32 sums,
+h rounded to bf16 as the reference's decode step stores it):
+
+- config 4: 2048 tokens, Zipf(1.1) routing over 384 experts, 4096/2048,
+  top-6 (shared route plan, fused gate/up + SwiGLU grouped GEMM, down
+  scattered to route order, combine), every token checked: the hottest
+  expert's ~10^3 routes span many 64-route tiles and its last tile is
+  partial, the tail experts hold a few routes each;
+- config 5 prefill: 512 tokens, 288 experts, top-8, 4096/1536, half the pool
+  absent (-inf served bias, tau 0.3) and the nested 3-bit tier (8-bit E8
+  residual) on 29 resident experts;
+- config 5 decode through the fused nested layer (keep_moe_layer_nested) at
+  I = 1536.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import keep_amd
+from keep_amd import synth
+from oracle import cpu, e8p, ops
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _check(got, want, tol=TOL):
+    g = got.float().cpu().numpy()
+    err = ops.max_rel_err(g, want)
+    assert err <= tol, f"max rel err {err:.3e}"
+    assert ops.elementwise_ok(g, want, rtol=tol), "elementwise bound violated"
+    return err
+
+
+def _host(p):
+    return p.codes.cpu().numpy().view(np.uint16), p.scales.float().cpu().numpy()
+
+
+def _glu(dev, E, H, I, seeds, hot_tier=None):
+    gate = synth.projection(E, I, H, seed=seeds[0], device=dev)
+    up = synth.projection(E, I, H, seed=seeds[1], device=dev)
+    down = synth.projection(E, H, I, seed=seeds[2], device=dev)
+
+    def lin(p, K, N):
+        return keep_amd.QuantizedVQSwitchLinear(input_dims=K, output_dims=N, num_experts=E, codes=p.codes,
+                                                scales=p.scales, group_size=K, code_bits=16)
+
+    glu = keep_amd.QuantizedVQSwitchGLU(gate_proj=lin(gate, H, I), up_proj=lin(up, H, I),
+                                        down_proj=lin(down, I, H), hot_tier=hot_tier)
+    return glu, (gate, up, down)
+
+
+def _tier(dev, E, H, I, resident, n_hot, seed):
+    rng = np.random.default_rng(seed)
+    hot = rng.choice(np.flatnonzero(resident), n_hot, replace=False)
+    hot_of_slot = np.full(E, keep_amd.ops.NO_RESIDUAL, np.uint32)
+    hot_of_slot[hot] = rng.permutation(n_hot).astype(np.uint32)
+
+    def res(N, K):
+        c = rng.integers(0, 256, (n_hot, N, K // 8), dtype=np.uint8)
+        s = (np.exp(rng.normal(0, 0.3, (n_hot, N, 1))) * 0.1).astype(np.float16)
+        return c, s
+
+    residual = {"gate": res(I, H), "up": res(I, H), "down": res(H, I)}
+    tier = keep_amd.HotTier(hot_of_slot, {n: (torch.from_numpy(c).to(dev), torch.from_numpy(s).to(dev))
+                                          for n, (c, s) in residual.items()})
+    return tier, hot_of_slot, {n: (c, s.astype(np.float32)) for n, (c, s) in residual.items()}
+
+
+def test_config4_prefill_full_shape(dev):
+    """Every token of the layer, in three parts. h is held in bf16 (as the
+    reference's decode step stores it), so where the exact gate/up value sits
+    within a few fp32 ulps of a bf16 rounding boundary the GPU's exact integer
+    sums and the oracle's fp32 sums round h to neighbouring bf16 values (~1e-5
+    of the 25M h values here), and one such flip moves the token's outputs by
+    up to ~1e-2 of their rms. So: (a) h within 2e-3 + one bf16 ulp of the
+    oracle's h, elementwise; (b) down + combine on the GPU's own h within 2e-3
+    of the oracle elementwise; (c) the whole layer within 2e-3 of the oracle
+    normwise (the path's bound), and equal bit for bit to RoutedVQMoE's."""
+    E, H, I, k, T = 384, 4096, 2048, 6, 2048
+    print(f"config 4 prefill: T={T} E={E} H={H} I={I} k={k}", flush=True)
+    glu, (gate, up, down) = _glu(dev, E, H, I, (1, 2, 3))
+    idx_np = synth.zipf_routes(T, E, k, s=1.1, seed=40)
+    counts = np.bincount(idx_np.ravel(), minlength=E)
+    assert counts.max() > 640 and counts.max() % 64 != 0, "want a hot expert spanning many tiles, the last partial"
+    assert (counts[counts > 0] < 8).any(), "want tail experts with a few routes"
+    idx = torch.from_numpy(idx_np).to(dev)
+    w = torch.softmax(torch.from_numpy(np.random.default_rng(41).standard_normal((T, k)).astype(np.float32)),
+                      -1).to(dev)
+    x = synth.rht_activations(T, H, seed=42, device=dev)
+    moe = keep_amd.RoutedVQMoE(glu, top_k=k)
+    with keep_amd.ops.trace_gather_vqmm_calls() as calls:
+        out = moe.experts(x, idx, w)
+    assert out.shape == (T, H) and out.dtype == torch.float32
+    assert not calls, "config 4 must take the shared-plan grouped GEMMs, not per-projection gathers"
+    # the module's kernels one by one: h in sorted order, y scattered to route order, the combine
+    kops = keep_amd.ops
+    R = T * k
+    flat = idx.reshape(-1).to(torch.int32).contiguous()
+    order, inverse, _, _, te, to, tc, _ = kops.route_plan(flat, E, kops.GEMM_ROUTE_TILE)
+    lhs = (torch.arange(R, dtype=torch.int32, device=dev) // k)[order.long()].contiguous()
+    cb = glu.gate_proj.codebook
+    h = kops.grouped_swiglu(x, gate.codes, gate.scales, up.codes, up.scales, cb, (te, to, tc), lhs=lhs, routes=R,
+                            input_dims=H, hidden_dims=I, group_size=H)
+    y = kops.grouped_gemm(h, down.codes, down.scales, cb, (te, to, tc), lhs=None, routes=R, input_dims=I,
+                          output_dims=H, group_size=I, out_dtype=torch.float32, out_index=order)
+    again = kops.route_combine(y.reshape(T, k, H), w)
+    assert torch.equal(again, out), "RoutedVQMoE differs from its own kernels run one by one"
+    torch.cuda.synchronize()
+    tab = e8p.e8p_packed_abs_grid()
+    xf = x.float().cpu().numpy()
+    G, U, D = _host(gate), _host(up), _host(down)
+    # (a) h
+    g_o = cpu.routed_matvec(xf, G[0], G[1], tab, idx_np.reshape(-1), x_div=k, group_size=H).astype(np.float64)
+    u_o = cpu.routed_matvec(xf, U[0], U[1], tab, idx_np.reshape(-1), x_div=k, group_size=H).astype(np.float64)
+    with np.errstate(over="ignore"):
+        h_o = ops.round_bf16(ops.swiglu(g_o, u_o))
+    h_g = h[inverse.long()].float().cpu().numpy()
+    assert ops.elementwise_ok(h_g, h_o, rtol=TOL + 2.0 ** -7), "h beyond one bf16 ulp of the oracle's"
+    flips = int((h_g != h_o).sum())
+    print(f"config 4 prefill: {flips} of {h_o.size} h values one bf16 ulp from the oracle's", flush=True)
+    # (b) down + combine on the GPU's h
+    y_o = cpu.routed_matvec(h_g.astype(np.float32), D[0], D[1], tab, idx_np.reshape(-1),
+                            lhs=np.arange(R, dtype=np.int32), group_size=I).astype(np.float64)
+    _check(y, y_o)
+    want_b = (y_o.reshape(T, k, H) * w.cpu().numpy().astype(np.float64)[..., None]).sum(1)
+    _check(out, want_b)
+    # (c) end to end against the oracle's own h
+    want = cpu.moe_decode(xf, idx_np, w.cpu().numpy(), G, U, D, tab)
+    err = ops.max_rel_err(out.cpu().numpy(), want)
+    assert err <= TOL, f"max rel err {err:.3e}"
+    print(f"config 4 prefill: max rel err {err:.2e} over {T} tokens", flush=True)
+
+
+def test_config5_prefill_with_tier_full_shape(dev):
+    E, H, I, k, T = 288, 4096, 1536, 8, 512
+    print(f"config 5 prefill with tier: T={T} E={E} H={H} I={I} k={k}", flush=True)
+    mask = synth.resident_mask(E, frac=0.5, seed=21)
+    tier, hot_of_slot, residual = _tier(dev, E, H, I, mask, E // 10, seed=23)
+    glu, (gate, up, down) = _glu(dev, E, H, I, (31, 32, 33), hot_tier=tier)
+    bias = keep_amd.resident_bias(torch.from_numpy(mask).to(dev))
+    moe = keep_amd.RoutedVQMoE(glu, top_k=k, bias_served=bias, tau=0.3)
+    x = synth.rht_activations(T, H, seed=34, device=dev)
+    z = synth.router_logits(T, E, seed=35, device=dev)
+    out, r = moe(x, z)
+    idx = r.idx.cpu().numpy()
+    assert set(idx.ravel()) <= set(np.flatnonzero(mask)), "a served expert is absent"
+    on = hot_of_slot[idx] != keep_amd.ops.NO_RESIDUAL
+    assert on.sum() > T and (~on).sum() > T, "want many routes on and off the tier"
+    oi, *_ = ops.router_dual_topk(z.cpu().numpy(), keep_amd.resident_bias(torch.from_numpy(mask)).numpy()
+                                  .astype(np.float64), np.zeros(E), k, tau=0.3)
+    np.testing.assert_array_equal(idx, oi)
+    want = cpu.moe_decode_nested(x.float().cpu().numpy(), idx, r.weight.cpu().numpy(), _host(gate), _host(up),
+                                 _host(down), e8p.e8p_packed_abs_grid(), hot_of_slot, residual, e8p.e8_1bit_packed())
+    err = _check(out, want)
+    print(f"config 5 prefill with tier: max rel err {err:.2e}, {int(on.sum())} hot routes", flush=True)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_config5_fused_nested_decode_full_shape(dev, xdt):
+    E, H, I, k = 288, 4096, 1536, 8
+    print(f"config 5 nested decode layer: E={E} I={I} k={k} x={xdt}", flush=True)
+    mask = synth.resident_mask(E, frac=0.5, seed=21)
+    tier, hot_of_slot, residual = _tier(dev, E, H, I, mask, E // 10, seed=24)
+    glu, (gate, up, down) = _glu(dev, E, H, I, (41, 42, 43), hot_tier=tier)
+    bias = keep_amd.resident_bias(torch.from_numpy(mask).to(dev))
+    moe = keep_amd.RoutedVQMoE(glu, top_k=k, bias_served=bias, tau=0.3)
+    checked_on = 0
+    for seed in range(40):  # logits until the served set holds routes on and off the tier
+        x = synth.rht_activations(1, H, seed=100 + seed, device=dev, dtype=xdt)
+        z = synth.router_logits(1, E, seed=200 + seed, device=dev)
+        assert moe._layer_path(x)
+        out, r = moe(x, z)
+        idx = r.idx.cpu().numpy()
+        on = hot_of_slot[idx] != keep_amd.ops.NO_RESIDUAL
+        if not on.any():
+            continue
+        want = cpu.moe_decode_nested(x.float().cpu().numpy(), idx, r.weight.cpu().numpy(), _host(gate),
+                                     _host(up), _host(down), e8p.e8p_packed_abs_grid(), hot_of_slot, residual,
+                                     e8p.e8_1bit_packed())
+        _check(out, want)
+        checked_on += 1
+        if checked_on == 3:
+            break
+    assert checked_on == 3, "fewer than three routings touched the tier"

@@ -93,7 +93,7 @@ def test_grouped_gemm_q8_nan_row_and_bad_expert(dev):
     x = synth.rht_activations(T, K, seed=43, device=dev)
     x[9, 17] = float("nan")  # token 9's routes are NaN
     flat = _t(rhs.reshape(-1), dev)
-    order, inverse, _, _, te, to, tc, _ = keep_amd.route_plan(flat, 8, 64)  # 8 buckets: expert 7 gets a tile
+    order, inverse, _, _, te, to, tc, _ = keep_amd.route_plan(flat, E, 64)  # expert 7: a tile of expert -1
     lhs = (torch.arange(flat.numel(), device=dev, dtype=torch.int32) // k)[order.long()].contiguous()
     cb = kops._default_codebook(16, dev)
     y = kops.grouped_gemm(x, _t(codes, dev), _t(scales, dev), cb, (te, to, tc), lhs=lhs, routes=flat.numel(),
@@ -137,3 +137,62 @@ def test_grouped_residual_add_vs_oracle(dev, G):
     got = (out - base).cpu().numpy()
     assert (got[rows < 0] == 0).all()
     assert ops.max_rel_err(got, want) <= TOL
+
+
+def test_out_of_range_route_is_nan_through_gather_and_glu(dev):
+    """R >= 128 takes the sorted-route GEMM: a route whose expert is out of
+    range sorts past every valid tile and its row comes back NaN (not
+    unwritten memory), through gather_vqmm and through the shared-plan
+    prefill of QuantizedVQSwitchGLU; every other row matches the oracle."""
+    from keep_amd.nn import QuantizedVQSwitchGLU, QuantizedVQSwitchLinear
+
+    E, H, I, T, k = 6, 256, 256, 48, 4
+    gate, up, down = (synth.projection_np(E, I, H, seed=61), synth.projection_np(E, I, H, seed=62),
+                      synth.projection_np(E, H, I, seed=63))
+    rng = np.random.default_rng(64)
+    rhs = rng.integers(0, E, size=(T, k)).astype(np.int32)
+    rhs[3, 2], rhs[17, 0], rhs[40, 3] = E, -1, E + 9
+    bad = (rhs < 0) | (rhs >= E)
+    x = synth.rht_activations(T, H, seed=65, device=dev)
+    for trial in range(2):  # the output buffer of the second call is recycled memory
+        y = kops.gather_vqmm(x, _t(gate[0], dev), _t(gate[1], dev), None, _t(rhs, dev), input_dims=H,
+                             output_dims=I, group_size=H, code_bits=16)
+        assert y.shape == (T, k, I)
+        yc = y.float().cpu()
+        assert torch.isnan(yc[torch.from_numpy(bad)]).all()
+        assert not torch.isnan(yc[torch.from_numpy(~bad)]).any()
+    want = ops.gather_token(x.float().cpu().numpy(), gate[0], gate[1], np.where(bad, 0, rhs))
+    _check(yc[torch.from_numpy(~bad)], want[~bad])
+
+    def lin(p, K, N):
+        return QuantizedVQSwitchLinear(input_dims=K, output_dims=N, num_experts=E, codes=_t(p[0], dev),
+                                       scales=_t(p[1], dev), group_size=K, code_bits=16)
+
+    glu = QuantizedVQSwitchGLU(gate_proj=lin(gate, H, I), up_proj=lin(up, H, I), down_proj=lin(down, I, H))
+    out = glu(x, _t(rhs, dev)).float().cpu()
+    assert out.shape == (T, k, H)
+    assert torch.isnan(out[torch.from_numpy(bad)]).all()
+    assert not torch.isnan(out[torch.from_numpy(~bad)]).any()
+
+
+def test_grouped_gemm_q8_blocks_run_many_items(dev):
+    """More work items than blocks: at N = 2048 (eight 256-column blocks)
+    and ~100 tiles every persistent block runs two or more non-empty items
+    back to back, so a block's next item must not overwrite the row scales
+    and output rows that its lagging waves still read in the previous
+    item's epilogue. Checked against the C oracle on every route."""
+    from oracle import cpu
+
+    E, N, K, T, k = 40, 2048, 512, 1200, 4
+    codes, scales = synth.projection_np(E, N, K, seed=71)
+    rhs = synth.zipf_routes(T, E, k, s=1.1, seed=72)
+    x = synth.rht_activations(T, K, seed=73, device=dev)
+    flat, order, inverse, counts, tiles, lhs = _plan(rhs, E, k, dev)
+    n_tiles = int((tiles[2] > 0).sum().item())
+    assert n_tiles * (N // 256) > 2 * 256, "fewer work items than two per block"
+    cb = kops._default_codebook(16, dev)
+    y = kops.grouped_gemm(x, _t(codes, dev), _t(scales, dev), cb, tiles, lhs=lhs, routes=flat.numel(),
+                          input_dims=K, output_dims=N, group_size=K, out_dtype=torch.float32, out_index=order)
+    want = cpu.routed_matvec(x.float().cpu().numpy(), codes, scales.astype(np.float32),
+                             kops.e8p_packed_abs_grid(), rhs.reshape(-1), x_div=k, group_size=K)
+    _check(y, want.astype(np.float64))

@@ -111,3 +111,8 @@ def test_expert_installer_fills_slots(dev, tmp_path):
         np.testing.assert_array_equal(scales.cpu().numpy()[2], arrays[f"{proj}_scales"][11])
     with pytest.raises(IndexError):
         inst.submit(1, S)
+    # a pool whose dtype would reinterpret the file's bits is refused
+    bad = dict(pools)
+    bad["w2"] = (pools["w2"][0], pools["w2"][1].to(torch.bfloat16))
+    with pytest.raises(ValueError, match="file's"):
+        loaders.ExpertInstaller(lf, bad, dev)

@@ -30,7 +30,7 @@ def _ref(x32, s, mode):
     return orht.hadamard_f32(x32)
 
 
-@pytest.mark.parametrize("n", [16, 32, 64, 128, 512, 2048, 4096, 8192])
+@pytest.mark.parametrize("n", [16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192])
 @pytest.mark.parametrize("mode", ["fwd", "inv", "plain"])
 def test_rht_f32_bit_exact(dev, n, mode):
     from keep_amd import rht
@@ -89,3 +89,9 @@ def test_rht_edges_and_errors(dev):
             rht.fwht(torch.zeros(1, n, device=dev))
     with pytest.raises(ValueError):
         rht.apply_rht(torch.zeros(1, 64, device=dev), torch.ones(32))
+    bad = torch.ones(64)
+    bad[5] = 0.5  # signs must be -1 or 1, as _validate_signs_np requires
+    with pytest.raises(ValueError, match="-1 or 1"):
+        rht.apply_rht(torch.zeros(1, 64, device=dev), bad)
+    with pytest.raises(ValueError, match="-1 or 1"):
+        rht.apply_inverse_rht(torch.zeros(1, 64, device=dev), bad.to(dev))

@@ -71,28 +71,35 @@ def test_router_fewer_resident_than_k(dev):
     np.testing.assert_allclose(wg, w, rtol=2e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("R,E,tile,skew", [(6, 384, 64, False), (384, 384, 4, False), (12288, 384, 64, False),
-                                           (1000, 7, 16, False), (0, 5, 8, False), (16384, 384, 64, False),
-                                           (20000, 384, 64, False), (5000, 1024, 32, False), (1025, 1, 4, False),
-                                           (12288, 384, 64, True)])
-def test_route_plan_exact(dev, R, E, tile, skew):
-    # R <= 16384 keeps the routes in registers, beyond that they are re-read per pass
+@pytest.mark.parametrize("R,E,tile,skew,bad", [(6, 384, 64, False, 0), (384, 384, 4, False, 0),
+                                                (12288, 384, 64, False, 0), (1000, 7, 16, False, 0),
+                                                (0, 5, 8, False, 0), (16384, 384, 64, False, 0),
+                                                (20000, 384, 64, False, 0), (5000, 1024, 32, False, 0),
+                                                (1025, 1, 4, False, 0), (12288, 384, 64, True, 0),
+                                                (300, 16, 8, False, 21), (20000, 384, 64, False, 130)])
+def test_route_plan_exact(dev, R, E, tile, skew, bad):
+    # R <= 16384 keeps the routes in registers, beyond that they are re-read per pass;
+    # `bad` routes get expert ids outside [0, E): they sort last, in tiles of expert -1
     rng = np.random.default_rng(R + E)
     rhs = rng.integers(0, E, size=R).astype(np.int32)
     if skew:  # a few hot experts: long same-expert runs inside each wave
         rhs = ((rng.zipf(1.3, size=R) - 1) % E).astype(np.int32)
+    if bad:
+        at = rng.choice(R, bad, replace=False)
+        rhs[at] = rng.choice(np.array([-1, -7, E, E + 3], dtype=np.int32), bad)
     order, inv, counts, offsets, te, to, tc, nt = keep_amd.route_plan(_t(rhs, dev), E, tile)
     o_order, o_inv, o_counts, o_offsets, o_te, o_to, o_tc = ops.route_plan(rhs, E, tile)
     np.testing.assert_array_equal(order.cpu().numpy(), o_order)
     np.testing.assert_array_equal(inv.cpu().numpy(), o_inv)
     np.testing.assert_array_equal(counts.cpu().numpy(), o_counts)
     np.testing.assert_array_equal(offsets.cpu().numpy(), o_offsets)
-    n = int(nt.item())
-    assert n == len(o_te)
+    n = len(o_te)
+    assert int(nt.item()) == int((o_te >= 0).sum())  # valid tiles only
     np.testing.assert_array_equal(te.cpu().numpy()[:n], o_te)
     np.testing.assert_array_equal(to.cpu().numpy()[:n], o_to)
     np.testing.assert_array_equal(tc.cpu().numpy()[:n], o_tc)
     assert (tc.cpu().numpy()[n:] == 0).all()
+    assert int((o_te < 0).sum()) == -(-bad // tile)
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])

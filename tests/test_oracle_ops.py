@@ -154,6 +154,13 @@ def test_route_plan_invariants():
     assert tc.sum() == R and tc.max() <= tile and len(te) <= -(-R // tile) + E
     for e_, o, c in zip(te, to, tc):
         assert np.all(rhs[order[o:o + c]] == e_)
+    # ids outside [0, E) sort after every valid route, stably, in tiles of expert -1
+    rhs2 = rhs.copy()
+    rhs2[[3, 9, 40]] = [-2, E, E + 5]
+    order, inv, counts, offsets, te, to, tc = ops.route_plan(rhs2, E, tile)
+    assert order[-3:].tolist() == [3, 9, 40]
+    assert te.tolist()[-1] == -1 and to.tolist()[-1] == R - 3 and tc.tolist()[-1] == 3
+    assert counts.sum() == R - 3 and len(te) <= -(-R // tile) + E
 
 
 def test_fwht_matches_sylvester_hadamard_and_round_trips():
@@ -186,13 +193,37 @@ def test_f32_hadamard_restatement_pins():
     np.testing.assert_array_equal(rht.hadamard_f32(xi).astype(np.float64), xi.astype(np.float64) @ H.T)
 
 
-def test_rht_signs_closed_form():
+# FIPS 202 SHAKE256 known answer for the empty message (the first 16 output
+# bytes of the published test vector).
+SHAKE256_EMPTY = bytes.fromhex("46b9dd2b0ba88d13233b3feb743eeb24")
+# deterministic_rht_signs(16, seed="") derived by hand from that vector:
+# 0x46 = 0100 0110 and 0xb9 = 1011 1001, bits taken least significant first,
+# bit 0 -> -1 and bit 1 -> +1.
+SIGNS_EMPTY_16 = [-1, 1, 1, -1, -1, -1, 1, -1, 1, -1, -1, 1, 1, 1, -1, 1]
+
+
+@pytest.mark.parametrize("mod", ["oracle", "product"])
+def test_rht_signs_known_answer(mod):
     import hashlib
-    raw = hashlib.shake_256(b"13").digest(2)
-    bits = np.unpackbits(np.frombuffer(raw, dtype=np.uint8), bitorder="little")
-    np.testing.assert_array_equal(rht.deterministic_rht_signs(16, seed=13), np.where(bits == 0, -1, 1))
+
+    from keep_amd import rht as krht
+    f = rht.deterministic_rht_signs if mod == "oracle" else krht.deterministic_rht_signs
+    assert hashlib.shake_256(b"").digest(16) == SHAKE256_EMPTY
+    got = f(16, seed="")
+    assert got.dtype == np.int8
+    assert got.tolist() == SIGNS_EMPTY_16
+    # longer streams continue the same digest: the first 16 of 128 signs are the same
+    assert f(128, seed="")[:16].tolist() == SIGNS_EMPTY_16
+    # every later byte of the known answer, least significant bit first
+    long = f(128, seed="").tolist()
+    for i, byte in enumerate(SHAKE256_EMPTY):
+        for b in range(8):
+            assert long[8 * i + b] == (1 if (byte >> b) & 1 else -1)
+    # the seed enters as str(seed) in UTF-8: an int seed equals its decimal string
+    assert f(64, seed=13).tolist() == f(64, seed="13").tolist()
+    assert f(64, seed=13).tolist() != f(64, seed=14).tolist()
     with pytest.raises(ValueError):
-        rht.deterministic_rht_signs(12, seed=0)
+        f(12, seed=0)
 
 
 def test_c_oracle_decode_matches_numpy_oracle_everywhere():
@@ -217,3 +248,36 @@ def test_c_oracle_matvec_and_moe_match_dense():
     got = cpu.moe_decode(x, rhs, w, gate, up, down, t, limit=0.0, h_bf16=True)
     want = ops.moe_layer(x, rhs, w, gate, up, down, limit=0.0, h_round="bfloat16")
     assert ops.max_rel_err(got, want) < 1e-5
+
+
+@pytest.mark.parametrize("rg", [1, 2])
+def test_c_oracle_nested_tier_matches_dense(rg):
+    """The C oracle's nested tier (8-bit E8 residual on the experts listed in
+    hot_of_slot, added before the SwiGLU and before the weighted sum) against
+    the float64 dense oracle, with per-row and grouped residual scales."""
+    t = e8p.e8p_packed_abs_grid()
+    E, H, I, k, nhot = 6, 256, 128, 3, 3
+    gate, up, down = _proj(E, I, H, 2, 20), _proj(E, I, H, 2, 21), _proj(E, H, I, 1, 22)
+    rng = np.random.default_rng(23)
+    hot = np.full(E, ops.NO_RESIDUAL, np.uint32)
+    hot[[1, 4, 5]] = [2, 0, 1]
+
+    def res(N, K):
+        return (rng.integers(0, 256, (nhot, N, K // 8), dtype=np.uint8),
+                (np.exp(rng.normal(0, 0.3, (nhot, N, rg))) * 0.1).astype(np.float16))
+
+    residual = {"gate": res(I, H), "up": res(I, H), "down": res(H, I)}
+    x = rng.standard_normal((3, H)).astype(np.float32)
+    idx = np.array([[1, 0, 4], [5, 2, 3], [0, 2, 3]], dtype=np.int32)  # the last token is all off the tier
+    w = rng.random((3, k)).astype(np.float32)
+    for limit, hb in ((7.0, False), (0.0, True)):
+        got = cpu.moe_decode_nested(x, idx, w, gate, up, down, t, hot, residual, e8p.e8_1bit_packed(),
+                                    limit=limit, h_bf16=hb)
+        want = ops.moe_layer(x, idx, w, gate, up, down, limit=limit, h_round="bfloat16" if hb else None,
+                             hot_of_slot=hot, residual=residual)
+        assert ops.max_rel_err(got, want) < 1e-5
+    # off the tier the nested form is the plain one, bit for bit
+    plain = cpu.moe_decode(x[2:], idx[2:], w[2:], gate, up, down, t, limit=7.0)
+    nested = cpu.moe_decode_nested(x[2:], idx[2:], w[2:], gate, up, down, t, hot, residual, e8p.e8_1bit_packed(),
+                                   limit=7.0)
+    np.testing.assert_array_equal(plain, nested)
