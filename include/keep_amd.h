@@ -216,6 +216,34 @@ int keep_moe_layer(const float* logits, const float* bias_served, const float* b
                    float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
                    uint8_t* admit, void* h_work, void* out, int out_dtype, void* stream);
 
+/* The same layer in ONE launch of 256 blocks (one per compute unit, all
+ * resident together): the router, gate/up/SwiGLU and down + combine, with
+ * the whole code stream (gate/up, then down) requested as soon as a block has
+ * routed the token. SwiGLU outputs pass between blocks through `workspace`
+ * as tagged words: keep_moe_layer1_workspace_bytes(k, I) bytes, 256-byte
+ * aligned, zero-filled before its first use and then handed unchanged to
+ * every call on the same stream (it holds the call counter; calls that
+ * overlap on one workspace race). A wait on another block that outlasts
+ * ~200 us gives up: the affected outputs are NaN and
+ * keep_moe_layer1_status() reports bit 1 (zero the workspace before the next
+ * call). Needs a device of at least 256 compute units. h is split into three
+ * int8 terms per 256-wide slice (two in keep_moe_layer). Serves H = 4096, I
+ * in {512, 1024, 1536, 2048}, k <= 8, E <= 1024, scale groups of
+ * 256-element multiples. Replaces the serving decode step of
+ * scripts/v41_build/omlx_lattice.py:327-371 for batch 1. */
+int64_t keep_moe_layer1_workspace_bytes(int64_t k, int64_t I);
+int keep_moe_layer1_status(const void* workspace, uint32_t* status, void* stream);
+int keep_moe_layer1(const float* logits, const float* bias_served, const float* bias_demand,
+                    int score_func, int renormalize, float route_scale, float tau,
+                    int64_t num_experts, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
+                    const uint16_t* gate_codes, const void* gate_scales,
+                    const uint16_t* up_codes, const void* up_scales,
+                    const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                    int64_t group_size_h, int64_t group_size_i, const void* prepared,
+                    float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                    uint8_t* admit, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
+                    void* stream);
+
 /* keep_moe_layer with the nested 3-bit tier: an expert e with a residual row
  * (hot_of_slot[e] < num_hot; 0xFFFFFFFF = none; any other value makes that
  * route's output NaN) adds R[row] . x to gate, up and down, R the 8-bit E8

@@ -56,6 +56,11 @@ _SIGS = {
     "keep_moe_layer": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64, c_int64,
                        _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P, _P,
                        c_int, _P],
+    "keep_moe_layer1": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64, c_int64,
+                        _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P,
+                        c_int64, _P, c_int, _P],
+    "keep_moe_layer1_workspace_bytes": [c_int64, c_int64],
+    "keep_moe_layer1_status": [_P, _P, _P],
     "keep_moe_layer_nested": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64,
                               c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P,
                               _P, _P, _P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, _P,
@@ -68,6 +73,7 @@ _SIGS = {
     "keep_e8p_prepared_bytes": [],
 }
 _RESTYPE = {"keep_last_error": c_char_p, "keep_moe_tiles_workspace_bytes": c_int64,
+            "keep_moe_layer1_workspace_bytes": c_int64,
             "keep_vq_grouped_gemm_q8_workspace_bytes": c_int64}
 EXPORTED = tuple(_SIGS)
 

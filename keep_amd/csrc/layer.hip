@@ -1,0 +1,578 @@
+// The routed MoE decode layer for one token in ONE launch on gfx950: dual
+// top-k router, gate/up + SwiGLU, down + weighted combine. One block per
+// CU (256 blocks of 16 waves, all resident together); block b owns three
+// 16-row gate/up tiles of the [k, I] intermediate and the 16 output rows
+// 16 b .. 16 b + 15 of down. The int8 decode of E8P codewords and the
+// activation term split are described in q8_dev.h.
+//
+// As soon as a block has routed the token it issues the loads of its gate/up
+// tiles; each wave issues its down rows (every route's 16 rows x the wave's
+// 256-wide K slice) once its gate/up codes are in, so down's 12.6 MB stream
+// behind gate/up's 25.2 MB with no kernel boundary and no second routing
+// read. Gate/up decode and MFMAs run as their codes land; the block's SwiGLU
+// outputs h are published, and down waits only for the h slices its waves
+// consume.
+//
+// The h exchange. Blocks on different XCDs have different L2s, so h is
+// exchanged through agent-scope atomic stores and loads (written through to,
+// and read back from, the memory side of the L2s), with no fences and no
+// cache flush. Each 64-bit word carries two bf16 h values and a 32-bit tag,
+// the call's epoch + 1: a reader knows a word is this call's by its tag,
+// word by word, so no flag has to be ordered after the data. The epoch lives
+// in the caller's workspace (zero-filled before its first use): every block
+// reads it at its start and then counts itself in; the last block to count
+// in (so every block has read it) advances it for the next call. A wait that
+// outlasts spin_ticks of the 100 MHz real-time counter gives up: the values
+// it lacks are NaN, the outputs of the rows that used them are NaN, and the
+// workspace's status word records it.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "moe_dev.h"
+#include "q8_dev.h"
+#include "route_dev.h"
+
+namespace keep {
+
+constexpr int FL_BLOCKS = 256;       // H / 16 down row tiles, one block per CU
+constexpr int FL_WAVES = 16;         // H / 256 gate/up K slices
+constexpr uint32_t FL_HDR_BYTES = 256;  // epoch, arrivals, status
+constexpr uint32_t FL_TIMEOUT = 1u;     // status bit: a wait gave up
+
+struct FLArgs {
+  const float* logits;
+  const float *bias_s, *bias_d;
+  int func, renorm, same_bias;
+  float route_scale, tau;
+  int32_t E, k;
+  int32_t* idx_out;
+  float* w_out;
+  int32_t* want_out;
+  float* want_score_out;
+  uint8_t* admit_out;
+  const void* x;
+  int xbf;  // x is bf16 (else fp16)
+  int32_t I;
+  const uint16_t *gc, *uc, *dc;
+  const void *gs, *us, *ds;
+  int sdt;
+  int32_t Gh, gsz_h, Gi, gsz_i;
+  const uint2* tq;  // T[256] then M[256], 8 bytes each (keep_e8p_prepare)
+  const uint32_t* tq_bad;
+  float limit;
+  int32_t qtiles;
+  uint32_t* hdr;      // [0] epoch, [1] arrivals, [2] status
+  uint64_t* hx;       // [k * I / 2] tagged h pairs
+  uint32_t spin_ticks;
+  void* out;
+  int odt;
+};
+
+__device__ __forceinline__ uint64_t fl_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void fl_store(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Position of dim d (0..7) inside a codeword's 8 values in packed-nibble
+// order (dims 0, 2, 4, 6, 1, 3, 5, 7), the order the A operands use.
+__device__ __forceinline__ uint32_t fl_pos(uint32_t d) { return (d & 1u) * 4u + (d >> 1); }
+
+// NT gate/up tiles per block (two per 16-row q-tile), PER logits per router
+// lane, NSL = I / 256 down K slices, RPW routes per down wave (RG = 16 / NSL
+// route groups of RPW routes: the waves w < NSL * RG own slice w % NSL and
+// route group w / NSL). G1: per-row gate and up scales (one scale group per
+// row), applied once to each row's sum instead of to every slice's partial.
+//
+// LDS is one array with the decode image at address 0, so a lookup address
+// is exactly the byte permute of q8_decode2 (no base to add).
+template <int NT, int PER, int NSL, int RPW, bool G1>
+__global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
+  constexpr int QT = NT / 2;
+  constexpr int RG = FL_WAVES / NSL;
+  static_assert(RPW * 4 <= 16, "at most four routes per down wave (A rows 4 r + t)");
+  constexpr int O_DSH = TQR_BYTES;                      // down terms [wave][row 4 r + t][g * 4 + i]
+  constexpr int O_ASH = O_DSH + FL_WAVES * 16 * 256;    // x terms [slice][term][g * 4 + i]
+  constexpr int O_GRED = O_ASH + 16 * 3 * 256;          // gate/up partials [wave][tile][row]
+  constexpr int O_RED = O_GRED + 16 * NT * 16 * 4;      // down partials [slice][route][row]
+  constexpr int O_SMALL = O_RED + NSL * 8 * 16 * 4;     // s_inv4s[16], s_idx[8], s_w[8]
+  constexpr int LDS_BYTES = O_SMALL + 256;
+  __shared__ uint4 smem[LDS_BYTES / 16];
+  char* lds = (char*)smem;
+  uint4* tqs = smem;
+  uint4* dsh = (uint4*)(lds + O_DSH);
+  uint4* ash = (uint4*)(lds + O_ASH);
+  float* gred = (float*)(lds + O_GRED);
+  float (*red)[8][16] = (float (*)[8][16])(lds + O_RED);
+  float* s_inv4s = (float*)(lds + O_SMALL);
+  int32_t* s_idx = (int32_t*)(lds + O_SMALL + 64);
+  float* s_w = (float*)(lds + O_SMALL + 96);
+  const char* tq = (const char*)tqs;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const Q8Keys lk = q8_keys((uint32_t)lane);
+  const uint32_t j = lane & 15, g = lane >> 4;
+  const uint32_t C = 4096u >> 3;  // H / 8 token chunks
+  const uint32_t CI = (uint32_t)a.I >> 3;
+  const uint32_t b = blockIdx.x;
+
+  // 0. the call's epoch; the router's inputs (wave 0); T and M for the image
+  //    (every thread builds four copies of one entry); the token slices this
+  //    wave builds terms for (wave w >= 2 slice w; waves 2 and 3 also slices
+  //    0 and 1)
+  const uint32_t ep = __builtin_amdgcn_readfirstlane((uint32_t)(fl_load((uint64_t*)a.hdr) & 0xffffffffu));
+  float z[PER], bsv[PER], bdv[PER];
+  if (wv == 0) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
+  const uint32_t te = threadIdx.x >> 2;
+  const uint2 tv = a.tq[te], mv = a.tq[256 + te];
+  const uint4 xc = ldg16_q((const uint4*)a.x + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
+  const uint4 xc2 = ldg16_q((const uint4*)a.x + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
+  {
+    const uint4 v = make_uint4(tv.x, tv.y, mv.x, mv.y);
+    uint4* row = tqs + te * 16 + (threadIdx.x & 3) * 4;
+    row[0] = v;
+    row[1] = v;
+    row[2] = v;
+    row[3] = v;
+  }
+
+  // 1. served routing (wave 0) | A terms: rows 0-2 of slice w are the three
+  //    int8 terms of x s, s the slice's power of two
+  float sc[PER];
+  int e_sel = -1;
+  auto build = [&](uint4 c, int slice) {
+    float v[4];
+    if (a.xbf) q8_half4<true>(c, lane & 1, v);
+    else q8_half4<false>(c, lane & 1, v);
+    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    float s, inv4s;
+    q8_scale(rt_wave_max_abs(mx), s, inv4s);
+    uint32_t tw[3];
+    q8_terms<3>(v, s, tw);
+    uint32_t* aw = (uint32_t*)ash;
+#pragma unroll
+    for (int n = 0; n < 3; ++n) aw[q8_aword((uint32_t)(slice * 3 + n), lane >> 1, lane & 1)] = tw[n];
+    if (lane == 0) s_inv4s[slice] = inv4s;
+  };
+  if (wv == 0) {
+    e_sel = rt_select_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, true, 0, lane, sc);
+    if (lane < a.k) s_idx[lane] = e_sel >= 0 && e_sel < a.E ? e_sel : -1;
+  } else if (wv >= 2) {
+    build(xc, wv);
+    if (wv < 4) build(xc2, wv - 2);
+  }
+  rt_lds_barrier();  // s_idx, the image and every slice's A terms visible
+
+  // 2. the gate/up loads of the block: scales and codes
+  uint32_t rbase[QT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    const uint32_t qt = b * QT + u;
+    const bool valid = qt < (uint32_t)a.qtiles;
+    const uint32_t q0 = (valid ? qt : 0u) * 16u;
+    const uint32_t route = q0 / (uint32_t)a.I;
+    const int32_t e = s_idx[route];
+    const bool ok = valid && e >= 0 && e < a.E;
+    rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
+  }
+  const uint32_t grp = G1 ? 0u : (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
+  // G1: the row scales of the reducing lanes (wave 0, lane 16 u + jj: row jj of q-tile u); else every
+  // wave's slice scales
+  ScaleRaw sr[NT];
+  if constexpr (G1) {
+    uint32_t rb = rbase[0];
+#pragma unroll
+    for (int u = 1; u < QT; ++u) rb = (lane >> 4) == (uint32_t)u ? rbase[u] : rb;
+    const uint32_t si = rb + j;
+    sr[0] = wv == 0 && lane < QT * 16 ? scale_raw(a.gs, a.sdt, si) : 0u;
+    sr[1] = wv == 0 && lane < QT * 16 ? scale_raw(a.us, a.sdt, si) : 0u;
+  } else {
+#pragma unroll
+    for (int u = 0; u < QT; ++u) {
+      const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
+      sr[2 * u] = scale_raw(a.gs, a.sdt, si);
+      sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
+    }
+  }
+  // the codes: every tile's 16 B per lane issued before any is needed
+  const uint32_t kc0 = wv * 32 + g * 8;
+  uint4 q[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + (size_t)(rbase[t >> 1] + j) * C + kc0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the served weights and outputs (wave 0), while the codes are in flight
+  if (wv == 0) {
+    const RouteLane r = rt_finish<PER>(e_sel, true, sc, bsv, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
+    if (lane < a.k) s_w[lane] = r.valid ? r.value : 0.f;
+    if (b == 0 && r.valid) {
+      a.idx_out[lane] = r.expert;
+      a.w_out[lane] = r.value;
+    }
+  }
+
+  q8v4 A[4];
+  {
+    const q8v4* as = (const q8v4*)ash + (wv * 3 + (j < 3 ? j : 0)) * 16 + g * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const q8v4 v = as[i];
+      A[i] = j < 3 ? v : q8v4{0, 0, 0, 0};
+    }
+  }
+  const float inv4s = s_inv4s[wv];
+
+  // 3. gate/up, tile by tile as the codes land
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    q8v4 B[4];
+    q8_decode8(tq, lk, q[t], B);
+    q8v4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
+    if (lane < 16) {
+      const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
+      if constexpr (G1) {
+        gred[(wv * NT + t) * 16 + j] = d * inv4s;
+      } else {
+        const uint32_t si = (rbase[t >> 1] + j) * (uint32_t)a.Gh + grp;
+        gred[(wv * NT + t) * 16 + j] = d * inv4s * scale_cvt(sr[t], a.sdt, si);
+      }
+    }
+  }
+  // down's loads, once this wave's gate/up codes are in (requested together
+  // they would share the memory system with gate/up, which gates the exchange)
+  __builtin_amdgcn_sched_barrier(0);
+  // down: this wave's slice sd and routes rg * RPW + r'
+  const bool dwave = wv < NSL * RG;  // wave-uniform
+  const int sd = dwave ? wv % NSL : 0, rg = dwave ? wv / NSL : 0;
+  uint32_t dbase[RPW];
+  bool dlive[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int route = rg * RPW + r;
+    const int32_t e = route < a.k ? s_idx[route] : -1;
+    dlive[r] = dwave && route < a.k;
+    dbase[r] = (e >= 0 && e < a.E ? (uint32_t)e * 4096u : 0u) + b * 16u;
+  }
+  const uint32_t dgrp = (uint32_t)(sd * 256) / (uint32_t)a.gsz_i;
+  ScaleRaw srd[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) srd[r] = scale_raw(a.ds, a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + dgrp);
+  uint4 qd[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) qd[r] = ldg16_q(a.dc + (size_t)(dbase[r] + j) * CI + sd * 32 + g * 8);
+  // this block counts itself in (it has read the epoch); the last block in advances it after the exchange
+  uint32_t arrived = 0u;
+  if (threadIdx.x == 0)
+    arrived = __hip_atomic_fetch_add(a.hdr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  rt_lds_barrier();  // every wave's partials (and s_w) visible
+
+  // 4. SwiGLU of the block's rows and their publication: lane (u, jj) owns
+  //    intermediate row 16 qt + jj; lanes with dim bit 1 clear publish the
+  //    word of their dim and dim + 2 (adjacent in packed-nibble order)
+  const uint32_t tag = ep + 1u;
+  if (wv == 0 && lane < QT * 16) {
+    const uint32_t u = lane >> 4, jj = lane & 15;
+    const uint32_t qt = b * QT + u;
+    float gsum = 0.f, usum = 0.f;
+    for (int w = 0; w < 16; ++w) {
+      gsum += gred[(w * NT + 2 * u) * 16 + jj];
+      usum += gred[(w * NT + 2 * u + 1) * 16 + jj];
+    }
+    const bool valid = qt < (uint32_t)a.qtiles;
+    const uint32_t q0 = (valid ? qt : 0u) * 16u;
+    const int32_t e = s_idx[q0 / (uint32_t)a.I];
+    if constexpr (G1) {
+      uint32_t rb = rbase[0];
+#pragma unroll
+      for (int v = 1; v < QT; ++v) rb = u == (uint32_t)v ? rbase[v] : rb;
+      gsum *= scale_cvt(sr[0], a.sdt, rb + jj);
+      usum *= scale_cvt(sr[1], a.sdt, rb + jj);
+    }
+    float hv = silu_mul(gsum, usum, a.limit);
+    if (*a.tq_bad || e < 0 || e >= a.E) hv = __builtin_nanf("");
+    const uint32_t hb = from_float<bf16s>(hv).bits;
+    const uint32_t hb2 = (uint32_t)__shfl((int)hb, lane ^ 2, 64);
+    if (valid && (jj & 2u) == 0u) {
+      const uint32_t i = q0 + jj;  // flat [k, I] index
+      const uint32_t widx = ((i & ~7u) + fl_pos(i & 7u)) >> 1;
+      fl_store(a.hx + widx, ((uint64_t)tag << 32) | hb | (hb2 << 16));
+    }
+  }
+
+  // the demand routing's outputs (block 0, wave 1), recomputed from the
+  // logits while the other blocks' h is awaited
+  if (wv == 1 && b == 0 && (a.want_out || a.want_score_out || a.admit_out)) {
+    float z1[PER], bs1[PER], bd1[PER], sc1[PER];
+    rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z1, bs1, bd1);
+    const int d_sel = rt_select_pair<PER>(z1, bs1, bd1, a.E, a.k, a.func, a.same_bias != 0, 1, lane, sc1);
+    const RouteLane r = rt_finish<PER>(d_sel, false, sc1, bs1, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
+    if (r.valid) {
+      if (a.want_out) a.want_out[lane] = r.expert;
+      if (a.want_score_out) a.want_score_out[lane] = r.value;
+      if (a.admit_out) a.admit_out[lane] = r.admit;
+    }
+  }
+
+  // 5. down: this wave's h slices (two words per lane and route: dims 2t +
+  //    (lane & 1) of codeword lane / 2), waiting word by word for this call's tag
+  if (dwave) {
+    // down's B operands do not depend on h: decode them while h is awaited
+    // (with four routes per wave they would not fit in the registers)
+    constexpr bool PRE = RPW <= 3;
+    q8v4 BD[RPW][4];
+    if constexpr (PRE) {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) q8_decode8(tq, lk, qd[r], BD[r]);
+    }
+    uint64_t hw[RPW][2];
+    bool have[RPW][2];
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    bool gave_up = false;
+    for (;;) {
+      bool all = true;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const uint32_t w0 = ((uint32_t)(rg * RPW + r) * (uint32_t)a.I + sd * 256u + lane * 4u) >> 1;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (dlive[r]) {
+            hw[r][h] = fl_load(a.hx + w0 + h);
+            have[r][h] = (uint32_t)(hw[r][h] >> 32) == tag;
+            all = all && have[r][h];
+          } else {
+            hw[r][h] = 0u;
+            have[r][h] = true;
+          }
+        }
+      }
+      if (__all(all)) break;  // every lane holds every word
+      if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin_ticks) {
+        gave_up = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (gave_up && lane == 0) {
+      __hip_atomic_fetch_or(a.hdr + 2, FL_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // A terms: rows 4 r + t of route r's slice, scaled by its own power of two
+    float inv4d[RPW];
+    uint32_t* aw = (uint32_t*)(dsh + wv * 256);
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      float v[4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t lo = (uint32_t)hw[r][h];
+        v[2 * h] = have[r][h] ? __uint_as_float(lo << 16) : __builtin_nanf("");
+        v[2 * h + 1] = have[r][h] ? __uint_as_float(lo & 0xffff0000u) : __builtin_nanf("");
+      }
+      bool nan = false;
+      float mx = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        nan |= v[t] != v[t];
+        mx = fmaxf(mx, fabsf(v[t]));
+      }
+      float s;
+      q8_scale(rt_wave_max_abs(mx), s, inv4d[r]);
+      if (__any(nan)) inv4d[r] = __builtin_nanf("");
+      uint32_t tw[3];
+      q8_terms<3>(v, s, tw);
+#pragma unroll
+      for (int n = 0; n < 3; ++n) aw[q8_aword((uint32_t)(4 * r + n), lane >> 1, lane & 1)] = tw[n];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes before its reads
+    q8v4 AD[4];
+    {
+      const bool live = (j & 3u) != 3u && (int)(j >> 2) < RPW;
+      const q8v4* as = (const q8v4*)aw + (live ? j : 0u) * 16 + g * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const q8v4 v = as[i];
+        AD[i] = live ? v : q8v4{0, 0, 0, 0};
+      }
+    }
+    // route r's dot is D rows 4 r .. 4 r + 2, held by lanes 16 r + jj
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      if constexpr (!PRE) q8_decode8(tq, lk, qd[r], BD[r]);
+      q8v4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = mfma_i8(AD[i], BD[r][i], acc);
+      if ((int)g == r && dlive[r]) {
+        const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
+        red[sd][rg * RPW + r][j] = d * inv4d[r] * scale_cvt(srd[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + dgrp);
+      }
+    }
+  }
+  if (threadIdx.x == 0 && arrived == FL_BLOCKS - 1) {  // every block has read the epoch: advance it
+    __hip_atomic_store(a.hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.hdr, ep + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  rt_lds_barrier();
+
+  // 6. the weighted sum over routes (each the sum over slices, in slice order)
+  if (threadIdx.x < 16) {
+    float o = 0.f;
+    bool bad = false;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      if (r < a.k) {
+        const int32_t e = s_idx[r];
+        const float wt = s_w[r];
+        const bool ok = e >= 0 && e < a.E;
+        bad |= wt != 0.f && !ok;
+        float v = 0.f;
+#pragma unroll
+        for (int s = 0; s < NSL; ++s) v += red[s][r][threadIdx.x];
+        o = (ok && wt != 0.f) ? fmaf(wt, v, o) : o;
+      }
+    }
+    if (bad || *a.tq_bad) o = __builtin_nanf("");
+    const size_t oi = b * 16u + threadIdx.x;
+    if (a.odt == KEEP_F16) ((_Float16*)a.out)[oi] = (_Float16)o;
+    else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;
+    else ((float*)a.out)[oi] = o;
+  }
+}
+
+// ------------------------------------------------------------------ host
+
+int64_t fl_workspace_bytes(int64_t k, int64_t I) { return FL_HDR_BYTES + k * I * 4; }
+
+bool fl_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
+  const int64_t qtiles = k * I / 16;
+  return H == 4096 && I % 512 == 0 && I >= 512 && I <= 2048 && k >= 1 && k <= 8 && k <= E && E <= 1024 &&
+         (qtiles + FL_BLOCKS - 1) / FL_BLOCKS <= 4 && group_h % 256 == 0 && group_i % 256 == 0 &&
+         k <= 4 * (FL_WAVES / (I / 256));
+}
+
+// All FL_BLOCKS blocks must be resident together: one block per CU.
+bool fl_device_ok() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+  return cus >= FL_BLOCKS;
+}
+
+// The (tiles per block, slices, routes per down wave) of each served (I, k):
+// gate/up q-tiles per block ceil(k I / 16 / 256), down route groups
+// RG = 16 / (I / 256) of ceil(k / RG) routes.
+template <int PER, bool G1>
+static bool fl_dispatch(const FLArgs& a, hipStream_t s) {
+  const dim3 grid(FL_BLOCKS), blk(1024);
+#define FL_K(NT, NSL, RPW) hipLaunchKernelGGL((k_moe_layer1<NT, PER, NSL, RPW, G1>), grid, blk, 0, s, a)
+  const int k = a.k;
+  switch (a.I) {
+    case 2048:
+      if (k <= 2) FL_K(2, 8, 1);
+      else if (k <= 4) FL_K(4, 8, 2);
+      else if (k <= 6) FL_K(6, 8, 3);
+      else FL_K(8, 8, 4);
+      return true;
+    case 1536:
+      if (k <= 2) FL_K(2, 6, 1);
+      else if (k <= 4) FL_K(4, 6, 2);
+      else if (k == 5) FL_K(4, 6, 3);
+      else if (k == 6) FL_K(6, 6, 3);
+      else FL_K(6, 6, 4);
+      return true;
+    case 1024:
+      if (k <= 4) FL_K(2, 4, 1);
+      else FL_K(4, 4, 2);
+      return true;
+    case 512:
+      FL_K(2, 2, 1);
+      return true;
+    default:
+      return false;
+  }
+#undef FL_K
+}
+
+void fl_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm, float route_scale,
+               float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t I, const uint16_t* gc,
+               const void* gs, const uint16_t* uc, const void* us, const uint16_t* dc, const void* ds, int sdt,
+               int64_t group_h, int64_t group_i, const void* prepared, float limit, int32_t* idx, float* w,
+               int32_t* want, float* want_score, uint8_t* admit, void* workspace, uint32_t spin_ticks, void* out,
+               int odt, hipStream_t s) {
+  FLArgs a{};
+  a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
+  a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
+  a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
+  a.x = x; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.dc = dc; a.gs = gs; a.us = us; a.ds = ds; a.sdt = sdt;
+  a.Gh = (int32_t)(4096 / group_h); a.gsz_h = (int32_t)group_h;
+  a.Gi = (int32_t)(I / group_i); a.gsz_i = (int32_t)group_i;
+  a.tq = (const uint2*)((const char*)prepared + TQ_OFFSET);
+  a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
+  a.limit = limit;
+  a.qtiles = (int32_t)(k * I / 16);
+  a.hdr = (uint32_t*)workspace;
+  a.hx = (uint64_t*)((char*)workspace + FL_HDR_BYTES);
+  a.spin_ticks = spin_ticks;
+  a.out = out; a.odt = odt;
+  a.xbf = x_dtype == KEEP_BF16;
+  const bool g1 = group_h == 4096;
+  if (g1) {
+    if (E <= 384) fl_dispatch<6, true>(a, s);
+    else fl_dispatch<16, true>(a, s);
+  } else {
+    if (E <= 384) fl_dispatch<6, false>(a, s);
+    else fl_dispatch<16, false>(a, s);
+  }
+}
+
+}  // namespace keep
+
+using namespace keep;
+
+extern "C" int64_t keep_moe_layer1_workspace_bytes(int64_t k, int64_t I) {
+  if (k < 1 || I < 1) return -1;
+  return fl_workspace_bytes(k, I);
+}
+
+extern "C" int keep_moe_layer1_status(const void* workspace, uint32_t* status, void* stream) {
+  KEEP_REQUIRE(workspace && status, "null pointer argument");
+  if (hipMemcpyAsync(status, (const char*)workspace + 8, 4, hipMemcpyDeviceToHost, (hipStream_t)stream) !=
+      hipSuccess)
+    return launch_status("keep_moe_layer1_status");
+  if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) return launch_status("keep_moe_layer1_status");
+  return KEEP_OK;
+}
+
+extern "C" int keep_moe_layer1(const float* logits, const float* bias_served, const float* bias_demand,
+                               int score_func, int renormalize, float route_scale, float tau, int64_t E, int64_t k,
+                               const void* x, int x_dtype, int64_t H, int64_t I, const uint16_t* gate_codes,
+                               const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
+                               const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                               int64_t group_size_h, int64_t group_size_i, const void* prepared, float swiglu_limit,
+                               int32_t* idx, float* w, int32_t* want, float* want_score, uint8_t* admit,
+                               void* workspace, int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
+  KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
+  KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);
+  KEEP_REQUIRE(group_size_h > 0 && H % group_size_h == 0 && group_size_i > 0 && I % group_size_i == 0,
+               "bad group sizes");
+  KEEP_REQUIRE(fl_supported(E, H, I, k, group_size_h, group_size_i),
+               "shape not served by the one-launch decode layer (needs H = 4096, I a multiple of 512 up to 2048, "
+               "k <= 8, E <= 1024, scale groups of 256-element multiples)");
+  KEEP_REQUIRE(fl_device_ok(), "the one-launch decode layer needs %d compute units", FL_BLOCKS);
+  KEEP_REQUIRE(logits && x && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
+                   prepared && idx && w && workspace && out,
+               "null pointer argument");
+  KEEP_REQUIRE(workspace_bytes >= fl_workspace_bytes(k, I), "workspace needs %lld bytes, got %lld",
+               (long long)fl_workspace_bytes(k, I), (long long)workspace_bytes);
+  KEEP_REQUIRE(aligned(x, 16) && aligned(workspace, 256) && aligned(prepared, 16),
+               "x and prepared must be 16-byte aligned, the workspace 256-byte aligned");
+  KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 16), "codes misaligned");
+  fl_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype, I,
+            gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype, group_size_h,
+            group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, workspace, 20000u, out, out_dtype,
+            (hipStream_t)stream);
+  return launch_status("keep_moe_layer1");
+}

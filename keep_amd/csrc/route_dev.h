@@ -79,6 +79,34 @@ __device__ __forceinline__ float rt_wave_reduce(float v, bool is_max) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Wave-uniform max / min of unsigned 32-bit values, every lane ending with
+// the result: DPP inside 16-lane rows (integer max/min take the DPP operand
+// directly, with no canonicalisation of a float max), then row pairs and
+// halves through v_permlane16_swap / v_permlane32_swap.
+template <bool MAX>
+__device__ __forceinline__ uint32_t rt_op_u32(uint32_t a, uint32_t b) {
+  return MAX ? (a > b ? a : b) : (a < b ? a : b);
+}
+template <bool MAX, int CTRL>
+__device__ __forceinline__ uint32_t rt_dpp_u32(uint32_t v) {  // folds into one v_max/min_u32_dpp
+  return rt_op_u32<MAX>(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true));
+}
+template <bool MAX>
+__device__ __forceinline__ uint32_t rt_wave_u32(uint32_t v) {
+  v = rt_dpp_u32<MAX, 0xB1>(v);   // quad_perm [1,0,3,2]
+  v = rt_dpp_u32<MAX, 0x4E>(v);   // quad_perm [2,3,0,1]
+  v = rt_dpp_u32<MAX, 0x141>(v);  // row_half_mirror
+  v = rt_dpp_u32<MAX, 0x140>(v);  // row_mirror
+  const auto p16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = rt_op_u32<MAX>(p16[0], p16[1]);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return rt_op_u32<MAX>(p32[0], p32[1]);
+}
+// Max over the wave of non-negative floats (or NaN, which wins), by their bits.
+__device__ __forceinline__ float rt_wave_max_abs(float v) {
+  return __uint_as_float(rt_wave_u32<true>(__float_as_uint(v)));
+}
+
 __device__ __forceinline__ float rt_score_of(float z, int func) {
   if (func == KEEP_SCORE_SIGMOID) return 1.f / (1.f + expf(-z));
   // sqrt(softplus(z)), softplus = max(z, 0) + log1p(exp(-|z|))

@@ -420,16 +420,52 @@ def moe_layer_supported(num_experts: int, hidden: int, intermediate: int, k: int
                                                      group_size_i))
 
 
+_LAYER_WS: dict = {}
+
+
+def layer_workspace(device: torch.device, k: int, intermediate: int) -> torch.Tensor:
+    """The one-launch layer's workspace for ``device`` and the current stream:
+    zero-filled once, then reused by every call on that stream (it carries the
+    call counter that tags the exchanged SwiGLU outputs)."""
+
+    need = int(_lib.load().keep_moe_layer1_workspace_bytes(k, intermediate))
+    key = (str(device), torch.cuda.current_stream(device).cuda_stream)
+    ws = _LAYER_WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 1 << 16), dtype=torch.uint8, device=device)
+        _LAYER_WS[key] = ws
+    return ws
+
+
+def layer_status(workspace: torch.Tensor) -> int:
+    """Status word of a one-launch layer workspace (bit 1: a wait gave up)."""
+
+    out = (_lib.c_uint32 * 1)()
+    _lib.call("keep_moe_layer1_status", workspace.data_ptr(), out, ops._stream(workspace.device))
+    return int(out[0])
+
+
+def _one_launch_ok(device: torch.device, E: int, H: int, I: int, k: int) -> bool:
+    props = torch.cuda.get_device_properties(device)
+    return (props.multi_processor_count >= 256 and H == 4096 and I in (512, 1024, 1536, 2048) and 1 <= k <= 8
+            and k <= E <= 1024)
+
+
 def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, bias_served=None, bias_demand=None,
               score_func: str = "softmax", renormalize: bool = True, route_scale: float = 1.0,
               tau: float = float("inf"), limit: float = 0.0, codebook: torch.Tensor | None = None,
               out_dtype: torch.dtype | None = None, h_work: torch.Tensor | None = None,
-              hot_tier: HotTier | None = None):
+              hot_tier: HotTier | None = None, one_launch: bool = False,
+              workspace: torch.Tensor | None = None):
     """One token's whole MoE layer in two launches (``keep_moe_layer``): the dual
     top-k router (as ``router_dual_topk``) fused with gate/up/SwiGLU, then down +
     weighted combine. ``x [1, H]`` (fp16/bf16), ``logits [1, E]``. With
     ``hot_tier`` (``keep_moe_layer_nested``) the routes of experts on the
-    nested tier add their 8-bit E8 residual to all three projections. Returns
+    nested tier add their 8-bit E8 residual to all three projections. With
+    ``one_launch`` (``keep_moe_layer1``) the same layer runs as one launch of
+    256 co-resident blocks that pass h through ``workspace`` (by default
+    ``layer_workspace(device, k, I)`` of the current stream); it serves
+    H = 4096, I in {512, 1024, 1536, 2048}, k <= 8, no hot tier. Returns
     ``(out [1, H], RouterOutput)``; the output is float32 by default."""
 
     device = x.device
@@ -450,7 +486,7 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
     if z.shape[1] != E:
         raise ValueError(f"logits must hold {E} experts, found {z.shape[1]}")
     gh, gi = H // gs.shape[-1], I // ds.shape[-1]
-    if not moe_layer_supported(E, H, I, k, gh, gi):
+    if not one_launch and not moe_layer_supported(E, H, I, k, gh, gi):
         raise ValueError("shape not served by the routed decode layer; use router_dual_topk + moe_decode")
     bs = None if bias_served is None else bias_served.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
     bd = None if bias_demand is None else bias_demand.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
@@ -465,12 +501,29 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
                      torch.empty((1, k), **f32), torch.empty((1, k), dtype=torch.uint8, device=device))
     od = out_dtype or torch.float32
     out = torch.empty((1, H), dtype=od, device=device)
+    cb = ops._codebook_tensor(codebook, 16, device)
+    prep = ops.prepared_table(cb)
+    if one_launch:
+        if hot_tier is not None:
+            raise ValueError("the one-launch layer has no hot tier; use one_launch=False")
+        if not _one_launch_ok(device, E, H, I, k):
+            raise ValueError("shape or device not served by the one-launch layer (H = 4096, I in {512, 1024, 1536, "
+                             "2048}, k <= 8, E <= 1024, 256 compute units)")
+        need = int(_lib.load().keep_moe_layer1_workspace_bytes(k, I))
+        ws = layer_workspace(device, k, I) if workspace is None else workspace
+        if ws.dtype != torch.uint8 or ws.device != device or ws.numel() < need or not ws.is_contiguous():
+            raise ValueError(f"workspace must be a contiguous uint8 tensor of at least {need} bytes on {device}")
+        _lib.call("keep_moe_layer1", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
+                  int(bool(renormalize)), float(route_scale), float(tau), E, k, x.data_ptr(), ops._DT[x.dtype], H,
+                  I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
+                  ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(), r.weight.data_ptr(),
+                  r.want.data_ptr(), r.want_score.data_ptr(), r.admit.data_ptr(), ws.data_ptr(), ws.numel(),
+                  out.data_ptr(), ops._DT[od], ops._stream(device))
+        return out, r
     if h_work is None:
         h_work = torch.empty((k * I,), dtype=torch.bfloat16, device=device)
     elif h_work.numel() < k * I or h_work.dtype != torch.bfloat16:
         raise ValueError("h_work must hold k*I bfloat16 elements")
-    cb = ops._codebook_tensor(codebook, 16, device)
-    prep = ops.prepared_table(cb)
     if hot_tier is not None:
         if hot_tier.hot_of_slot.numel() != E:
             raise ValueError(f"hot_of_slot must have {E} entries")
