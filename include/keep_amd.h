@@ -216,6 +216,25 @@ int keep_moe_layer(const float* logits, const float* bias_served, const float* b
                    float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
                    uint8_t* admit, void* h_work, void* out, int out_dtype, void* stream);
 
+/* keep_moe_layer without h_work: it allocates nothing and takes no
+ * workspace. No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). h lives in a static device array of
+ * 12,288 bf16 values (24 KiB, one copy per GPU for the life of the process),
+ * so k * I <= 12288 (every shape keep_moe_layer serves); larger k * I returns
+ * KEEP_EINVAL. Calls that overlap on one GPU (on different streams) share
+ * that array and race; calls in one stream's order do not. Same outputs as
+ * keep_moe_layer, bit for bit. */
+int keep_moe_layer_noalloc(const float* logits, const float* bias_served, const float* bias_demand,
+                           int score_func, int renormalize, float route_scale, float tau,
+                           int64_t num_experts, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
+                           const uint16_t* gate_codes, const void* gate_scales,
+                           const uint16_t* up_codes, const void* up_scales,
+                           const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                           int64_t group_size_h, int64_t group_size_i, const void* prepared,
+                           float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                           uint8_t* admit, void* out, int out_dtype, void* stream);
+
 /* The same layer in ONE launch of 256 blocks (one per compute unit, all
  * resident together): the router, gate/up/SwiGLU and down + combine, with
  * the whole code stream (gate/up, then down) requested as soon as a block has

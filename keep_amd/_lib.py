@@ -56,6 +56,9 @@ _SIGS = {
     "keep_moe_layer": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64, c_int64,
                        _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P, _P,
                        c_int, _P],
+    "keep_moe_layer_noalloc": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64,
+                               c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P,
+                               _P, _P, c_int, _P],
     "keep_moe_layer1": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64, c_int64,
                         _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P,
                         c_int64, _P, c_int, _P],

@@ -21,6 +21,8 @@
 // then all of its code, activation and scale loads, and only then writes the
 // table to LDS and joins the barrier, so the HBM stream is in flight while
 // the table is staged. Lane reductions use DPP row ops plus readlane.
+#include <mutex>
+
 #include "common.h"
 #include "moe_dev.h"
 #include "route_dev.h"
@@ -946,4 +948,61 @@ extern "C" int keep_moe_layer(const float* logits, const float* bias_served, con
                       group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, h_work,
                       out, out_dtype, (hipStream_t)stream);
   return launch_status("keep_moe_layer");
+}
+
+// ------------------------------------------------------------------ keep_moe_layer_noalloc
+//
+// keep_moe_layer with h in a file-scope device array instead of a caller's
+// h_work, for callers that cannot allocate. Each GPU holds its own copy of
+// the array for the life of the process; its address on a device is taken
+// with hipGetSymbolAddress once, with that device current, and kept (the
+// array's name in host code is not a device address). The gate/up launch
+// writes every one of the k * I values before the down launch reads them,
+// so nothing in it has to start at zero; calls that overlap on one GPU
+// (two streams) share it and race.
+constexpr int64_t NOALLOC_H_ELEMS = 12288;  // k * I bf16 values: 24 KiB, every shape keep_moe_layer serves
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static __device__ __align__(256) uint16_t scratch[NOALLOC_H_ELEMS];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// The current device's copy of `scratch`, or null (with the error recorded).
+static void* noalloc_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+    set_error("keep_moe_layer_noalloc: no current device below %d", NOALLOC_MAX_DEVICES);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("keep_moe_layer_noalloc: hipGetSymbolAddress failed on device %d: %s", dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+extern "C" int keep_moe_layer_noalloc(const float* logits, const float* bias_served, const float* bias_demand,
+                                      int score_func, int renormalize, float route_scale, float tau, int64_t E,
+                                      int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
+                                      const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
+                                      const void* up_scales, const uint16_t* down_codes, const void* down_scales,
+                                      int scale_dtype, int64_t group_size_h, int64_t group_size_i,
+                                      const void* prepared, float swiglu_limit, int32_t* idx, float* w,
+                                      int32_t* want, float* want_score, uint8_t* admit, void* out, int out_dtype,
+                                      void* stream) {
+  KEEP_REQUIRE(k >= 1 && I >= 1 && k * I <= NOALLOC_H_ELEMS,
+               "keep_moe_layer_noalloc holds at most %lld SwiGLU values (k * I) in its static scratch, got %lld",
+               (long long)NOALLOC_H_ELEMS, (long long)(k * I));
+  void* h = noalloc_scratch();
+  if (!h) return KEEP_ELAUNCH;
+  return keep_moe_layer(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype,
+                        H, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
+                        group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, h, out,
+                        out_dtype, stream);
 }
