@@ -46,6 +46,13 @@ int keep_e8_1bit_packed(uint32_t* out256);
 int keep_e8p_decode(const uint16_t* codes, int64_t n, const uint32_t* table,
                     const void* scales, int scale_dtype, int64_t codewords_per_row,
                     int64_t group_codewords, float* out, void* stream);
+/* 8-bit E8 decode (code_bits = 8): code byte c indexes the packed table
+ * (nibble d = dim d, value (nibble - 8) / 2), times the same optional group
+ * scales. Replaces decode_e8_1bit / decode_weight_matrix(code_bits=8)
+ * (src/keep/vq/e8.py:542-571). */
+int keep_e8_1bit_decode(const uint8_t* codes, int64_t n, const uint32_t* table, const void* scales,
+                        int scale_dtype, int64_t codewords_per_row, int64_t group_codewords, float* out,
+                        void* stream);
 
 /* Routed VQ mat-vec: out[r, :] = W[rhs[r]] . x[row(r), :] for r < routes,
  * row(r) = lhs ? lhs[r] : r / x_div. W[e] is [N, K] given by codes [E, N, K/8]
@@ -82,11 +89,13 @@ int keep_e8_1bit_matvec(const void* x, int x_dtype, int64_t x_rows, const uint8_
  * expert (tile_offset/tile_count index the sorted routes; tile_expert is
  * the expert). Routes of a tile share every code load and decode. Output row
  * sorted_route is written at out[sorted_route] (sorted order). Bit-identical
- * per route with keep_vq_matvec (same lane accumulation order).
+ * per route with keep_vq_matvec (same lane accumulation order). code_bits 8:
+ * uint8 codes indexing a packed 8-bit E8 table (nibble d = dim d, value
+ * (nibble - 8) / 2), the reference verify kernel's format; 16: E8P uint16.
  * Replaces gather_vqmm_verify_rows (src/ramp/ops/vq_switch.py:286-377) and
  * its kernel gather_vqmm_verify_mrows (src/ramp/kernels/gather_vqmm.py:287-419). */
 int keep_vq_matvec_tiles(const void* x, int x_dtype, int64_t x_rows,
-                         const uint16_t* codes, const void* scales, int scale_dtype,
+                         const void* codes, int code_bits, const void* scales, int scale_dtype,
                          const uint32_t* table, const int32_t* sorted_lhs, int64_t routes,
                          const int32_t* tile_expert, const int32_t* tile_offset,
                          const int32_t* tile_count, int64_t n_tiles, int64_t m_rows,
@@ -120,21 +129,6 @@ int keep_route_plan(const int32_t* rhs, int64_t R, int64_t E, int64_t tile,
                     int32_t* order, int32_t* inverse, int32_t* counts, int32_t* offsets,
                     int32_t* tile_expert, int32_t* tile_offset, int32_t* tile_count,
                     int64_t max_tiles, int32_t* n_tiles_out, void* stream);
-
-/* Prefill grouped GEMM over expert-sorted routes on MFMA: for every tile t and
- * route i < tile_count[t]: out[tile_offset[t] + i, :] =
- * W[tile_expert[t]] . x[lhs[tile_offset[t] + i], :] (lhs NULL: identity).
- * E8P decoded into fp16/bf16 LDS tiles (exact), fp32 accumulate, scales applied
- * per group in fp32. Tiles hold at most 64 routes.
- * Replaces gather_vqmm_sorted_routes with the NAX E8P kernels
- * (src/ramp/ops/vq_switch.py:620-913; native/vq_nax_ext/kernels/nax_fp16_matmul.metal:904-1062). */
-int keep_vq_grouped_gemm(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
-                         const uint16_t* codes, const void* scales, int scale_dtype,
-                         const uint32_t* table,
-                         const int32_t* tile_expert, const int32_t* tile_offset,
-                         const int32_t* tile_count, int64_t n_tiles, int64_t routes,
-                         int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
-                         void* out, int out_dtype, void* stream);
 
 /* Decode tables for the fused MoE kernels, built on the device from the
  * 256-entry packed abs grid: at offset 0, 2 x 128 KiB expanded tables (fp16

@@ -26,15 +26,14 @@ _SIGS = {
     "keep_e8p_packed_abs_grid": [POINTER(c_uint32)],
     "keep_e8_1bit_packed": [POINTER(c_uint32)],
     "keep_e8p_decode": [_P, c_int64, _P, _P, c_int, c_int64, c_int64, _P, _P],
+    "keep_e8_1bit_decode": [_P, c_int64, _P, _P, c_int, c_int64, c_int64, _P, _P],
     "keep_vq_matvec": [_P, c_int, c_int64, _P, c_int, _P, c_int, _P, _P, _P, c_int64, c_int64, c_int64, c_int64,
                        c_int64, c_int64, _P, _P, c_int64, _P, _P, c_int64, _P, c_int, _P],
-    "keep_vq_matvec_tiles": [_P, c_int, c_int64, _P, _P, c_int, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64,
+    "keep_vq_matvec_tiles": [_P, c_int, c_int64, _P, c_int, _P, c_int, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64,
                              c_int64, c_int64, c_int64, c_int64, _P, c_int, _P],
     "keep_router_dual_topk": [_P, c_int64, c_int64, c_int64, _P, _P, c_int, c_int, c_float, c_float, _P, _P, _P,
                               _P, _P, _P],
     "keep_route_plan": [_P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P],
-    "keep_vq_grouped_gemm": [_P, c_int, c_int64, _P, _P, _P, c_int, _P, _P, _P, _P, c_int64, c_int64, c_int64,
-                             c_int64, c_int64, c_int64, _P, c_int, _P],
     "keep_moe_decode": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
                         c_int, c_int64, c_int64, _P, _P, c_float, _P, _P, c_int, _P],
     "keep_moe_tiles": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int,

@@ -83,6 +83,31 @@ __global__ __launch_bounds__(256) void k_e8p_decode(const uint16_t* codes, int64
   }
 }
 
+// 8-bit E8 decode: code byte c -> the packed entry table[c], nibble d = dim d,
+// value (nibble - 8) / 2 (exact in fp32), times the group scale.
+__global__ __launch_bounds__(256) void k_e8_decode(const uint8_t* codes, int64_t n, const uint32_t* table,
+                                                   const void* scales, int sdt, int64_t cpr, int64_t gcw,
+                                                   float* out) {
+  __shared__ uint32_t tab[256];
+  tab[threadIdx.x] = table[threadIdx.x];
+  __syncthreads();
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint32_t p = tab[codes[i]];
+    float s = 1.f;
+    if (scales) {
+      const int64_t row = i / cpr, cw = i - row * cpr;
+      s = scale_at(scales, sdt, row * (cpr / gcw) + cw / gcw);
+    }
+    float v[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) v[d] = ((float)((p >> (4 * d)) & 15u) - 8.f) * 0.5f * s;
+    float4* o = (float4*)(out + i * 8);
+    o[0] = make_float4(v[0], v[1], v[2], v[3]);
+    o[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
 // ------------------------------------------------------------------ routed mat-vec
 
 struct MatvecArgs {
@@ -205,7 +230,7 @@ __global__ __launch_bounds__(256) void k_vq_matvec(MatvecArgs a) {
 struct TileArgs {
   const void* x;
   int64_t x_rows;
-  const uint16_t* codes;
+  const void* codes;
   const void* scales;
   int sdt;
   const uint32_t* table;
@@ -219,15 +244,16 @@ struct TileArgs {
   int64_t row_blocks;
 };
 
-// One wave: MV_ROWS rows of one expert for up to m_rows routes. Codes are
-// loaded and kept in registers once; each route re-reads only its own
-// activation chunk (L1/L2 resident). Per route, the lane order and the
-// chunk/scale/butterfly sequence equal k_vq_matvec's, so results are
-// bit-identical with the flat mat-vec.
-template <typename XT, int CH>
+// One wave: MV_ROWS rows of one expert for up to m_rows routes. Codes
+// (CB = 16: E8P uint16, CB = 8: 8-bit E8 uint8) are loaded and kept in
+// registers once; each route re-reads only its own activation chunk (L1/L2
+// resident). Per route, the lane order and the chunk/scale/butterfly
+// sequence equal k_vq_matvec's, so results are bit-identical with the flat
+// mat-vec.
+template <int CB, typename XT, int CH>
 __global__ __launch_bounds__(256) void k_vq_matvec_tiles(TileArgs a) {
   constexpr int PK = PairOf<XT>::value;
-  constexpr int NW = (CH * 2 + 3) / 4;
+  constexpr int NW = (CH * CB / 8 + 3) / 4;
   constexpr int MMAX = 8;
   __shared__ uint4 tab[256];
   const int lane = threadIdx.x & 63;
@@ -244,21 +270,21 @@ __global__ __launch_bounds__(256) void k_vq_matvec_tiles(TileArgs a) {
   const bool live = row0 < a.N && cnt > 0;
   const bool bad = e < 0 || e >= a.E || off < 0 || off + m > a.routes;
   const int64_t C = a.K >> 3;
-  const char* cbase = (const char*)a.codes + (e * a.N) * C * 2;
+  const char* cbase = (const char*)a.codes + (e * a.N) * C * (CB / 8);
   uint32_t words[MV_ROWS][NW], sb[MV_ROWS];
   auto load_chunk = [&](int64_t cw) {  // rows past N load row N - 1 and are never used
     const int64_t g = cw / a.cpg;
 #pragma unroll
     for (int r = 0; r < MV_ROWS; ++r) {
       const int64_t row = row0 + r < a.N ? row0 + r : a.N - 1;
-      load_codes<16, CH>(cbase + row * C * 2, cw, words[r]);
+      load_codes<CB, CH>(cbase + row * C * (CB / 8), cw, words[r]);
       sb[r] = scale_bits(a.scales, a.sdt, (e * a.N + row) * a.G + g);
     }
   };
   const uint32_t tpk = a.table[threadIdx.x];  // blockDim.x == 256: one codebook entry per thread
   int64_t cw = (int64_t)lane * CH;
   if (live && !bad && cw < C) load_chunk(cw);
-  codebook_entry<16, PK>(tab, threadIdx.x, tpk);
+  codebook_entry<CB, PK>(tab, threadIdx.x, tpk);
   __syncthreads();
   if (!live) return;
   if (bad) {
@@ -286,7 +312,7 @@ __global__ __launch_bounds__(256) void k_vq_matvec_tiles(TileArgs a) {
         xc.load((const XT*)a.x + xr[i] * a.K, cw);
 #pragma unroll
         for (int r = 0; r < MV_ROWS; ++r) {
-          if (row0 + r < a.N) acc[i][r] += chunk_dot<16, XT, CH>(words[r], tab, xc) * scale_of_bits(sb[r], a.sdt);
+          if (row0 + r < a.N) acc[i][r] += chunk_dot<CB, XT, CH>(words[r], tab, xc) * scale_of_bits(sb[r], a.sdt);
         }
       }
     }
@@ -531,6 +557,26 @@ extern "C" int keep_e8p_decode(const uint16_t* codes, int64_t n, const uint32_t*
   return launch_status("keep_e8p_decode");
 }
 
+extern "C" int keep_e8_1bit_decode(const uint8_t* codes, int64_t n, const uint32_t* table, const void* scales,
+                                   int scale_dtype, int64_t codewords_per_row, int64_t group_codewords, float* out,
+                                   void* stream) {
+  KEEP_REQUIRE(n >= 0, "n must be >= 0");
+  if (n == 0) return KEEP_OK;
+  KEEP_REQUIRE(codes && table && out, "codes, table and out must be non-null");
+  KEEP_REQUIRE(aligned(out, 16), "out must be 16-byte aligned");
+  if (scales) {
+    KEEP_REQUIRE(dtype_ok(scale_dtype), "bad scale dtype %d", scale_dtype);
+    KEEP_REQUIRE(codewords_per_row > 0 && n % codewords_per_row == 0, "n must be a multiple of codewords_per_row");
+    KEEP_REQUIRE(group_codewords > 0 && codewords_per_row % group_codewords == 0,
+                 "codewords_per_row must be a multiple of group_codewords");
+  }
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(k_e8_decode, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, codes, n, table, scales,
+                     scale_dtype, codewords_per_row, group_codewords, out);
+  return launch_status("keep_e8_1bit_decode");
+}
+
 extern "C" int keep_vq_matvec(const void* x, int x_dtype, int64_t x_rows, const void* codes, int code_bits,
                               const void* scales, int scale_dtype, const uint32_t* table, const int32_t* rhs,
                               const int32_t* lhs, int64_t routes, int64_t x_div, int64_t num_experts, int64_t N,
@@ -578,23 +624,29 @@ extern "C" int keep_vq_matvec(const void* x, int x_dtype, int64_t x_rows, const 
   return launch_status("keep_vq_matvec");
 }
 
-template <typename XT>
-static void launch_tiles(int ch, dim3 grid, hipStream_t s, const TileArgs& a) {
+template <int CB, typename XT>
+static void launch_tiles_cb(int ch, dim3 grid, hipStream_t s, const TileArgs& a) {
   switch (ch) {
-    case 8: hipLaunchKernelGGL((k_vq_matvec_tiles<XT, 8>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_vq_matvec_tiles<XT, 4>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_vq_matvec_tiles<XT, 2>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((k_vq_matvec_tiles<XT, 1>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_vq_matvec_tiles<CB, XT, 8>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_vq_matvec_tiles<CB, XT, 4>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_vq_matvec_tiles<CB, XT, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((k_vq_matvec_tiles<CB, XT, 1>), grid, dim3(256), 0, s, a); break;
   }
 }
+template <typename XT>
+static void launch_tiles(int code_bits, int ch, dim3 grid, hipStream_t s, const TileArgs& a) {
+  if (code_bits == 16) launch_tiles_cb<16, XT>(ch, grid, s, a);
+  else launch_tiles_cb<8, XT>(ch, grid, s, a);
+}
 
-extern "C" int keep_vq_matvec_tiles(const void* x, int x_dtype, int64_t x_rows, const uint16_t* codes,
+extern "C" int keep_vq_matvec_tiles(const void* x, int x_dtype, int64_t x_rows, const void* codes, int code_bits,
                                     const void* scales, int scale_dtype, const uint32_t* table,
                                     const int32_t* sorted_lhs, int64_t routes, const int32_t* tile_expert,
                                     const int32_t* tile_offset, const int32_t* tile_count, int64_t n_tiles,
                                     int64_t m_rows, int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
                                     void* out, int out_dtype, void* stream) {
   KEEP_REQUIRE(dtype_ok(x_dtype) && dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
+  KEEP_REQUIRE(code_bits == 8 || code_bits == 16, "code_bits must be 8 or 16, got %d", code_bits);
   KEEP_REQUIRE(N > 0 && K > 0 && K % 8 == 0, "need N > 0 and K divisible by 8");
   KEEP_REQUIRE(group_size > 0 && group_size % 8 == 0 && K % group_size == 0, "bad group_size");
   KEEP_REQUIRE(m_rows >= 1 && m_rows <= 8, "m_rows must be in 1..8, got %lld", (long long)m_rows);
@@ -605,7 +657,7 @@ extern "C" int keep_vq_matvec_tiles(const void* x, int x_dtype, int64_t x_rows, 
   KEEP_REQUIRE(x_rows > 0 && aligned(x, 16), "x must be non-empty and 16-byte aligned");
   const int64_t C = K / 8, cpg = group_size / 8;
   const int ch = pick_chunk(C, cpg, 0);
-  KEEP_REQUIRE(aligned(codes, (uintptr_t)(ch * 2)), "codes misaligned");
+  KEEP_REQUIRE(aligned(codes, (uintptr_t)(ch * code_bits / 8)), "codes misaligned");
   TileArgs a{};
   a.x = x; a.x_rows = x_rows; a.codes = codes; a.scales = scales; a.sdt = scale_dtype; a.table = table;
   a.lhs = sorted_lhs; a.routes = routes; a.te = tile_expert; a.to = tile_offset; a.tc = tile_count;
@@ -616,9 +668,9 @@ extern "C" int keep_vq_matvec_tiles(const void* x, int x_dtype, int64_t x_rows, 
   KEEP_REQUIRE(blocks <= 0x7fffffffLL, "too many blocks");
   dim3 grid((unsigned)blocks);
   hipStream_t s = (hipStream_t)stream;
-  if (x_dtype == KEEP_F16) launch_tiles<_Float16>(ch, grid, s, a);
-  else if (x_dtype == KEEP_BF16) launch_tiles<bf16s>(ch, grid, s, a);
-  else launch_tiles<float>(ch, grid, s, a);
+  if (x_dtype == KEEP_F16) launch_tiles<_Float16>(code_bits, ch, grid, s, a);
+  else if (x_dtype == KEEP_BF16) launch_tiles<bf16s>(code_bits, ch, grid, s, a);
+  else launch_tiles<float>(code_bits, ch, grid, s, a);
   return launch_status("keep_vq_matvec_tiles");
 }
 

@@ -1,5 +1,6 @@
 """Module layer of the routed E8P expert path (torch, GPU).
 
+- ``QuantizedVQLinear`` -- dense E8P/E8 linear (``src/ramp/nn/linear.py:17-121``).
 - ``QuantizedVQSwitchLinear`` -- stacked E8P/E8 expert projection, drop-in for
   ``src/ramp/nn/switch_linear.py:93-463`` (core routing; the continuous
   sidecars -- scale delta, low-rank and sparse-row residuals, rotation
@@ -43,6 +44,75 @@ class LimitedSwiGLU:
             g = torch.clamp(g, max=self.limit)
             u = torch.clamp(u, -self.limit, self.limit)
         return (torch.nn.functional.silu(g) * u).to(dtype)
+
+
+class QuantizedVQLinear:
+    """Dense linear layer on E8 VQ codes (torch, GPU): ``vq_qmv`` for one row,
+    ``vq_qmm`` for more, after the optional RHT or input rotation, plus bias
+    (reference ``src/ramp/nn/linear.py:17-121``). ``x @ rotation_matrix`` runs
+    in ``x``'s dtype, as ``apply_rotation_mx`` does (``keep/quant/rotation.py:39-43``)."""
+
+    def __init__(self, *, input_dims: int, output_dims: int, codes, scales, codebook=None, bias=None,
+                 group_size: int = 512, code_bits: int = 8, rht_signs=None, rotation_matrix=None):
+        if input_dims <= 0 or output_dims <= 0:
+            raise ValueError("input_dims and output_dims must be positive")
+        if input_dims % CODEWORD_DIM != 0:
+            raise ValueError("input_dims must be divisible by 8")
+        if input_dims % group_size != 0:
+            raise ValueError("input_dims must be divisible by group_size")
+        if code_bits not in (8, 16):
+            raise ValueError("code_bits must be 8 or 16")
+        if tuple(codes.shape) != (output_dims, input_dims // CODEWORD_DIM):
+            raise ValueError(f"codes must have shape ({output_dims}, {input_dims // CODEWORD_DIM}), "
+                             f"found {tuple(codes.shape)}")
+        if tuple(scales.shape) != (output_dims, input_dims // group_size):
+            raise ValueError(f"scales must have shape ({output_dims}, {input_dims // group_size}), "
+                             f"found {tuple(scales.shape)}")
+        if bias is not None and tuple(bias.shape) != (output_dims,):
+            raise ValueError(f"bias must have shape ({output_dims},), found {tuple(bias.shape)}")
+        if rht_signs is not None and rotation_matrix is not None:
+            raise ValueError("rht_signs and rotation_matrix are mutually exclusive")
+        if rht_signs is not None and tuple(rht_signs.shape) != (input_dims,):
+            raise ValueError(f"rht_signs must have shape ({input_dims},), found {tuple(rht_signs.shape)}")
+        if rotation_matrix is not None and tuple(rotation_matrix.shape) != (input_dims, input_dims):
+            raise ValueError(f"rotation_matrix must have shape ({input_dims}, {input_dims}), "
+                             f"found {tuple(rotation_matrix.shape)}")
+        device = codes.device if isinstance(codes, torch.Tensor) and codes.is_cuda else ops._device_of(codes)
+        self.input_dims, self.output_dims = input_dims, output_dims
+        self.group_size, self.code_bits = group_size, code_bits
+        self.codes = ops._codes_tensor(codes, code_bits, device)
+        self.scales = ops._to_dev(scales, device)
+        self.codebook = ops._codebook_tensor(codebook, code_bits, device)
+        self.bias = None if bias is None else ops._to_dev(bias, device)
+        self.rht_signs = None if rht_signs is None else ops._to_dev(rht_signs, device, torch.float32)
+        if self.rht_signs is not None:
+            from keep_amd.rht import check_signs
+            check_signs(self.rht_signs)
+        self.rotation_matrix = None if rotation_matrix is None else ops._to_dev(rotation_matrix, device,
+                                                                                torch.float32)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        if x.shape[-1] != self.input_dims:
+            raise ValueError(f"input trailing dimension must be {self.input_dims}, found {x.shape[-1]}")
+        if self.rht_signs is not None:
+            from keep_amd.rht import apply_rht
+            x = apply_rht(x, self.rht_signs, validate_signs=False)  # checked once, at construction
+        if self.rotation_matrix is not None:
+            x = x @ self.rotation_matrix.to(x.dtype)
+        flat = x.reshape(-1, self.input_dims)
+        kw = dict(in_dim=self.input_dims, out_dim=self.output_dims, group_size=self.group_size,
+                  code_bits=self.code_bits)
+        if flat.shape[0] == 1:
+            y = ops.vq_qmv(flat[0], self.codes, self.scales, self.codebook, **kw).reshape(1, self.output_dims)
+        else:
+            y = ops.vq_qmm(flat, self.codes, self.scales, self.codebook, **kw)
+        y = y.reshape(tuple(x.shape[:-1]) + (self.output_dims,))
+        if self.bias is not None:
+            y = y + self.bias  # type promotion as MLX's: a float32 bias gives a float32 result
+        return y
+
+    def _extra_repr(self) -> str:
+        return f"{self.input_dims}, {self.output_dims}, group_size={self.group_size}, code_bits={self.code_bits}"
 
 
 class QuantizedVQSwitchLinear:

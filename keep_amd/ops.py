@@ -189,6 +189,17 @@ def _codes_tensor(codes, code_bits: int, device) -> torch.Tensor:
     return out.view(torch.int16) if code_bits == 16 and out.dtype == torch.uint16 else out
 
 
+def _code_bits_of(codes) -> int:
+    """8 for uint8/int8 codes (8-bit E8), 16 for uint16/int16 (E8P)."""
+
+    name = str(codes.dtype if isinstance(codes, torch.Tensor) else np.asarray(codes).dtype).rsplit(".", 1)[-1]
+    if name in ("uint8", "int8"):
+        return 8
+    if name in ("uint16", "int16"):
+        return 16
+    raise ValueError(f"codes dtype must be uint8 (8-bit E8) or uint16 (E8P), found {name}")
+
+
 def _codebook_tensor(codebook, code_bits: int, device) -> torch.Tensor:
     if codebook is None:
         return _default_codebook(code_bits, device)
@@ -422,19 +433,20 @@ def decode_e8p(codes, codebook=None) -> torch.Tensor:
     return out
 
 
-def decode_weight_matrix(codes, scales=None, *, code_bits: int = 16, codebook=None) -> torch.Tensor:
-    """Dense float32 weights ``[..., 8*C]`` (reference ``e8.py:542-571``), E8P only."""
+def decode_weight_matrix(codes, scales=None, *, code_bits: int = 8, codebook=None) -> torch.Tensor:
+    """Dense float32 weights ``[..., 8*C]`` (reference ``e8.py:542-571``): 8-bit
+    E8 codes (uint8, the reference's default) or E8P (uint16)."""
 
-    if code_bits != 16:
-        raise ValueError("the GPU dense decode serves E8P (code_bits=16)")
+    if code_bits not in (8, 16):
+        raise ValueError("code_bits must be 8 or 16")
+    fn = "keep_e8p_decode" if code_bits == 16 else "keep_e8_1bit_decode"
     device = _device_of(codes, scales, codebook)
-    c = _codes_tensor(codes, 16, device)
-    cb = _codebook_tensor(codebook, 16, device)
+    c = _codes_tensor(codes, code_bits, device)
+    cb = _codebook_tensor(codebook, code_bits, device)
     C = c.shape[-1]
     out = torch.empty(tuple(c.shape[:-1]) + (C * 8,), dtype=torch.float32, device=device)
     if scales is None:
-        _lib.call("keep_e8p_decode", c.data_ptr(), c.numel(), cb.data_ptr(), None, 0, 1, 1, out.data_ptr(),
-                  _stream(device))
+        _lib.call(fn, c.data_ptr(), c.numel(), cb.data_ptr(), None, 0, 1, 1, out.data_ptr(), _stream(device))
         return out
     s = _to_dev(scales, device)
     G = s.shape[-1]
@@ -442,8 +454,8 @@ def decode_weight_matrix(codes, scales=None, *, code_bits: int = 16, codebook=No
         raise ValueError("codeword count must be divisible by scale count")
     if tuple(s.shape[:-1]) != tuple(c.shape[:-1]):
         raise ValueError(f"scales leading shape {tuple(s.shape[:-1])} must match codes {tuple(c.shape[:-1])}")
-    _lib.call("keep_e8p_decode", c.data_ptr(), c.numel(), cb.data_ptr(), s.data_ptr(), _dtype_code(s, "scales"), C,
-              C // G, out.data_ptr(), _stream(device))
+    _lib.call(fn, c.data_ptr(), c.numel(), cb.data_ptr(), s.data_ptr(), _dtype_code(s, "scales"), C, C // G,
+              out.data_ptr(), _stream(device))
     return out
 
 
@@ -696,8 +708,11 @@ def verify_m_rows(route_count: int, top_k: int) -> int:
 def gather_vqmm_verify_rows(x, codes, scales, codebook, rhs_indices, *, lhs_indices=None, input_dims: int,
                             output_dims: int, group_size: int = 512, grouping: str = "flat",
                             m_rows: int | str = "auto", rows_per_threadgroup: int | str = "auto") -> torch.Tensor:
-    """Wide-M verify pass over E8P routed experts (reference ``vq_switch.py:286-377``).
+    """Wide-M verify pass over routed experts (reference ``vq_switch.py:286-377``).
 
+    The code format follows ``codes``' dtype: uint8 codes index a packed 8-bit
+    E8 table (the reference kernel's contract, ``gather_vqmm.py:387-388``;
+    default ``codebook`` the E8 table), uint16 codes are E8P.
     ``grouping="flat"``: one launch, every route on the decode mat-vec.
     ``grouping="expert"``: routes sorted by expert on the device and folded in
     tiles of up to ``m_rows`` same-expert routes that share every code load;
@@ -713,7 +728,7 @@ def gather_vqmm_verify_rows(x, codes, scales, codebook, rhs_indices, *, lhs_indi
     if xt.ndim != 2:
         raise ValueError(f"x must be 2D [rows, input_dims], found {tuple(xt.shape)}")
     rhs = _index_tensor(rhs_indices, device)
-    code_bits = 16
+    code_bits = _code_bits_of(codes)
     c = _codes_tensor(codes, code_bits, device)
     s = _to_dev(scales, device)
     cb = _codebook_tensor(codebook, code_bits, device)
@@ -745,19 +760,19 @@ def gather_vqmm_verify_rows(x, codes, scales, codebook, rhs_indices, *, lhs_indi
             raise ValueError(f"m_rows must be one of {VERIFY_MROWS_VALUES}")
         mr = int(m_rows)
     _trace(token_rows=int(xt.shape[0]), route_count=int(R), has_lhs_indices=lhs_indices is not None,
-           input_dims=int(input_dims), output_dims=int(output_dims), group_size=int(group_size), code_bits=16,
-           strategy=f"verify_{grouping}", implementation="hip_matvec")
+           input_dims=int(input_dims), output_dims=int(output_dims), group_size=int(group_size),
+           code_bits=code_bits, strategy=f"verify_{grouping}", implementation="hip_matvec")
     if grouping == "flat":
         y = routed_matvec(xt, c, s, cb, flat_rhs, lhs=flat_lhs, input_dims=input_dims, output_dims=output_dims,
-                          group_size=group_size)
+                          group_size=group_size, code_bits=code_bits)
         return y.reshape(out_shape)
     order, inverse, _, _, te, to, tc, _ = route_plan(flat_rhs, E, mr)
     sorted_lhs = flat_lhs[order.long()].contiguous()
     routed = torch.empty((R, output_dims), dtype=output_dtype(xt.dtype), device=device)
-    _lib.call("keep_vq_matvec_tiles", xt.data_ptr(), _dtype_code(xt, "x"), xt.shape[0], c.data_ptr(), s.data_ptr(),
-              _dtype_code(s, "scales"), cb.data_ptr(), sorted_lhs.data_ptr(), R, te.data_ptr(), to.data_ptr(),
-              tc.data_ptr(), te.numel(), mr, E, output_dims, input_dims, group_size, routed.data_ptr(),
-              _DT[routed.dtype], _stream(device))
+    _lib.call("keep_vq_matvec_tiles", xt.data_ptr(), _dtype_code(xt, "x"), xt.shape[0], c.data_ptr(), code_bits,
+              s.data_ptr(), _dtype_code(s, "scales"), cb.data_ptr(), sorted_lhs.data_ptr(), R, te.data_ptr(),
+              to.data_ptr(), tc.data_ptr(), te.numel(), mr, E, output_dims, input_dims, group_size,
+              routed.data_ptr(), _DT[routed.dtype], _stream(device))
     return routed[inverse.long()].reshape(out_shape)
 
 

@@ -79,8 +79,6 @@ def test_other_entry_points_validate():
     assert b"E must be" in lib.keep_last_error()
     assert lib.keep_route_plan(1, 10, 4, 4, 1, 1, 1, 1, 1, 1, 1, 2, 1, None) == -1
     assert b"max_tiles" in lib.keep_last_error()
-    assert lib.keep_vq_grouped_gemm(16, 0, 1, None, 16, 16, 1, 16, 1, 1, 1, 1, 1, 1, 16, 256, 256, 16, 1, None) == -1
-    assert b"fp16 or bf16" in lib.keep_last_error()
     assert lib.keep_moe_decode(16, 1, 1, 4096, 2048, 1, 1, 6, 384, 16, 16, 16, 16, 16, 16, 1, 100, 2048, 16, None,
                                0.0, 16, 16, 1, None) == -1
     assert b"group_size_h" in lib.keep_last_error()

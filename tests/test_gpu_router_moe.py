@@ -163,6 +163,54 @@ def test_verify_rows_expert_grouping_bit_identical_to_flat(dev, M):
     _check(flat, want)
 
 
+def _verify_routes(pattern, M, k, E, rng):
+    """Verify-row routing patterns of increasing same-expert overlap (as the
+    reference's tests/test_gather_vqmm_verify_rows.py:_routes)."""
+    if pattern == "uniform":
+        return rng.integers(0, E, size=(M, k), dtype=np.int32)
+    if pattern == "skewed":
+        return rng.integers(0, max(2, E // 3), size=(M, k), dtype=np.int32)
+    if pattern == "duplicate":
+        return np.tile(rng.choice(E, size=k, replace=False).astype(np.int32), (M, 1))
+    return np.zeros((M, k), dtype=np.int32)  # single expert: full tiles, then a partial tail
+
+
+@pytest.mark.parametrize("M,pattern,xdt", [(2, "uniform", torch.float16), (8, "skewed", torch.bfloat16),
+                                           (8, "duplicate", torch.float32), (33, "single_expert", torch.float16),
+                                           (64, "uniform", torch.bfloat16)])
+def test_verify_rows_uint8_codes(dev, M, pattern, xdt):
+    """The reference verify operator's own format: uint8 codes indexing the
+    packed 8-bit E8 table (gather_vqmm.py:387-388). Expert grouping is bit
+    identical to flat and to the M = 1 gather run per verify row; both match the
+    dense 8-bit decode (oracle) within 2e-3. N = 93 leaves a ragged row block."""
+    E, N, K, k, G = 8, 93, 1024, 6, 512
+    rng = np.random.default_rng(M)
+    codes = torch.from_numpy(rng.integers(0, 256, size=(E, N, K // 8), dtype=np.uint8)).to(dev)
+    scales = torch.from_numpy(np.exp(rng.normal(0, 0.3, size=(E, N, K // G))).astype(np.float16)).to(dev)
+    x = synth.rht_activations(M, K, seed=M + 7, device=dev).to(xdt)
+    rhs = torch.from_numpy(_verify_routes(pattern, M, k, E, rng)).to(dev)
+    flat = keep_amd.gather_vqmm_verify_rows(x, codes, scales, None, rhs, input_dims=K, output_dims=N,
+                                            group_size=G, grouping="flat")
+    for mr in (1, 4, 8):
+        grouped = keep_amd.gather_vqmm_verify_rows(x, codes, scales, None, rhs, input_dims=K, output_dims=N,
+                                                   group_size=G, grouping="expert", m_rows=mr)
+        assert torch.equal(flat, grouped), f"expert grouping (m_rows={mr}) differs from flat"
+    for t in range(M):
+        one = keep_amd.gather_vqmm(x[t:t + 1], codes, scales, None, rhs[t:t + 1], input_dims=K, output_dims=N,
+                                   group_size=G, code_bits=8)
+        assert torch.equal(one[0], flat[t]), f"verify row {t} differs from the M = 1 gather"
+    r = rhs.cpu().numpy()
+    c_np, s_np = codes.cpu().numpy(), scales.float().cpu().numpy()
+    xf = x.float().cpu().numpy().astype(np.float64)
+    want = np.zeros((M, k, N))
+    for e in np.unique(r):
+        W = ops.dense(c_np[e], s_np[e], code_bits=8)
+        for t, j in zip(*np.nonzero(r == e)):
+            want[t, j] = W @ xf[t]
+    assert flat.dtype == xdt  # the output takes x's dtype, as the reference kernel's OUT_T
+    _check(flat, want, {torch.bfloat16: TOL_BF16_OUT, torch.float16: TOL + 2.0 ** -11}.get(xdt, TOL))
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 def test_moe_decode_small_vs_oracle(dev, xdt):
     E, H, I, k, T = 16, 512, 256, 4, 3
