@@ -369,6 +369,33 @@ int keep_route_combine(const float* y, const float* w, int64_t T, int64_t k, int
 int keep_rht(const void* x, int x_dtype, const float* signs, int inverse, int64_t T, int64_t n, void* out,
              int out_dtype, void* stream);
 
+/* The steps in front of the routed experts, one row pass per token (rows of
+ * n = 64..8192 values, a power of two):
+ *   y = round_x(gamma * (x / sqrt(mean(x^2) + eps)))   RMSNorm in fp32, rounded to
+ *       x's dtype (gamma NULL: 1); written to `normed` (x's dtype) when non-null
+ *       (the router's input);
+ *   q = round_x(e4m3(clamp(y / s, +-448)) * s) per quant_block values, s =
+ *       max(amax, 1e-4) / 448, rounded up to a power of two when pow2_scales,
+ *       e4m3 = nearest FP8 e4m3fn value, ties to even (quant_block 0: q = y);
+ *   out = RHT(q, signs) as keep_rht (signs NULL: out = q), in out_dtype.
+ * Replaces the expert-input preparation of the serving step: ffn_norm
+ * (src/ramp/models/deepseek_v4_flash_adapter.py:1792-1807), act_quant
+ * (scripts/runpod/v41_reap/torch_kernel.py:40-53, used at
+ * scripts/v41_build/omlx_lattice.py:332,357) and apply_rht_mx
+ * (src/keep/quant/rht.py:84-91). */
+int keep_rmsnorm_quant_rht(const void* x, int x_dtype, int64_t T, int64_t n, const void* gamma,
+                           int gamma_dtype, float eps, int64_t quant_block, int pow2_scales,
+                           const float* signs, void* normed, void* out, int out_dtype, void* stream);
+
+/* After the routed combine: out[i] = round_out(residual[i] + (routed[i] +
+ * shared[i])) over n values, fp32 sums in that order (shared and residual
+ * optional, any dtype; out may alias routed or residual). The MoE's routed sum
+ * plus the shared expert (src/ramp/models/deepseek_v4_flash_adapter.py:1784;
+ * the serving step's shared down adds the fp32 routed sum and rounds to bf16,
+ * scripts/v41_build/omlx_lattice.py:374-388), with the block's residual add. */
+int keep_moe_combine_add(const float* routed, const void* shared, int shared_dtype, const void* residual,
+                         int residual_dtype, int64_t n, void* out, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,8 @@ _SIGS = {
     "keep_vq_grouped_gemm_q8_workspace_bytes": [c_int64, c_int64],
     "keep_route_combine": [_P, _P, c_int64, c_int64, c_int64, _P, c_int, _P],
     "keep_rht": [_P, c_int, _P, c_int, c_int64, c_int64, _P, c_int, _P],
+    "keep_rmsnorm_quant_rht": [_P, c_int, c_int64, c_int64, _P, c_int, c_float, c_int64, c_int, _P, _P, _P, c_int, _P],
+    "keep_moe_combine_add": [_P, _P, c_int, _P, c_int, c_int64, _P, c_int, _P],
     "keep_e8_1bit_matvec": [_P, c_int, c_int64, _P, _P, c_int, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64,
                             c_int64, _P, c_int, _P],
     "keep_vq_grouped_gemm_q8": [_P, c_int, c_int64, _P, _P, _P, c_int, _P, c_int, _P, _P, _P, _P, c_int64, c_int64,

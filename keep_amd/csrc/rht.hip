@@ -15,6 +15,12 @@
 // padded LDS row to the next pass's arrangement. The first pass loads 16
 // consecutive values (two or four 16-byte loads), the last stores straight to
 // HBM. HBM-bound: n * (in + out bytes) per row.
+//
+// keep_rmsnorm_quant_rht fuses the steps in front of the routed experts into
+// the same row pass: RMSNorm, block-wise FP8 e4m3 activation quantisation
+// (the act_quant of scripts/runpod/v41_reap/torch_kernel.py:40-53, whose
+// values the serving step feeds to the experts, omlx_lattice.py:332,357) and
+// the forward RHT.
 #include <cmath>
 
 #include "common.h"
@@ -70,16 +76,12 @@ __device__ __forceinline__ void store1(void* out, int dt, size_t i, float v) {
   else ((_Float16*)out)[i] = (_Float16)v;
 }
 
+// The passes over the 16 values r[] of thread t (forward signs applied first
+// unless INV), then the store of row `row`.
 template <int L, bool INV>
-__global__ __launch_bounds__(512) void k_rht(const void* x, int xdt, const float* signs, void* out, int odt,
-                                            float scale) {
-  constexpr uint32_t N = 1u << L;
+__device__ __forceinline__ void rht_core(float (&r)[16], float* s, uint32_t t, const float* signs, void* out, int odt,
+                                         size_t row, float scale) {
   constexpr int PASSES = (L + 3) / 4;
-  __shared__ float s[N + N / 16];
-  const uint32_t t = threadIdx.x;
-  const size_t row = (size_t)blockIdx.x * N;
-  float r[16];
-  load16(x, xdt, row + (size_t)t * 16, r);
   if (!INV && signs) {
     const float4* sp = (const float4*)(signs + t * 16);
 #pragma unroll
@@ -123,6 +125,111 @@ __global__ __launch_bounds__(512) void k_rht(const void* x, int xdt, const float
   }
 }
 
+template <int L, bool INV>
+__global__ __launch_bounds__(512) void k_rht(const void* x, int xdt, const float* signs, void* out, int odt,
+                                            float scale) {
+  constexpr uint32_t N = 1u << L;
+  __shared__ float s[N + N / 16];
+  const uint32_t t = threadIdx.x;
+  const size_t row = (size_t)blockIdx.x * N;
+  float r[16];
+  load16(x, xdt, row + (size_t)t * 16, r);
+  rht_core<L, INV>(r, s, t, signs, out, odt, row, scale);
+}
+
+// ------------------------------------------------------------------ RMSNorm + FP8 act-quant (+ RHT)
+
+// v rounded to the row dtype (fp32 rows: unchanged).
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == KEEP_BF16) return to_float(from_float<bf16s>(v));
+  if (dt == KEEP_F16) return (float)(_Float16)v;
+  return v;
+}
+
+// Nearest FP8 e4m3fn value (ties to even) of v, |v| <= 448: 3 mantissa bits
+// for |v| >= 2^-6, a fixed quantum of 2^-9 below (the subnormals).
+__device__ __forceinline__ float e4m3_round(float v) {
+  const float a = fabsf(v);
+  float q;
+  if (a >= 0.015625f) {
+    uint32_t b = __float_as_uint(a);
+    b += 0x7FFFFu + ((b >> 20) & 1u);
+    q = __uint_as_float(b & 0xFFF00000u);
+  } else {
+    q = __builtin_rintf(a * 512.f) * 0.001953125f;
+  }
+  return copysignf(q, v);
+}
+
+// 2^ceil(log2(v)) of a positive normal fp32 v.
+__device__ __forceinline__ float pow2_ceil(float v) {
+  const uint32_t b = __float_as_uint(v);
+  const int e = (int)((b >> 23) & 0xFFu) - 127 + ((b & 0x7FFFFFu) != 0u ? 1 : 0);
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// One row per block, N / 16 threads of 16 consecutive values:
+//   y  = round_T(gamma * (x * (1 / sqrt(mean(x^2) + eps))))      (RMSNorm, fp32 math)
+//   q  = round_T(e4m3(clamp(y / s, +-448)) * s) per qblock values, s = max(amax, 1e-4) / 448
+//        (2^ceil(log2 s) with pow2), qblock = 0: q = y
+//   out = RHT(q, signs) when signs are given, else q.
+// `normed` (optional) receives y in the row dtype.
+template <int L, bool RHT>
+__global__ __launch_bounds__(512) void k_norm_quant(const void* x, int xdt, const void* gamma, int gdt, float eps,
+                                                   int qblock, int pow2, const float* signs, void* normed, void* out,
+                                                   int odt, float scale) {
+  constexpr uint32_t N = 1u << L;
+  constexpr uint32_t NT = N / 16;
+  constexpr uint32_t NW = (NT + 63) / 64;
+  __shared__ float s[N + N / 16];
+  __shared__ float part[NW];
+  const uint32_t t = threadIdx.x;
+  const size_t row = (size_t)blockIdx.x * N;
+  float r[16], g[16];
+  load16(x, xdt, row + (size_t)t * 16, r);
+  if (gamma) load16(gamma, gdt, (size_t)t * 16, g);
+  float ss = 0.f;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) ss = fmaf(r[m], r[m], ss);
+  for (int o = (NT < 64 ? NT : 64) / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);  // live lanes only
+  if (NT >= 64) {
+    if ((t & 63u) == 0u) part[t >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (uint32_t w = 0; w < NW; ++w) ss += part[w];
+  }
+  const float inv = 1.f / sqrtf(ss / (float)N + eps);
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const float v = r[m] * inv;
+    r[m] = round_to(gamma ? g[m] * v : v, xdt);
+  }
+  if (normed) {
+#pragma unroll
+    for (int m = 0; m < 16; ++m) store1(normed, xdt, row + (size_t)t * 16 + m, r[m]);
+  }
+  if (qblock > 0) {
+    float amax = 0.f;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) amax = fmaxf(amax, fabsf(r[m]));
+    for (int o = 1; o < qblock / 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    float sc = fmaxf(amax, 1e-4f) * (1.f / 448.f);
+    if (pow2) sc = pow2_ceil(sc);
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float q = e4m3_round(fminf(fmaxf(r[m] / sc, -448.f), 448.f));
+      r[m] = round_to(q * sc, xdt);
+    }
+  }
+  if constexpr (RHT) {
+    rht_core<L, false>(r, s, t, signs, out, odt, row, scale);
+  } else {
+#pragma unroll
+    for (int m = 0; m < 16; ++m) store1(out, odt, row + (size_t)t * 16 + m, r[m]);
+  }
+}
+
 template <int L>
 void launch_rht(const void* x, int xdt, const float* signs, int inverse, int64_t T, void* out, int odt, float scale,
                 hipStream_t s) {
@@ -163,4 +270,58 @@ extern "C" int keep_rht(const void* x, int x_dtype, const float* signs, int inve
     default: launch_rht<13>(x, x_dtype, signs, inverse, T, out, out_dtype, scale, s); break;
   }
   return launch_status("keep_rht");
+}
+
+namespace {
+
+template <int L>
+void launch_norm_quant(const void* x, int xdt, const void* gamma, int gdt, float eps, int qblock, int pow2,
+                       const float* signs, void* normed, int64_t T, void* out, int odt, float scale, hipStream_t s) {
+  const dim3 grid((unsigned)T), blk((1u << L) / 16);
+  if (signs)
+    hipLaunchKernelGGL((k_norm_quant<L, true>), grid, blk, 0, s, x, xdt, gamma, gdt, eps, qblock, pow2, signs, normed,
+                       out, odt, scale);
+  else
+    hipLaunchKernelGGL((k_norm_quant<L, false>), grid, blk, 0, s, x, xdt, gamma, gdt, eps, qblock, pow2, signs,
+                       normed, out, odt, scale);
+}
+
+}  // namespace
+
+extern "C" int keep_rmsnorm_quant_rht(const void* x, int x_dtype, int64_t T, int64_t n, const void* gamma,
+                                      int gamma_dtype, float eps, int64_t quant_block, int pow2_scales,
+                                      const float* signs, void* normed, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE(dtype_ok(x_dtype) && dtype_ok(out_dtype) && (!gamma || dtype_ok(gamma_dtype)), "bad dtype enum");
+  KEEP_REQUIRE(n >= 64 && n <= (1 << RHT_MAX_LOG) && (n & (n - 1)) == 0,
+               "keep_rmsnorm_quant_rht serves power-of-two rows of 64..8192 values, got %lld", (long long)n);
+  KEEP_REQUIRE(quant_block == 0 || (quant_block >= 16 && quant_block <= 1024 && quant_block <= n &&
+                                    (quant_block & (quant_block - 1)) == 0),
+               "quant_block must be 0 or a power of two in 16..min(1024, n), got %lld", (long long)quant_block);
+  KEEP_REQUIRE(eps >= 0.f, "eps must be non-negative");
+  KEEP_REQUIRE(T >= 0 && T <= 0x7FFFFFFF, "row count out of range");
+  if (T == 0) return KEEP_OK;
+  KEEP_REQUIRE(x && out, "null pointer argument");
+  KEEP_REQUIRE(aligned(x, 16) && aligned(out, 16) && (!gamma || aligned(gamma, 16)) &&
+                   (!signs || aligned(signs, 16)) && (!normed || aligned(normed, 16)),
+               "x, gamma, signs, normed and out must be 16-byte aligned");
+  KEEP_REQUIRE(x != out && x != normed, "keep_rmsnorm_quant_rht does not run in place");
+  const float scale = (float)(1.0 / std::sqrt((double)n));
+  const hipStream_t s = (hipStream_t)stream;
+  const int q = (int)quant_block;
+  int L = 0;
+  while ((int64_t(1) << L) < n) ++L;
+#define NQ(LL) launch_norm_quant<LL>(x, x_dtype, gamma, gamma_dtype, eps, q, pow2_scales, signs, normed, T, out, \
+                                     out_dtype, scale, s)
+  switch (L) {
+    case 6: NQ(6); break;
+    case 7: NQ(7); break;
+    case 8: NQ(8); break;
+    case 9: NQ(9); break;
+    case 10: NQ(10); break;
+    case 11: NQ(11); break;
+    case 12: NQ(12); break;
+    default: NQ(13); break;
+  }
+#undef NQ
+  return launch_status("keep_rmsnorm_quant_rht");
 }

@@ -626,12 +626,19 @@ class RoutedVQMoE:
     ``__call__(x, logits)`` evaluates the residency-biased dual top-k router
     once, then runs the experts: the fused decode pair for few tokens, the
     shared-plan MFMA path for prefill. Returns ``(out [T, H], RouterOutput)``.
+
+    ``shared_experts`` (a one-expert ``QuantizedVQSwitchGLU``, every token on
+    expert 0 with weight 1) adds the shared expert to the routed sum, and
+    ``__call__(..., residual=h)`` adds the residual stream, both in fp32 and
+    rounded once to ``out_dtype`` (``DeepseekV4FlashVQMoE.__call__``,
+    ``deepseek_v4_flash_adapter.py:1777-1784``; ``omlx_lattice.py:374-388``).
     """
 
     def __init__(self, glu: QuantizedVQSwitchGLU, *, top_k: int, score_func: str = "softmax",
                  renormalize: bool = True, route_scale: float = 1.0, swiglu_limit: float = 0.0,
                  bias_served: torch.Tensor | None = None, bias_demand: torch.Tensor | None = None,
-                 tau: float = float("inf"), decode_max_tokens: int = 64, out_dtype=torch.float32):
+                 tau: float = float("inf"), decode_max_tokens: int = 64, out_dtype=torch.float32,
+                 shared_experts: QuantizedVQSwitchGLU | None = None):
         self.glu, self.top_k, self.score_func = glu, top_k, score_func
         self.renormalize, self.route_scale, self.limit = renormalize, route_scale, float(swiglu_limit)
         self.bias_served, self.bias_demand, self.tau = bias_served, bias_demand, tau
@@ -639,16 +646,40 @@ class RoutedVQMoE:
         self.out_dtype = out_dtype
         if glu.activation is None and self.limit > 0:
             glu.activation = LimitedSwiGLU(self.limit)
+        if shared_experts is not None:
+            if shared_experts.num_experts != 1:
+                raise ValueError("shared_experts must be a one-expert QuantizedVQSwitchGLU")
+            if shared_experts.input_dims != glu.input_dims:
+                raise ValueError("shared_experts input dimension must match the routed experts'")
+            if shared_experts.activation is None and self.limit > 0:
+                shared_experts.activation = LimitedSwiGLU(self.limit)
+        self.shared_experts = shared_experts
 
-    def experts(self, x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    def shared(self, x: torch.Tensor) -> torch.Tensor:
+        """The shared expert's output for every row of ``x``, float32 ``[T, H]``."""
+
+        se = self.shared_experts
+        T = x.shape[0]
+        idx = torch.zeros((T, 1), dtype=torch.int32, device=x.device)
+        w = torch.ones((T, 1), dtype=torch.float32, device=x.device)
+        g, u, d = se.gate_proj, se.up_proj, se.down_proj
+        if (T <= self.decode_max_tokens and se._all_e8p() and se.hot_tier is None
+                and x.dtype in (torch.float16, torch.bfloat16)):
+            return moe_decode(x, idx, w, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
+                              limit=self.limit, codebook=g.codebook, out_dtype=torch.float32)
+        return se(x, idx).reshape(T, -1).float()
+
+    def experts(self, x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, *,
+                out_dtype: torch.dtype | None = None) -> torch.Tensor:
         g, u, d = self.glu.gate_proj, self.glu.up_proj, self.glu.down_proj
+        od = out_dtype or self.out_dtype
         T = x.shape[0]
         if (T <= self.decode_max_tokens and self.glu._all_e8p() and self.glu.hot_tier is None
                 and x.dtype in (torch.float16, torch.bfloat16)):
             return moe_decode(x, idx, weight, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
-                              limit=self.limit, codebook=g.codebook, out_dtype=self.out_dtype)
+                              limit=self.limit, codebook=g.codebook, out_dtype=od)
         y = self.glu(x, idx)  # [T, k, H]
-        return ops.route_combine(y, weight, self.out_dtype)
+        return ops.route_combine(y, weight, od)
 
     def _layer_path(self, x: torch.Tensor) -> bool:
         g, d = self.glu.gate_proj, self.glu.down_proj
@@ -659,15 +690,23 @@ class RoutedVQMoE:
                 moe_layer_supported(g.num_experts, g.input_dims, g.output_dims, self.top_k,
                                     g.input_dims // g.scales.shape[-1], d.input_dims // d.scales.shape[-1]))
 
-    def __call__(self, x: torch.Tensor, logits: torch.Tensor):
+    def __call__(self, x: torch.Tensor, logits: torch.Tensor, *, residual: torch.Tensor | None = None):
+        extra = self.shared_experts is not None or residual is not None
+        od = torch.float32 if extra else self.out_dtype
         if self._layer_path(x):
             g, u, d = self.glu.gate_proj, self.glu.up_proj, self.glu.down_proj
-            return moe_layer(x, logits, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
-                             k=self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
-                             score_func=self.score_func, renormalize=self.renormalize,
-                             route_scale=self.route_scale, tau=self.tau, limit=self.limit, codebook=g.codebook,
-                             out_dtype=self.out_dtype, hot_tier=self.glu.hot_tier)
-        r = router_dual_topk(logits, self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
-                             score_func=self.score_func, renormalize=self.renormalize, route_scale=self.route_scale,
-                             tau=self.tau)
-        return self.experts(x, r.idx, r.weight), r
+            out, r = moe_layer(x, logits, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
+                               k=self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
+                               score_func=self.score_func, renormalize=self.renormalize,
+                               route_scale=self.route_scale, tau=self.tau, limit=self.limit, codebook=g.codebook,
+                               out_dtype=od, hot_tier=self.glu.hot_tier)
+        else:
+            r = router_dual_topk(logits, self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
+                                 score_func=self.score_func, renormalize=self.renormalize,
+                                 route_scale=self.route_scale, tau=self.tau)
+            out = self.experts(x, r.idx, r.weight, out_dtype=od)
+        if not extra:
+            return out, r
+        from keep_amd.block import combine_add
+        sh = self.shared(x) if self.shared_experts is not None else None
+        return combine_add(out, sh, residual, self.out_dtype), r
