@@ -146,7 +146,7 @@ def main() -> int:
 
     def router(i):
         _lib.check(lib.keep_router_dual_topk(logits[i].data_ptr(), 1, E, K_TOP, None, None, 0, 1, 1.0,
-                                             float("inf"), idx[i].data_ptr(), w[i].data_ptr(), want[i].data_ptr(),
+                                             float("inf"), None, 0, idx[i].data_ptr(), w[i].data_ptr(), want[i].data_ptr(),
                                              want_s[i].data_ptr(), admit[i].data_ptr(), stream.cuda_stream),
                    "router")
 
@@ -168,7 +168,7 @@ def main() -> int:
         down_(i)
 
     def layer1(i):  # the whole layer: router + gate/up in one launch, down in a second
-        _lib.check(lib.keep_moe_layer(logits[i].data_ptr(), None, None, 0, 1, 1.0, float("inf"), E, K_TOP,
+        _lib.check(lib.keep_moe_layer(logits[i].data_ptr(), None, None, 0, 1, 1.0, float("inf"), None, 0, E, K_TOP,
                                       x.data_ptr(), F16, H, I, gate.codes.data_ptr(), gate.scales.data_ptr(),
                                       up.codes.data_ptr(), up.scales.data_ptr(), down.codes.data_ptr(),
                                       down.scales.data_ptr(), F16, H, I, prep.data_ptr(), 0.0, idx1[i].data_ptr(),

@@ -109,12 +109,19 @@ int keep_vq_matvec_tiles(const void* x, int x_dtype, int64_t x_rows,
  * top-k of scores + bias_demand with raw scores; admit[t, j] = want absent and
  * its normalised demand weight >= tau. Ties: larger key, then lower index.
  * bias_* may be NULL (zeros); want/want_score/admit may be NULL.
+ * slot_map (int32 [E], NULL: none): the pool holds num_slots rows, expert e in
+ * row slot_map[e]; the served idx are then rows (-1 for an entry outside
+ * [0, num_slots)), as the serving router writes slot_of[chosen] (the demand
+ * outputs stay expert ids). Callers map absent experts to any row (their
+ * weight is 0); the same holds for every routed layer below that takes a
+ * slot map, whose pools (codes, scales, hot_of_slot) are then per row.
  * Replaces MoEGate._expert_select (src/ramp/models/deepseek_v4_flash_adapter.py:923-940),
  * gate_masked (scripts/runpod/v41_reap/local_eval.py:69-91) and the dual top-k
  * kernel _TOPK (scripts/v41_build/omlx_lattice.py:77-97). */
 int keep_router_dual_topk(const float* logits, int64_t T, int64_t E, int64_t k,
                           const float* bias_served, const float* bias_demand,
                           int score_func, int renormalize, float route_scale, float tau,
+                          const int32_t* slot_map, int64_t num_slots,
                           int32_t* idx, float* w, int32_t* want, float* want_score,
                           uint8_t* admit, void* stream);
 
@@ -202,6 +209,7 @@ int keep_moe_layer_supported(int64_t num_experts, int64_t H, int64_t I, int64_t 
                              int64_t group_size_h, int64_t group_size_i);
 int keep_moe_layer(const float* logits, const float* bias_served, const float* bias_demand,
                    int score_func, int renormalize, float route_scale, float tau,
+                   const int32_t* slot_map, int64_t num_slots,
                    int64_t num_experts, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
                    const uint16_t* gate_codes, const void* gate_scales,
                    const uint16_t* up_codes, const void* up_scales,
@@ -221,6 +229,7 @@ int keep_moe_layer(const float* logits, const float* bias_served, const float* b
  * keep_moe_layer, bit for bit. */
 int keep_moe_layer_noalloc(const float* logits, const float* bias_served, const float* bias_demand,
                            int score_func, int renormalize, float route_scale, float tau,
+                           const int32_t* slot_map, int64_t num_slots,
                            int64_t num_experts, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
                            const uint16_t* gate_codes, const void* gate_scales,
                            const uint16_t* up_codes, const void* up_scales,
@@ -248,6 +257,7 @@ int64_t keep_moe_layer1_workspace_bytes(int64_t k, int64_t I);
 int keep_moe_layer1_status(const void* workspace, uint32_t* status, void* stream);
 int keep_moe_layer1(const float* logits, const float* bias_served, const float* bias_demand,
                     int score_func, int renormalize, float route_scale, float tau,
+                    const int32_t* slot_map, int64_t num_slots,
                     int64_t num_experts, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
                     const uint16_t* gate_codes, const void* gate_scales,
                     const uint16_t* up_codes, const void* up_scales,
@@ -272,6 +282,7 @@ int keep_e8_1bit_image_bytes(void);
 int keep_e8_1bit_image(const uint32_t* packed_table, void* image, void* stream);
 int keep_moe_layer_nested(const float* logits, const float* bias_served, const float* bias_demand,
                           int score_func, int renormalize, float route_scale, float tau,
+                          const int32_t* slot_map, int64_t num_slots,
                           int64_t num_experts, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
                           const uint16_t* gate_codes, const void* gate_scales,
                           const uint16_t* up_codes, const void* up_scales,

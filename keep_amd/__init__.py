@@ -30,10 +30,11 @@ from keep_amd.ops import (
     vq_qmm,
     vq_qmv,
 )
+from keep_amd.residency import ResidencyCache, ResidencyPolicy, residual_cache
 from keep_amd.router import expert_select, resident_bias, router_dual_topk
 
 __all__ = [
-    "HotTier", "LimitedSwiGLU", "combine_add", "rmsnorm_quant_rht", "QuantizedVQLinear", "QuantizedVQSwitchGLU", "QuantizedVQSwitchLinear", "RoutedVQMoE", "decode_e8p",
+    "HotTier", "LimitedSwiGLU", "ResidencyCache", "ResidencyPolicy", "residual_cache", "combine_add", "rmsnorm_quant_rht", "QuantizedVQLinear", "QuantizedVQSwitchGLU", "QuantizedVQSwitchLinear", "RoutedVQMoE", "decode_e8p",
     "decode_weight_matrix", "e8_1bit_m1_per_route", "e8_1bit_m1_token_layout", "e8_1bit_packed", "e8p_m1_per_route",
     "e8p_m1_token_layout", "e8p_nested_m1_per_route", "e8p_nested_m1_token_layout", "e8p_packed_abs_grid",
     "expert_select", "gather_vqmm", "gather_vqmm_sorted_routes", "gather_vqmm_verify_rows", "half2_pairs",

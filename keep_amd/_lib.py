@@ -31,8 +31,8 @@ _SIGS = {
                        c_int64, c_int64, _P, _P, c_int64, _P, _P, c_int64, _P, c_int, _P],
     "keep_vq_matvec_tiles": [_P, c_int, c_int64, _P, c_int, _P, c_int, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64,
                              c_int64, c_int64, c_int64, c_int64, _P, c_int, _P],
-    "keep_router_dual_topk": [_P, c_int64, c_int64, c_int64, _P, _P, c_int, c_int, c_float, c_float, _P, _P, _P,
-                              _P, _P, _P],
+    "keep_router_dual_topk": [_P, c_int64, c_int64, c_int64, _P, _P, c_int, c_int, c_float, c_float, _P, c_int64, _P,
+                              _P, _P, _P, _P, _P],
     "keep_route_plan": [_P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P],
     "keep_moe_decode": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
                         c_int, c_int64, c_int64, _P, _P, c_float, _P, _P, c_int, _P],
@@ -54,21 +54,21 @@ _SIGS = {
     "keep_moe_gateup": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, c_int,
                         c_int64, _P, _P, c_float, _P, _P],
     "keep_moe_layer_supported": [c_int64, c_int64, c_int64, c_int64, c_int64, c_int64],
-    "keep_moe_layer": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64, c_int64,
-                       _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P, _P,
-                       c_int, _P],
-    "keep_moe_layer_noalloc": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64,
-                               c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P,
-                               _P, _P, c_int, _P],
-    "keep_moe_layer1": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64, c_int64,
-                        _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P,
+    "keep_moe_layer": [_P, _P, _P, c_int, c_int, c_float, c_float, _P, c_int64, c_int64, c_int64, _P, c_int, c_int64,
+                       c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P,
+                       _P, c_int, _P],
+    "keep_moe_layer_noalloc": [_P, _P, _P, c_int, c_int, c_float, c_float, _P, c_int64, c_int64, c_int64, _P, c_int,
+                               c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P,
+                               _P, _P, _P, _P, c_int, _P],
+    "keep_moe_layer1": [_P, _P, _P, c_int, c_int, c_float, c_float, _P, c_int64, c_int64, c_int64, _P, c_int, c_int64,
+                        c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P,
                         c_int64, _P, c_int, _P],
     "keep_moe_layer1_workspace_bytes": [c_int64, c_int64],
     "keep_moe_layer1_status": [_P, _P, _P],
-    "keep_moe_layer_nested": [_P, _P, _P, c_int, c_int, c_float, c_float, c_int64, c_int64, _P, c_int, c_int64,
-                              c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P,
-                              _P, _P, _P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, _P,
-                              _P],
+    "keep_moe_layer_nested": [_P, _P, _P, c_int, c_int, c_float, c_float, _P, c_int64, c_int64, c_int64, _P, c_int,
+                              c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P,
+                              _P, _P, _P, _P, _P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64,
+                              _P, _P, _P],
     "keep_e8_1bit_image": [_P, _P, _P],
     "keep_e8_1bit_image_bytes": [],
     "keep_moe_down": [c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, c_int, c_int64, _P, _P, _P,

@@ -45,6 +45,8 @@ struct FLArgs {
   int func, renorm, same_bias;
   float route_scale, tau;
   int32_t E, k;
+  const int32_t* slot_map;  // expert -> pool row (null: the pool holds every expert)
+  int32_t S;                // pool rows
   int32_t* idx_out;
   float* w_out;
   int32_t* want_out;
@@ -123,7 +125,9 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
   //    0 and 1)
   const uint32_t ep = __builtin_amdgcn_readfirstlane((uint32_t)(fl_load((uint64_t*)a.hdr) & 0xffffffffu));
   float z[PER], bsv[PER], bdv[PER];
+  int sm[PER];
   if (wv == 0) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
+  if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, a.E, lane, sm);
   const uint32_t te = threadIdx.x >> 2;
   const uint2 tv = a.tq[te], mv = a.tq[256 + te];
   const uint4 xc = ldg16_q((const uint4*)a.x + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
@@ -140,7 +144,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
   // 1. served routing (wave 0) | A terms: rows 0-2 of slice w are the three
   //    int8 terms of x s, s the slice's power of two
   float sc[PER];
-  int e_sel = -1;
+  int e_sel = -1, sl = -1;
   auto build = [&](uint4 c, int slice) {
     float v[4];
     if (a.xbf) q8_half4<true>(c, lane & 1, v);
@@ -157,7 +161,8 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
   };
   if (wv == 0) {
     e_sel = rt_select_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, true, 0, lane, sc);
-    if (lane < a.k) s_idx[lane] = e_sel >= 0 && e_sel < a.E ? e_sel : -1;
+    sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+    if (lane < a.k) s_idx[lane] = sl;
   } else if (wv >= 2) {
     build(xc, wv);
     if (wv < 4) build(xc2, wv - 2);
@@ -173,7 +178,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
     const uint32_t q0 = (valid ? qt : 0u) * 16u;
     const uint32_t route = q0 / (uint32_t)a.I;
     const int32_t e = s_idx[route];
-    const bool ok = valid && e >= 0 && e < a.E;
+    const bool ok = valid && e >= 0 && e < a.S;
     rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
   }
   const uint32_t grp = G1 ? 0u : (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
@@ -208,7 +213,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
     const RouteLane r = rt_finish<PER>(e_sel, true, sc, bsv, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
     if (lane < a.k) s_w[lane] = r.valid ? r.value : 0.f;
     if (b == 0 && r.valid) {
-      a.idx_out[lane] = r.expert;
+      a.idx_out[lane] = sl;  // the pool row (the expert itself without a slot map)
       a.w_out[lane] = r.value;
     }
   }
@@ -255,7 +260,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
     const int route = rg * RPW + r;
     const int32_t e = route < a.k ? s_idx[route] : -1;
     dlive[r] = dwave && route < a.k;
-    dbase[r] = (e >= 0 && e < a.E ? (uint32_t)e * 4096u : 0u) + b * 16u;
+    dbase[r] = (e >= 0 && e < a.S ? (uint32_t)e * 4096u : 0u) + b * 16u;
   }
   const uint32_t dgrp = (uint32_t)(sd * 256) / (uint32_t)a.gsz_i;
   ScaleRaw srd[RPW];
@@ -293,7 +298,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
       usum *= scale_cvt(sr[1], a.sdt, rb + jj);
     }
     float hv = silu_mul(gsum, usum, a.limit);
-    if (*a.tq_bad || e < 0 || e >= a.E) hv = __builtin_nanf("");
+    if (*a.tq_bad || e < 0 || e >= a.S) hv = __builtin_nanf("");
     const uint32_t hb = from_float<bf16s>(hv).bits;
     const uint32_t hb2 = (uint32_t)__shfl((int)hb, lane ^ 2, 64);
     if (valid && (jj & 2u) == 0u) {
@@ -425,7 +430,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
       if (r < a.k) {
         const int32_t e = s_idx[r];
         const float wt = s_w[r];
-        const bool ok = e >= 0 && e < a.E;
+        const bool ok = e >= 0 && e < a.S;
         bad |= wt != 0.f && !ok;
         float v = 0.f;
 #pragma unroll
@@ -496,7 +501,7 @@ static bool fl_dispatch(const FLArgs& a, hipStream_t s) {
 }
 
 void fl_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm, float route_scale,
-               float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t I, const uint16_t* gc,
+               float tau, const int32_t* slot_map, int64_t S, int64_t E, int64_t k, const void* x, int x_dtype, int64_t I, const uint16_t* gc,
                const void* gs, const uint16_t* uc, const void* us, const uint16_t* dc, const void* ds, int sdt,
                int64_t group_h, int64_t group_i, const void* prepared, float limit, int32_t* idx, float* w,
                int32_t* want, float* want_score, uint8_t* admit, void* workspace, uint32_t spin_ticks, void* out,
@@ -504,6 +509,7 @@ void fl_launch(const float* logits, const float* bias_s, const float* bias_d, in
   FLArgs a{};
   a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
   a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
+  a.slot_map = slot_map; a.S = (int32_t)(slot_map ? S : E);
   a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
   a.x = x; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.dc = dc; a.gs = gs; a.us = us; a.ds = ds; a.sdt = sdt;
   a.Gh = (int32_t)(4096 / group_h); a.gsz_h = (int32_t)group_h;
@@ -546,7 +552,8 @@ extern "C" int keep_moe_layer1_status(const void* workspace, uint32_t* status, v
 }
 
 extern "C" int keep_moe_layer1(const float* logits, const float* bias_served, const float* bias_demand,
-                               int score_func, int renormalize, float route_scale, float tau, int64_t E, int64_t k,
+                               int score_func, int renormalize, float route_scale, float tau,
+                               const int32_t* slot_map, int64_t num_slots, int64_t E, int64_t k,
                                const void* x, int x_dtype, int64_t H, int64_t I, const uint16_t* gate_codes,
                                const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
                                const uint16_t* down_codes, const void* down_scales, int scale_dtype,
@@ -562,6 +569,8 @@ extern "C" int keep_moe_layer1(const float* logits, const float* bias_served, co
                "shape not served by the one-launch decode layer (needs H = 4096, I a multiple of 512 up to 2048, "
                "k <= 8, E <= 1024, scale groups of 256-element multiples)");
   KEEP_REQUIRE(fl_device_ok(), "the one-launch decode layer needs %d compute units", FL_BLOCKS);
+  KEEP_REQUIRE(!slot_map || (num_slots >= 1 && num_slots <= 0x7fffffffLL / (I * 512)),
+               "num_slots out of range");
   KEEP_REQUIRE(logits && x && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
                    prepared && idx && w && workspace && out,
                "null pointer argument");
@@ -570,9 +579,9 @@ extern "C" int keep_moe_layer1(const float* logits, const float* bias_served, co
   KEEP_REQUIRE(aligned(x, 16) && aligned(workspace, 256) && aligned(prepared, 16),
                "x and prepared must be 16-byte aligned, the workspace 256-byte aligned");
   KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 16), "codes misaligned");
-  fl_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype, I,
-            gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype, group_size_h,
-            group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, workspace, 20000u, out, out_dtype,
-            (hipStream_t)stream);
+  fl_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, slot_map, num_slots, E, k, x,
+            x_dtype, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
+            group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, workspace, 20000u,
+            out, out_dtype, (hipStream_t)stream);
   return launch_status("keep_moe_layer1");
 }

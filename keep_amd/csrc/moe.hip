@@ -892,7 +892,8 @@ void moe_v3_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t H
 void tq_build(const uint32_t* table, void* prepared, hipStream_t s);
 bool moe_q_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i);
 int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm,
-                        float route_scale, float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H,
+                        float route_scale, float tau, const int32_t* slot_map, int64_t S, int64_t E, int64_t k,
+                        const void* x, int x_dtype, int64_t H,
                         int64_t I, const uint16_t* gc, const void* gs, const uint16_t* uc, const void* us,
                         const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
                         const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
@@ -922,7 +923,8 @@ extern "C" int keep_moe_layer_supported(int64_t E, int64_t H, int64_t I, int64_t
 }
 
 extern "C" int keep_moe_layer(const float* logits, const float* bias_served, const float* bias_demand, int score_func,
-                              int renormalize, float route_scale, float tau, int64_t E, int64_t k, const void* x,
+                              int renormalize, float route_scale, float tau, const int32_t* slot_map,
+                              int64_t num_slots, int64_t E, int64_t k, const void* x,
                               int x_dtype, int64_t H, int64_t I, const uint16_t* gate_codes, const void* gate_scales,
                               const uint16_t* up_codes, const void* up_scales, const uint16_t* down_codes,
                               const void* down_scales, int scale_dtype, int64_t group_size_h, int64_t group_size_i,
@@ -937,14 +939,15 @@ extern "C" int keep_moe_layer(const float* logits, const float* bias_served, con
   KEEP_REQUIRE(moe_q_layer_supported(E, H, I, k, group_size_h, group_size_i),
                "shape not served by the routed decode layer kernels (needs H = 4096, I a multiple of 512 up to "
                "2048, k <= 8, E <= 1024, scale groups of 256-element multiples)");
+  KEEP_REQUIRE(!slot_map || (num_slots >= 1 && num_slots <= 1024), "num_slots must be in 1..1024");
   KEEP_REQUIRE(logits && x && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
                    prepared && idx && w && h_work && out,
                "null pointer argument");
   KEEP_REQUIRE(aligned(x, 16) && aligned(h_work, 16) && aligned(prepared, 16),
                "x, h_work and prepared must be 16-byte aligned");
   KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 8), "codes misaligned");
-  moe_q_layer_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype,
-                      H, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
+  moe_q_layer_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, slot_map, num_slots,
+                      E, k, x, x_dtype, H, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
                       group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, h_work,
                       out, out_dtype, (hipStream_t)stream);
   return launch_status("keep_moe_layer");
@@ -988,8 +991,8 @@ static void* noalloc_scratch() {
 }
 
 extern "C" int keep_moe_layer_noalloc(const float* logits, const float* bias_served, const float* bias_demand,
-                                      int score_func, int renormalize, float route_scale, float tau, int64_t E,
-                                      int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
+                                      int score_func, int renormalize, float route_scale, float tau,
+                                      const int32_t* slot_map, int64_t num_slots, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
                                       const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
                                       const void* up_scales, const uint16_t* down_codes, const void* down_scales,
                                       int scale_dtype, int64_t group_size_h, int64_t group_size_i,
@@ -1001,7 +1004,8 @@ extern "C" int keep_moe_layer_noalloc(const float* logits, const float* bias_ser
                (long long)NOALLOC_H_ELEMS, (long long)(k * I));
   void* h = noalloc_scratch();
   if (!h) return KEEP_ELAUNCH;
-  return keep_moe_layer(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype,
+  return keep_moe_layer(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, slot_map,
+                        num_slots, E, k, x, x_dtype,
                         H, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
                         group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, h, out,
                         out_dtype, stream);

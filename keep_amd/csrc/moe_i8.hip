@@ -79,6 +79,8 @@ struct MQLayer {
   int func, renorm, same_bias;
   float route_scale, tau;
   int32_t E, k;
+  const int32_t* slot_map;  // expert -> pool row (null: the pool holds every expert)
+  int32_t S;                // pool rows
   int32_t* idx_out;
   float* w_out;
   int32_t* want_out;
@@ -127,7 +129,9 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   //    DMAs 4 KiB) and the token slices this wave builds A terms for (16
   //    bytes per lane pair): wave w >= 2 slice w, waves 2 and 3 also slices 0, 1
   float z[PER], bsv[PER], bdv[PER];
+  int sm[PER];
   if (wv < 2) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
+  if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, a.E, lane, sm);
 #pragma unroll
   for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
   if constexpr (RES) {
@@ -135,8 +139,8 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     for (int u = 0; u < 2; ++u) dma16_q(a.n.t8 + (wv * 2 + u) * 64 + lane, t8s + (wv * 2 + u) * 64);
     if (wv >= 2) {  // hot[0 .. E): 64 entries per wave, waves 2 and 3 also 896 ..
       const int i0 = (wv - 2) * 64;
-      dma4_q(a.n.hot + min(i0 + lane, a.E - 1), (uint32_t*)s_hot + i0);
-      if (wv < 4 && a.E > 896) dma4_q(a.n.hot + min(896 + i0 + lane, a.E - 1), (uint32_t*)s_hot + 896 + i0);
+      dma4_q(a.n.hot + min(i0 + lane, a.S - 1), (uint32_t*)s_hot + i0);
+      if (wv < 4 && a.S > 896) dma4_q(a.n.hot + min(896 + i0 + lane, a.S - 1), (uint32_t*)s_hot + 896 + i0);
     }
   }
   const uint4 xc = ldg16_q((const uint4*)a.x + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   // 1. routing (waves 0, 1) | A terms: rows 0-2 of slice w are the three int8
   //    terms of x s, s the slice's power of two (1 / (4 s) kept for the epilogue)
   float sc[PER];
-  int e_sel = -1;
+  int e_sel = -1, sl = -1;
   auto build = [&](uint4 c, int slice) {
     float v[4];
     q8_half4<XBF>(c, lane & 1, v);
@@ -162,7 +166,10 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   };
   if (wv < 2) {
     e_sel = rt_select_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, a.same_bias != 0, wv, lane, sc);
-    if (wv == 0 && lane < a.k) s_idx[lane] = e_sel >= 0 && e_sel < a.E ? e_sel : -1;
+    if (wv == 0) {
+      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+      if (lane < a.k) s_idx[lane] = sl;
+    }
   } else {
     build(xc, wv);
     if (wv < 4) build(xc2, wv - 2);
@@ -180,7 +187,7 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     const uint32_t q0 = (valid ? qt : 0u) * 16u;
     const uint32_t route = q0 / (uint32_t)a.I;
     const int32_t e = s_idx[route];
-    const bool ok = valid && e >= 0 && e < a.E;
+    const bool ok = valid && e >= 0 && e < a.S;
     rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
     if constexpr (RES) {
       const int32_t hr = __builtin_amdgcn_readfirstlane(ok ? s_hot[e] : -1);
@@ -225,7 +232,7 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     const RouteLane r = rt_finish<PER>(e_sel, wv == 0, sc, bsv, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
     if (blockIdx.x == 0 && r.valid) {
       if (wv == 0) {
-        a.idx_out[lane] = r.expert;
+        a.idx_out[lane] = sl;  // the pool row (the expert itself without a slot map)
         a.w_out[lane] = r.value;
       } else {
         if (a.want_out) a.want_out[lane] = r.expert;
@@ -289,16 +296,16 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
       float hv = silu_mul(gsum, usum, a.limit);
       if (*a.tq_bad) hv = __builtin_nanf("");
       if constexpr (RES) {
-        const int32_t hr = e >= 0 && e < a.E ? s_hot[e] : -1;
+        const int32_t hr = e >= 0 && e < a.S ? s_hot[e] : -1;
         if (hr < -1 || hr >= a.n.nhot) hv = __builtin_nanf("");
       }
-      if (e >= 0 && e < a.E) a.h[q0 + jj] = from_float<bf16s>(hv).bits;
+      if (e >= 0 && e < a.S) a.h[q0 + jj] = from_float<bf16s>(hv).bits;
     }
   }
   if constexpr (RES) {
     if (blockIdx.x == 0 && wv == 0 && lane < a.k) {
       const int32_t e = s_idx[lane];
-      a.n.hot_route[lane] = e >= 0 && e < a.E ? s_hot[e] : -1;
+      a.n.hot_route[lane] = e >= 0 && e < a.S ? s_hot[e] : -1;
     }
   }
 }
@@ -533,7 +540,8 @@ void moe_q_down_launch(const int32_t* idx, const float* w, int64_t k, int64_t E,
 }
 
 int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bias_d, int func, int renorm,
-                       float route_scale, float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H,
+                       float route_scale, float tau, const int32_t* slot_map, int64_t S, int64_t E, int64_t k,
+                       const void* x, int x_dtype, int64_t H,
                        int64_t I, const uint16_t* gc, const void* gs, const uint16_t* uc, const void* us,
                        const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
                        const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
@@ -541,6 +549,7 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
   MQLayer a{};
   a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
   a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
+  a.slot_map = slot_map; a.S = (int32_t)(slot_map ? S : E);
   a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
   a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.gs = gs; a.us = us;
   a.sdt = sdt; a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h;
@@ -565,7 +574,7 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
 #undef LY_NT
 #undef LY_PER
 #undef LY
-  moe_q_down_launch(idx, w, k, E, H, I, dc, ds, sdt, group_i, prepared, h, out, odt, s, nest);
+  moe_q_down_launch(idx, w, k, a.S, H, I, dc, ds, sdt, group_i, prepared, h, out, odt, s, nest);
   return 0;
 }
 
@@ -592,7 +601,8 @@ extern "C" int keep_e8_1bit_image_bytes(void) { return T8R_BYTES; }
 
 extern "C" int keep_moe_layer_nested(
     const float* logits, const float* bias_served, const float* bias_demand, int score_func, int renormalize,
-    float route_scale, float tau, int64_t E, int64_t k, const void* x, int x_dtype, int64_t H, int64_t I,
+    float route_scale, float tau, const int32_t* slot_map, int64_t num_slots, int64_t E, int64_t k, const void* x,
+    int x_dtype, int64_t H, int64_t I,
     const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
     const uint16_t* down_codes, const void* down_scales, int scale_dtype, int64_t group_size_h, int64_t group_size_i,
     const void* prepared, float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
@@ -605,6 +615,7 @@ extern "C" int keep_moe_layer_nested(
   KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);
   KEEP_REQUIRE(group_size_h > 0 && H % group_size_h == 0 && group_size_i > 0 && I % group_size_i == 0,
                "bad group sizes");
+  KEEP_REQUIRE(!slot_map || (num_slots >= 1 && num_slots <= 1024), "num_slots must be in 1..1024");
   KEEP_REQUIRE(moe_q_layer_supported(E, H, I, k, group_size_h, group_size_i),
                "shape not served by the routed decode layer kernels (needs H = 4096, I a multiple of 512 up to "
                "2048, k <= 8, E <= 1024, scale groups of 256-element multiples)");
@@ -630,7 +641,8 @@ extern "C" int keep_moe_layer_nested(
   n.Gh = (int32_t)(H / res_group_size_h); n.gsz_h = (int32_t)res_group_size_h;
   n.Gi = (int32_t)(I / res_group_size_i); n.gsz_i = (int32_t)res_group_size_i;
   n.t8 = (const uint4*)res_image; n.hot_route = hot_route;
-  moe_q_layer_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, E, k, x, x_dtype,
+  moe_q_layer_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, slot_map,
+                     num_slots, E, k, x, x_dtype,
                      H, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
                      group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, h_work,
                      out, out_dtype, (hipStream_t)stream, &n);

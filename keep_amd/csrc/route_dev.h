@@ -323,6 +323,33 @@ __device__ __forceinline__ void rt_load(const float* lrow, const float* bias_s, 
   }
 }
 
+// The expert -> slot map of a pool smaller than the expert count: this lane's
+// entries (experts lane + 64 i), loaded beside the logits; -1 past E.
+template <int PER>
+__device__ __forceinline__ void rt_load_slots(const int32_t* slot_map, int E, int lane, int (&sm)[PER]) {
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    sm[i] = e < E ? slot_map[e] : -1;
+  }
+}
+// The slot of expert e (every lane of the wave takes part; each lane may ask
+// for another expert) from its owner lane; -1 for e outside [0, E) or a slot
+// outside [0, S).
+template <int PER>
+__device__ __forceinline__ int rt_slot_of(const int (&sm)[PER], int e, int E, int S) {
+  const bool in = e >= 0 && e < E;
+  const int ee = in ? e : 0;
+  const int owner = ee & 63, i0 = ee >> 6;
+  int v = -1;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int x = __shfl(sm[i], owner, 64);
+    v = i == i0 ? x : v;
+  }
+  return in && v >= 0 && v < S ? v : -1;
+}
+
 // The same routing on two waves of a block: wave 0 forms the served
 // selection and wave 1 the demand selection (the served one again when the
 // biases are the same), each over all experts. Scores, sums and weights are

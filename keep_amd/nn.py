@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from keep_amd import _lib, ops
-from keep_amd.router import RouterOutput, router_dual_topk
+from keep_amd.router import RouterOutput, _slot_args, router_dual_topk
 
 CODEWORD_DIM = 8
 
@@ -210,7 +210,8 @@ class HotTier:
         if not isinstance(hot_of_slot, torch.Tensor):
             hot_of_slot = torch.from_numpy(np.asarray(hot_of_slot, dtype=np.uint32).view(np.int32).copy())
         self.hot_of_slot = hot_of_slot.to(dev)
-        self.residual_arrays = {n: (ops._codes_tensor(c, 8, dev), ops._to_dev(sc, dev)) for n, (c, sc) in residual.items()}
+        self.residual_arrays = {n: (ops._codes_tensor(c, 8, dev), ops._to_dev(sc, dev))
+                                for n, (c, sc) in residual.items()}
         self.rows = int(self.residual_arrays["gate"][0].shape[0])
         # every table form made here, so that no call copies from the host (graph capture)
         self._pairs = ops._to_dev(ops.e8_1bit_half2_table().view(np.int32), dev)
@@ -526,7 +527,7 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
               tau: float = float("inf"), limit: float = 0.0, codebook: torch.Tensor | None = None,
               out_dtype: torch.dtype | None = None, h_work: torch.Tensor | None = None,
               hot_tier: HotTier | None = None, one_launch: bool = False,
-              workspace: torch.Tensor | None = None):
+              workspace: torch.Tensor | None = None, slot_map=None):
     """One token's whole MoE layer in two launches (``keep_moe_layer``): the dual
     top-k router (as ``router_dual_topk``) fused with gate/up/SwiGLU, then down +
     weighted combine. ``x [1, H]`` (fp16/bf16), ``logits [1, E]``. With
@@ -535,8 +536,11 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
     ``one_launch`` (``keep_moe_layer1``) the same layer runs as one launch of
     256 co-resident blocks that pass h through ``workspace`` (by default
     ``layer_workspace(device, k, I)`` of the current stream); it serves
-    H = 4096, I in {512, 1024, 1536, 2048}, k <= 8, no hot tier. Returns
-    ``(out [1, H], RouterOutput)``; the output is float32 by default."""
+    H = 4096, I in {512, 1024, 1536, 2048}, k <= 8, no hot tier. With
+    ``slot_map`` (int32 ``[E]``, expert -> pool row) the pools hold fewer rows
+    than the router has experts (a residency cache's slots); ``RouterOutput.idx``
+    then holds rows. Returns ``(out [1, H], RouterOutput)``; the output is
+    float32 by default."""
 
     device = x.device
     if x.dtype not in (torch.float16, torch.bfloat16):
@@ -553,8 +557,12 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
     if not (gs.dtype == us.dtype == ds.dtype):
         raise ValueError("gate/up/down scales must share a dtype")
     z = logits.to(device=device, dtype=torch.float32).reshape(1, -1).contiguous()
-    if z.shape[1] != E:
+    S = E  # pool rows
+    if slot_map is not None:
+        E = z.shape[1]
+    elif z.shape[1] != E:
         raise ValueError(f"logits must hold {E} experts, found {z.shape[1]}")
+    sm, ns = _slot_args(slot_map, S if slot_map is not None else None, E, device)
     gh, gi = H // gs.shape[-1], I // ds.shape[-1]
     if not one_launch and not moe_layer_supported(E, H, I, k, gh, gi):
         raise ValueError("shape not served by the routed decode layer; use router_dual_topk + moe_decode")
@@ -584,9 +592,10 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
         if ws.dtype != torch.uint8 or ws.device != device or ws.numel() < need or not ws.is_contiguous():
             raise ValueError(f"workspace must be a contiguous uint8 tensor of at least {need} bytes on {device}")
         _lib.call("keep_moe_layer1", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
-                  int(bool(renormalize)), float(route_scale), float(tau), E, k, x.data_ptr(), ops._DT[x.dtype], H,
-                  I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
-                  ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(), r.weight.data_ptr(),
+                  int(bool(renormalize)), float(route_scale), float(tau), ops._ptr(sm), ns, E, k, x.data_ptr(),
+                  ops._DT[x.dtype], H, I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(),
+                  ds.data_ptr(), ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(),
+                  r.weight.data_ptr(),
                   r.want.data_ptr(), r.want_score.data_ptr(), r.admit.data_ptr(), ws.data_ptr(), ws.numel(),
                   out.data_ptr(), ops._DT[od], ops._stream(device))
         return out, r
@@ -595,28 +604,29 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
     elif h_work.numel() < k * I or h_work.dtype != torch.bfloat16:
         raise ValueError("h_work must hold k*I bfloat16 elements")
     if hot_tier is not None:
-        if hot_tier.hot_of_slot.numel() != E:
-            raise ValueError(f"hot_of_slot must have {E} entries")
+        if hot_tier.hot_of_slot.numel() != S:
+            raise ValueError(f"hot_of_slot must have {S} entries (one per pool row)")
         groups = hot_tier.layer_groups(H, I)
         if groups is None:
             raise ValueError("residual scale groups must be 256-element multiples (one dtype) for the decode layer")
         (rgc, rgs), (ruc, rus), (rdc, rds) = (hot_tier.residual_arrays[n] for n in ("gate", "up", "down"))
         hot_route = torch.empty((k,), **i32)
         _lib.call("keep_moe_layer_nested", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
-                  int(bool(renormalize)), float(route_scale), float(tau), E, k, x.data_ptr(), ops._DT[x.dtype], H,
-                  I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
-                  ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(), r.weight.data_ptr(),
+                  int(bool(renormalize)), float(route_scale), float(tau), ops._ptr(sm), ns, E, k, x.data_ptr(),
+                  ops._DT[x.dtype], H, I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(),
+                  ds.data_ptr(), ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(),
+                  r.weight.data_ptr(),
                   r.want.data_ptr(), r.want_score.data_ptr(), r.admit.data_ptr(), h_work.data_ptr(), out.data_ptr(),
                   ops._DT[od], hot_tier._hot32.data_ptr(), hot_tier.rows, rgc.data_ptr(), rgs.data_ptr(),
                   ruc.data_ptr(), rus.data_ptr(), rdc.data_ptr(), rds.data_ptr(), ops._DT[rgs.dtype], groups[0],
                   groups[1], hot_tier.image().data_ptr(), hot_route.data_ptr(), ops._stream(device))
         return out, r
     _lib.call("keep_moe_layer", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
-              int(bool(renormalize)), float(route_scale), float(tau), E, k, x.data_ptr(), ops._DT[x.dtype], H, I,
-              gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(), ds.data_ptr(),
-              ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(), r.weight.data_ptr(),
-              r.want.data_ptr(), r.want_score.data_ptr(), r.admit.data_ptr(), h_work.data_ptr(), out.data_ptr(),
-              ops._DT[od], ops._stream(device))
+              int(bool(renormalize)), float(route_scale), float(tau), ops._ptr(sm), ns, E, k, x.data_ptr(),
+              ops._DT[x.dtype], H, I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(),
+              ds.data_ptr(), ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(),
+              r.weight.data_ptr(), r.want.data_ptr(), r.want_score.data_ptr(), r.admit.data_ptr(), h_work.data_ptr(),
+              out.data_ptr(), ops._DT[od], ops._stream(device))
     return out, r
 
 
@@ -626,6 +636,10 @@ class RoutedVQMoE:
     ``__call__(x, logits)`` evaluates the residency-biased dual top-k router
     once, then runs the experts: the fused decode pair for few tokens, the
     shared-plan MFMA path for prefill. Returns ``(out [T, H], RouterOutput)``.
+
+    ``slot_map`` (int32 ``[E]``, expert -> row of ``glu``'s pools, e.g. a
+    ``ResidencyCache``'s, with its ``bias_served``) serves a pool smaller than
+    the router's ``num_experts``; ``RouterOutput.idx`` then holds pool rows.
 
     ``shared_experts`` (a one-expert ``QuantizedVQSwitchGLU``, every token on
     expert 0 with weight 1) adds the shared expert to the routed sum, and
@@ -638,7 +652,7 @@ class RoutedVQMoE:
                  renormalize: bool = True, route_scale: float = 1.0, swiglu_limit: float = 0.0,
                  bias_served: torch.Tensor | None = None, bias_demand: torch.Tensor | None = None,
                  tau: float = float("inf"), decode_max_tokens: int = 64, out_dtype=torch.float32,
-                 shared_experts: QuantizedVQSwitchGLU | None = None):
+                 shared_experts: QuantizedVQSwitchGLU | None = None, slot_map: torch.Tensor | None = None):
         self.glu, self.top_k, self.score_func = glu, top_k, score_func
         self.renormalize, self.route_scale, self.limit = renormalize, route_scale, float(swiglu_limit)
         self.bias_served, self.bias_demand, self.tau = bias_served, bias_demand, tau
@@ -654,6 +668,7 @@ class RoutedVQMoE:
             if shared_experts.activation is None and self.limit > 0:
                 shared_experts.activation = LimitedSwiGLU(self.limit)
         self.shared_experts = shared_experts
+        self.slot_map = slot_map
 
     def shared(self, x: torch.Tensor) -> torch.Tensor:
         """The shared expert's output for every row of ``x``, float32 ``[T, H]``."""
@@ -699,11 +714,12 @@ class RoutedVQMoE:
                                k=self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
                                score_func=self.score_func, renormalize=self.renormalize,
                                route_scale=self.route_scale, tau=self.tau, limit=self.limit, codebook=g.codebook,
-                               out_dtype=od, hot_tier=self.glu.hot_tier)
+                               out_dtype=od, hot_tier=self.glu.hot_tier, slot_map=self.slot_map)
         else:
             r = router_dual_topk(logits, self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
                                  score_func=self.score_func, renormalize=self.renormalize,
-                                 route_scale=self.route_scale, tau=self.tau)
+                                 route_scale=self.route_scale, tau=self.tau, slot_map=self.slot_map,
+                                 num_slots=self.glu.num_experts)
             out = self.experts(x, r.idx, r.weight, out_dtype=od)
         if not extra:
             return out, r

@@ -30,14 +30,18 @@ class RouterOutput(NamedTuple):
 
 
 def router_dual_topk(logits, k: int, *, bias_served=None, bias_demand=None, score_func: str = "softmax",
-                     renormalize: bool = True, route_scale: float = 1.0, tau: float = float("inf")) -> RouterOutput:
+                     renormalize: bool = True, route_scale: float = 1.0, tau: float = float("inf"),
+                     slot_map=None, num_slots: int | None = None) -> RouterOutput:
     """Served and demanded top-k from one router evaluation.
 
     ``logits [T, E]`` are cast to float32. ``bias_served`` holds the score
     correction bias plus the residency mask (``OFF`` for absent experts);
     ``bias_demand`` the correction bias alone. Weights are the served scores
     (0 for an absent pick), renormalised to sum 1 (``+1e-20``) when
-    ``renormalize``, times ``route_scale``.
+    ``renormalize``, times ``route_scale``. With ``slot_map`` (int32 ``[E]``,
+    expert -> row of a pool of ``num_slots`` rows) ``idx`` holds the served
+    experts' rows (-1 outside the pool), as the serving router's
+    ``slot_of[chosen]`` (``omlx_lattice.py:77-97``); ``want`` stays expert ids.
     """
 
     if score_func not in _lib.SCORE_FUNCS:
@@ -54,6 +58,7 @@ def router_dual_topk(logits, k: int, *, bias_served=None, bias_demand=None, scor
     for name, b in (("bias_served", bs), ("bias_demand", bd)):
         if b is not None and b.numel() != E:
             raise ValueError(f"{name} must have {E} entries, found {b.numel()}")
+    sm, ns = _slot_args(slot_map, num_slots, E, device)
     i32 = dict(dtype=torch.int32, device=device)
     f32 = dict(dtype=torch.float32, device=device)
     out = RouterOutput(torch.empty((T, k), **i32), torch.empty((T, k), **f32), torch.empty((T, k), **i32),
@@ -61,9 +66,23 @@ def router_dual_topk(logits, k: int, *, bias_served=None, bias_demand=None, scor
     if T == 0:
         return out
     _lib.call("keep_router_dual_topk", z.data_ptr(), T, E, k, _ptr(bs), _ptr(bd), _lib.SCORE_FUNCS[score_func],
-              int(bool(renormalize)), float(route_scale), float(tau), out.idx.data_ptr(), out.weight.data_ptr(),
-              out.want.data_ptr(), out.want_score.data_ptr(), out.admit.data_ptr(), _stream(device))
+              int(bool(renormalize)), float(route_scale), float(tau), _ptr(sm), ns, out.idx.data_ptr(),
+              out.weight.data_ptr(), out.want.data_ptr(), out.want_score.data_ptr(), out.admit.data_ptr(),
+              _stream(device))
     return out
+
+
+def _slot_args(slot_map, num_slots, E: int, device):
+    """``(slot_map int32 [E] on device or None, num_slots)`` for the C ABI."""
+
+    if slot_map is None:
+        return None, 0
+    sm = _to_dev(slot_map, device, torch.int32).reshape(-1).contiguous()
+    if sm.numel() != E:
+        raise ValueError(f"slot_map must have {E} entries, found {sm.numel()}")
+    if num_slots is None or num_slots < 1:
+        raise ValueError("a slot_map needs num_slots >= 1 (the pool's rows)")
+    return sm, int(num_slots)
 
 
 def expert_select(logits, e_score_correction_bias, top_k: int, routed_scaling_factor: float, norm_topk_prob: bool,

@@ -75,7 +75,8 @@ def test_zero_routes_is_a_no_op():
 
 def test_other_entry_points_validate():
     lib = _lib.load()
-    assert lib.keep_router_dual_topk(1, 1, 2000, 6, None, None, 0, 1, 1.0, 0.3, 1, 1, None, None, None, None) == -1
+    assert lib.keep_router_dual_topk(1, 1, 2000, 6, None, None, 0, 1, 1.0, 0.3, None, 0, 1, 1, None, None, None,
+                                     None) == -1
     assert b"E must be" in lib.keep_last_error()
     assert lib.keep_route_plan(1, 10, 4, 4, 1, 1, 1, 1, 1, 1, 1, 2, 1, None) == -1
     assert b"max_tiles" in lib.keep_last_error()

@@ -37,7 +37,7 @@ def _outputs(dev, k, H):
 def _call(name, a, o, h_work=None):
     lib = _lib.load()
     g, u, d = a["gate"], a["up"], a["down"]
-    head = [a["z"].data_ptr(), None, None, _lib.SCORE_FUNCS["softmax"], 1, 1.0, float("inf"), a["E"], a["k"],
+    head = [a["z"].data_ptr(), None, None, _lib.SCORE_FUNCS["softmax"], 1, 1.0, float("inf"), None, 0, a["E"], a["k"],
             a["x"].data_ptr(), ops._DT[a["x"].dtype], a["H"], a["I"], g.codes.data_ptr(), g.scales.data_ptr(),
             u.codes.data_ptr(), u.scales.data_ptr(), d.codes.data_ptr(), d.scales.data_ptr(),
             ops._DT[g.scales.dtype], a["H"], a["I"], a["prep"].data_ptr(), 0.0, o["idx"].data_ptr(),
