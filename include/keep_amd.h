@@ -54,6 +54,27 @@ int keep_e8_1bit_decode(const uint8_t* codes, int64_t n, const uint32_t* table, 
                         int scale_dtype, int64_t codewords_per_row, int64_t group_codewords, float* out,
                         void* stream);
 
+/* Nearest-codeword encoder: codes[i] = the codeword (code_bits 16: E8P uint16
+ * of the packed abs table; 8: the 8-bit E8 uint8 index of the packed E8
+ * table) nearest to vector i (fp32 [n, 8], divided by scales[i /
+ * vectors_per_scale] when scales is non-null, the quotient correctly rounded
+ * to fp32) under the diagonal metric diagonal (diag_mode 0: none; 1: one
+ * shared [8]; 2: one [8] per vector): the minimiser of
+ * ((q0+q1)+(q2+q3))+((q4+q5)+(q6+q7)), q_d = w_d (v_d - c_d)^2 in double,
+ * ties to the lowest code, as the exhaustive scan. The E8P search is factored
+ * (2 shifts x 256 abs rows with the sign-parity fix).
+ * Replaces encode_e8p_rtn / encode_e8p_rtn_diagonal_hessian
+ * (src/keep/vq/e8.py:367-539), encode_e8_1bit_rtn (:283-287) and the RTN
+ * search of quantize_weight_rtn (src/keep/quant/rtn.py:299-310). */
+int keep_vq_encode(const float* vectors, int64_t n, int code_bits, const float* diagonal, int diag_mode,
+                   const uint32_t* table, const float* scales, int64_t vectors_per_scale, void* codes,
+                   void* stream);
+/* scales[g] = max |x[g * group_size + j]| / divisor (fp32, correctly rounded)
+ * over groups_total contiguous groups: the max_abs scale estimator of
+ * src/keep/quant/rtn.py:253-264. */
+int keep_group_absmax(const float* x, int64_t groups_total, int64_t group_size, float divisor, float* scales,
+                      void* stream);
+
 /* Routed VQ mat-vec: out[r, :] = W[rhs[r]] . x[row(r), :] for r < routes,
  * row(r) = lhs ? lhs[r] : r / x_div. W[e] is [N, K] given by codes [E, N, K/8]
  * and scales [E, N, K/group_size]. fp32 accumulate.

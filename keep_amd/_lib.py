@@ -27,6 +27,8 @@ _SIGS = {
     "keep_e8_1bit_packed": [POINTER(c_uint32)],
     "keep_e8p_decode": [_P, c_int64, _P, _P, c_int, c_int64, c_int64, _P, _P],
     "keep_e8_1bit_decode": [_P, c_int64, _P, _P, c_int, c_int64, c_int64, _P, _P],
+    "keep_vq_encode": [_P, c_int64, c_int, _P, c_int, _P, _P, c_int64, _P, _P],
+    "keep_group_absmax": [_P, c_int64, c_int64, c_float, _P, _P],
     "keep_vq_matvec": [_P, c_int, c_int64, _P, c_int, _P, c_int, _P, _P, _P, c_int64, c_int64, c_int64, c_int64,
                        c_int64, c_int64, _P, _P, c_int64, _P, _P, c_int64, _P, c_int, _P],
     "keep_vq_matvec_tiles": [_P, c_int, c_int64, _P, c_int, _P, c_int, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64,

@@ -20,7 +20,7 @@ OUT = PKG / "libkeep_amd.so"
 OBJ = PKG / "_build"
 ARCH = os.environ.get("KEEP_AMD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["abi.cpp", "matvec.hip", "moe.hip", "moe_i8.hip", "moe_tiles.hip", "router.hip", "plan.hip", "gemm_q8.hip", "rht.hip", "layer.hip", "block.hip"]
+SOURCES = ["abi.cpp", "matvec.hip", "moe.hip", "moe_i8.hip", "moe_tiles.hip", "router.hip", "plan.hip", "gemm_q8.hip", "rht.hip", "layer.hip", "block.hip", "encode.hip"]
 FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wno-unused-command-line-argument"]

@@ -114,6 +114,32 @@ class QuantizedVQLinear:
     def _extra_repr(self) -> str:
         return f"{self.input_dims}, {self.output_dims}, group_size={self.group_size}, code_bits={self.code_bits}"
 
+    @classmethod
+    def from_weights(cls, weight, bias=None, *, group_size: int = 512, code_bits: int = 8, rht_signs=None,
+                     rotation_matrix=None) -> "QuantizedVQLinear":
+        """Quantise a dense ``[out, in]`` weight on the GPU (``linear.py:123-160``):
+        the RHT (or rotation) is applied to the weight's rows as it will be to
+        the inputs, then the data-free RTN (``encode.quantize_weight_rtn``)."""
+
+        from keep_amd.encode import quantize_weight_rtn
+
+        if rht_signs is not None and rotation_matrix is not None:
+            raise ValueError("rht_signs and rotation_matrix are mutually exclusive")
+        w = weight if isinstance(weight, torch.Tensor) else torch.from_numpy(np.asarray(weight, dtype=np.float32))
+        device = w.device if w.is_cuda else torch.device("cuda", torch.cuda.current_device())
+        w = w.to(device=device, dtype=torch.float32)
+        if rht_signs is not None:
+            from keep_amd.rht import apply_rht
+            w = apply_rht(w, torch.as_tensor(rht_signs).to(device))
+        if rotation_matrix is not None:
+            w = w @ torch.as_tensor(rotation_matrix).to(device=device, dtype=torch.float32)
+        q = quantize_weight_rtn(w, group_size=group_size, code_bits=code_bits)
+        out_dim, in_dim = w.shape
+        return cls(input_dims=in_dim, output_dims=out_dim, codes=q.codes, scales=q.scales,
+                   codebook=torch.from_numpy(q.codebook.view(np.int32)).to(device), bias=bias,
+                   group_size=q.group_size, code_bits=q.code_bits, rht_signs=rht_signs,
+                   rotation_matrix=rotation_matrix)
+
 
 class QuantizedVQSwitchLinear:
     """Switch-linear layer backed by stacked VQ expert tensors (torch, GPU)."""

@@ -41,6 +41,8 @@ def load():
                                                  c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
                                                  c_void_p, c_int]
         lib.oracle_moe_decode_nested.restype = None
+        lib.oracle_nearest.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p]
+        lib.oracle_nearest.restype = None
         lib.oracle_max_threads.restype = c_int
         _lib = lib
     return _lib
@@ -119,4 +121,22 @@ def moe_decode_nested(x, idx, w, gate, up, down, table, hot_of_slot, residual, t
                                     _p(ds), H // gs.shape[-1], I // ds.shape[-1], _p(t), float(limit),
                                     int(bool(h_bf16)), _p(hot), _p(rgc), _p(rgs), _p(ruc), _p(rus), _p(rdc), _p(rds),
                                     H // rgs.shape[-1], I // rds.shape[-1], _p(t8), _p(out), int(threads))
+    return out
+
+
+def nearest(vectors, grid, w=None) -> np.ndarray:
+    """Exhaustive weighted nearest codeword (``oracle_nearest``): ``w`` None,
+    ``[8]`` (shared) or ``[n, 8]``; ties to the lowest grid index."""
+
+    v = np.ascontiguousarray(vectors, dtype=np.float32).reshape(-1, 8)
+    g = np.ascontiguousarray(grid, dtype=np.float32).reshape(-1, 8)
+    out = np.empty(v.shape[0], dtype=np.int64)
+    stride = 0
+    wa = None
+    if w is not None:
+        wa = np.ascontiguousarray(w, dtype=np.float32)
+        stride = 0 if wa.ndim == 1 else 8
+        if wa.size not in (8, v.size):
+            raise ValueError("w must be [8] or [n, 8]")
+    load().oracle_nearest(_p(v), v.shape[0], _p(wa), stride, _p(g), g.shape[0], _p(out))
     return out

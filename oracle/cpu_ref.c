@@ -185,4 +185,39 @@ void oracle_moe_decode(const float* x, int64_t T, int64_t H, int64_t I, const in
                            NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1, 1, NULL, out, threads);
 }
 
+/* Weighted nearest codeword by exhaustive scan (the definition the GPU
+ * encoder keeps): for vector i (fp32 [8]) and weights w (NULL: 1; w_stride 0:
+ * one shared [8]; 8: one [8] per vector) the grid index g minimising
+ *   D = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7)),  q_d = w_d * ((v_d - c_d)^2)
+ * in double, ties to the lowest index (src/keep/quant/rtn.py:92-135, the
+ * exhaustive reference of tests/test_e8p_diagonal_hessian.py:14-19). Each
+ * statement rounds once: the file is built in ISO C mode (-std=c11), so no
+ * multiply-add is contracted. */
+void oracle_nearest(const float* v, int64_t n, const float* w, int64_t w_stride, const float* grid, int64_t G,
+                    int64_t* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    double wd[8];
+    for (int d = 0; d < 8; ++d) wd[d] = w ? (double)w[i * w_stride + d] : 1.0;
+    double best = INFINITY;
+    int64_t bi = 0;
+    for (int64_t g = 0; g < G; ++g) {
+      double q[8];
+      for (int d = 0; d < 8; ++d) {
+        const double df = (double)v[i * 8 + d] - (double)grid[g * 8 + d];
+        const double sq = df * df;
+        q[d] = wd[d] * sq;
+      }
+      const double a = q[0] + q[1], b = q[2] + q[3], c = q[4] + q[5], e = q[6] + q[7];
+      const double ab = a + b, ce = c + e;
+      const double D = ab + ce;
+      if (D < best) {
+        best = D;
+        bi = g;
+      }
+    }
+    out[i] = bi;
+  }
+}
+
 int oracle_max_threads(void) { return omp_get_max_threads(); }
