@@ -145,6 +145,11 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
   //    int8 terms of x s, s the slice's power of two
   float sc[PER];
   int e_sel = -1, sl = -1;
+  // the routes this block's gate/up tiles belong to: 0 .. kneed - 1 (the
+  // later selection rounds run while the codes are in flight)
+  const int qlast = min((int)(b * QT + QT - 1), a.qtiles - 1);
+  const int kneed = qlast < (int)(b * QT) ? 1 : min(a.k, qlast * 16 / a.I + 1);
+  RtSel<PER> sel;
   auto build = [&](uint4 c, int slice) {
     float v[4];
     if (a.xbf) q8_half4<true>(c, lane & 1, v);
@@ -160,14 +165,19 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
     if (lane == 0) s_inv4s[slice] = inv4s;
   };
   if (wv == 0) {
-    e_sel = rt_select_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, true, 0, lane, sc);
+    rt_scores<PER>(z, a.E, a.func, lane, sc);
+    uint32_t kk[PER];
+    rt_keys<PER>(sc, bsv, a.E, lane, kk);
+    sel.init(kk, lane);
+    sel.rounds(0, kneed, lane, 0);
+    e_sel = sel.mine;
     sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
-    if (lane < a.k) s_idx[lane] = sl;
+    if (lane < kneed) s_idx[lane] = sl;
   } else if (wv >= 2) {
     build(xc, wv);
     if (wv < 4) build(xc2, wv - 2);
   }
-  rt_lds_barrier();  // s_idx, the image and every slice's A terms visible
+  rt_lds_barrier();  // this block's routes in s_idx, the image and every slice's A terms visible
 
   // 2. the gate/up loads of the block: scales and codes
   uint32_t rbase[QT];
@@ -208,6 +218,17 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
     q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + (size_t)(rbase[t >> 1] + j) * C + kc0);
   __builtin_amdgcn_sched_barrier(0);
 
+  // the remaining routes (wave 0) while the codes are in flight: every wave
+  // waits for them here, ahead of the data it would otherwise wait for
+  if (kneed < a.k) {
+    if (wv == 0) {
+      sel.rounds(kneed, a.k, lane, 0);
+      e_sel = sel.mine;
+      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+      if (lane >= kneed && lane < a.k) s_idx[lane] = sl;
+    }
+    rt_lds_barrier();
+  }
   // the served weights and outputs (wave 0), while the codes are in flight
   if (wv == 0) {
     const RouteLane r = rt_finish<PER>(e_sel, true, sc, bsv, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);

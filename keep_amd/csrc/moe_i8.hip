@@ -101,10 +101,11 @@ struct MQLayer {
 };
 
 // One block per NT / 2 q-tiles (16 rows of the [k, I] intermediate each), 16
-// waves, H = 4096 (a 256-wide K slice per wave). Waves 0 and 1 select the
-// experts (rt_select_pair) while waves 2-15 build the A terms of all sixteen
-// slices; after one barrier every wave issues all of its scale and code loads
-// at once, the router waves finish the weights while those are in flight, and
+// waves, H = 4096 (a 256-wide K slice per wave). Wave 0 selects the routes the
+// block's own tiles belong to while waves 2-15 build the A terms of all
+// sixteen slices; after one barrier every wave issues all of its scale and
+// code loads at once, block 0's waves 0 and 1 finish the served and demand
+// selections and write the router's outputs while those are in flight, and
 // gate/up runs tile by tile, then SwiGLU, h in bf16. RES: the nested tier's
 // residual image and hot[] come into LDS with the table, and a tile of a hot
 // expert adds its residual dot (same A terms) before the SwiGLU.
@@ -128,9 +129,10 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   // 0. the router's inputs (waves 0, 1), the table image (64 KiB; every wave
   //    DMAs 4 KiB) and the token slices this wave builds A terms for (16
   //    bytes per lane pair): wave w >= 2 slice w, waves 2 and 3 also slices 0, 1
+  const uint32_t b = blockIdx.x;
   float z[PER], bsv[PER], bdv[PER];
   int sm[PER];
-  if (wv < 2) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
+  if (wv == 0 || (wv == 1 && b == 0)) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
   if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, a.E, lane, sm);
 #pragma unroll
   for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
@@ -147,10 +149,15 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   const uint4 xc2 = ldg16_q((const uint4*)a.x + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
   __builtin_amdgcn_sched_barrier(0);
 
-  // 1. routing (waves 0, 1) | A terms: rows 0-2 of slice w are the three int8
-  //    terms of x s, s the slice's power of two (1 / (4 s) kept for the epilogue)
+  // 1. the block's routes (wave 0) | A terms: rows 0-2 of slice w are the
+  //    three int8 terms of x s, s the slice's power of two (1 / (4 s) kept for
+  //    the epilogue). The block's tiles lie in routes 0 .. kneed - 1; the later
+  //    selection rounds run only in block 0, once its codes are in flight.
   float sc[PER];
   int e_sel = -1, sl = -1;
+  const int qlast = min((int)(b * QT + QT - 1), a.qtiles - 1);
+  const int kneed = qlast < (int)(b * QT) ? 1 : min(a.k, qlast * 16 / a.I + 1);
+  RtSel<PER> sel;
   auto build = [&](uint4 c, int slice) {
     float v[4];
     q8_half4<XBF>(c, lane & 1, v);
@@ -164,25 +171,28 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     for (int n = 0; n < 3; ++n) aw[q8_aword((uint32_t)(slice * 3 + n), lane >> 1, lane & 1)] = tw[n];
     if (lane == 0) s_inv4s[slice] = inv4s;
   };
-  if (wv < 2) {
-    e_sel = rt_select_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, a.same_bias != 0, wv, lane, sc);
-    if (wv == 0) {
-      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
-      if (lane < a.k) s_idx[lane] = sl;
-    }
-  } else {
+  if (wv == 0) {
+    rt_scores<PER>(z, a.E, a.func, lane, sc);
+    uint32_t kk[PER];
+    rt_keys<PER>(sc, bsv, a.E, lane, kk);
+    sel.init(kk, lane);
+    sel.rounds(0, kneed, lane, 0);
+    e_sel = sel.mine;
+    sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+    if (lane < kneed) s_idx[lane] = sl;
+  } else if (wv >= 2) {
     build(xc, wv);
     if (wv < 4) build(xc2, wv - 2);
   }
   wait_vm_q<0>();  // this wave's table pieces
-  rt_lds_barrier();  // s_idx, the table and every slice's A terms visible
+  rt_lds_barrier();  // the block's routes in s_idx, the table and every slice's A terms visible
 
   // 2. this block's tiles: scales, then every tile's codes
   uint32_t rbase[QT], rres[QT];
   bool hot_t[QT];
 #pragma unroll
   for (int u = 0; u < QT; ++u) {
-    const uint32_t qt = blockIdx.x * QT + u;
+    const uint32_t qt = b * QT + u;
     const bool valid = qt < (uint32_t)a.qtiles;
     const uint32_t q0 = (valid ? qt : 0u) * 16u;
     const uint32_t route = q0 / (uint32_t)a.I;
@@ -227,10 +237,20 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // the router waves' weights and outputs, while the codes are in flight
-  if (wv < 2) {
+  // block 0: the remaining served routes (wave 0) and the demand selection
+  // (wave 1), their weights and the router's outputs, while the codes are in
+  // flight (s_idx of the later routes is read only after the next barrier)
+  if (b == 0 && wv < 2) {
+    if (wv == 0) {
+      sel.rounds(kneed, a.k, lane, 0);
+      e_sel = sel.mine;
+      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+      if (lane >= kneed && lane < a.k) s_idx[lane] = sl;
+    } else {
+      e_sel = rt_select_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, a.same_bias != 0, 1, lane, sc);
+    }
     const RouteLane r = rt_finish<PER>(e_sel, wv == 0, sc, bsv, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
-    if (blockIdx.x == 0 && r.valid) {
+    if (r.valid) {
       if (wv == 0) {
         a.idx_out[lane] = sl;  // the pool row (the expert itself without a slot map)
         a.w_out[lane] = r.value;

@@ -164,45 +164,63 @@ __device__ __forceinline__ uint64_t rt_wave_max_word(double v) {
   return (uint64_t)__double_as_longlong(v);
 }
 
-// k rounds over the sortable keys kk (0 = no expert) of experts lane + 64 i:
-// lane slot0 + j (j < k) receives winner j, or -1 when fewer than j + 1
-// experts hold a key; other lanes receive -1.
+// The selection over the sortable keys kk (0 = no expert) of experts
+// lane + 64 i, kept as state so that its rounds can run in pieces: init sorts
+// each lane's words once, rounds(j0, j1, ...) finds winners j0 .. j1 - 1
+// (lane slot0 + j receives winner j, or -1 when fewer than j + 1 experts hold
+// a key). A block that needs only the first routes can act on them before the
+// later rounds run.
+template <int PER>
+struct RtSel {
+  uint32_t lo[PER], hi[PER];  // the sorted words as bit fields, popped with bitfield selects
+  int mine;
+
+  __device__ __forceinline__ void init(const uint32_t (&kk)[PER], int lane) {
+    double d[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) d[i] = rt_dkey(kk[i], lane + 64 * i);
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {  // odd-even transposition sort, descending
+#pragma unroll
+      for (int i = p & 1; i + 1 < PER; i += 2) {
+        const double a = d[i], b = d[i + 1];
+        d[i] = __builtin_fmax(a, b);
+        d[i + 1] = __builtin_fmin(a, b);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint64_t u = (uint64_t)__double_as_longlong(d[i]);
+      lo[i] = (uint32_t)u;
+      hi[i] = (uint32_t)(u >> 32);
+    }
+    mine = -1;
+  }
+
+  __device__ __forceinline__ void rounds(int j0, int j1, int lane, int slot0) {
+    for (int j = j0; j < j1; ++j) {
+      const uint64_t m = rt_wave_max_word(__longlong_as_double((long long)(((uint64_t)hi[0] << 32) | lo[0])));
+      const uint32_t pm = (((uint64_t)hi[0] << 32) | lo[0]) == m ? 0xffffffffu : 0u;
+#pragma unroll
+      for (int i = 0; i + 1 < PER; ++i) {
+        lo[i] = ((lo[i + 1] & pm) | (lo[i] & ~pm));
+        hi[i] = (hi[i + 1] & pm) | (hi[i] & ~pm);
+      }
+      lo[PER - 1] &= ~pm;
+      hi[PER - 1] &= ~pm;
+      const int e = m ? (int)(0x3FFFFFFFu - (uint32_t)(m & 0x3FFFFFFFu)) : -1;
+      mine = lane == slot0 + j ? e : mine;
+    }
+  }
+};
+
+// k rounds at once: lane slot0 + j (j < k) receives winner j, or -1; other lanes -1.
 template <int PER>
 __device__ __forceinline__ int rt_topk(const uint32_t (&kk)[PER], int k, int lane, int slot0) {
-  double d[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) d[i] = rt_dkey(kk[i], lane + 64 * i);
-#pragma unroll
-  for (int p = 0; p < PER; ++p) {  // odd-even transposition sort, descending
-#pragma unroll
-    for (int i = p & 1; i + 1 < PER; i += 2) {
-      const double a = d[i], b = d[i + 1];
-      d[i] = __builtin_fmax(a, b);
-      d[i + 1] = __builtin_fmin(a, b);
-    }
-  }
-  uint32_t lo[PER], hi[PER];  // the sorted words as bit fields, popped with bitfield selects
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const uint64_t u = (uint64_t)__double_as_longlong(d[i]);
-    lo[i] = (uint32_t)u;
-    hi[i] = (uint32_t)(u >> 32);
-  }
-  int mine = -1;
-  for (int j = 0; j < k; ++j) {
-    const uint64_t m = rt_wave_max_word(__longlong_as_double((long long)(((uint64_t)hi[0] << 32) | lo[0])));
-    const uint32_t pm = (((uint64_t)hi[0] << 32) | lo[0]) == m ? 0xffffffffu : 0u;
-#pragma unroll
-    for (int i = 0; i + 1 < PER; ++i) {
-      lo[i] = ((lo[i + 1] & pm) | (lo[i] & ~pm));
-      hi[i] = (hi[i + 1] & pm) | (hi[i] & ~pm);
-    }
-    lo[PER - 1] &= ~pm;
-    hi[PER - 1] &= ~pm;
-    const int e = m ? (int)(0x3FFFFFFFu - (uint32_t)(m & 0x3FFFFFFFu)) : -1;
-    mine = lane == slot0 + j ? e : mine;
-  }
-  return mine;
+  RtSel<PER> sel;
+  sel.init(kk, lane);
+  sel.rounds(0, k, lane, slot0);
+  return sel.mine;
 }
 
 struct RouteLane {
