@@ -3,7 +3,11 @@
 Each source is compiled separately (in parallel) with ``hipcc`` for gfx950 and
 the objects are linked into one shared library with a C ABI
 (``include/keep_amd.h``). Packed-FP32 instructions are disabled on the device
-side (``-packed-fp32-ops``).
+side (``-packed-fp32-ops``). The decode-layer sources have their leading
+kernel arguments preloaded into SGPRs by the dispatcher
+(``-amdgpu-kernarg-preload-count``; the compiler keeps a loading prologue for
+firmware without the feature), so their first loads do not wait for a
+kernel-argument fetch.
 """
 
 from __future__ import annotations
@@ -24,11 +28,14 @@ SOURCES = ["abi.cpp", "matvec.hip", "moe.hip", "moe_i8.hip", "moe_tiles.hip", "r
 FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wno-unused-command-line-argument"]
+# sources whose kernels take their first-needed arguments as leading scalars (at most 14 dwords)
+PRELOAD = {"moe_i8.hip", "layer.hip"}
+PRELOAD_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=14"]
 
 
 def _compile(src: str) -> Path:
     obj = OBJ / (src + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *(PRELOAD_FLAGS if src in PRELOAD else []), "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
         cmd.insert(1, "-x")
         cmd.insert(2, "hip")

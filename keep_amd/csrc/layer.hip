@@ -39,12 +39,22 @@ constexpr int FL_WAVES = 16;         // H / 256 gate/up K slices
 constexpr uint32_t FL_HDR_BYTES = 256;  // epoch, arrivals, status
 constexpr uint32_t FL_TIMEOUT = 1u;     // status bit: a wait gave up
 
-struct FLArgs {
+// The arguments the first loads need: the kernel's leading arguments,
+// preloaded into SGPRs by the dispatcher (-amdgpu-kernarg-preload-count).
+struct FLHead {
   const float* logits;
   const float *bias_s, *bias_d;
+  const uint2* tq;  // T[256] then M[256], 8 bytes each (keep_e8p_prepare)
+  const void* x;
+  uint32_t* hdr;    // [0] epoch, [1] arrivals, [2] status
+  int32_t E;
+};
+
+// The rest.
+struct FLArgs {
   int func, renorm, same_bias;
   float route_scale, tau;
-  int32_t E, k;
+  int32_t k;
   const int32_t* slot_map;  // expert -> pool row (null: the pool holds every expert)
   int32_t S;                // pool rows
   int32_t* idx_out;
@@ -52,18 +62,15 @@ struct FLArgs {
   int32_t* want_out;
   float* want_score_out;
   uint8_t* admit_out;
-  const void* x;
   int xbf;  // x is bf16 (else fp16)
   int32_t I;
   const uint16_t *gc, *uc, *dc;
   const void *gs, *us, *ds;
   int sdt;
   int32_t Gh, gsz_h, Gi, gsz_i;
-  const uint2* tq;  // T[256] then M[256], 8 bytes each (keep_e8p_prepare)
   const uint32_t* tq_bad;
   float limit;
   int32_t qtiles;
-  uint32_t* hdr;      // [0] epoch, [1] arrivals, [2] status
   uint64_t* hx;       // [k * I / 2] tagged h pairs
   uint32_t spin_ticks;
   void* out;
@@ -90,7 +97,9 @@ __device__ __forceinline__ uint32_t fl_pos(uint32_t d) { return (d & 1u) * 4u + 
 // LDS is one array with the decode image at address 0, so a lookup address
 // is exactly the byte permute of q8_decode2 (no base to add).
 template <int NT, int PER, int NSL, int RPW, bool G1>
-__global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
+__global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const float* bias_s, const float* bias_d,
+                                                     const uint2* tqe, const void* xin, uint32_t* hdr, int32_t E,
+                                                     FLArgs a) {
   constexpr int QT = NT / 2;
   constexpr int RG = FL_WAVES / NSL;
   static_assert(RPW * 4 <= 16, "at most four routes per down wave (A rows 4 r + t)");
@@ -122,16 +131,21 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
   // 0. the call's epoch; the router's inputs (wave 0); T and M for the image
   //    (every thread builds four copies of one entry); the token slices this
   //    wave builds terms for (wave w >= 2 slice w; waves 2 and 3 also slices
-  //    0 and 1)
-  const uint32_t ep = __builtin_amdgcn_readfirstlane((uint32_t)(fl_load((uint64_t*)a.hdr) & 0xffffffffu));
+  //    0 and 1), all from the preloaded arguments; then the table flag and the
+  //    slot map, which need the others
+  const uint32_t ep_word = __hip_atomic_load(hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   float z[PER], bsv[PER], bdv[PER];
   int sm[PER];
-  if (wv == 0) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
-  if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, a.E, lane, sm);
+  if (wv == 0) rt_load<PER>(logits, bias_s, bias_d, E, lane, z, bsv, bdv);
   const uint32_t te = threadIdx.x >> 2;
-  const uint2 tv = a.tq[te], mv = a.tq[256 + te];
-  const uint4 xc = ldg16_q((const uint4*)a.x + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
-  const uint4 xc2 = ldg16_q((const uint4*)a.x + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
+  const uint2 tv = tqe[te], mv = tqe[256 + te];
+  const uint4 xc = ldg16_q((const uint4*)xin + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
+  const uint4 xc2 = ldg16_q((const uint4*)xin + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
+  if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, E, lane, sm);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t ep = __builtin_amdgcn_readfirstlane(ep_word);
   {
     const uint4 v = make_uint4(tv.x, tv.y, mv.x, mv.y);
     uint4* row = tqs + te * 16 + (threadIdx.x & 3) * 4;
@@ -165,13 +179,13 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
     if (lane == 0) s_inv4s[slice] = inv4s;
   };
   if (wv == 0) {
-    rt_scores<PER>(z, a.E, a.func, lane, sc);
+    rt_scores<PER>(z, E, a.func, lane, sc);
     uint32_t kk[PER];
-    rt_keys<PER>(sc, bsv, a.E, lane, kk);
+    rt_keys<PER>(sc, bsv, E, lane, kk);
     sel.init(kk, lane);
     sel.rounds(0, kneed, lane, 0);
     e_sel = sel.mine;
-    sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+    sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, E, a.S) : (e_sel >= 0 && e_sel < E ? e_sel : -1);
     if (lane < kneed) s_idx[lane] = sl;
   } else if (wv >= 2) {
     build(xc, wv);
@@ -224,14 +238,14 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
     if (wv == 0) {
       sel.rounds(kneed, a.k, lane, 0);
       e_sel = sel.mine;
-      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, E, a.S) : (e_sel >= 0 && e_sel < E ? e_sel : -1);
       if (lane >= kneed && lane < a.k) s_idx[lane] = sl;
     }
     rt_lds_barrier();
   }
   // the served weights and outputs (wave 0), while the codes are in flight
   if (wv == 0) {
-    const RouteLane r = rt_finish<PER>(e_sel, true, sc, bsv, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
+    const RouteLane r = rt_finish<PER>(e_sel, true, sc, bsv, E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
     if (lane < a.k) s_w[lane] = r.valid ? r.value : 0.f;
     if (b == 0 && r.valid) {
       a.idx_out[lane] = sl;  // the pool row (the expert itself without a slot map)
@@ -293,7 +307,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
   // this block counts itself in (it has read the epoch); the last block in advances it after the exchange
   uint32_t arrived = 0u;
   if (threadIdx.x == 0)
-    arrived = __hip_atomic_fetch_add(a.hdr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    arrived = __hip_atomic_fetch_add(hdr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   rt_lds_barrier();  // every wave's partials (and s_w) visible
 
   // 4. SwiGLU of the block's rows and their publication: lane (u, jj) owns
@@ -319,7 +333,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
       usum *= scale_cvt(sr[1], a.sdt, rb + jj);
     }
     float hv = silu_mul(gsum, usum, a.limit);
-    if (*a.tq_bad || e < 0 || e >= a.S) hv = __builtin_nanf("");
+    if (tq_bad || e < 0 || e >= a.S) hv = __builtin_nanf("");
     const uint32_t hb = from_float<bf16s>(hv).bits;
     const uint32_t hb2 = (uint32_t)__shfl((int)hb, lane ^ 2, 64);
     if (valid && (jj & 2u) == 0u) {
@@ -333,9 +347,9 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
   // logits while the other blocks' h is awaited
   if (wv == 1 && b == 0 && (a.want_out || a.want_score_out || a.admit_out)) {
     float z1[PER], bs1[PER], bd1[PER], sc1[PER];
-    rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z1, bs1, bd1);
-    const int d_sel = rt_select_pair<PER>(z1, bs1, bd1, a.E, a.k, a.func, a.same_bias != 0, 1, lane, sc1);
-    const RouteLane r = rt_finish<PER>(d_sel, false, sc1, bs1, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
+    rt_load<PER>(logits, bias_s, bias_d, E, lane, z1, bs1, bd1);
+    const int d_sel = rt_select_pair<PER>(z1, bs1, bd1, E, a.k, a.func, a.same_bias != 0, 1, lane, sc1);
+    const RouteLane r = rt_finish<PER>(d_sel, false, sc1, bs1, E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
     if (r.valid) {
       if (a.want_out) a.want_out[lane] = r.expert;
       if (a.want_score_out) a.want_score_out[lane] = r.value;
@@ -383,7 +397,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
       __builtin_amdgcn_s_sleep(1);
     }
     if (gave_up && lane == 0) {
-      __hip_atomic_fetch_or(a.hdr + 2, FL_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_or(hdr + 2, FL_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // A terms: rows 4 r + t of route r's slice, scaled by its own power of two
     float inv4d[RPW];
@@ -437,8 +451,8 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
     }
   }
   if (threadIdx.x == 0 && arrived == FL_BLOCKS - 1) {  // every block has read the epoch: advance it
-    __hip_atomic_store(a.hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(a.hdr, ep + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(hdr, ep + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   rt_lds_barrier();
 
@@ -459,7 +473,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(FLArgs a) {
         o = (ok && wt != 0.f) ? fmaf(wt, v, o) : o;
       }
     }
-    if (bad || *a.tq_bad) o = __builtin_nanf("");
+    if (bad || tq_bad) o = __builtin_nanf("");
     const size_t oi = b * 16u + threadIdx.x;
     if (a.odt == KEEP_F16) ((_Float16*)a.out)[oi] = (_Float16)o;
     else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;
@@ -490,9 +504,11 @@ bool fl_device_ok() {
 // gate/up q-tiles per block ceil(k I / 16 / 256), down route groups
 // RG = 16 / (I / 256) of ceil(k / RG) routes.
 template <int PER, bool G1>
-static bool fl_dispatch(const FLArgs& a, hipStream_t s) {
+static bool fl_dispatch(const FLHead& h, const FLArgs& a, hipStream_t s) {
   const dim3 grid(FL_BLOCKS), blk(1024);
-#define FL_K(NT, NSL, RPW) hipLaunchKernelGGL((k_moe_layer1<NT, PER, NSL, RPW, G1>), grid, blk, 0, s, a)
+#define FL_K(NT, NSL, RPW)                                                                                  \
+  hipLaunchKernelGGL((k_moe_layer1<NT, PER, NSL, RPW, G1>), grid, blk, 0, s, h.logits, h.bias_s, h.bias_d, h.tq, \
+                     h.x, h.hdr, h.E, a)
   const int k = a.k;
   switch (a.I) {
     case 2048:
@@ -527,30 +543,31 @@ void fl_launch(const float* logits, const float* bias_s, const float* bias_d, in
                int64_t group_h, int64_t group_i, const void* prepared, float limit, int32_t* idx, float* w,
                int32_t* want, float* want_score, uint8_t* admit, void* workspace, uint32_t spin_ticks, void* out,
                int odt, hipStream_t s) {
+  FLHead h{};
+  h.logits = logits; h.bias_s = bias_s; h.bias_d = bias_d; h.E = (int32_t)E;
+  h.x = x; h.tq = (const uint2*)((const char*)prepared + TQ_OFFSET); h.hdr = (uint32_t*)workspace;
   FLArgs a{};
-  a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
-  a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
+  a.func = func; a.renorm = renorm;
+  a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.k = (int32_t)k;
   a.slot_map = slot_map; a.S = (int32_t)(slot_map ? S : E);
   a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
-  a.x = x; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.dc = dc; a.gs = gs; a.us = us; a.ds = ds; a.sdt = sdt;
+  a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.dc = dc; a.gs = gs; a.us = us; a.ds = ds; a.sdt = sdt;
   a.Gh = (int32_t)(4096 / group_h); a.gsz_h = (int32_t)group_h;
   a.Gi = (int32_t)(I / group_i); a.gsz_i = (int32_t)group_i;
-  a.tq = (const uint2*)((const char*)prepared + TQ_OFFSET);
   a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
   a.limit = limit;
   a.qtiles = (int32_t)(k * I / 16);
-  a.hdr = (uint32_t*)workspace;
   a.hx = (uint64_t*)((char*)workspace + FL_HDR_BYTES);
   a.spin_ticks = spin_ticks;
   a.out = out; a.odt = odt;
   a.xbf = x_dtype == KEEP_BF16;
   const bool g1 = group_h == 4096;
   if (g1) {
-    if (E <= 384) fl_dispatch<6, true>(a, s);
-    else fl_dispatch<16, true>(a, s);
+    if (E <= 384) fl_dispatch<6, true>(h, a, s);
+    else fl_dispatch<16, true>(h, a, s);
   } else {
-    if (E <= 384) fl_dispatch<6, false>(a, s);
-    else fl_dispatch<16, false>(a, s);
+    if (E <= 384) fl_dispatch<6, false>(h, a, s);
+    else fl_dispatch<16, false>(h, a, s);
   }
 }
 

@@ -73,12 +73,12 @@ __device__ __forceinline__ void t8_decode8(const char* img, uint32_t lane, uint2
 
 // ------------------------------------------------------------------ router + gate/up
 
+// The rest of the gate/up launch's arguments (the ones read first, before
+// any other, are kernel arguments of their own: see k_moeq_route_gateup).
 struct MQLayer {
-  const float* logits;
-  const float *bias_s, *bias_d;
   int func, renorm, same_bias;
   float route_scale, tau;
-  int32_t E, k;
+  int32_t k;
   const int32_t* slot_map;  // expert -> pool row (null: the pool holds every expert)
   int32_t S;                // pool rows
   int32_t* idx_out;
@@ -86,13 +86,11 @@ struct MQLayer {
   int32_t* want_out;
   float* want_score_out;
   uint8_t* admit_out;
-  const void* x;
   int32_t H, I;
   const uint16_t *gc, *uc;
   const void *gs, *us;
   int sdt;
   int32_t Gh, gsz_h;
-  const uint4* tq;
   const uint32_t* tq_bad;
   float limit;
   uint16_t* h;  // [k, I] bf16
@@ -106,11 +104,16 @@ struct MQLayer {
 // sixteen slices; after one barrier every wave issues all of its scale and
 // code loads at once, block 0's waves 0 and 1 finish the served and demand
 // selections and write the router's outputs while those are in flight, and
-// gate/up runs tile by tile, then SwiGLU, h in bf16. RES: the nested tier's
+// gate/up runs tile by tile, then SwiGLU, h in bf16. The arguments the first
+// loads need (logits, biases, the table image, x and E) come first and are
+// preloaded into SGPRs by the dispatcher (-amdgpu-kernarg-preload-count), so
+// no load waits for a kernel-argument fetch. RES: the nested tier's
 // residual image and hot[] come into LDS with the table, and a tile of a hot
 // expert adds its residual dot (same A terms) before the SwiGLU.
 template <int NT, bool XBF, int PER, bool RES>
-__global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
+__global__ __launch_bounds__(1024) void k_moeq_route_gateup(const float* logits, const float* bias_s,
+                                                            const float* bias_d, const uint4* tqr, const void* xin,
+                                                            int32_t E, MQLayer a) {
   __shared__ uint4 tqs[TQR_BYTES / 16];
   __shared__ uint4 t8s[RES ? T8R_BYTES / 16 : 1];
   __shared__ int32_t s_hot[RES ? 1024 : 1];
@@ -128,14 +131,20 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
 
   // 0. the router's inputs (waves 0, 1), the table image (64 KiB; every wave
   //    DMAs 4 KiB) and the token slices this wave builds A terms for (16
-  //    bytes per lane pair): wave w >= 2 slice w, waves 2 and 3 also slices 0, 1
+  //    bytes per lane pair): wave w >= 2 slice w, waves 2 and 3 also slices 0,
+  //    1. These use the preloaded arguments only; what needs the others (the
+  //    table flag, the slot map, the nested tier) is issued after them.
   const uint32_t b = blockIdx.x;
   float z[PER], bsv[PER], bdv[PER];
   int sm[PER];
-  if (wv == 0 || (wv == 1 && b == 0)) rt_load<PER>(a.logits, a.bias_s, a.bias_d, a.E, lane, z, bsv, bdv);
-  if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, a.E, lane, sm);
+  if (wv == 0 || (wv == 1 && b == 0)) rt_load<PER>(logits, bias_s, bias_d, E, lane, z, bsv, bdv);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
+  for (int u = 0; u < 4; ++u) dma16_q(tqr + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
+  const uint4 xc = ldg16_q((const uint4*)xin + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
+  const uint4 xc2 = ldg16_q((const uint4*)xin + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
+  if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, E, lane, sm);
   if constexpr (RES) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) dma16_q(a.n.t8 + (wv * 2 + u) * 64 + lane, t8s + (wv * 2 + u) * 64);
@@ -145,8 +154,6 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
       if (wv < 4 && a.S > 896) dma4_q(a.n.hot + min(896 + i0 + lane, a.S - 1), (uint32_t*)s_hot + 896 + i0);
     }
   }
-  const uint4 xc = ldg16_q((const uint4*)a.x + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
-  const uint4 xc2 = ldg16_q((const uint4*)a.x + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
   __builtin_amdgcn_sched_barrier(0);
 
   // 1. the block's routes (wave 0) | A terms: rows 0-2 of slice w are the
@@ -172,13 +179,13 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     if (lane == 0) s_inv4s[slice] = inv4s;
   };
   if (wv == 0) {
-    rt_scores<PER>(z, a.E, a.func, lane, sc);
+    rt_scores<PER>(z, E, a.func, lane, sc);
     uint32_t kk[PER];
-    rt_keys<PER>(sc, bsv, a.E, lane, kk);
+    rt_keys<PER>(sc, bsv, E, lane, kk);
     sel.init(kk, lane);
     sel.rounds(0, kneed, lane, 0);
     e_sel = sel.mine;
-    sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+    sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, E, a.S) : (e_sel >= 0 && e_sel < E ? e_sel : -1);
     if (lane < kneed) s_idx[lane] = sl;
   } else if (wv >= 2) {
     build(xc, wv);
@@ -244,12 +251,12 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
     if (wv == 0) {
       sel.rounds(kneed, a.k, lane, 0);
       e_sel = sel.mine;
-      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, a.E, a.S) : (e_sel >= 0 && e_sel < a.E ? e_sel : -1);
+      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, E, a.S) : (e_sel >= 0 && e_sel < E ? e_sel : -1);
       if (lane >= kneed && lane < a.k) s_idx[lane] = sl;
     } else {
-      e_sel = rt_select_pair<PER>(z, bsv, bdv, a.E, a.k, a.func, a.same_bias != 0, 1, lane, sc);
+      e_sel = rt_select_pair<PER>(z, bsv, bdv, E, a.k, a.func, a.same_bias != 0, 1, lane, sc);
     }
-    const RouteLane r = rt_finish<PER>(e_sel, wv == 0, sc, bsv, a.E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
+    const RouteLane r = rt_finish<PER>(e_sel, wv == 0, sc, bsv, E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
     if (r.valid) {
       if (wv == 0) {
         a.idx_out[lane] = sl;  // the pool row (the expert itself without a slot map)
@@ -314,7 +321,7 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
       const uint32_t q0 = qt * 16u;
       const int32_t e = s_idx[q0 / (uint32_t)a.I];
       float hv = silu_mul(gsum, usum, a.limit);
-      if (*a.tq_bad) hv = __builtin_nanf("");
+      if (tq_bad) hv = __builtin_nanf("");
       if constexpr (RES) {
         const int32_t hr = e >= 0 && e < a.S ? s_hot[e] : -1;
         if (hr < -1 || hr >= a.n.nhot) hv = __builtin_nanf("");
@@ -332,17 +339,14 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(MQLayer a) {
 
 // ------------------------------------------------------------------ down + combine
 
+// The rest of the down launch's arguments (see k_moeq_down for the first ones).
 struct MQDown {
-  int32_t H, I, E;
-  const int32_t* idx;
-  const float* w;
+  int32_t H, E;
   const uint16_t* dc;
   const void* ds;
   int sdt;
   int32_t Gi, gsz_i;
-  const uint4* tq;
   const uint32_t* tq_bad;
-  const uint16_t* h;  // [k, I] bf16
   void* out;
   int odt;
   MQNest n;  // RES only
@@ -352,8 +356,10 @@ struct MQDown {
 // slice). A rows 2r and 2r + 1 hold the two int8 terms of route r's h slice
 // (x its own scale); route r's dot is D rows 2r, 2r + 1. RES: a route with a
 // residual row (hot_route, from the gate/up launch) adds its residual dot.
+// The routes, the table image, h and I are the first (SGPR-preloaded) arguments.
 template <int KMAX, bool RES>
-__global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
+__global__ __launch_bounds__(512) void k_moeq_down(const int32_t* idx, const float* wts, const uint4* tqr,
+                                                   const uint16_t* hin, int32_t I, MQDown a) {
   static_assert(KMAX <= 8, "two A rows per route");
   __shared__ uint4 tqs[TQR_BYTES / 16];
   __shared__ uint4 t8s[RES ? T8R_BYTES / 16 : 1];
@@ -363,33 +369,37 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
   const Q8Keys lk = q8_keys(threadIdx.x & 63);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nwd = a.I >> 8;
+  const int nwd = I >> 8;
   const bool dec = wv < nwd;  // wave-uniform
   const uint32_t j = lane & 15, g = lane >> 4;
-  const uint32_t C = (uint32_t)a.I >> 3;
+  const uint32_t C = (uint32_t)I >> 3;
   const uint32_t n0 = blockIdx.x * 16;
 
-  // 1. routes (scalar loads; KMAX == k), the table (4 pieces), this wave's h slices
+  // 1. routes (scalar loads; KMAX == k), the table (8 pieces), this wave's h
+  //    slices, all from preloaded arguments; then what needs the others
   typedef const __attribute__((address_space(4))) int32_t* cidx;
   typedef const __attribute__((address_space(4))) float* cw;
   int32_t e_r[KMAX], h_r[KMAX];
   float w_r[KMAX];
 #pragma unroll
   for (int r = 0; r < KMAX; ++r) {
-    e_r[r] = ((cidx)a.idx)[r];
-    w_r[r] = ((cw)a.w)[r];
-    if constexpr (RES) h_r[r] = ((cidx)a.n.hot_route)[r];
+    e_r[r] = ((cidx)idx)[r];
+    w_r[r] = ((cw)wts)[r];
   }
 #pragma unroll
-  for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
-  if constexpr (RES) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) dma16_q(a.n.t8 + (wv * 4 + u) * 64 + lane, t8s + (wv * 4 + u) * 64);
-  }
+  for (int u = 0; u < 8; ++u) dma16_q(tqr + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
   const uint32_t wslice = (dec ? wv : 0) * 32 + (lane >> 1);
   uint4 hq[KMAX];
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) hq[r] = ldg16_q((const uint4*)(a.h + (size_t)r * a.I) + wslice);
+  for (int r = 0; r < KMAX; ++r) hq[r] = ldg16_q((const uint4*)(hin + (size_t)r * I) + wslice);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
+  if constexpr (RES) {
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) h_r[r] = ((cidx)a.n.hot_route)[r];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dma16_q(a.n.t8 + (wv * 4 + u) * 64 + lane, t8s + (wv * 4 + u) * 64);
+  }
   __builtin_amdgcn_sched_barrier(0);
   uint32_t dbase[KMAX], rres[KMAX];
   bool hot[KMAX];
@@ -509,7 +519,7 @@ __global__ __launch_bounds__(512) void k_moeq_down(MQDown a) {
       for (int w = 0; w < nwd; ++w) v += red[w][r][threadIdx.x];
       o = wt[r] != 0.f ? fmaf(wt[r], v, o) : o;
     }
-    if (bad || *a.tq_bad) o = __builtin_nanf("");
+    if (bad || tq_bad) o = __builtin_nanf("");
     const size_t oi = n0 + threadIdx.x;
     if (a.odt == KEEP_F16) ((_Float16*)a.out)[oi] = (_Float16)o;
     else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;
@@ -536,16 +546,18 @@ void moe_q_down_launch(const int32_t* idx, const float* w, int64_t k, int64_t E,
                        const uint16_t* dc, const void* ds, int sdt, int64_t group_i, const void* prepared,
                        const void* h, void* out, int odt, hipStream_t s, const MQNest* nest) {
   MQDown d{};
-  d.H = (int32_t)H; d.I = (int32_t)I; d.E = (int32_t)E; d.idx = idx; d.w = w; d.dc = dc; d.ds = ds; d.sdt = sdt;
+  d.H = (int32_t)H; d.E = (int32_t)E; d.dc = dc; d.ds = ds; d.sdt = sdt;
   d.Gi = (int32_t)(I / group_i); d.gsz_i = (int32_t)group_i;
-  d.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
   d.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
-  d.h = (const uint16_t*)h; d.out = out; d.odt = odt;
+  d.out = out; d.odt = odt;
+  const uint4* tqr = (const uint4*)((const char*)prepared + TQR_OFFSET);
+  const uint16_t* hin = (const uint16_t*)h;
+  const int32_t Ii = (int32_t)I;
   if (nest) d.n = *nest;
   const dim3 grid((unsigned)(H / 16)), blk(512u);
 #define DN(K)                                                                        \
-  if (nest) hipLaunchKernelGGL((k_moeq_down<K, true>), grid, blk, 0, s, d);          \
-  else hipLaunchKernelGGL((k_moeq_down<K, false>), grid, blk, 0, s, d)
+  if (nest) hipLaunchKernelGGL((k_moeq_down<K, true>), grid, blk, 0, s, idx, w, tqr, hin, Ii, d); \
+  else hipLaunchKernelGGL((k_moeq_down<K, false>), grid, blk, 0, s, idx, w, tqr, hin, Ii, d)
   switch (k) {
     case 1: DN(1); break;
     case 2: DN(2); break;
@@ -567,22 +579,27 @@ int moe_q_layer_launch(const float* logits, const float* bias_s, const float* bi
                        const void* prepared, float limit, int32_t* idx, float* w, int32_t* want, float* want_score,
                        uint8_t* admit, void* h, void* out, int odt, hipStream_t s, const MQNest* nest) {
   MQLayer a{};
-  a.logits = logits; a.bias_s = bias_s; a.bias_d = bias_d; a.func = func; a.renorm = renorm;
-  a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.E = (int32_t)E; a.k = (int32_t)k;
+  a.func = func; a.renorm = renorm;
+  a.same_bias = bias_s == bias_d; a.route_scale = route_scale; a.tau = tau; a.k = (int32_t)k;
   a.slot_map = slot_map; a.S = (int32_t)(slot_map ? S : E);
   a.idx_out = idx; a.w_out = w; a.want_out = want; a.want_score_out = want_score; a.admit_out = admit;
-  a.x = x; a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.gs = gs; a.us = us;
+  a.H = (int32_t)H; a.I = (int32_t)I; a.gc = gc; a.uc = uc; a.gs = gs; a.us = us;
   a.sdt = sdt; a.Gh = (int32_t)(H / group_h); a.gsz_h = (int32_t)group_h;
-  a.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
+  const uint4* tqr = (const uint4*)((const char*)prepared + TQR_OFFSET);
   a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
   a.limit = limit; a.h = (uint16_t*)h;
+  const int32_t Ei = (int32_t)E;
   a.qtiles = (int32_t)(k * I / 16);
   if (nest) a.n = *nest;
   const int qt = (int)((a.qtiles + 255) / 256);
   const dim3 grid((unsigned)((a.qtiles + qt - 1) / qt)), blk(1024);
 #define LY(NT, BF, PER)                                                                    \
-  if (nest) hipLaunchKernelGGL((k_moeq_route_gateup<NT, BF, PER, true>), grid, blk, 0, s, a); \
-  else hipLaunchKernelGGL((k_moeq_route_gateup<NT, BF, PER, false>), grid, blk, 0, s, a)
+  if (nest)                                                                                    \
+    hipLaunchKernelGGL((k_moeq_route_gateup<NT, BF, PER, true>), grid, blk, 0, s, logits, bias_s, bias_d, tqr, x, \
+                       Ei, a);                                                                    \
+  else                                                                                         \
+    hipLaunchKernelGGL((k_moeq_route_gateup<NT, BF, PER, false>), grid, blk, 0, s, logits, bias_s, bias_d, tqr, x, \
+                       Ei, a)
 #define LY_PER(NT, BF)                 \
   if (E <= 256) LY(NT, BF, 4);         \
   else if (E <= 384) LY(NT, BF, 6);    \
