@@ -48,11 +48,15 @@ import time
 import numpy as np
 
 HBM_PEAK_GBPS = 8000.0
-# the arithmetic of every int8 matrix-core path: decoded E8P weights x 4 are exact int8; activations are split
+# the arithmetic of the int8 matrix-core paths (decode layer, few-token tiles): decoded E8P weights x 4 are exact int8; activations are split
 # exactly into int8 terms under a power-of-two scale (residual below the fp32 rounding of the sums)
 DTYPE_Q8 = ("fp16 activations x E8P-2bit (uint16) codes on the int8 matrix cores: x as 3 int8 terms per "
             "256-wide slice (residual < 2^-21 of the slice max), SwiGLU output h in bf16 as 2 int8 terms "
             "(residual < 2^-14), exact int32 MFMA sums, fp32 scaling, SwiGLU and route combine")
+# the prefill grouped GEMMs (configs 4 and 5 prefill): fp16 matrix cores, as the reference's fp16 sorted matmul
+DTYPE_F16 = ("fp16 activations (bf16 h times a power of two per row, then fp16) x E8P-2bit (uint16) codes "
+             "decoded to exact fp16 on the fp16 matrix cores (v_mfma_f32_32x32x16_f16): exact products, fp32 sums, "
+             "fp32 scaling, SwiGLU and route combine")
 E, H, I, K_TOP = 384, 4096, 2048, 6
 GRAPH_STEPS = 64
 N_SETS = 64
@@ -65,14 +69,16 @@ def log(*a):
 
 LAYER_KERNELS = ("k_moeq_route_gateup", "k_moeq_down")  # the two launches of one layer
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_layer_config2_counters.md")
+PROFILE_C4 = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "grouped_gemm_config4_kernel_trace.md")
+PREFILL_KERNELS = ("k_gemm_e8_gateup", "k_gemm_e8_down")  # the two grouped GEMMs of a config-4 layer
 
 
-def measured_traffic(kernels):
+def measured_traffic(kernels, profile=PROFILE):
     """HBM bytes of one launch of each of `kernels`, summed, from the committed rocprofv3 counter
     summary (None if any is absent)."""
     found = {}
     try:
-        with open(PROFILE) as f:
+        with open(profile) as f:
             for line in f:
                 m = re.match(r"traffic_bytes_per_launch\[(\w+)\] = (\d+)", line.strip())
                 if m:
@@ -593,11 +599,14 @@ def other_config(args) -> int:
                   {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I,
                    "distinct_experts": distinct, "hbm_gbps_distinct": round(gbps, 1),
                    "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2)},
-                  DTYPE_Q8,
-                  roofline={"bound": "mfma", "kernel": "k_gemm_q8 (gate/up + SwiGLU, then down) with k_q8_rows, "
-                                                       "k_route_plan, k_route_combine", "achieved": round(tf, 2),
+                  DTYPE_F16,
+                  roofline={"bound": "mfma", "kernel": "k_gemm_e8 (gate/up + SwiGLU, then down) with k_gq_rowscale "
+                                                       "(h), k_route_plan, k_route_combine", "achieved": round(tf, 2),
                             "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4),
-                            "flops_per_layer": flops, "us_per_layer": round(us, 1), "traffic": None})
+                            "flops_per_layer": flops, "us_per_layer": round(us, 1),
+                            "traffic": measured_traffic(PREFILL_KERNELS, PROFILE_C4),
+                            "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
+                                              "profiles/grouped_gemm_config4_kernel_trace.md"})
             continue
         logits = synth.router_logits(n_sets * T, E, seed=50 + T, device=dev).reshape(n_sets, T, E).contiguous()
         with torch.no_grad():
@@ -633,7 +642,7 @@ def other_config(args) -> int:
                **extra,
                "tok_per_s": round(T / (us * 1e-6), 1), "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2),
                "tflops": round(T * k * flops_per_route / (us * 1e-6) / 1e12, 2)},
-              DTYPE_Q8,
+              DTYPE_Q8 if T <= 64 else DTYPE_F16,
               roofline={"bound": "hbm", "kernel": "layer", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                         "bytes_per_layer": int(layer_b), "us_per_layer": round(us, 2), "traffic": None})

@@ -341,17 +341,19 @@ int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, 
                    float swiglu_limit, void* h_work, void* workspace, int64_t workspace_bytes,
                    void* out, int out_dtype, void* stream);
 
-/* Prefill grouped GEMM on the int8 matrix cores over expert-sorted routes
+/* Prefill grouped GEMM on the fp16 matrix cores over expert-sorted routes
  * (tiles of <= 64 routes of one expert from keep_route_plan): for every tile
  * t and route i < tile_count[t], with p = tile_offset[t] + i,
  *   out[out_index[p], :] = W[tile_expert[t]] . x[lhs[p], :]
- * (lhs / out_index NULL: p itself). x is fp16, bf16 or fp32 [x_rows, K]; each
- * row is split into int8 terms under a power-of-two row scale (three for
- * fp16/fp32 rows, residual at most 2^-20 of the row's max; two for bf16 rows,
- * 2^-13), weights are E8P decoded exactly (x 4) from
- * the `prepared` image (keep_e8p_prepare), int32 sums per term, scales per
- * group in fp32. `workspace` (caller-owned, 256-byte aligned) holds the terms:
- * keep_vq_grouped_gemm_q8_workspace_bytes(x_rows, K) bytes. code_bits = 8
+ * (lhs / out_index NULL: p itself). x is fp16, bf16 or fp32 [x_rows, K]; the
+ * rows enter the matrix cores as fp16, as the reference casts them
+ * (vq_switch.py:712-715,759-771): fp16 rows as they are, bf16 and fp32 rows
+ * times a power of two per row (max |x| in [2^14, 2^15): no overflow, bf16
+ * exact), rounded to nearest even; weights are E8P decoded exactly (x 4) from
+ * T and M of `prepared` (keep_e8p_prepare), products exact, fp32 sums, scales
+ * per group in fp32. `workspace` (caller-owned, 16-byte aligned) holds the
+ * row factors of bf16 / fp32 input: keep_vq_grouped_gemm_q8_workspace_bytes(
+ * x_rows, K) bytes (fp16 input reads none; NULL allowed). code_bits = 8
  * runs the nested tier's 8-bit E8 residual instead ([H, N, K/8] uint8 codes,
  * `prepared` = the packed 8-bit E8 table uint32[256]) and adds it to `out`,
  * which must then be fp32 (the base projection's output, e8p_nested_m1.py:
@@ -371,7 +373,7 @@ int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_rows, const in
 /* The gate and up projections of the same tiles in one pass, with SwiGLU
  * (silu(min(g, L)) * clip(u, -L, L), plain for L <= 0) in fp32 and h stored
  * in bf16 at the route's sorted position: h_out[p, :] for p < routes, I
- * columns. Workspace as keep_vq_grouped_gemm_q8 with K = H. Replaces the
+ * columns. Arithmetic and workspace as keep_vq_grouped_gemm_q8 with K = H. Replaces the
  * gate/up GEMM pair and the activation of QuantizedVQSwitchGLU's shared
  * sorted-route prefill (src/ramp/models/glm4_moe_adapter.py:274-353,355-365). */
 int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,

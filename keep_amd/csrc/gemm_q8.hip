@@ -1,45 +1,47 @@
-// Prefill grouped GEMM over expert-sorted routes on the int8 matrix cores
-// (v_mfma_i32_32x32x32_i8), for tiles of up to 64 routes of one expert
-// (the sorted-route prefill of src/ramp/ops/vq_switch.py:286-377 and
+// Prefill grouped GEMM over expert-sorted routes on the fp16 matrix cores
+// (v_mfma_f32_32x32x16_f16), for tiles of up to 64 routes of one expert (the
+// sorted-route prefill of src/ramp/ops/vq_switch.py:286-377 and
 // glm4_moe_adapter.py:274-353: one route plan shared by gate, up and down).
 //
-// Operands.
-//  * B = decoded weights x 4 (odd integers, |q| <= 15): T[idx] ^ M[signs]
-//    from the 64 KiB LDS image, as the decode-layer kernels read it (see
-//    q8_dev.h). A 32x32x32 MFMA takes 16 k of one column per lane (lane half
-//    h = l / 32 holds k 16h .. 16h + 15); over a 128-wide K block, lane half
-//    h loads codewords 8h .. 8h + 7 of its column (one 16-byte load) and at
-//    k-step s feeds codewords 8h + 2s, 8h + 2s + 1 (q8_decode8's b[s]).
-//  * A = activations as NTERM int8 terms under a per-row power of two s
-//    (max |x| s in [32, 64)): x s = t0 + t1 / 128 (+ t2 / 128^2) + r. Three
-//    terms for fp16 / fp32 rows (residual at most 2^-20 of the row's max, as
-//    the decode layer's activations): gate/up outputs are rounded to bf16 in
-//    h, and two terms (2^-13) flip that rounding often enough to cost ~1e-3
-//    at the layer output. Three for bf16 rows (h of the down projection)
-//    too: h is heavy tailed and two terms under the row's scale left 5.8e-3
-//    of the output rms at single outputs of the 2048-token layer.
-//    k_q8_rows writes the terms once per row ([row][term][K],
-//    each codeword's 8 values in packed-nibble order), so the A bytes of lane
-//    (m, h) at k-step s are row m's bytes 64h + 16s .. + 15 of the K block of
-//    each term: the same k as B.
-//  * D = (D0 + D1 / 128 + D2 / 128^2) / (4 s) x row scale, exact int32 sums per term.
+// Arithmetic. As the reference's sorted path (vq_switch.py:712-715,759-771:
+// the gathered rows cast to float16, then an fp16 matmul), the A rows are fp16:
+// fp16 rows as they are; bf16 and fp32 rows times a power of two r per row
+// (k_gq_rowscale: max |x| r in [2^14, 2^15), so no row overflows fp16 and a
+// bf16 row converts exactly), rounded to nearest even. B is the decoded weight
+// x 4, an odd integer |q| <= 15 (E8P) or an even one in [-16, 14] (the nested
+// tier's 8-bit E8), exact in fp16; products are exact in fp32 and the MFMA sums
+// them in fp32. D / (4 r) x the column's scale is the output.
 //
-// Block = 8 waves, one work item = (route tile, 256 output columns); wave w
-// owns 32 columns and both 32-route m-tiles (the second is skipped when the
-// tile holds <= 32 routes). The gate/up form pairs 16 gate rows with the same
-// 16 up rows in a wave's 32 columns, so lanes l and l ^ 16 hold gate and up
-// of one (route, row) and SwiGLU runs in the epilogue; h is written once, in
-// bf16, at the route's sorted position.
+// B decode. The block's 64 KiB LDS image (built from T and M of
+// keep_e8p_prepare, in natural dim order, T with every byte XOR 0x80) gives a
+// codeword's 8 bytes q + 128 (mod 256) as T' ^ M in two 8-byte lookups (the
+// decode-layer lookup addresses of q8_dev.h). A byte b becomes fp16 by placing
+// it under the byte 0x64 (fp16 1024 + b) and subtracting 1152: four byte
+// permutes and four packed fp16 adds per codeword.
 //
-// Pipeline. Persistent blocks (the LDS image is loaded once per block); a
-// work item streams its K blocks with four blocks' code loads and A tiles
-// in flight in registers (unrolled by four over four buffers, every load
-// unconditional and clamped at the end), the A tile of the next block
-// staged into a second LDS buffer while the current one feeds the MFMAs.
-// Work items are spread XCD-aware: item w = column block x tiles + tile, and
-// each XCD runs a contiguous range of w, so the tiles of an expert at one
-// column block (sharing its code rows) run side by side on one XCD and hit
-// its L2 (measured faster than keeping a tile's column blocks together).
+// Layout. A 32x32x16 MFMA takes 8 k of one row (A) / column (B) per lane:
+// lane half h = l / 32 at k-step s of a 128-wide K block takes codeword 8 h + s
+// (the permutation of K within the block is the same for A and B), so a lane's
+// codes for a K block are 8 consecutive codewords (one 16-byte load) and its A
+// bytes at k-step s are row bytes 128 h + 16 s of the block. D element v of lane
+// l is row 8 (v / 4) + 4 h + v % 4, column l % 32.
+//
+// Block = 8 waves, one work item = (route tile, 512 output columns); wave w
+// owns 64 columns as two 32-column n-tiles and both 32-route m-tiles (the second
+// is skipped when the tile holds <= 32 routes): each A operand read from LDS
+// feeds two MFMAs. (Problems with fewer than four such items per CU take items
+// of 256 columns, one n-tile per wave, to spread over the CUs.) The gate/up form pairs 16 gate rows with the same 16 up rows
+// in each n-tile, so lanes l and l ^ 16 hold gate and up of one (route, row)
+// and SwiGLU runs in the epilogue; h is written once, in bf16, at the route's
+// sorted position.
+//
+// Pipeline. Persistent blocks (the LDS image is built once per block); a work
+// item streams its K blocks with D blocks' code loads and A rows in flight in
+// registers (every load unconditional and clamped at the end), the A rows of
+// the next block staged into a second LDS buffer while the current one feeds
+// the MFMAs; each k-step's B operands are decoded during the one before.
+// Work items are spread XCD-aware (see the item loop).
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.h"
@@ -49,94 +51,105 @@
 namespace keep {
 
 constexpr int GQ_WAVES = 8;
-constexpr int GQ_M = 64;                 // routes per tile (two 32-row m-tiles)
-constexpr int GQ_KB = 128;               // k per K block
-// LDS bytes per A row: the terms of one K block, padded so the rows of a
-// 16-lane group start 4 banks apart (272 B) or 36 apart (400 B): no conflicts
-template <int NTERM>
-constexpr int gq_row() { return NTERM * GQ_KB + 16; }
+constexpr int GQ_THREADS = 64 * GQ_WAVES;
+constexpr int GQ_M = 64;                // routes per tile (two 32-row m-tiles)
+constexpr int GQ_KB = 128;              // k per K block
+constexpr int GQ_ROW = 2 * GQ_KB + 16;  // LDS bytes per A row: rows 4 banks apart (no conflicts)
 constexpr int GQ_XCDS = 8;
 
-typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ i32x16 mfma32_i8(q8v4 a, q8v4 b, i32x16 c) {
-  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x16 mfma32_f16(h8 a, h8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// ------------------------------------------------------------------ row terms
+// Bytes q + 128 (mod 256) of eight integer weights q -> the fp16 values q.
+__device__ __forceinline__ h8 gq_f16_of_bytes(uint2 b) {
+  const uint32_t k = 0x64646464u;
+  const uint32_t d[4] = {__builtin_amdgcn_perm(k, b.x, 0x04010400u), __builtin_amdgcn_perm(k, b.x, 0x04030402u),
+                         __builtin_amdgcn_perm(k, b.y, 0x04010400u), __builtin_amdgcn_perm(k, b.y, 0x04030402u)};
+  h8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const h2v v = __builtin_bit_cast(h2v, d[i]) - h2v{(_Float16)1152.f, (_Float16)1152.f};
+    r[2 * i] = v[0];
+    r[2 * i + 1] = v[1];
+  }
+  return r;
+}
 
-// One wave per row: s from max |x| (NaN anywhere in the row -> inv NaN), then
-// the NTERM terms of each codeword's 8 values in packed-nibble order (dims
-// 0, 2, 4, 6, 1, 3, 5, 7).
-template <typename XT, int NTERM>
-__global__ __launch_bounds__(256) void k_q8_rows(const XT* x, int64_t rows, int K, uint8_t* terms, float* inv) {
+// Natural-order bytes of a packed-nibble-order pair (dims 0, 2, 4, 6 | 1, 3, 5, 7).
+__device__ __forceinline__ uint2 gq_natural(uint2 v) {
+  return make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x05010400u), __builtin_amdgcn_perm(v.y, v.x, 0x07030602u));
+}
+
+// E8P codeword (the low or high half of a code dword) -> its 8 bytes q + 128, from the LDS image.
+__device__ __forceinline__ uint2 gq_lookup(const char* img, const Q8Keys& k, uint32_t w, bool hi) {
+  const uint32_t a1 = __builtin_amdgcn_perm(w, k.base1, hi ? k.s1hi : k.s1lo);
+  const uint32_t a2 = __builtin_amdgcn_perm(w, k.base2, hi ? k.s2hi : k.s2lo);
+  const uint2 x1 = *(const uint2*)(img + a1), x2 = *(const uint2*)(img + a2);
+  return make_uint2(x1.x ^ x2.x, x1.y ^ x2.y);
+}
+
+// ------------------------------------------------------------------ row scales
+
+// One wave per row: r = 2^(14 - floor(log2 max |x|)) (1 for a zero row, NaN for a
+// row holding NaN or inf, which then reaches the row's outputs) and 1 / r.
+template <typename XT>
+__global__ __launch_bounds__(256) void k_gq_rowscale(const XT* x, int64_t rows, int K, float2* rs) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int C = K >> 3;
   const XT* xr = x + row * K;
-  auto load8 = [&](int c, float (&v)[8]) {
-    if constexpr (sizeof(XT) == 4) {
-      const float4 p = ((const float4*)(xr + 8 * c))[0], q = ((const float4*)(xr + 8 * c))[1];
-      v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
-    } else {
-      const uint4 w = *(const uint4*)(xr + 8 * c);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = ww[i] & 0xffffu, hi = ww[i] >> 16;
-        if constexpr (__is_same(XT, bf16s)) {
-          v[2 * i] = __uint_as_float(lo << 16);
-          v[2 * i + 1] = __uint_as_float(hi << 16);
-        } else {
-          v[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)lo);
-          v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)hi);
-        }
-      }
-    }
-  };
   float mx = 0.f;
-  bool nan = false;
-  for (int c = lane; c < C; c += 64) {
-    float v[8];
-    load8(c, v);
+  bool bad = false;
+  for (int i = lane * 4; i < K; i += 256) {
+    float v[4];
+    if constexpr (sizeof(XT) == 4) {
+      const float4 p = *(const float4*)(xr + i);
+      v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
+    } else {
+      const uint2 p = *(const uint2*)(xr + i);
+      v[0] = __uint_as_float(p.x << 16); v[1] = __uint_as_float(p.x & 0xffff0000u);
+      v[2] = __uint_as_float(p.y << 16); v[3] = __uint_as_float(p.y & 0xffff0000u);
+    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      mx = fmaxf(mx, fabsf(v[i]));
-      nan |= v[i] != v[i];
+    for (int t = 0; t < 4; ++t) {
+      bad |= !(fabsf(v[t]) <= 3.4028235e38f);  // NaN or inf
+      mx = fmaxf(mx, fabsf(v[t]));
     }
   }
   mx = wave_max(mx);
-  nan = __any(nan);
-  float s, inv4s;
-  q8_scale(mx, s, inv4s);
-  if (nan) inv4s = __builtin_nanf("");
-  uint8_t* t0 = terms + row * NTERM * K;
-  for (int c = lane; c < C; c += 64) {
-    float v[8];
-    load8(c, v);
-    const float p[4] = {v[0], v[2], v[4], v[6]}, q[4] = {v[1], v[3], v[5], v[7]};
-    uint32_t lo[NTERM], hi[NTERM];
-    q8_terms<NTERM>(p, s, lo);
-    q8_terms<NTERM>(q, s, hi);
-#pragma unroll
-    for (int n = 0; n < NTERM; ++n) *(uint2*)(t0 + n * K + 8 * c) = make_uint2(lo[n], hi[n]);
+  bad = __any(bad);
+  if (lane == 0) {
+    float r = 1.f, ri = 1.f;
+    if (bad) {
+      r = ri = __builtin_nanf("");
+    } else if (mx > 0.f) {
+      const int e = (int)((__float_as_uint(mx) >> 23) & 0xffu) - 127;  // floor(log2 mx) for a normal mx
+      const int k = min(max(14 - e, -126), 127);
+      r = __uint_as_float((uint32_t)(127 + k) << 23);
+      ri = __uint_as_float((uint32_t)(127 - k) << 23);
+    }
+    rs[row] = make_float2(r, ri);
   }
-  if (lane == 0) inv[row] = inv4s;
 }
 
 // ------------------------------------------------------------------ grouped GEMM
 
 struct GQArgs {
-  const uint8_t* xt;   // [x_rows][2][K] int8 terms
-  const float* xinv;   // [x_rows] 1 / (4 s)
+  const void* x;        // A rows [x_rows][K], fp16 / bf16 / fp32
+  int xdt;
+  const float2* rs;     // per A row (r, 1 / r) for bf16 / fp32 rows (null: fp16, r = 1)
   int64_t x_rows;
   const int32_t* lhs;   // sorted position -> A row (null: the position itself)
   const int32_t* oidx;  // sorted position -> output row (null: the position itself)
   const uint16_t *c0, *c1;  // codes [E][N][K / 8] (gate/up: gate, up)
   const void *s0, *s1;      // scales [E][N][G]
   int sdt;
-  const uint4* tq;
+  const void* tq;           // E8P: T and M (keep_e8p_prepare); residual: the packed 8-bit E8 table
   const uint32_t* tq_bad;
   const int32_t *te, *to, *tc;
   int64_t n_tiles, routes;
@@ -147,58 +160,69 @@ struct GQArgs {
   int64_t ncb, total, per_xcd;  // column blocks, work items, items per XCD
 };
 
-// RES: the nested tier's 8-bit E8 residual instead of E8P base codes (t8_entry
-// and t8_decode2 in q8_dev.h); the block builds the 32 KiB residual image from
-// the packed table and the result is added to the fp32 output (the base
-// projection's).
-template <bool GATEUP, bool GROUPED, int NTERM, bool RES = false>
-__global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
-  constexpr int D = NTERM == 3 ? 3 : 4;  // K blocks in flight
-  constexpr int ROW = gq_row<NTERM>();
+// RES: the nested tier's 8-bit E8 residual instead of E8P base codes (one code
+// byte per codeword, one 8-byte lookup); the result is added to the fp32
+// output (the base projection's). XT: the A rows' element type.
+// NTW: 32-column n-tiles per wave (2: items of 512 columns; 1: of 256, for
+// problems with too few items to spread over the CUs).
+template <bool GATEUP, bool GROUPED, typename XT, bool RES = false, int NTW = 2>
+__global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
+  constexpr int D = 2;                         // K blocks in flight
+  constexpr int NCOL = GQ_WAVES * 32 * NTW;    // output columns per work item
+  constexpr int XV = sizeof(XT) == 4 ? 4 : 2;           // 16-byte A loads per thread and K block
   __shared__ uint4 tqs[TQR_BYTES / 16];
-  __shared__ __attribute__((aligned(16))) uint8_t ash[2][GQ_M * ROW];
-  __shared__ float s_inv[GQ_M];
+  __shared__ __attribute__((aligned(16))) uint8_t ash[2][GQ_M * GQ_ROW];
+  __shared__ float s_ok[GQ_M];  // 1 / r of the row (NaN: no valid row)
   __shared__ int32_t s_orow[GQ_M];
-  const char* tq = (const char*)tqs;
+  const char* img = (const char*)tqs;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, h = lane >> 5;
   const Q8Keys lk = q8_keys(lane);
   const uint32_t tq_bad = GATEUP ? ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0] : 0u;
-  if constexpr (RES) {
-    const uint2 v = t8_entry(((const uint32_t*)a.tq)[tid >> 1]);  // entry tid / 2, copies 8 (tid & 1) .. + 7
-    uint2* row = (uint2*)((char*)tqs + (tid >> 1) * 128 + (tid & 1) * 64);
+  {  // the LDS image: entry tid / 2, copies 8 (tid & 1) .. + 7
+    const int e = tid >> 1;
+    if constexpr (RES) {  // row e: sixteen copies of the 8 bytes 2 (nibble d - 8) + 128, d = 0..7
+      const uint32_t p = ((const uint32_t*)a.tq)[e];
+      uint32_t b[2] = {0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) row[i] = v;
-  } else {
+      for (int d = 0; d < 8; ++d) b[d >> 2] |= ((uint32_t)(2 * ((int)((p >> (4 * d)) & 15u) - 8) + 128) & 0xffu) << (8 * (d & 3));
+      uint2* row = (uint2*)(img + e * 128 + (tid & 1) * 64);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
+      for (int i = 0; i < 8; ++i) row[i] = make_uint2(b[0], b[1]);
+    } else {  // row e: sixteen copies of (T'[e], M[e]), T' = T ^ 0x80 per byte, natural dim order
+      const uint2 t = gq_natural(((const uint2*)a.tq)[e]), m = gq_natural(((const uint2*)a.tq)[256 + e]);
+      const uint4 v = make_uint4(t.x ^ 0x80808080u, t.y ^ 0x80808080u, m.x, m.y);
+      uint4* row = tqs + e * 16 + (tid & 1) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) row[i] = v;
+    }
   }
-  wait_vm_q<0>();
   __syncthreads();
 
   const int64_t C = a.K >> 3;
   const int nkb = (int)(a.K / GQ_KB);
   const int xcd = blockIdx.x % GQ_XCDS;
   const int nb = gridDim.x / GQ_XCDS;
-  const int sr = tid >> 3, sp = tid & 7;  // A staging: row sr, 16-byte chunk sp of each term
-  // B operands of k-step s from a code word: E8P dword (two codewords) or two residual bytes
-  auto decode = [&](uint32_t w) -> q8v4 {
-    if constexpr (RES) {
-      return t8_decode2(tq, (uint32_t)lane, w);
-    } else {
-      return q8_decode2(tq, lk, w);
-    }
-  };
-  auto words = [&](const uint4& q, uint32_t (&w)[4]) {
-    if constexpr (RES) {
-      w[0] = q.x & 0xffffu; w[1] = q.x >> 16; w[2] = q.y & 0xffffu; w[3] = q.y >> 16;
-    } else {
-      w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
-    }
-  };
+  // A staging: row sr, 8-element chunks sp and sp + 8 of its K block (the 8 threads of a row
+  // write 128 consecutive LDS bytes per store: no bank conflicts)
+  const int sr = tid >> 3, sp = tid & 7;
   const uint32_t sbytes = a.sdt == KEEP_F32 ? 4u : 2u;
+  // B operand of k-step s of one n-tile from this lane's 8 codewords of the K block
+  auto bop = [&](const uint4& q, int s) -> h8 {
+    if constexpr (RES) {  // code bytes: codeword s is byte s of q.x / q.y
+      const uint32_t w = s < 4 ? q.x : q.y;
+      const uint32_t byte = (w >> (8 * (s & 3))) & 0xffu;
+      return gq_f16_of_bytes(*(const uint2*)(img + byte * 128u + (uint32_t)(lane & 15) * 8u));
+    } else {
+      const uint32_t w = s < 2 ? q.x : (s < 4 ? q.y : (s < 6 ? q.z : q.w));
+      return gq_f16_of_bytes(gq_lookup(img, lk, w, (s & 1) != 0));
+    }
+  };
 
+  // XCD-aware order: item w = column block x tiles + tile, each XCD running a
+  // contiguous range of w, so the tiles of an expert at one column block (its
+  // code rows) run side by side on one XCD and share its L2.
   for (int64_t j = blockIdx.x / GQ_XCDS; j < a.per_xcd; j += nb) {
     const int64_t w = xcd * a.per_xcd + j;
     if (w >= a.total) break;
@@ -212,127 +236,157 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
     const bool bad = e < 0 || e >= a.E || cnt_raw > GQ_M;  // rows written as NaN
     const bool two = cnt > 32;
 
-    // this lane's column: a code row and its scale row
-    int64_t n;
-    const uint16_t* cbase;
-    const void* sbase;
-    if constexpr (GATEUP) {
-      n = cb * 128 + wv * 16 + (c & 15);
-      cbase = c < 16 ? a.c0 : a.c1;
-      sbase = c < 16 ? a.s0 : a.s1;
-    } else {
-      n = cb * 256 + wv * 32 + c;
-      cbase = a.c0;
-      sbase = a.s0;
+    // this lane's column of each n-tile: a code row and its scale row
+    int64_t n[NTW], crow[NTW];
+    bool nv[NTW];
+    const uint8_t* cp[NTW];
+    const void* sbase[NTW];
+#pragma unroll
+    for (int jn = 0; jn < NTW; ++jn) {
+      const uint16_t* cbase;
+      if constexpr (GATEUP) {
+        n[jn] = cb * (NCOL / 2) + (wv * NTW + jn) * 16 + (c & 15);
+        cbase = c < 16 ? a.c0 : a.c1;
+        sbase[jn] = c < 16 ? a.s0 : a.s1;
+      } else {
+        n[jn] = cb * NCOL + (wv * NTW + jn) * 32 + c;
+        cbase = a.c0;
+        sbase[jn] = a.s0;
+      }
+      nv[jn] = n[jn] < a.N;
+      crow[jn] = (bad || !nv[jn]) ? 0 : e * a.N + n[jn];
+      // E8P: 16 bytes per K block (codewords 8 h ..); residual: 8 bytes (one byte per codeword)
+      cp[jn] = RES ? (const uint8_t*)cbase + crow[jn] * C + 8 * h : (const uint8_t*)(cbase + crow[jn] * C + 8 * h);
     }
-    const bool nv = n < a.N;
-    const int64_t crow = (bad || !nv) ? 0 : e * a.N + n;
-    const uint16_t* cp = cbase + crow * C + 8 * h;  // E8P: 16 bytes per K block
-    const uint8_t* cp8 = (const uint8_t*)cbase + crow * C + 8 * h;  // residual: 8 bytes per K block
     // A staging row of this thread
     int64_t xs = off + min(sr, cnt - 1);
     xs = a.lhs ? (int64_t)a.lhs[xs] : xs;
     if (xs < 0 || xs >= a.x_rows) xs = 0;
-    const uint8_t* ap = a.xt + xs * NTERM * a.K + 16 * sp;
-    // every wave has left the previous item's epilogue, which reads s_inv and
+    const uint8_t* ap = (const uint8_t*)a.x + (xs * a.K + 8 * sp) * (int64_t)sizeof(XT);
+    const float rsc = a.rs ? a.rs[xs].x : 1.f;  // this thread's row factor r
+    // every wave has left the previous item's epilogue, which reads s_ok and
     // s_orow after the run loop's last barrier (block-uniform: every skip
     // above is taken by the whole block)
     __syncthreads();
     if (tid < GQ_M) {
       const int64_t pos = off + min(tid, cnt - 1);
       const int64_t xr = a.lhs ? (int64_t)a.lhs[pos] : pos;
-      s_inv[tid] = (xr >= 0 && xr < a.x_rows) ? a.xinv[xr] : __builtin_nanf("");
+      s_ok[tid] = (xr >= 0 && xr < a.x_rows) ? (a.rs ? a.rs[xr].y : 1.f) : __builtin_nanf("");
       s_orow[tid] = a.oidx ? a.oidx[pos] : (int32_t)pos;
     }
 
     struct Buf {
-      uint4 q, at[NTERM];  // codes of block u, A terms of block u + 1
+      uint4 q[NTW], ax[XV];  // codes of block u, A row elements of block u + 1
     };
     auto issue = [&](int u, Buf& b) {
       const int kq = min(u, nkb - 1), ka = min(u + 1, nkb - 1);
-      if constexpr (RES) {
-        const uint2 v = ldg8_q(cp8 + kq * 16);
-        b.q = make_uint4(v.x, v.y, 0u, 0u);
-      } else {
-        b.q = ldg16_q(cp + kq * 16);
+#pragma unroll
+      for (int jn = 0; jn < NTW; ++jn) {
+        if constexpr (RES) {
+          const uint2 v = ldg8_q(cp[jn] + kq * 16);
+          b.q[jn] = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+          b.q[jn] = ldg16_q(cp[jn] + kq * 32);
+        }
       }
 #pragma unroll
-      for (int t = 0; t < NTERM; ++t) b.at[t] = ldg16_q(ap + t * a.K + ka * GQ_KB);
+      for (int i = 0; i < XV; ++i) b.ax[i] = ldg16_q(ap + ((int64_t)ka * GQ_KB + 64 * (i / (XV / 2))) * sizeof(XT) +
+                                                     16 * (i % (XV / 2)));
     };
-    auto stage = [&](int buf, const uint4 (&at)[NTERM]) {
-      uint8_t* d = &ash[buf][sr * ROW + 16 * sp];
+    // 16 elements of the row (x r for bf16 / fp32) -> fp16 (round to nearest even), into the A buffer
+    auto stage = [&](int buf, const uint4 (&ax)[XV]) {
+      uint4 o[2];
+      if constexpr (sizeof(XT) == 2 && !std::is_same<XT, bf16s>::value) {
+        o[0] = ax[0];
+        o[1] = ax[1];
+      } else {
+        uint32_t* ow = (uint32_t*)o;
 #pragma unroll
-      for (int t = 0; t < NTERM; ++t) *(uint4*)(d + t * GQ_KB) = at[t];
+        for (int i = 0; i < 8; ++i) {
+          float f0, f1;
+          if constexpr (sizeof(XT) == 4) {
+            const uint32_t* xw = (const uint32_t*)ax;
+            f0 = __uint_as_float(xw[2 * i]);
+            f1 = __uint_as_float(xw[2 * i + 1]);
+          } else {
+            const uint32_t wd = ((const uint32_t*)ax)[i];
+            f0 = __uint_as_float(wd << 16);
+            f1 = __uint_as_float(wd & 0xffff0000u);
+          }
+          const h2v hv = {(_Float16)(f0 * rsc), (_Float16)(f1 * rsc)};
+          ow[i] = __builtin_bit_cast(uint32_t, hv);
+        }
+      }
+      uint8_t* d = &ash[buf][sr * GQ_ROW + 16 * sp];
+      *(uint4*)d = o[0];
+      *(uint4*)(d + 128) = o[1];
     };
     {
-      uint4 at0[NTERM];
+      uint4 ax0[XV];
 #pragma unroll
-      for (int t = 0; t < NTERM; ++t) at0[t] = ldg16_q(ap + t * a.K);
+      for (int i = 0; i < XV; ++i) ax0[i] = ldg16_q(ap + 64 * (i / (XV / 2)) * sizeof(XT) + 16 * (i % (XV / 2)));
       wait_vm_q<0>();
-      stage(0, at0);
+      stage(0, ax0);
     }
     Buf bb[D];
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(i, bb[i]);
-    __syncthreads();  // A block 0, s_inv, s_orow; the previous item's readers are done
+    __syncthreads();  // A block 0, s_ok, s_orow; the previous item's readers are done
 
-    i32x16 acc[2][NTERM];
-    float accf[2][16];
+    f32x16 acc[2][NTW];
+    float accf[2][NTW][GROUPED ? 16 : 1];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int t = 0; t < NTERM; ++t) acc[mt][t] = i32x16{};
+      for (int jn = 0; jn < NTW; ++jn) {
+        acc[mt][jn] = f32x16{};
 #pragma unroll
-      for (int v = 0; v < 16; ++v) accf[mt][v] = 0.f;
-    }
-    auto dot = [&](int mt, int v) {  // the K block sums of D element v, in units of 1 / (4 s)
-      float d = (float)acc[mt][0][v] + (float)acc[mt][1][v] * 0.0078125f;
-      if constexpr (NTERM == 3) d += (float)acc[mt][2][v] * 0.00006103515625f;
-      return d;
-    };
+        for (int v = 0; v < (GROUPED ? 16 : 1); ++v) accf[mt][jn][v] = 0.f;
+      }
     auto fold = [&](int g) {  // scale group g ends: add its partial sums
-      const float sc = nv && !bad ? scale_cvt(ldg4_q((const char*)sbase + (((crow * a.G + g) * sbytes) & ~(int64_t)3)),
-                                              a.sdt, (uint32_t)(crow * a.G + g))
-                                  : 0.f;
+      if constexpr (GROUPED) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+        for (int jn = 0; jn < NTW; ++jn) {
+          const int64_t si = crow[jn] * a.G + g;
+          const float sc = nv[jn] && !bad ? scale_cvt(ldg4_q((const char*)sbase[jn] + ((si * sbytes) & ~(int64_t)3)),
+                                                      a.sdt, (uint32_t)si)
+                                          : 0.f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) accf[mt][v] += dot(mt, v) * sc;
+          for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-        for (int t = 0; t < NTERM; ++t) acc[mt][t] = i32x16{};
+            for (int v = 0; v < 16; ++v) accf[mt][jn][v] = fmaf(acc[mt][jn][v], sc, accf[mt][jn][v]);
+            acc[mt][jn] = f32x16{};
+          }
+        }
       }
     };
-    // NT live m-tiles. Unit u multiplies with the B operands of block u
-    // (decoded during unit u - 1) while it decodes block u + 1 one dword per
-    // k-step, stages the A terms of block u + 1 and issues the loads of
-    // block u + D: the matrix cores run under the decode and the staging.
-    q8v4 Bx[2][4];
-    {
-      uint32_t w4[4];
-      words(bb[0].q, w4);
+    // NT live m-tiles. Unit u stages the A rows of block u + 1, runs the MFMAs
+    // of block u k-step by k-step, decoding each k-step's B operands during the
+    // one before (the last k-step decodes block u + 1's first), and issues the
+    // loads of block u + D.
+    h8 Bc[NTW];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Bx[0][i] = decode(w4[i]);
-    }
+    for (int jn = 0; jn < NTW; ++jn) Bc[jn] = bop(bb[0].q[jn], 0);
     auto run = [&](auto nt_c) {
       constexpr int NT = decltype(nt_c)::value;
-      auto unit = [&](int u, Buf& b, const Buf& bn, const q8v4 (&Bc)[4], q8v4 (&Bn)[4]) {
-        stage((u + 1) & 1, b.at);
-        uint32_t wn[4];
-        words(bn.q, wn);
+      auto unit = [&](int u, Buf& b, const Buf& bn) {
+        stage((u + 1) & 1, b.ax);
         if (u < nkb) {
-          const uint8_t* abase = &ash[u & 1][c * ROW + 64 * h];
+          const uint8_t* abase = &ash[u & 1][c * GQ_ROW + 128 * h];
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            q8v4 A[NT][NTERM];
+          for (int s = 0; s < 8; ++s) {
+            h8 A[NT];
 #pragma unroll
-            for (int mt = 0; mt < NT; ++mt)
+            for (int mt = 0; mt < NT; ++mt) A[mt] = *(const h8*)(abase + mt * 32 * GQ_ROW + 16 * s);
+            h8 Bn[NTW];
 #pragma unroll
-              for (int t = 0; t < NTERM; ++t) A[mt][t] = *(const q8v4*)(abase + mt * 32 * ROW + t * GQ_KB + 16 * s);
+            for (int jn = 0; jn < NTW; ++jn) Bn[jn] = s < 7 ? bop(b.q[jn], s + 1) : bop(bn.q[jn], 0);
 #pragma unroll
-            for (int mt = 0; mt < NT; ++mt)
+            for (int jn = 0; jn < NTW; ++jn)
 #pragma unroll
-              for (int t = 0; t < NTERM; ++t) acc[mt][t] = mfma32_i8(A[mt][t], Bc[s], acc[mt][t]);
-            Bn[s] = decode(wn[s]);
+              for (int mt = 0; mt < NT; ++mt) acc[mt][jn] = mfma32_f16(A[mt], Bc[jn], acc[mt][jn]);
+#pragma unroll
+            for (int jn = 0; jn < NTW; ++jn) Bc[jn] = Bn[jn];
           }
           if constexpr (GROUPED) {
             if ((u + 1) % a.kpg == 0) fold(u / (int)a.kpg);
@@ -341,45 +395,46 @@ __global__ __launch_bounds__(512) void k_gemm_q8(GQArgs a) {
         issue(u + D, b);
         __syncthreads();
       };
-      constexpr int UN = D % 2 == 0 ? D : 2 * D;  // a multiple of D (buffers) and of 2 (B operands)
-      for (int u = 0; u < nkb; u += UN) {  // every call unconditional: blocks past the end only reload
+      for (int u = 0; u < nkb; u += D) {  // every call unconditional: blocks past the end only reload
 #pragma unroll
-        for (int i = 0; i < UN; ++i) unit(u + i, bb[i % D], bb[(i + 1) % D], Bx[i & 1], Bx[(i + 1) & 1]);
+        for (int i = 0; i < D; ++i) unit(u + i, bb[i], bb[(i + 1) % D]);
       }
     };
     if (two) run(std::integral_constant<int, 2>{});
     else run(std::integral_constant<int, 1>{});
     wait_vm_q<0>();
 
-    // epilogue: D row m = 8 (v / 4) + 4 h + v % 4 of m-tile mt, column c
-    float sc = 1.f;
-    if constexpr (!GROUPED) {
-      sc = nv && !bad ? scale_cvt(ldg4_q((const char*)sbase + ((crow * sbytes) & ~(int64_t)3)), a.sdt, (uint32_t)crow)
-                      : 0.f;
-    }
+    // epilogue: D row m = 8 (v / 4) + 4 h + v % 4 of m-tile mt, column c of n-tile jn
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int jn = 0; jn < NTW; ++jn) {
+      float sc = 0.25f;
+      if constexpr (!GROUPED) {
+        sc = nv[jn] && !bad ? 0.25f * scale_cvt(ldg4_q((const char*)sbase[jn] + ((crow[jn] * sbytes) & ~(int64_t)3)),
+                                                a.sdt, (uint32_t)crow[jn])
+                            : 0.f;
+      }
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        float val;
-        if constexpr (GROUPED) val = accf[mt][v] * s_inv[m];
-        else val = dot(mt, v) * s_inv[m] * sc;
-        if (bad) val = __builtin_nanf("");
-        if constexpr (GATEUP) {
-          const float other = __shfl_xor(val, 16, 64);
-          float hv = c < 16 ? silu_mul(val, other, a.limit) : silu_mul(other, val, a.limit);
-          if (tq_bad) hv = __builtin_nanf("");
-          const bool mine = (c < 16) == ((v & 1) == 0);
-          if (mine && m < cnt && nv)
-            ((uint16_t*)a.out)[(off + m) * a.N + n] = from_float<bf16s>(hv).bits;
-        } else {
-          if (m < cnt && nv) {
-            const int64_t o = (int64_t)s_orow[m] * a.N + n;
-            if constexpr (RES) ((float*)a.out)[o] += val;
-            else if (a.odt == KEEP_F32) ((float*)a.out)[o] = val;
-            else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[o] = from_float<bf16s>(val).bits;
-            else ((_Float16*)a.out)[o] = (_Float16)val;
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int m = mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          float val = (GROUPED ? accf[mt][jn][v] : acc[mt][jn][v]) * sc * s_ok[m];
+          if (bad) val = __builtin_nanf("");
+          if constexpr (GATEUP) {
+            const float other = __shfl_xor(val, 16, 64);
+            float hv = c < 16 ? silu_mul(val, other, a.limit) : silu_mul(other, val, a.limit);
+            if (tq_bad) hv = __builtin_nanf("");
+            const bool mine = (c < 16) == ((v & 1) == 0);
+            if (mine && m < cnt && nv[jn])
+              ((uint16_t*)a.out)[(off + m) * a.N + n[jn]] = from_float<bf16s>(hv).bits;
+          } else {
+            if (m < cnt && nv[jn]) {
+              const int64_t o = (int64_t)s_orow[m] * a.N + n[jn];
+              if constexpr (RES) ((float*)a.out)[o] += val;
+              else if (a.odt == KEEP_F32) ((float*)a.out)[o] = val;
+              else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[o] = from_float<bf16s>(val).bits;
+              else ((_Float16*)a.out)[o] = (_Float16)val;
+            }
           }
         }
       }
@@ -422,51 +477,57 @@ __global__ __launch_bounds__(256) void k_route_combine(const float* y, const flo
 
 // ------------------------------------------------------------------ host side
 
-// Three terms for every row dtype. Two terms for bf16 rows (h of the down
-// projection) leave a residual of 2^-13 of the row's maximum; h is heavy
-// tailed (a row's maximum is ~12x its rms at config 4), and that residual
-// measured 5.8e-3 of the output rms at single outputs of a 2048-token layer,
-// where three terms leave 2^-20.
-int gq_nterm(int) { return 3; }
-int64_t gq_ws_terms(int64_t rows, int64_t K) { return (rows * 3 * K + 255) / 256 * 256; }
-int64_t gq_ws_bytes(int64_t rows, int64_t K) { return gq_ws_terms(rows, K) + (rows * 4 + 255) / 256 * 256; }
+// Workspace: the row factors of bf16 / fp32 rows.
+int64_t gq_ws_bytes(int64_t rows) { return (rows * (int64_t)sizeof(float2) + 255) / 256 * 256; }
 
-void gq_rows(const void* x, int x_dtype, int64_t rows, int64_t K, uint8_t* ws, hipStream_t s) {
+const float2* gq_rowscale(const void* x, int x_dtype, int64_t rows, int64_t K, void* ws, hipStream_t s) {
+  if (x_dtype == KEEP_F16) return nullptr;
+  float2* rs = (float2*)ws;
   const dim3 grid((unsigned)((rows + 3) / 4));
-  uint8_t* terms = ws;
-  float* inv = (float*)(ws + gq_ws_terms(rows, K));
-  if (x_dtype == KEEP_F16)
-    hipLaunchKernelGGL((k_q8_rows<_Float16, 3>), grid, dim3(256), 0, s, (const _Float16*)x, rows, (int)K, terms, inv);
-  else if (x_dtype == KEEP_BF16)
-    hipLaunchKernelGGL((k_q8_rows<bf16s, 3>), grid, dim3(256), 0, s, (const bf16s*)x, rows, (int)K, terms, inv);
+  if (x_dtype == KEEP_BF16)
+    hipLaunchKernelGGL((k_gq_rowscale<bf16s>), grid, dim3(256), 0, s, (const bf16s*)x, rows, (int)K, rs);
   else
-    hipLaunchKernelGGL((k_q8_rows<float, 3>), grid, dim3(256), 0, s, (const float*)x, rows, (int)K, terms, inv);
+    hipLaunchKernelGGL((k_gq_rowscale<float>), grid, dim3(256), 0, s, (const float*)x, rows, (int)K, rs);
+  return rs;
 }
 
-template <bool GATEUP, int NTERM>
+template <bool GATEUP, bool RES, typename XT, int NTW>
+void gq_launch_x(const GQArgs& a, dim3 grid, hipStream_t s) {
+  if (a.G > 1) hipLaunchKernelGGL((k_gemm_e8<GATEUP, true, XT, RES, NTW>), grid, dim3(GQ_THREADS), 0, s, a);
+  else hipLaunchKernelGGL((k_gemm_e8<GATEUP, false, XT, RES, NTW>), grid, dim3(GQ_THREADS), 0, s, a);
+}
+
+template <bool GATEUP, bool RES, int NTW>
 void gq_launch_t(const GQArgs& a, dim3 grid, hipStream_t s) {
-  if (a.G > 1) hipLaunchKernelGGL((k_gemm_q8<GATEUP, true, NTERM>), grid, dim3(512), 0, s, a);
-  else hipLaunchKernelGGL((k_gemm_q8<GATEUP, false, NTERM>), grid, dim3(512), 0, s, a);
+  if (a.xdt == KEEP_F16) gq_launch_x<GATEUP, RES, _Float16, NTW>(a, grid, s);
+  else if (a.xdt == KEEP_BF16) gq_launch_x<GATEUP, RES, bf16s, NTW>(a, grid, s);
+  else gq_launch_x<GATEUP, RES, float, NTW>(a, grid, s);
 }
 
-template <int NTERM>
-void gq_launch_res(const GQArgs& a, dim3 grid, hipStream_t s) {
-  if (a.G > 1) hipLaunchKernelGGL((k_gemm_q8<false, true, NTERM, true>), grid, dim3(512), 0, s, a);
-  else hipLaunchKernelGGL((k_gemm_q8<false, false, NTERM, true>), grid, dim3(512), 0, s, a);
-}
-
-void gq_launch(GQArgs& a, bool gateup, int nterm, hipStream_t s, bool res = false) {
-  a.ncb = gateup ? (a.N + 127) / 128 : (a.N + 255) / 256;
-  a.total = a.ncb * a.n_tiles;
-  a.per_xcd = (a.total + GQ_XCDS - 1) / GQ_XCDS;
+void gq_launch(GQArgs& a, bool gateup, hipStream_t s, bool res = false) {
   int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  auto shape = [&](int64_t ncol) {
+    const int64_t cols = gateup ? ncol / 2 : ncol;
+    a.ncb = (a.N + cols - 1) / cols;
+    a.total = a.ncb * a.n_tiles;
+    a.per_xcd = (a.total + GQ_XCDS - 1) / GQ_XCDS;
+  };
+  shape(512);
+  const bool wide = a.total >= 4 * (int64_t)cus;
+  if (!wide) shape(256);
   const int64_t per = std::max<int64_t>(1, std::min<int64_t>(a.per_xcd, cus / GQ_XCDS));
   const dim3 grid((unsigned)(per * GQ_XCDS));
-  (void)nterm;  // always 3 (gq_nterm)
-  if (res) gq_launch_res<3>(a, grid, s);
-  else if (gateup) gq_launch_t<true, 3>(a, grid, s);
-  else gq_launch_t<false, 3>(a, grid, s);
+  if (wide) {
+    if (res) gq_launch_t<false, true, 2>(a, grid, s);
+    else if (gateup) gq_launch_t<true, false, 2>(a, grid, s);
+    else gq_launch_t<false, false, 2>(a, grid, s);
+  } else {
+    if (res) gq_launch_t<false, true, 1>(a, grid, s);
+    else if (gateup) gq_launch_t<true, false, 1>(a, grid, s);
+    else gq_launch_t<false, false, 1>(a, grid, s);
+  }
 }
 
 bool gq_shape_ok(int64_t K, int64_t group_size) {
@@ -478,9 +539,11 @@ bool gq_shape_ok(int64_t K, int64_t group_size) {
 
 using namespace keep;
 
+// Workspace of the grouped GEMMs: one (r, 1 / r) pair per row of bf16 / fp32 input
+// (fp16 input uses none).
 extern "C" int64_t keep_vq_grouped_gemm_q8_workspace_bytes(int64_t x_rows, int64_t K) {
   if (x_rows < 0 || K <= 0) return -1;
-  return gq_ws_bytes(x_rows, K);
+  return gq_ws_bytes(x_rows);
 }
 
 extern "C" int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
@@ -500,31 +563,29 @@ extern "C" int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_row
                GQ_KB, (long long)K, (long long)group_size);
   KEEP_REQUIRE(N > 0 && n_tiles >= 0 && routes >= 0 && num_experts > 0 && x_rows >= 0, "bad sizes");
   if (n_tiles == 0 || routes == 0) return KEEP_OK;
-  KEEP_REQUIRE(x_rows > 0 && x && codes && scales && prepared && tile_expert && tile_offset && tile_count && out &&
-                   workspace,
+  KEEP_REQUIRE(x_rows > 0 && x && codes && scales && prepared && tile_expert && tile_offset && tile_count && out,
                "null pointer argument");
-  KEEP_REQUIRE(workspace_bytes >= gq_ws_bytes(x_rows, K), "workspace needs %lld bytes, got %lld",
-               (long long)gq_ws_bytes(x_rows, K), (long long)workspace_bytes);
-  KEEP_REQUIRE(aligned(x, 16) && aligned(codes, code_bits == 16 ? 16 : 8) && aligned(prepared, 16) &&
-                   aligned(workspace, 256),
-               "x and prepared must be 16-byte aligned, codes 16 (E8P) or 8 (residual) bytes, the workspace 256");
+  KEEP_REQUIRE(aligned(x, 16) && aligned(codes, code_bits == 16 ? 16 : 8) && aligned(prepared, 16),
+               "x and prepared must be 16-byte aligned, codes 16 (E8P) or 8 (residual) bytes");
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || (workspace && aligned(workspace, 16) && workspace_bytes >= gq_ws_bytes(x_rows)),
+               "bf16 / fp32 input needs a 16-byte aligned workspace of %lld bytes, got %lld",
+               (long long)gq_ws_bytes(x_rows), (long long)workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
-  uint8_t* ws = (uint8_t*)workspace;
-  gq_rows(x, x_dtype, x_rows, K, ws, s);
   GQArgs a{};
-  a.xt = ws; a.xinv = (const float*)(ws + gq_ws_terms(x_rows, K)); a.x_rows = x_rows; a.lhs = lhs;
+  a.x = x; a.xdt = x_dtype; a.x_rows = x_rows; a.lhs = lhs;
+  a.rs = gq_rowscale(x, x_dtype, x_rows, K, workspace, s);
   a.oidx = out_index; a.c0 = a.c1 = (const uint16_t*)codes; a.s0 = a.s1 = scales; a.sdt = scale_dtype;
   if (code_bits == 8) {  // `prepared` is the packed 8-bit E8 table, uint32[256]
-    a.tq = (const uint4*)prepared;
+    a.tq = prepared;
     a.tq_bad = nullptr;
   } else {
-    a.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
+    a.tq = (const char*)prepared + TQ_OFFSET;
     a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
   }
   a.te = tile_expert; a.to = tile_offset; a.tc = tile_count; a.n_tiles = n_tiles; a.routes = routes;
   a.E = num_experts; a.N = N; a.K = K; a.G = K / group_size; a.kpg = group_size / GQ_KB; a.limit = 0.f;
   a.out = out; a.odt = out_dtype;
-  gq_launch(a, false, gq_nterm(x_dtype), s, code_bits == 8);
+  gq_launch(a, false, s, code_bits == 8);
   return launch_status("keep_vq_grouped_gemm_q8");
 }
 
@@ -545,26 +606,25 @@ extern "C" int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_r
   KEEP_REQUIRE(I > 0 && n_tiles >= 0 && routes >= 0 && num_experts > 0 && x_rows >= 0, "bad sizes");
   if (n_tiles == 0 || routes == 0) return KEEP_OK;
   KEEP_REQUIRE(x_rows > 0 && x && gate_codes && gate_scales && up_codes && up_scales && prepared && tile_expert &&
-                   tile_offset && tile_count && h_out && workspace,
+                   tile_offset && tile_count && h_out,
                "null pointer argument");
-  KEEP_REQUIRE(workspace_bytes >= gq_ws_bytes(x_rows, H), "workspace needs %lld bytes, got %lld",
-               (long long)gq_ws_bytes(x_rows, H), (long long)workspace_bytes);
-  KEEP_REQUIRE(aligned(x, 16) && aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(prepared, 16) &&
-                   aligned(workspace, 256),
-               "x, codes and prepared must be 16-byte aligned, the workspace 256-byte aligned");
+  KEEP_REQUIRE(aligned(x, 16) && aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(prepared, 16),
+               "x, codes and prepared must be 16-byte aligned");
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || (workspace && aligned(workspace, 16) && workspace_bytes >= gq_ws_bytes(x_rows)),
+               "bf16 / fp32 input needs a 16-byte aligned workspace of %lld bytes, got %lld",
+               (long long)gq_ws_bytes(x_rows), (long long)workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
-  uint8_t* ws = (uint8_t*)workspace;
-  gq_rows(x, x_dtype, x_rows, H, ws, s);
   GQArgs a{};
-  a.xt = ws; a.xinv = (const float*)(ws + gq_ws_terms(x_rows, H)); a.x_rows = x_rows; a.lhs = lhs;
+  a.x = x; a.xdt = x_dtype; a.x_rows = x_rows; a.lhs = lhs;
+  a.rs = gq_rowscale(x, x_dtype, x_rows, H, workspace, s);
   a.oidx = nullptr; a.c0 = gate_codes; a.c1 = up_codes; a.s0 = gate_scales; a.s1 = up_scales;
   a.sdt = scale_dtype;
-  a.tq = (const uint4*)((const char*)prepared + TQR_OFFSET);
+  a.tq = (const char*)prepared + TQ_OFFSET;
   a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
   a.te = tile_expert; a.to = tile_offset; a.tc = tile_count; a.n_tiles = n_tiles; a.routes = routes;
   a.E = num_experts; a.N = I; a.K = H; a.G = H / group_size; a.kpg = group_size / GQ_KB; a.limit = swiglu_limit;
   a.out = h_out; a.odt = KEEP_BF16;
-  gq_launch(a, true, gq_nterm(x_dtype), s);
+  gq_launch(a, true, s);
   return launch_status("keep_vq_grouped_swiglu_q8");
 }
 

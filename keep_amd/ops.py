@@ -323,7 +323,7 @@ def grouped_gemm(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor, cod
                  tile_descriptors, *, lhs: torch.Tensor | None, routes: int, input_dims: int, output_dims: int,
                  group_size: int, out_dtype: torch.dtype | None = None,
                  out_index: torch.Tensor | None = None) -> torch.Tensor:
-    """``keep_vq_grouped_gemm_q8``: sorted-route GEMM on the int8 matrix cores ->
+    """``keep_vq_grouped_gemm_q8``: sorted-route GEMM on the fp16 matrix cores ->
     ``[routes, N]``, row ``p`` in sorted order, or row ``out_index[p]`` when
     ``out_index`` is given (the scatter back to route order folded in)."""
 

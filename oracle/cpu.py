@@ -31,6 +31,9 @@ def load():
         lib.oracle_routed_matvec.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
                                              c_int64, c_int64, c_int64, c_int64, c_void_p, c_int]
         lib.oracle_routed_matvec.restype = None
+        lib.oracle_routed_matvec8.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                                              c_int64, c_int64, c_int64, c_int64, c_void_p, c_int]
+        lib.oracle_routed_matvec8.restype = None
         lib.oracle_moe_decode.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                           c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
                                           c_int64, c_void_p, c_float, c_int, c_void_p, c_int]
@@ -75,6 +78,24 @@ def routed_matvec(x, codes, scales, table, rhs, lhs=None, *, x_div=1, group_size
     out = np.empty((rhs.size, N), dtype=np.float32)
     load().oracle_routed_matvec(_p(x), _p(codes), _p(scales), _p(t), _p(rhs), _p(lhs), rhs.size, x_div, N, C * 8,
                                 group_size, _p(out), int(threads))
+    return out
+
+
+def routed_matvec8(x, codes, scales, table8, rhs, lhs=None, *, x_div=1, group_size, threads=0) -> np.ndarray:
+    """The nested tier's residual projection per route: rows ``rhs[r]`` of the
+    8-bit E8 codes ``[nhot, N, K/8]`` (``rhs[r] < 0``: zeros), the same fp32
+    row dot as ``moe_decode_nested``'s residual."""
+
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    t8 = np.ascontiguousarray(table8, dtype=np.uint32)
+    rhs = np.ascontiguousarray(rhs, dtype=np.int32).reshape(-1)
+    lhs = None if lhs is None else np.ascontiguousarray(lhs, dtype=np.int32).reshape(-1)
+    _, N, C = codes.shape
+    out = np.empty((rhs.size, N), dtype=np.float32)
+    load().oracle_routed_matvec8(_p(x), _p(codes), _p(scales), _p(t8), _p(rhs), _p(lhs), rhs.size, x_div, N, C * 8,
+                                 group_size, _p(out), int(threads))
     return out
 
 

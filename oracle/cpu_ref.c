@@ -115,6 +115,25 @@ static inline float row_dot8(const uint8_t* crow, const float* srow, int64_t C, 
   return total;
 }
 
+/* out[r, n] = dot(8-bit E8 code row (rhs[r], n), x row lhs[r] (or r / x_div)):
+ * the nested tier's residual projection per route (rows rhs[r] of the residual
+ * codes [nhot, N, K/8], scales [nhot, N, G]); routes with rhs[r] < 0 get 0. */
+void oracle_routed_matvec8(const float* x, const uint8_t* codes, const float* scales, const uint32_t* table8,
+                           const int32_t* rhs, const int32_t* lhs, int64_t routes, int64_t x_div, int64_t N, int64_t K,
+                           int64_t group_size, float* out, int threads) {
+  float lut8[256 * 8];
+  e8_lut(table8, lut8);
+  const int64_t C = K / 8, G = K / group_size, cpg = group_size / 8;
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < routes * N; ++i) {
+    const int64_t r = i / N, n = i % N;
+    const int64_t e = rhs[r];
+    const int64_t xr = lhs ? lhs[r] : r / x_div;
+    out[i] = e < 0 ? 0.f : row_dot8(codes + (e * N + n) * C, scales + (e * N + n) * G, C, cpg, x + xr * K, lut8);
+  }
+}
+
 /* Routed SwiGLU MoE for T tokens; x [T, H] fp32, scales fp32, out [T, H].
  * h_bf16 != 0 rounds the SwiGLU output to bf16 before the down projection.
  * With hot != NULL, the nested 3-bit tier: an expert e with hot[e] = r >= 0

@@ -135,6 +135,15 @@ def test_config4_prefill_full_shape(dev):
 
 
 def test_config5_prefill_with_tier_full_shape(dev):
+    """Config 5 prefill with the nested tier, checked in three parts as config
+    4 is (h is held in bf16, so an h value whose exact gate/up sits within a
+    few fp32 ulps of a bf16 rounding boundary rounds to the neighbouring bf16
+    value on the GPU or in the oracle, and one such flip moves its token's
+    outputs by up to ~1e-2 of their rms): (a) h within 2e-3 + one bf16 ulp of
+    the oracle's (base + residual gate and up, SwiGLU), elementwise; (b) down
+    + residual on the GPU's own h within 2e-3 of the oracle, elementwise; (c)
+    the layer within 2e-3 of the nested oracle normwise and equal bit for bit
+    to the module's kernels run one by one."""
     E, H, I, k, T = 288, 4096, 1536, 8, 512
     print(f"config 5 prefill with tier: T={T} E={E} H={H} I={I} k={k}", flush=True)
     mask = synth.resident_mask(E, frac=0.5, seed=21)
@@ -152,10 +161,60 @@ def test_config5_prefill_with_tier_full_shape(dev):
     oi, *_ = ops.router_dual_topk(z.cpu().numpy(), keep_amd.resident_bias(torch.from_numpy(mask)).numpy()
                                   .astype(np.float64), np.zeros(E), k, tau=0.3)
     np.testing.assert_array_equal(idx, oi)
-    want = cpu.moe_decode_nested(x.float().cpu().numpy(), idx, r.weight.cpu().numpy(), _host(gate), _host(up),
-                                 _host(down), e8p.e8p_packed_abs_grid(), hot_of_slot, residual, e8p.e8_1bit_packed())
-    err = _check(out, want)
-    print(f"config 5 prefill with tier: max rel err {err:.2e}, {int(on.sum())} hot routes", flush=True)
+    # the module's kernels one by one (the tiered sorted-route prefill): h in sorted order, y in route order
+    kops = keep_amd.ops
+    R = T * k
+    flat = r.idx.reshape(-1).to(torch.int32).contiguous()
+    flat_lhs = (torch.arange(R, dtype=torch.int32, device=dev) // k).contiguous()
+    order, inverse, _, _, te, to, tc, _ = kops.route_plan(flat, E, kops.GEMM_ROUTE_TILE)
+    sorted_lhs = flat_lhs[order.long()].contiguous()
+    rrows = tier.route_rows(flat)
+    r_order, _, _, _, rte, rto, rtc, _ = kops.route_plan(rrows, tier.rows, kops.GEMM_ROUTE_TILE)
+    at_base = inverse[r_order.long()].to(torch.int32).contiguous()
+    cb = glu.gate_proj.codebook
+    f32 = torch.float32
+    gu = {}
+    for name, p in (("gate", gate), ("up", up)):
+        o = kops.grouped_gemm(x, p.codes, p.scales, cb, (te, to, tc), lhs=sorted_lhs, routes=R, input_dims=H,
+                              output_dims=I, group_size=H, out_dtype=f32)
+        rc, rs = tier.residual_arrays[name]
+        kops.grouped_residual_add(o, x, rc, rs, (rte, rto, rtc), lhs=flat_lhs[r_order.long()].contiguous(),
+                                  out_index=at_base, routes=R, input_dims=H, output_dims=I,
+                                  group_size=H // rs.shape[-1], table=tier._table_packed)
+        gu[name] = o
+    hidden = glu._apply_activation(gu["up"], gu["gate"]).to(torch.bfloat16).contiguous()
+    y = kops.grouped_gemm(hidden, down.codes, down.scales, cb, (te, to, tc), lhs=None, routes=R, input_dims=I,
+                          output_dims=H, group_size=I, out_dtype=f32, out_index=order)
+    rc, rs = tier.residual_arrays["down"]
+    kops.grouped_residual_add(y, hidden, rc, rs, (rte, rto, rtc), lhs=at_base, out_index=r_order, routes=R,
+                              input_dims=I, output_dims=H, group_size=I // rs.shape[-1], table=tier._table_packed)
+    again = kops.route_combine(y.reshape(T, k, H), r.weight)
+    assert torch.equal(again, out), "RoutedVQMoE differs from its own kernels run one by one"
+    tab, t8 = e8p.e8p_packed_abs_grid(), e8p.e8_1bit_packed()
+    xf = x.float().cpu().numpy()
+    rows = np.where(on.reshape(-1), hot_of_slot[idx].reshape(-1).astype(np.int64), -1).astype(np.int32)
+    G, U, D = _host(gate), _host(up), _host(down)
+
+    def proj(v, base, name, K, lhs=None, x_div=1):
+        b = cpu.routed_matvec(v, base[0], base[1], tab, idx.reshape(-1), lhs, x_div=x_div, group_size=K)
+        c8, s8 = residual[name]
+        return b.astype(np.float64) + cpu.routed_matvec8(v, c8, s8, t8, rows, lhs, x_div=x_div,
+                                                         group_size=K // s8.shape[-1])
+    # (a) h
+    with np.errstate(over="ignore"):
+        h_o = ops.round_bf16(ops.swiglu(proj(xf, G, "gate", H, x_div=k), proj(xf, U, "up", H, x_div=k)))
+    h_g = hidden[inverse.long()].float().cpu().numpy()
+    assert ops.elementwise_ok(h_g, h_o, rtol=TOL + 2.0 ** -7), "h beyond one bf16 ulp of the oracle's"
+    flips = int((h_g != h_o).sum())
+    # (b) down + residual on the GPU's h
+    y_o = proj(h_g.astype(np.float32), D, "down", I, lhs=np.arange(R, dtype=np.int32))
+    _check(y, y_o)
+    # (c) the layer against the nested oracle with its own h
+    want = cpu.moe_decode_nested(xf, idx, r.weight.cpu().numpy(), G, U, D, tab, hot_of_slot, residual, t8)
+    err = ops.max_rel_err(out.cpu().numpy(), want)
+    assert err <= TOL, f"max rel err {err:.3e}"
+    print(f"config 5 prefill with tier: max rel err {err:.2e}, {int(on.sum())} hot routes, {flips} of {h_o.size} "
+          f"h values one bf16 ulp from the oracle's", flush=True)
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])

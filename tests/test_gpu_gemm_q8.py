@@ -1,10 +1,10 @@
-"""GPU parity of the int8 prefill grouped GEMM (keep_vq_grouped_gemm_q8) and
-its fused gate/up + SwiGLU form (keep_vq_grouped_swiglu_q8) against the
-float64 oracle: partial column blocks, tiles of one and two 32-route
-m-tiles, per-row and grouped scales, fp16 / bf16 / fp32 activations, the
-scatter back to route order, and NaN rows / out-of-range experts (the
-sorted-route prefill of src/ramp/ops/vq_switch.py:620-913 and
-src/ramp/models/glm4_moe_adapter.py:274-353)."""
+"""GPU parity of the prefill grouped GEMM (keep_vq_grouped_gemm_q8, fp16
+matrix cores) and its fused gate/up + SwiGLU form (keep_vq_grouped_swiglu_q8)
+against the float64 oracle: partial column blocks, tiles of one and two
+32-route m-tiles, per-row and grouped scales, fp16 / bf16 / fp32
+activations, work items of 256 and of 512 columns, the scatter back to route
+order, and NaN rows / out-of-range experts (the sorted-route prefill of
+src/ramp/ops/vq_switch.py:620-913 and src/ramp/models/glm4_moe_adapter.py:274-353)."""
 
 import numpy as np
 import pytest
@@ -13,7 +13,7 @@ import torch
 import keep_amd
 from keep_amd import ops as kops
 from keep_amd import synth
-from oracle import ops
+from oracle import cpu, e8p, ops
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -196,3 +196,43 @@ def test_grouped_gemm_q8_blocks_run_many_items(dev):
     want = cpu.routed_matvec(x.float().cpu().numpy(), codes, scales.astype(np.float32),
                              kops.e8p_packed_abs_grid(), rhs.reshape(-1), x_div=k, group_size=K)
     _check(y, want.astype(np.float64))
+
+
+@pytest.mark.parametrize("G", [1, 2])
+@pytest.mark.parametrize("form", ["plain", "swiglu"])
+def test_grouped_gemm_wide_items(dev, form, G):
+    """Enough route tiles for work items of 512 columns (two n-tiles per
+    wave): 160 experts with ~32 routes each (tiles of one and two m-tiles),
+    N = 4096 (plain) or I = 2048 (gate/up + SwiGLU), per-row and grouped
+    scales, against the C oracle's fp32 row dots."""
+    E, K, T, k = 160, 256, 2560, 2
+    rng = np.random.default_rng(50 + G)
+    rhs = rng.integers(0, E, (T, k)).astype(np.int32)
+    x = synth.rht_activations(T, K, seed=51, device=dev)
+    flat, order, inverse, counts, tiles, lhs = _plan(rhs, E, k, dev)
+    c = counts.cpu().numpy()
+    assert tiles[0].numel() >= 128 and (c > 32).any() and ((c > 0) & (c <= 32)).any()
+    cb = kops._default_codebook(16, dev)
+    tab = e8p.e8p_packed_abs_grid()
+    xf = x.float().cpu().numpy()
+    R = flat.numel()
+
+    def oracle(codes, scales):
+        return cpu.routed_matvec(xf, codes, scales.astype(np.float32), tab, rhs.reshape(-1), x_div=k,
+                                 group_size=K // G).astype(np.float64)
+    if form == "plain":
+        N = 4096
+        codes, scales = synth.projection_np(E, N, K, group_size=K // G, seed=52)
+        y = kops.grouped_gemm(x, _t(codes, dev), _t(scales, dev), cb, tiles, lhs=lhs, routes=R, input_dims=K,
+                              output_dims=N, group_size=K // G, out_dtype=torch.float32)
+        _check(y[inverse.long()], oracle(codes, scales))
+    else:
+        I = 2048
+        gate = synth.projection_np(E, I, K, group_size=K // G, seed=53)
+        up = synth.projection_np(E, I, K, group_size=K // G, seed=54)
+        h = kops.grouped_swiglu(x, _t(gate[0], dev), _t(gate[1], dev), _t(up[0], dev), _t(up[1], dev), cb, tiles,
+                                lhs=lhs, routes=R, input_dims=K, hidden_dims=I, group_size=K // G, limit=7.0)
+        with np.errstate(over="ignore"):
+            want = ops.round_bf16(ops.swiglu(oracle(*gate), oracle(*up), limit=7.0))
+        got = h[inverse.long()].float().cpu().numpy()
+        assert ops.elementwise_ok(got, want, rtol=TOL + 2.0 ** -7), "h beyond one bf16 ulp of the oracle's"

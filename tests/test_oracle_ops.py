@@ -281,3 +281,46 @@ def test_c_oracle_nested_tier_matches_dense(rg):
     nested = cpu.moe_decode_nested(x[2:], idx[2:], w[2:], gate, up, down, t, hot, residual, e8p.e8_1bit_packed(),
                                    limit=7.0)
     np.testing.assert_array_equal(plain, nested)
+
+
+def test_c_oracle_residual_matvec_composes_nested_layer():
+    """oracle_routed_matvec8 (the tier's residual projection per route) pinned
+    by the nested layer oracle: base + residual gate and up, SwiGLU, base +
+    residual down on those h, the weighted sum, equal to moe_decode_nested
+    (h unrounded) within fp32 rounding; routes off the tier get zeros."""
+    t = e8p.e8p_packed_abs_grid()
+    t8 = e8p.e8_1bit_packed()
+    E, H, I, k, nhot = 6, 256, 128, 3, 3
+    gate, up, down = _proj(E, I, H, 2, 30), _proj(E, I, H, 2, 31), _proj(E, H, I, 1, 32)
+    rng = np.random.default_rng(33)
+    hot = np.full(E, ops.NO_RESIDUAL, np.uint32)
+    hot[[1, 4, 5]] = [2, 0, 1]
+
+    def res(N, K, rg):
+        return (rng.integers(0, 256, (nhot, N, K // 8), dtype=np.uint8),
+                (np.exp(rng.normal(0, 0.3, (nhot, N, rg))) * 0.1).astype(np.float32))
+
+    residual = {"gate": res(I, H, 2), "up": res(I, H, 2), "down": res(H, I, 1)}
+    x = rng.standard_normal((3, H)).astype(np.float32)
+    idx = np.array([[1, 0, 4], [5, 2, 3], [0, 2, 3]], dtype=np.int32)
+    w = rng.random((3, k)).astype(np.float32)
+    flat = idx.reshape(-1)
+    rows = np.where(hot[flat] == ops.NO_RESIDUAL, -1, hot[flat].astype(np.int64)).astype(np.int32)
+    f32 = lambda p: (p[0], p[1].astype(np.float32))  # noqa: E731
+
+    def proj(v, base, name, K, lhs=None, x_div=1):
+        b = cpu.routed_matvec(v, *f32(base), t, flat, lhs, x_div=x_div, group_size=K // base[1].shape[-1])
+        rc, rs = residual[name]
+        r = cpu.routed_matvec8(v, rc, rs, t8, rows, lhs, x_div=x_div, group_size=K // rs.shape[-1])
+        return b, r
+
+    gb, gr = proj(x, gate, "gate", H, x_div=k)
+    ub, ur = proj(x, up, "up", H, x_div=k)
+    assert not gr[rows < 0].any() and gr[rows >= 0].any()
+    g, u = gb + gr, ub + ur
+    gc, uc = np.minimum(g, 7.0), np.clip(u, -7.0, 7.0)
+    h = (gc / (1.0 + np.exp(-gc.astype(np.float64))) * uc).astype(np.float32)
+    db, dr = proj(h, down, "down", I, lhs=np.arange(flat.size, dtype=np.int32))
+    got = ((db + dr).reshape(3, k, H) * w[..., None]).sum(1)
+    want = cpu.moe_decode_nested(x, idx, w, gate, up, down, t, hot, residual, t8, limit=7.0, h_bf16=False)
+    assert ops.max_rel_err(got, want) < 1e-5
