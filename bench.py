@@ -168,7 +168,7 @@ def main() -> int:
                                      prep.data_ptr(), h[i].data_ptr(), out[i].data_ptr(), F32, stream.cuda_stream),
                    "down")
 
-    def layer(i):  # the split path: router, gate/up, down as three launches
+    def layer(i):  # the split path: router, then gate/up and down on the packed-table kernels
         router(i)
         gateup(i)
         down_(i)
@@ -267,7 +267,7 @@ def main() -> int:
     gu_gbps = gu_bytes / (gu_us * 1e-6) / 1e9
     dn_gbps = dn_bytes / (dn_us * 1e-6) / 1e9
     layer_us = ms_per_step * 1e3
-    log(f"bench: layer {layer_us:.2f} us ({value:.0f} GB/s) | split path {split_us:.2f} us: "
+    log(f"bench: layer {layer_us:.2f} us ({value:.0f} GB/s) | split path (packed-table kernels) {split_us:.2f} us: "
         f"router {rt_us:.2f}  gateup {gu_us:.2f} ({gu_gbps:.0f} GB/s)  down {dn_us:.2f} ({dn_gbps:.0f} GB/s)")
 
     result = {
@@ -298,7 +298,7 @@ def main() -> int:
                     "median_us_per_layer": round(float(np.median(samples_us)), 3) if samples_us else None,
                     "min_us_per_layer": round(samples_us[0], 3) if samples_us else None,
                     "max_us_per_layer": round(samples_us[-1], 3) if samples_us else None},
-        "kernels_us": {"moe_layer (route_gateup + down)": round(layer_us, 3), "split_path_total": round(split_us, 3),
+        "kernels_us": {"moe_layer (route_gateup + down)": round(layer_us, 3), "split_path_packed_table_total": round(split_us, 3),
                        "router": round(rt_us, 3), "moe_gateup": round(gu_us, 3), "moe_down": round(dn_us, 3)},
         "roofline": {"bound": "hbm", "kernel": " + ".join(LAYER_KERNELS), "achieved": round(value, 2),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(value / HBM_PEAK_GBPS, 4),

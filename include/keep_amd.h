@@ -158,35 +158,29 @@ int keep_route_plan(const int32_t* rhs, int64_t R, int64_t E, int64_t tile,
                     int32_t* tile_expert, int32_t* tile_offset, int32_t* tile_count,
                     int64_t max_tiles, int32_t* n_tiles_out, void* stream);
 
-/* Decode tables for the fused MoE kernels, built on the device from the
- * 256-entry packed abs grid: at offset 0, 2 x 128 KiB expanded tables (fp16
- * then bf16), 16384 entries of four packed values each, addressed by
- * (parity, abs index, 4 sign bits) so one decode is two lookups with the
- * signs, parity and +-1/4 shift already applied (src/keep/vq/e8.py:203-234);
- * at offset 256 KiB, the 4 KiB int8 T / M tables (T[idx]: the 8 bytes 4 x the
- * unsigned even-parity codeword; M[signs]: its sign and parity mask, so a
- * codeword's int8 weights x 4 are T[idx] ^ M[signs]), then a 256-byte word
- * that is nonzero when the grid holds a value those tables cannot express
- * (the int8 kernels then write NaN), then the 64 KiB LDS image of T and M
- * (256 rows of sixteen copies) that the int8 kernels stage per block:
- * 332,032 bytes in all. `prepared` must hold keep_e8p_prepared_bytes() bytes. No reference
+/* Decode tables for the matrix-core kernels, built on the device from the
+ * 256-entry packed abs grid: at offset 0 the 4 KiB int8 T / M tables (T[idx]:
+ * the 8 bytes 4 x the unsigned even-parity codeword; M[signs]: its sign and
+ * parity mask, so a codeword's int8 weights x 4 are T[idx] ^ M[signs],
+ * src/keep/vq/e8.py:203-234), then a 256-byte word that is nonzero when the
+ * grid holds a value those tables cannot express (the kernels then write
+ * NaN), then the 64 KiB LDS image of T and M (256 rows of sixteen copies)
+ * that the int8 kernels stage per block: 69,888 bytes in all. `prepared` must hold keep_e8p_prepared_bytes() bytes. No reference
  * counterpart: it replaces the per-threadgroup half2 pair decode of
  * src/ramp/kernels/e8p_m1.metal:36-45 at a larger scale. */
 int keep_e8p_prepare(const uint32_t* table, void* prepared, void* stream);
 int keep_e8p_prepared_bytes(void);
 
-/* Fused routed SwiGLU MoE for few tokens (decode / verify):
+/* Fused routed SwiGLU MoE for few tokens (decode / verify), any shape:
  * h[t, j, :] = swiglu(Wg[e] x_t, Wu[e] x_t) (clamped by swiglu_limit if > 0),
  * out[t, :] = sum_j w[t, j] * Wd[e] h[t, j, :], e = idx[t, j].
  * Gate/up codes [E, I, H/8], down codes [E, H, I/8]; h_work is caller-provided
  * [T * k * I] bf16 (SwiGLU in fp32, stored as bf16 as the reference's serving
- * step stores it; fp16 would overflow). Two launches on `stream`. With
- * `prepared` (keep_e8p_prepare of `table`) the kernels decode through the
- * expanded table: one token (T = 1; H <= 4096 and a multiple of 256, I a
- * multiple of 512 up to 2048, k <= 8, scale groups of 256-element multiples)
- * on the matrix cores, other served shapes with 1024-thread blocks;
- * `prepared` = NULL uses the packed-table kernels. h_work holds h in natural
- * [T, k, I] order whichever kernels ran.
+ * step stores it; fp16 would overflow), in natural [T, k, I] order. Two
+ * launches on `stream` of the packed-table mat-vec kernels (H and I multiples
+ * of 8, scale groups of 8-element multiples); `prepared` is accepted and not
+ * read. The shapes keep_moe_tiles serves (T <= 256, H and I multiples of 256)
+ * run faster there; keep_amd.moe_decode picks between the two.
  * Replaces QuantizedVQSwitchGLU.__call__ (src/ramp/models/glm4_moe_adapter.py:367-372)
  * plus the weighted combine of DeepseekV4FlashVQMoE.__call__
  * (src/ramp/models/deepseek_v4_flash_adapter.py:1776-1784) and the decode step

@@ -490,18 +490,6 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
 
 // ------------------------------------------------------------------ host side
 
-bool moe_v2_supported(int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i);
-bool moe_v3_gateup_supported(int64_t T, int64_t H, int64_t I, int64_t k, int64_t group_h);
-bool moe_v3_down_supported(int64_t T, int64_t H, int64_t I, int64_t k, int64_t group_i);
-void moe_v3_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t H, int64_t I, const int32_t* idx,
-                   const float* w, int64_t k, int64_t E, const uint16_t* gc, const void* gs, const uint16_t* uc,
-                   const void* us, const uint16_t* dc, const void* ds, int sdt, int64_t group_h, int64_t group_i,
-                   const void* prepared, float limit, void* h, void* out, int odt, hipStream_t s);
-int moe_v2_launch(bool gateup, bool down, const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
-                  const int32_t* idx, const float* w, int64_t k, int64_t E, const uint16_t* gc, const void* gs,
-                  const uint16_t* uc, const void* us, const uint16_t* dc, const void* ds, int sdt, int64_t group_h,
-                  int64_t group_i, const void* prepared, float limit, void* h, void* out, int odt, hipStream_t s);
-
 // Codewords per lane chunk: must divide the codewords of a scale group (and of
 // the residual's group) so a chunk never straddles two scales; prefer the
 // widest load that keeps all 64 lanes busy.
@@ -695,13 +683,6 @@ static void launch_moe(int ch_h, int ch_i, bool gateup, bool down, hipStream_t s
   }
 }
 
-static int moe_legacy(bool gateup, bool down, const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
-                      const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
-                      const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
-                      const void* up_scales, const uint16_t* down_codes, const void* down_scales, int scale_dtype,
-                      int64_t group_size_h, int64_t group_size_i, const uint32_t* table, const void* prepared,
-                      float swiglu_limit, void* h_work, void* out, int out_dtype, int ch_h, int ch_i, hipStream_t s);
-
 static int moe_common(bool gateup, bool down, const char* what, const void* x, int x_dtype, int64_t T, int64_t H,
                       int64_t I, const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
                       const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
@@ -725,45 +706,7 @@ static int moe_common(bool gateup, bool down, const char* what, const void* x, i
   KEEP_REQUIRE((!gateup || (aligned(gate_codes, ch_h * 2) && aligned(up_codes, ch_h * 2))) &&
                    (!down || aligned(down_codes, ch_i * 2)),
                "codes misaligned");
-  KEEP_REQUIRE(!prepared || aligned(prepared, 16), "prepared table must be 16-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
-  // Every path writes and reads h in natural [T, k, I] order, so the two
-  // halves pick their kernels independently; gate/up is always enqueued first.
-  const bool v3g = gateup && prepared && moe_v3_gateup_supported(T, H, I, k, group_size_h);
-  const bool v3d = down && prepared && moe_v3_down_supported(T, H, I, k, group_size_i);
-  if (v3g)
-    moe_v3_launch(true, false, x, x_dtype, H, I, idx, w, k, num_experts, gate_codes, gate_scales, up_codes,
-                  up_scales, down_codes, down_scales, scale_dtype, group_size_h, group_size_i, prepared,
-                  swiglu_limit, h_work, out, out_dtype, s);
-  const bool lg = gateup && !v3g, ld = down && !v3d;
-  if (lg || ld) {
-    const int rc = moe_legacy(lg, ld, x, x_dtype, T, H, I, idx, w, k, num_experts, gate_codes, gate_scales,
-                              up_codes, up_scales, down_codes, down_scales, scale_dtype, group_size_h, group_size_i,
-                              table, prepared, swiglu_limit, h_work, out, out_dtype, ch_h, ch_i, s);
-    if (rc != KEEP_OK) return rc;
-  }
-  if (v3d)
-    moe_v3_launch(false, true, x, x_dtype, H, I, idx, w, k, num_experts, gate_codes, gate_scales, up_codes,
-                  up_scales, down_codes, down_scales, scale_dtype, group_size_h, group_size_i, prepared,
-                  swiglu_limit, h_work, out, out_dtype, s);
-  return launch_status(what);
-}
-
-// The expanded-table (v2) and plain-codebook (v1) kernels for the shapes the
-// matrix-core path does not cover.
-static int moe_legacy(bool gateup, bool down, const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
-                      const int32_t* idx, const float* w, int64_t k, int64_t num_experts,
-                      const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
-                      const void* up_scales, const uint16_t* down_codes, const void* down_scales, int scale_dtype,
-                      int64_t group_size_h, int64_t group_size_i, const uint32_t* table, const void* prepared,
-                      float swiglu_limit, void* h_work, void* out, int out_dtype, int ch_h, int ch_i, hipStream_t s) {
-  if (prepared && moe_v2_supported(H, I, k, group_size_h, group_size_i)) {
-    KEEP_REQUIRE((int64_t)T * k * I <= 0x7fffffffLL * 16LL && T * ((H + 15) / 16) <= 0x7fffffffLL, "too many blocks");
-    moe_v2_launch(gateup, down, x, x_dtype, T, H, I, idx, w, k, num_experts, gate_codes, gate_scales, up_codes,
-                  up_scales, down_codes, down_scales, scale_dtype, group_size_h, group_size_i, prepared,
-                  swiglu_limit, h_work, out, out_dtype, s);
-    return KEEP_OK;
-  }
+  (void)prepared;
   MoeArgs a{};
   a.x = x; a.T = T; a.H = H; a.I = I; a.idx = idx; a.w = w; a.k = k; a.E = num_experts;
   a.gc = gate_codes; a.uc = up_codes; a.dc = down_codes; a.gs = gate_scales; a.us = up_scales; a.ds = down_scales;
@@ -772,9 +715,10 @@ static int moe_legacy(bool gateup, bool down, const void* x, int x_dtype, int64_
   a.rb_gu = (I + MV_WAVES * MV_ROWS - 1) / (MV_WAVES * MV_ROWS);
   a.rb_d = (H + MV_WAVES * MV_ROWS - 1) / (MV_WAVES * MV_ROWS);
   KEEP_REQUIRE(a.rb_gu * T * k <= 0x7fffffffLL && a.rb_d * T <= 0x7fffffffLL, "too many blocks");
+  hipStream_t s = (hipStream_t)stream;
   if (x_dtype == KEEP_F16) launch_moe<_Float16>(ch_h, ch_i, gateup, down, s, a);
   else launch_moe<bf16s>(ch_h, ch_i, gateup, down, s, a);
-  return KEEP_OK;
+  return launch_status(what);
 }
 
 extern "C" int keep_moe_decode(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, const int32_t* idx,

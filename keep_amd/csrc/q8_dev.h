@@ -201,9 +201,9 @@ __device__ __forceinline__ void wait_vm_q() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Offsets in the prepared buffer (keep_e8p_prepare): the two 128 KiB
-// expanded tables, then T and M, then the flag word, then the 64 KiB LDS image.
-constexpr size_t TQ_OFFSET = 2u * 131072u;
+// Offsets in the prepared buffer (keep_e8p_prepare): T and M, then the flag
+// word, then the 64 KiB LDS image.
+constexpr size_t TQ_OFFSET = 0;
 constexpr size_t TQ_FLAG_OFFSET = TQ_OFFSET + TQ_BYTES;
 constexpr size_t TQR_OFFSET = TQ_FLAG_OFFSET + 256u;
 

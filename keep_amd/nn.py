@@ -451,15 +451,16 @@ def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, u
                codebook: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
                h_work: torch.Tensor | None = None, prepared: bool = True) -> torch.Tensor:
     """Fused routed SwiGLU MoE for few tokens: ``keep_moe_tiles`` (routes grouped
-    per expert, each hit expert read once; five launches) for T > 1 where it
-    serves the shape, else ``keep_moe_decode`` (two launches).
+    per expert, each hit expert read once, on the int8 matrix cores; five
+    launches) where it serves the shape, else ``keep_moe_decode`` (two launches
+    of the packed-table kernels, any shape).
 
     ``gate``/``up``/``down`` are ``(codes, scales)``: gate/up ``[E, I, H/8]``,
     down ``[E, H, I/8]``. ``out[t] = sum_j w[t,j] * down_e(swiglu(gate_e x_t, up_e x_t))``
     with fp32 accumulation; h is held in bf16 and the routed sum is returned in
     float32 by default, as the reference's decode step keeps them
-    (``scripts/v41_build/omlx_lattice.py:368-371``). ``prepared`` selects the
-    expanded-table kernels (served shapes); ``False`` forces the packed-table ones.
+    (``scripts/v41_build/omlx_lattice.py:368-371``). ``prepared=False`` forces the
+    packed-table kernels.
     """
 
     device = x.device
@@ -486,7 +487,7 @@ def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, u
     w32 = weight.to(torch.float32).contiguous()
     prep = ops.prepared_table(cb) if prepared else None
     gh, gi = H // gs.shape[-1], I // ds.shape[-1]
-    if T > 1 and prep is not None and moe_tiles_supported(T, E, H, I, k, gh, gi):
+    if prep is not None and moe_tiles_supported(T, E, H, I, k, gh, gi):
         ws = torch.empty(int(_lib.load().keep_moe_tiles_workspace_bytes(T, k, E, H)), dtype=torch.uint8,
                          device=device)
         _lib.call("keep_moe_tiles", x.data_ptr(), ops._DT[x.dtype], T, H, I, idx32.data_ptr(), w32.data_ptr(), k, E,

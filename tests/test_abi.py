@@ -32,8 +32,8 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_empty_error():
     lib = _lib.load()
     assert lib.keep_abi_version() == 4
-    # two 128 KiB expanded tables, the 4 KiB int8 T / M tables, their check word, the 64 KiB LDS image
-    assert lib.keep_e8p_prepared_bytes() == 2 * 128 * 1024 + 4096 + 256 + 65536 == 332032
+    # the 4 KiB int8 T / M tables, their check word, the 64 KiB LDS image
+    assert lib.keep_e8p_prepared_bytes() == 4096 + 256 + 65536 == 69888
     assert isinstance(lib.keep_last_error(), bytes)
 
 

@@ -276,8 +276,9 @@ def test_routed_moe_module_prefill_matches_decode_path(dev):
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("gh,gi", [(2048, 1024), (512, 256)])
-def test_moe_decode_expanded_table_path(dev, xdt, gh, gi):
-    """The expanded-table kernels (H=2048, I=1024) against the oracle and the packed-table kernels."""
+def test_moe_decode_tiles_and_packed_table_paths(dev, xdt, gh, gi):
+    """H = 2048, I = 1024, three tokens: the int8 tiles kernels and the packed-table kernels
+    (prepared=False) against the oracle."""
     E, H, I, k, T = 32, 2048, 1024, 4, 3
     gate = synth.projection_np(E, I, H, group_size=gh, seed=21)
     up = synth.projection_np(E, I, H, group_size=gh, seed=22)
@@ -286,12 +287,12 @@ def test_moe_decode_expanded_table_path(dev, xdt, gh, gi):
     z = synth.router_logits(T, E, seed=25, device=dev)
     r = keep_amd.router_dual_topk(z, k)
     tt = lambda p: (_t(p[0], dev), _t(p[1], dev))  # noqa: E731
-    v2 = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=10.0)
-    v1 = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=10.0, prepared=False)
+    tiles = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=10.0)
+    packed = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), limit=10.0, prepared=False)
     want = ops.moe_layer(x.float().cpu().numpy(), r.idx.cpu().numpy(), r.weight.cpu().numpy(), gate, up, down,
                          limit=10.0, h_round="bfloat16")
-    _check(v2, want)
-    _check(v1, want)
+    _check(tiles, want)
+    _check(packed, want)
 
 
 @pytest.mark.parametrize("T", [1, 3])
@@ -323,8 +324,8 @@ def test_moe_decode_config5_shapes_with_absent_experts(dev, T):
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("gh,gi", [(1024, 512), (256, 256), (512, 128)])
 def test_moe_decode_matrix_core_path(dev, xdt, gh, gi):
-    """One token through the MFMA decode kernels (gi = 128 sends down through the expanded-table
-    kernel, so h written by one path is read by the other)."""
+    """One token through the int8 tiles kernels where they serve the scale groups (gi = 128 is
+    not a multiple of 256: the packed-table kernels), against the oracle and prepared=False."""
     E, H, I, k, T = 32, 1024, 512, 5, 1
     gate = synth.projection_np(E, I, H, group_size=gh, seed=41)
     up = synth.projection_np(E, I, H, group_size=gh, seed=42)
