@@ -22,9 +22,9 @@
 // in the caller's workspace (zero-filled before its first use): every block
 // reads it at its start and then counts itself in; the last block to count
 // in (so every block has read it) advances it for the next call. A wait that
-// outlasts spin_ticks of the 100 MHz real-time counter gives up: the values
-// it lacks are NaN, the outputs of the rows that used them are NaN, and the
-// workspace's status word records it.
+// outlasts spin_ticks of the 100 MHz real-time counter gives up: the routes
+// of the waiting wave are NaN, and so are the outputs of its block (each sums
+// every route), and the workspace's status word records it.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -106,8 +106,8 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   constexpr int O_DSH = TQR_BYTES;                      // down terms [wave][row 4 r + t][g * 4 + i]
   constexpr int O_ASH = O_DSH + FL_WAVES * 16 * 256;    // x terms [slice][term][g * 4 + i]
   constexpr int O_GRED = O_ASH + 16 * 3 * 256;          // gate/up partials [wave][tile][row]
-  constexpr int O_RED = O_GRED + 16 * NT * 16 * 4;      // down partials [slice][route][row]
-  constexpr int O_SMALL = O_RED + NSL * 8 * 16 * 4;     // s_inv4s[16], s_idx[8], s_w[8]
+  constexpr int O_RED = O_GRED + 16 * NT * 16 * 4;      // down partials [row][wave]
+  constexpr int O_SMALL = O_RED + 16 * 16 * 4;         // s_inv4s[16], s_idx[8], s_w[8]
   constexpr int LDS_BYTES = O_SMALL + 256;
   __shared__ uint4 smem[LDS_BYTES / 16];
   char* lds = (char*)smem;
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   uint4* dsh = (uint4*)(lds + O_DSH);
   uint4* ash = (uint4*)(lds + O_ASH);
   float* gred = (float*)(lds + O_GRED);
-  float (*red)[8][16] = (float (*)[8][16])(lds + O_RED);
+  float* red = (float*)(lds + O_RED);
   float* s_inv4s = (float*)(lds + O_SMALL);
   int32_t* s_idx = (int32_t*)(lds + O_SMALL + 64);
   float* s_w = (float*)(lds + O_SMALL + 96);
@@ -289,13 +289,14 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   const bool dwave = wv < NSL * RG;  // wave-uniform
   const int sd = dwave ? wv % NSL : 0, rg = dwave ? wv / NSL : 0;
   uint32_t dbase[RPW];
-  bool dlive[RPW];
+  bool dlive[RPW], dok[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const int route = rg * RPW + r;
     const int32_t e = route < a.k ? s_idx[route] : -1;
     dlive[r] = dwave && route < a.k;
-    dbase[r] = (e >= 0 && e < a.S ? (uint32_t)e * 4096u : 0u) + b * 16u;
+    dok[r] = dlive[r] && e >= 0 && e < a.S;
+    dbase[r] = (dok[r] ? (uint32_t)e * 4096u : 0u) + b * 16u;
   }
   const uint32_t dgrp = (uint32_t)(sd * 256) / (uint32_t)a.gsz_i;
   ScaleRaw srd[RPW];
@@ -368,27 +369,28 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
 #pragma unroll
       for (int r = 0; r < RPW; ++r) q8_decode8(tq, lk, qd[r], BD[r]);
     }
+    // every pass issues all of the wave's loads before it waits (a route
+    // past k reads route 0's words and ignores them)
+    const uint64_t* hp[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+      hp[r] = a.hx + (((dlive[r] ? (uint32_t)(rg * RPW + r) : 0u) * (uint32_t)a.I + sd * 256u + lane * 4u) >> 1);
     uint64_t hw[RPW][2];
-    bool have[RPW][2];
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     bool gave_up = false;
     for (;;) {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) hw[r][h] = fl_load(hp[r] + h);
       bool all = true;
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const uint32_t w0 = ((uint32_t)(rg * RPW + r) * (uint32_t)a.I + sd * 256u + lane * 4u) >> 1;
+      for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          if (dlive[r]) {
-            hw[r][h] = fl_load(a.hx + w0 + h);
-            have[r][h] = (uint32_t)(hw[r][h] >> 32) == tag;
-            all = all && have[r][h];
-          } else {
-            hw[r][h] = 0u;
-            have[r][h] = true;
-          }
+          all = all && (!dlive[r] || (uint32_t)(hw[r][h] >> 32) == tag);
+          if (!dlive[r]) hw[r][h] = 0u;
         }
-      }
       if (__all(all)) break;  // every lane holds every word
       if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin_ticks) {
         gave_up = true;
@@ -399,37 +401,30 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     if (gave_up && lane == 0) {
       __hip_atomic_fetch_or(hdr + 2, FL_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // A terms: rows 4 r + t of route r's slice, scaled by its own power of two
+    // A terms: rows 4 r and 4 r + 1 of route r's slice, the two int8 digits of
+    // h s with s the slice's power of two (a wave that gave up makes every
+    // route it holds NaN)
     float inv4d[RPW];
     uint32_t* aw = (uint32_t*)(dsh + wv * 256);
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      float v[4];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t lo = (uint32_t)hw[r][h];
-        v[2 * h] = have[r][h] ? __uint_as_float(lo << 16) : __builtin_nanf("");
-        v[2 * h + 1] = have[r][h] ? __uint_as_float(lo & 0xffff0000u) : __builtin_nanf("");
-      }
-      bool nan = false;
-      float mx = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        nan |= v[t] != v[t];
-        mx = fmaxf(mx, fabsf(v[t]));
-      }
+      const uint32_t w0 = (uint32_t)hw[r][0], w1 = (uint32_t)hw[r][1];
+      const float v[4] = {__uint_as_float(w0 << 16), __uint_as_float(w0 & 0xffff0000u), __uint_as_float(w1 << 16),
+                          __uint_as_float(w1 & 0xffff0000u)};
+      // max |h| by the bits: a NaN outranks every number and makes inv4d NaN
+      const uint32_t m = max(max((w0 & 0x7fffu) << 16, w0 & 0x7fff0000u), max((w1 & 0x7fffu) << 16, w1 & 0x7fff0000u));
       float s;
-      q8_scale(rt_wave_max_abs(mx), s, inv4d[r]);
-      if (__any(nan)) inv4d[r] = __builtin_nanf("");
-      uint32_t tw[3];
-      q8_terms<3>(v, s, tw);
+      q8_scale(rt_wave_max_abs(__uint_as_float(m)), s, inv4d[r]);
+      if (gave_up) inv4d[r] = __builtin_nanf("");
+      uint32_t tw[2];
+      q8_digits2(v, s, tw);
 #pragma unroll
-      for (int n = 0; n < 3; ++n) aw[q8_aword((uint32_t)(4 * r + n), lane >> 1, lane & 1)] = tw[n];
+      for (int n = 0; n < 2; ++n) aw[q8_aword((uint32_t)(4 * r + n), lane >> 1, lane & 1)] = tw[n];
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes before its reads
     q8v4 AD[4];
     {
-      const bool live = (j & 3u) != 3u && (int)(j >> 2) < RPW;
+      const bool live = (j & 3u) < 2u && (int)(j >> 2) < RPW;
       const q8v4* as = (const q8v4*)aw + (live ? j : 0u) * 16 + g * 4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -437,18 +432,31 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
         AD[i] = live ? v : q8v4{0, 0, 0, 0};
       }
     }
-    // route r's dot is D rows 4 r .. 4 r + 2, held by lanes 16 r + jj
+    // route r's dot is D rows 4 r and 4 r + 1, held by lanes 16 r + jj; lane
+    // (g, jj) keeps route g's weighted value for output row jj
+    float c = 0.f;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       if constexpr (!PRE) q8_decode8(tq, lk, qd[r], BD[r]);
       q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc = mfma_i8(AD[i], BD[r][i], acc);
-      if ((int)g == r && dlive[r]) {
-        const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
-        red[sd][rg * RPW + r][j] = d * inv4d[r] * scale_cvt(srd[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + dgrp);
+      if ((int)g == r) {
+        const int route = rg * RPW + r;
+        const float wt = dlive[r] ? s_w[route] : 0.f;
+        const float d = (float)acc[0] + (float)acc[1] * 0.0078125f;
+        const float val = d * inv4d[r] * scale_cvt(srd[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + dgrp);
+        c = dok[r] && wt != 0.f ? wt * val : 0.f;
       }
     }
+    // the sum over the wave's routes (lane rows 0 + 1, then + rows 2 + 3)
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+    c = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+    c = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+    if (lane < 16) red[lane * 16 + wv] = c;
+  } else if (lane < 16) {
+    red[lane * 16 + wv] = 0.f;
   }
   if (threadIdx.x == 0 && arrived == FL_BLOCKS - 1) {  // every block has read the epoch: advance it
     __hip_atomic_store(hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -456,22 +464,26 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   }
   rt_lds_barrier();
 
-  // 6. the weighted sum over routes (each the sum over slices, in slice order)
+  // 6. the sum of the waves' weighted partials, in wave order (a route with
+  //    a nonzero weight and no pool row makes the output NaN)
   if (threadIdx.x < 16) {
-    float o = 0.f;
     bool bad = false;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       if (r < a.k) {
         const int32_t e = s_idx[r];
-        const float wt = s_w[r];
-        const bool ok = e >= 0 && e < a.S;
-        bad |= wt != 0.f && !ok;
-        float v = 0.f;
-#pragma unroll
-        for (int s = 0; s < NSL; ++s) v += red[s][r][threadIdx.x];
-        o = (ok && wt != 0.f) ? fmaf(wt, v, o) : o;
+        bad |= s_w[r] != 0.f && !(e >= 0 && e < a.S);
       }
+    }
+    const float4* rp = (const float4*)(red + threadIdx.x * 16);
+    float o = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 v = rp[q];
+      o += v.x;
+      o += v.y;
+      o += v.z;
+      o += v.w;
     }
     if (bad || tq_bad) o = __builtin_nanf("");
     const size_t oi = b * 16u + threadIdx.x;

@@ -165,6 +165,26 @@ __device__ __forceinline__ void q8_terms(const float (&v)[4], float s, uint32_t 
   }
 }
 
+// The two int8 terms t0 + t1 / 128 = rint(v s 128) / 128 of four values
+// (|v| s < 64), the sum q8_terms<2> represents: the FMA with 1.5 * 2^23
+// leaves rint(v s 128) in the low 16 bits of the result (two's complement,
+// |.| < 2^13), and the digits t0 = (F + 64) >> 7, t1 = ((F + 64) & 127) - 64
+// are formed two values at a time in 16-bit halves.
+__device__ __forceinline__ void q8_digits2(const float (&v)[4], float s, uint32_t (&out)[2]) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  const float s128 = s * 128.f;
+  uint32_t f[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) f[t] = __float_as_uint(fmaf(v[t], s128, 12582912.0f));
+  const s16x2 g01 = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(f[1], f[0], 0x05040100u)) + (short)64;
+  const s16x2 g23 = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(f[3], f[2], 0x05040100u)) + (short)64;
+  const s16x2 h01 = g01 >> (short)7, h23 = g23 >> (short)7;
+  const s16x2 l01 = (g01 & (short)127) - (short)64, l23 = (g23 & (short)127) - (short)64;
+  // the low byte of each half, values 0..3 in bytes 0..3
+  out[0] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h23), __builtin_bit_cast(uint32_t, h01), 0x06040200u);
+  out[1] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, l23), __builtin_bit_cast(uint32_t, l01), 0x06040200u);
+}
+
 // Word index in an A-term buffer of 16-byte slots [row][g * 4 + i] for the
 // lane writing chunk c (0..31 of the wave's slice), half `half`.
 __device__ __forceinline__ uint32_t q8_aword(uint32_t row, uint32_t c, uint32_t half) {
