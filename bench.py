@@ -2,22 +2,25 @@
 """Benchmark: one routed 384-expert top-6 E8P-2bit MoE layer at batch-1 decode
 on one MI355X.
 
-A *step* is one pass of the hot path for one token: the whole layer
-(``keep_moe_layer``: dual top-k router over 384 logits fused with
-gate/up/SwiGLU in one launch, then down + weighted combine in a second). Every step uses a fresh routing (64 pre-drawn logit
-sets), so the 2.42 GB resident code pool streams from HBM, not from the
-256 MB Infinity Cache. Steps are captured in HIP graphs (64 per graph) and
-replayed; inputs are resident in HBM before the timed region. The same layer
-as three launches (router, gate/up, down) is timed alongside for reference.
+A *step* is one pass of the hot path for one token: the whole layer in one
+launch (``keep_moe_layer1``, ``moe_layer(one_launch=True)``: dual top-k
+router over 384 logits, gate/up/SwiGLU, down and weighted combine, 256
+co-resident blocks passing h through a workspace). Every step uses a fresh
+routing (64 pre-drawn logit sets), so the 2.42 GB resident code pool streams
+from HBM, not from the 256 MB Infinity Cache. Steps are captured in HIP
+graphs (64 per graph) and replayed; inputs are resident in HBM before the
+timed region. The same layer as two launches (``keep_moe_layer``: router +
+gate/up, then down) and as three (router, gate/up, down on the packed-table
+kernels) is timed alongside.
 
 ``value`` = code-stream bytes of one layer (37,748,736 B: 18 projections of
 2048 x 512 uint16 codes; 37,847,040 B with the fp16 row scales, reported as
 ``layer_bytes_with_scales``) / time per layer, in GB/s, over exactly K timed
-steps; 32 more replays of the 64-step graph are each timed on their own,
+steps (after max(W, 1024) untimed warmup steps: the clocks settle over the
+first ~5 ms of layers); 32 more replays of the 64-step graph are each timed on their own,
 and the median and minimum per layer over those samples are reported beside it.
-``roofline`` covers the layer's two launches (``k_moeq_route_gateup`` then
-``k_moeq_down``) as one unit, timed with HIP events on the stream they are
-launched on. ``cpu_baseline`` times the C/OpenMP restatement
+``roofline`` covers the layer's one launch (``k_moe_layer1``), timed with HIP
+events on the stream it is launched on. ``cpu_baseline`` times the C/OpenMP restatement
 of the same layer (``oracle/cpu_ref.c``) on the host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--config {1,2,3,4,5}]
@@ -61,13 +64,15 @@ E, H, I, K_TOP = 384, 4096, 2048, 6
 GRAPH_STEPS = 64
 N_SETS = 64
 N_SAMPLES = 32  # timed graph replays behind the median / min
+MIN_WARMUP_STEPS = 1024  # untimed layers before the timed region, whatever --warmup asks (at least)
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-LAYER_KERNELS = ("k_moeq_route_gateup", "k_moeq_down")  # the two launches of one layer
+LAYER_KERNELS = ("k_moe_layer1",)  # the one launch of a layer (keep_moe_layer1)
+TWO_LAUNCH_KERNELS = ("k_moeq_route_gateup", "k_moeq_down")  # keep_moe_layer, timed beside it
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_layer_config2_counters.md")
 PROFILE_C4 = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "grouped_gemm_config4_kernel_trace.md")
 PREFILL_KERNELS = ("k_gemm_e8_gateup", "k_gemm_e8_down")  # the two grouped GEMMs of a config-4 layer
@@ -148,6 +153,9 @@ def main() -> int:
     h = torch.empty((N_SETS, K_TOP * I), dtype=torch.bfloat16, device=dev)  # SwiGLU output held in bf16
     out = torch.empty((N_SETS, H), dtype=torch.float32, device=dev)  # routed sum in fp32
     idx1, w1, h1, out1 = torch.empty_like(idx), torch.empty_like(w), torch.empty_like(h), torch.empty_like(out)
+    idx2, w2, out2 = torch.empty_like(idx), torch.empty_like(w), torch.empty_like(out)
+    ws_bytes = int(lib.keep_moe_layer1_workspace_bytes(K_TOP, I))
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # h exchange + call counter, zeroed once
     F16, BF16, F32 = _lib.KEEP_F16, _lib.KEEP_BF16, _lib.KEEP_F32
 
     def router(i):
@@ -173,7 +181,15 @@ def main() -> int:
         gateup(i)
         down_(i)
 
-    def layer1(i):  # the whole layer: router + gate/up in one launch, down in a second
+    def layer_one(i):  # the whole layer in one launch (the headline)
+        _lib.check(lib.keep_moe_layer1(logits[i].data_ptr(), None, None, 0, 1, 1.0, float("inf"), None, 0, E, K_TOP,
+                                       x.data_ptr(), F16, H, I, gate.codes.data_ptr(), gate.scales.data_ptr(),
+                                       up.codes.data_ptr(), up.scales.data_ptr(), down.codes.data_ptr(),
+                                       down.scales.data_ptr(), F16, H, I, prep.data_ptr(), 0.0, idx2[i].data_ptr(),
+                                       w2[i].data_ptr(), None, None, None, ws.data_ptr(), ws_bytes,
+                                       out2[i].data_ptr(), F32, stream.cuda_stream), "moe_layer1")
+
+    def layer_two(i):  # keep_moe_layer: router + gate/up in one launch, down in a second
         _lib.check(lib.keep_moe_layer(logits[i].data_ptr(), None, None, 0, 1, 1.0, float("inf"), None, 0, E, K_TOP,
                                       x.data_ptr(), F16, H, I, gate.codes.data_ptr(), gate.scales.data_ptr(),
                                       up.codes.data_ptr(), up.scales.data_ptr(), down.codes.data_ptr(),
@@ -185,17 +201,20 @@ def main() -> int:
         copy_calibration(torch, dev)
     torch.cuda.synchronize()
     # eager pass: routes for every set, sanity
-    for i in range(N_SETS):
-        layer(i)
-        layer1(i)
+    with torch.cuda.stream(stream):
+        for i in range(N_SETS):
+            layer(i)
+            layer_two(i)
+            layer_one(i)
     torch.cuda.synchronize()
-    if not torch.isfinite(out.float()).all() or not torch.isfinite(out1).all():
+    if not (torch.isfinite(out.float()).all() and torch.isfinite(out1).all() and torch.isfinite(out2).all()):
         raise RuntimeError("non-finite layer output")
-    if not torch.equal(idx1, idx):
+    if not (torch.equal(idx1, idx) and torch.equal(idx2, idx)):
         raise RuntimeError("layer kernel routed differently from the router kernel")
-    rel = ((out1 - out).abs().max() / out.abs().max()).item()
-    if not rel <= 2e-3:
-        raise RuntimeError(f"layer kernels differ from the split path: max rel {rel:.3e}")
+    for name, o in (("two-launch", out1), ("one-launch", out2)):
+        rel = ((o - out).abs().max() / out.abs().max()).item()
+        if not rel <= 2e-3:
+            raise RuntimeError(f"{name} layer differs from the split path: max rel {rel:.3e}")
 
     def capture(fn, n, offset=0):
         g = torch.cuda.CUDAGraph()
@@ -231,18 +250,20 @@ def main() -> int:
 
     # capture graphs inside the torch stream context so our raw calls use the capture stream
     with torch.cuda.stream(stream):
-        full = capture(layer1, GRAPH_STEPS)
+        full = capture(layer_one, GRAPH_STEPS)
         tail_n = args.steps % GRAPH_STEPS
-        tail = capture(layer1, tail_n, GRAPH_STEPS) if tail_n else None
+        tail = capture(layer_one, tail_n, GRAPH_STEPS) if tail_n else None
+        g_two = capture(layer_two, GRAPH_STEPS)
         g_split = capture(layer, GRAPH_STEPS)
         g_gateup = capture(gateup, GRAPH_STEPS)
         g_down = capture(down_, GRAPH_STEPS)
         g_router = capture(router, GRAPH_STEPS)
 
     n_full = args.steps // GRAPH_STEPS
-    # warmup (untimed)
+    # warmup (untimed): W steps, and at least MIN_WARMUP_STEPS (the GPU's clocks settle over the first
+    # ~5 ms of back-to-back layers; before that a layer takes up to 10% longer)
     with torch.cuda.stream(stream):
-        for _ in range(max(1, math.ceil(args.warmup / GRAPH_STEPS))):
+        for _ in range(math.ceil(max(args.warmup, MIN_WARMUP_STEPS) / GRAPH_STEPS)):
             full.replay()
     torch.cuda.synchronize()
     graphs = [full] * n_full + ([tail] if tail is not None else [])
@@ -259,6 +280,7 @@ def main() -> int:
     # per-kernel averages (HIP events over graph replays on the launch stream)
     reps = max(2, min(16, args.steps // GRAPH_STEPS))
     split_us = timed_replay([g_split], reps) * 1e3 / (reps * GRAPH_STEPS)
+    two_us = timed_replay([g_two], reps) * 1e3 / (reps * GRAPH_STEPS)
     gu_us = timed_replay([g_gateup], reps) * 1e3 / (reps * GRAPH_STEPS)
     dn_us = timed_replay([g_down], reps) * 1e3 / (reps * GRAPH_STEPS)
     rt_us = timed_replay([g_router], reps) * 1e3 / (reps * GRAPH_STEPS)
@@ -267,7 +289,8 @@ def main() -> int:
     gu_gbps = gu_bytes / (gu_us * 1e-6) / 1e9
     dn_gbps = dn_bytes / (dn_us * 1e-6) / 1e9
     layer_us = ms_per_step * 1e3
-    log(f"bench: layer {layer_us:.2f} us ({value:.0f} GB/s) | split path (packed-table kernels) {split_us:.2f} us: "
+    log(f"bench: layer {layer_us:.2f} us ({value:.0f} GB/s), two-launch layer {two_us:.2f} us | split path "
+        f"(packed-table kernels) {split_us:.2f} us: "
         f"router {rt_us:.2f}  gateup {gu_us:.2f} ({gu_gbps:.0f} GB/s)  down {dn_us:.2f} ({dn_gbps:.0f} GB/s)")
 
     result = {
@@ -298,12 +321,17 @@ def main() -> int:
                     "median_us_per_layer": round(float(np.median(samples_us)), 3) if samples_us else None,
                     "min_us_per_layer": round(samples_us[0], 3) if samples_us else None,
                     "max_us_per_layer": round(samples_us[-1], 3) if samples_us else None},
-        "kernels_us": {"moe_layer (route_gateup + down)": round(layer_us, 3), "split_path_packed_table_total": round(split_us, 3),
+        "path": "keep_moe_layer1 (moe_layer(one_launch=True)): router, gate/up/SwiGLU, down and combine in one "
+                "launch of 256 co-resident blocks; keep_moe_layer (two launches) timed beside it",
+        "kernels_us": {"moe_layer1 (one launch)": round(layer_us, 3),
+                       "moe_layer (two launches: route_gateup + down)": round(two_us, 3),
+                       "split_path_packed_table_total": round(split_us, 3),
                        "router": round(rt_us, 3), "moe_gateup": round(gu_us, 3), "moe_down": round(dn_us, 3)},
         "roofline": {"bound": "hbm", "kernel": " + ".join(LAYER_KERNELS), "achieved": round(value, 2),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(value / HBM_PEAK_GBPS, 4),
                      "bytes_per_launch": code_bytes, "us_per_launch": round(layer_us, 3),
                      "traffic": measured_traffic(LAYER_KERNELS),
+                     "traffic_two_launch": measured_traffic(TWO_LAUNCH_KERNELS),
                      "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
                                        "profiles/moe_layer_config2_counters.md"},
         "cpu_baseline": None,

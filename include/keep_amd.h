@@ -261,10 +261,10 @@ int keep_moe_layer_noalloc(const float* logits, const float* bias_served, const 
  * aligned, zero-filled before its first use and then handed unchanged to
  * every call on the same stream (it holds the call counter; calls that
  * overlap on one workspace race). A wait on another block that outlasts
- * ~200 us gives up: the affected outputs are NaN and
+ * ~200 us gives up: the outputs of the blocks that waited are NaN and
  * keep_moe_layer1_status() reports bit 1 (zero the workspace before the next
- * call). Needs a device of at least 256 compute units. h is split into three
- * int8 terms per 256-wide slice (two in keep_moe_layer). Serves H = 4096, I
+ * call). Needs a device of at least 256 compute units. h is split into two
+ * int8 terms per 256-wide slice, as in keep_moe_layer. Serves H = 4096, I
  * in {512, 1024, 1536, 2048}, k <= 8, E <= 1024, scale groups of
  * 256-element multiples. Replaces the serving decode step of
  * scripts/v41_build/omlx_lattice.py:327-371 for batch 1. */

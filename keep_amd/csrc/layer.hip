@@ -433,7 +433,8 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       }
     }
     // route r's dot is D rows 4 r and 4 r + 1, held by lanes 16 r + jj; lane
-    // (g, jj) keeps route g's weighted value for output row jj
+    // (g, jj) keeps route g's weighted value for output row jj (NaN for a
+    // route with a nonzero weight and no pool row, which makes the output NaN)
     float c = 0.f;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -446,7 +447,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
         const float wt = dlive[r] ? s_w[route] : 0.f;
         const float d = (float)acc[0] + (float)acc[1] * 0.0078125f;
         const float val = d * inv4d[r] * scale_cvt(srd[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + dgrp);
-        c = dok[r] && wt != 0.f ? wt * val : 0.f;
+        c = wt == 0.f ? 0.f : dok[r] ? wt * val : __builtin_nanf("");
       }
     }
     // the sum over the wave's routes (lane rows 0 + 1, then + rows 2 + 3)
@@ -464,17 +465,8 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   }
   rt_lds_barrier();
 
-  // 6. the sum of the waves' weighted partials, in wave order (a route with
-  //    a nonzero weight and no pool row makes the output NaN)
+  // 6. the sum of the waves' weighted partials, in wave order
   if (threadIdx.x < 16) {
-    bool bad = false;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      if (r < a.k) {
-        const int32_t e = s_idx[r];
-        bad |= s_w[r] != 0.f && !(e >= 0 && e < a.S);
-      }
-    }
     const float4* rp = (const float4*)(red + threadIdx.x * 16);
     float o = 0.f;
 #pragma unroll
@@ -485,7 +477,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       o += v.z;
       o += v.w;
     }
-    if (bad || tq_bad) o = __builtin_nanf("");
+    if (tq_bad) o = __builtin_nanf("");
     const size_t oi = b * 16u + threadIdx.x;
     if (a.odt == KEEP_F16) ((_Float16*)a.out)[oi] = (_Float16)o;
     else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;

@@ -458,7 +458,7 @@ __global__ __launch_bounds__(512) void k_moeq_down(const int32_t* idx, const flo
       float s;
       q8_scale(rt_wave_reduce(mx, true), s, inv4s[r]);
       uint32_t tw[2];
-      q8_terms<2>(v, s, tw);
+      q8_digits2(v, s, tw);
       aw[q8_aword((uint32_t)(wv * 2 * KMAX + 2 * r), lane >> 1, lane & 1)] = tw[0];
       aw[q8_aword((uint32_t)(wv * 2 * KMAX + 2 * r + 1), lane >> 1, lane & 1)] = tw[1];
     }

@@ -285,7 +285,7 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
         float sc, inv4s;
         q8_scale(rt_wave_reduce(mx, true), sc, inv4s);
         uint32_t tw[2];
-        q8_terms<2>(v, sc, tw);
+        q8_digits2(v, sc, tw);
         aw[q8_aword((uint32_t)(2 * i), lane >> 1, lane & 1)] = tw[0];
         aw[q8_aword((uint32_t)(2 * i + 1), lane >> 1, lane & 1)] = tw[1];
         if (lane == 0) s_inv[wv][i] = inv4s;
