@@ -77,7 +77,9 @@ int keep_group_absmax(const float* x, int64_t groups_total, int64_t group_size, 
 
 /* Routed VQ mat-vec: out[r, :] = W[rhs[r]] . x[row(r), :] for r < routes,
  * row(r) = lhs ? lhs[r] : r / x_div. W[e] is [N, K] given by codes [E, N, K/8]
- * and scales [E, N, K/group_size]. fp32 accumulate.
+ * and scales [E, N, K/group_size]. fp32 accumulate. rhs may be NULL when
+ * num_experts == 1 (a single matrix: every route reads W[0], with no load of
+ * a route vector before the code loads).
  * Optional nested residual (res_codes != NULL): 8-bit E8 codes [H, N, K/8],
  * res_scales [H, N, K/res_group_size], res_table = half2 pairs uint32[256*4]
  * (fp16 bits of dims 2k | 2k+1 << 16) and hot_of_slot[E] (row in the residual

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void k_vq_matvec(MatvecArgs a) {
   const bool live = row0 < a.N;
   // The route's expert and activation row, then the first chunk's codes,
   // scales and activations are in flight while the codebook is built.
-  const int64_t e = a.rhs[route];
+  const int64_t e = a.rhs ? (int64_t)a.rhs[route] : 0;  // no route vector: one matrix, no dependent load
   const int64_t xr = a.lhs ? (int64_t)a.lhs[route] : route / a.x_div;
   uint32_t hot = NO_RESIDUAL;
   bool bad = e < 0 || e >= a.E || xr < 0 || xr >= a.x_rows;
@@ -579,7 +579,8 @@ extern "C" int keep_vq_matvec(const void* x, int x_dtype, int64_t x_rows, const 
                "group_size must be a positive multiple of 8 dividing K (group_size=%lld)", (long long)group_size);
   KEEP_REQUIRE(routes >= 0 && num_experts > 0, "need routes >= 0 and num_experts > 0");
   if (routes == 0) return KEEP_OK;
-  KEEP_REQUIRE(x && codes && scales && table && rhs && out, "null pointer argument");
+  KEEP_REQUIRE(x && codes && scales && table && out, "null pointer argument");
+  KEEP_REQUIRE(rhs || num_experts == 1, "rhs may be NULL only for one matrix (num_experts == 1)");
   KEEP_REQUIRE(lhs || x_div > 0, "x_div must be > 0 without lhs");
   KEEP_REQUIRE(x_rows > 0, "x_rows must be > 0");
   KEEP_REQUIRE(aligned(x, 16), "x must be 16-byte aligned");

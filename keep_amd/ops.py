@@ -258,17 +258,21 @@ def _ptr(t: torch.Tensor | None):
 
 
 def routed_matvec(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor, codebook: torch.Tensor,
-                  rhs: torch.Tensor, *, lhs: torch.Tensor | None = None, x_div: int = 1, input_dims: int,
+                  rhs: torch.Tensor | None, *, lhs: torch.Tensor | None = None, x_div: int = 1, input_dims: int,
                   output_dims: int, group_size: int, code_bits: int = 16, residual=None, hot_of_slot=None,
-                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
+                  out_dtype: torch.dtype | None = None, routes: int | None = None) -> torch.Tensor:
     """``out[r] = W[rhs[r]] . x[lhs[r] or r // x_div]`` -> ``[routes, N]`` (``keep_vq_matvec``).
+    ``rhs=None`` (one matrix, ``codes [1, N, K/8]``): every one of ``routes`` routes reads it.
 
     ``residual`` = ``(res_codes uint8 [H, N, K/8], res_scales [H, N, G'], res_table [256, 4])``
     with ``hot_of_slot`` ``uint32 [E]``.
     """
 
     device = x.device
-    routes = rhs.numel()
+    if rhs is not None:
+        routes = rhs.numel()
+    elif routes is None or codes.shape[0] != 1:
+        raise ValueError("rhs=None needs routes and a single matrix")
     od = out_dtype or output_dtype(x.dtype)
     out = torch.empty((routes, output_dims), dtype=od, device=device)
     if routes == 0:
@@ -285,7 +289,7 @@ def routed_matvec(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor, co
         if rs.dtype != scales.dtype:
             rs = rs.to(scales.dtype)
     _lib.call("keep_vq_matvec", x.data_ptr(), _dtype_code(x, "x"), x.shape[0], codes.data_ptr(), code_bits,
-              scales.data_ptr(), _dtype_code(scales, "scales"), codebook.data_ptr(), rhs.data_ptr(), _ptr(lhs),
+              scales.data_ptr(), _dtype_code(scales, "scales"), codebook.data_ptr(), _ptr(rhs), _ptr(lhs),
               routes, x_div, E, output_dims, input_dims, group_size, _ptr(rc), _ptr(rs), rgs, _ptr(rt), _ptr(hot),
               nhot, out.data_ptr(), _DT[od], _stream(device))
     return out
@@ -462,21 +466,6 @@ def decode_weight_matrix(codes, scales=None, *, code_bits: int = 8, codebook=Non
 # --------------------------------------------------------------------------- vq_qmv / vq_qmm
 
 
-_ZERO_ROUTES: dict = {}
-
-
-def _zero_routes(n: int, device: torch.device) -> torch.Tensor:
-    """A cached int32 zeros vector of length >= n on `device` (every route on
-    expert 0), so a single-matrix call launches no fill kernel."""
-
-    key = (device.type, device.index)
-    z = _ZERO_ROUTES.get(key)
-    if z is None or z.numel() < n:
-        z = torch.zeros(max(n, 64), dtype=torch.int32, device=device)
-        _ZERO_ROUTES[key] = z
-    return z[:n]
-
-
 def vq_qmv(x, codes, scales, codebook=None, *, in_dim: int, out_dim: int, group_size: int = 512,
            code_bits: Literal[8, 16] = 8, implementation: str = "hip",
            codebook_duplication: Literal[1, 4, 8] = 1) -> torch.Tensor:
@@ -496,9 +485,8 @@ def vq_qmv(x, codes, scales, codebook=None, *, in_dim: int, out_dim: int, group_
     if tuple(s.shape) != (out_dim, in_dim // group_size):
         raise ValueError(f"scales must have shape ({out_dim}, {in_dim // group_size}), found {tuple(s.shape)}")
     cb = _codebook_tensor(codebook, code_bits, device)
-    rhs = _zero_routes(1, device)
-    y = routed_matvec(xt.reshape(1, in_dim), c.reshape(1, out_dim, -1), s.reshape(1, out_dim, -1), cb, rhs,
-                      input_dims=in_dim, output_dims=out_dim, group_size=group_size, code_bits=code_bits)
+    y = routed_matvec(xt.reshape(1, in_dim), c.reshape(1, out_dim, -1), s.reshape(1, out_dim, -1), cb, None,
+                      input_dims=in_dim, output_dims=out_dim, group_size=group_size, code_bits=code_bits, routes=1)
     return y.reshape(out_dim)
 
 
@@ -522,9 +510,8 @@ def vq_qmm(x, codes, scales, codebook=None, *, in_dim: int, out_dim: int, group_
         raise ValueError(f"scales must have shape ({out_dim}, {in_dim // group_size}), found {tuple(s.shape)}")
     cb = _codebook_tensor(codebook, code_bits, device)
     M = xt.shape[0]
-    rhs = _zero_routes(M, device)
-    return routed_matvec(xt, c.reshape(1, out_dim, -1), s.reshape(1, out_dim, -1), cb, rhs, input_dims=in_dim,
-                         output_dims=out_dim, group_size=group_size, code_bits=code_bits)
+    return routed_matvec(xt, c.reshape(1, out_dim, -1), s.reshape(1, out_dim, -1), cb, None, input_dims=in_dim,
+                         output_dims=out_dim, group_size=group_size, code_bits=code_bits, routes=M)
 
 
 # --------------------------------------------------------------------------- routed operators

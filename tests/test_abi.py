@@ -63,6 +63,7 @@ def _matvec(**over):
     (dict(x=None), "null"),
     (dict(x=3), "aligned"),
     (dict(rc=16, rs=None), "nested"),
+    (dict(rhs=None, E=2), "rhs may be NULL only"),
 ])
 def test_matvec_argument_validation_before_launch(over, msg):
     assert _matvec(**over) == _lib.KEEP_EINVAL
