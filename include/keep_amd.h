@@ -337,6 +337,29 @@ int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, 
                    float swiglu_limit, void* h_work, void* workspace, int64_t workspace_bytes,
                    void* out, int out_dtype, void* stream);
 
+/* The few-token layer from the router logits: keep_router_dual_topk's outputs
+ * (idx, w, want, want_score, admit; same contract, k <= 16) and
+ * keep_moe_tiles' result, byte for byte. For T <= 32 the router, the
+ * activation terms and the route plan run as ONE launch (one block routes
+ * every token, one wave each, and plans from the routes it holds in LDS,
+ * while the other blocks build the tokens' terms), so the layer is four
+ * launches; larger T runs the router and then keep_moe_tiles. With slot_map
+ * the pools hold num_slots rows (the plan's buckets). `workspace` holds
+ * keep_moe_tiles_workspace_bytes(T, k, pool rows, H) bytes. Replaces the
+ * speculative-verify decode step of scripts/v41_build/omlx_lattice.py:327-371
+ * for T tokens (router :77-97, experts gather_vqmm_verify_rows
+ * src/ramp/ops/vq_switch.py:286-377). */
+int keep_moe_tiles_layer(const float* logits, const float* bias_served, const float* bias_demand,
+                         int score_func, int renormalize, float route_scale, float tau,
+                         const int32_t* slot_map, int64_t num_slots, int64_t num_experts, int64_t k,
+                         const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
+                         const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
+                         const void* up_scales, const uint16_t* down_codes, const void* down_scales,
+                         int scale_dtype, int64_t group_size_h, int64_t group_size_i, const void* prepared,
+                         float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                         uint8_t* admit, void* h_work, void* workspace, int64_t workspace_bytes, void* out,
+                         int out_dtype, void* stream);
+
 /* Prefill grouped GEMM on the fp16 matrix cores over expert-sorted routes
  * (tiles of <= 64 routes of one expert from keep_route_plan): for every tile
  * t and route i < tile_count[t], with p = tile_offset[t] + i,

@@ -10,7 +10,7 @@ from keep_amd.block import combine_add, rmsnorm_quant_rht
 from keep_amd.encode import (encode_e8_1bit_rtn, encode_e8p_rtn, encode_e8p_rtn_diagonal_hessian,
                              quantize_weight_rtn)
 from keep_amd.nn import (HotTier, LimitedSwiGLU, QuantizedVQLinear, QuantizedVQSwitchGLU, QuantizedVQSwitchLinear,
-                         RoutedVQMoE, moe_decode, moe_layer, moe_layer_supported)
+                         RoutedVQMoE, moe_decode, moe_layer, moe_layer_supported, moe_tiles_layer)
 from keep_amd.ops import (
     decode_e8p,
     decode_weight_matrix,
@@ -41,6 +41,6 @@ __all__ = [
     "decode_weight_matrix", "e8_1bit_m1_per_route", "e8_1bit_m1_token_layout", "e8_1bit_packed", "e8p_m1_per_route",
     "e8p_m1_token_layout", "e8p_nested_m1_per_route", "e8p_nested_m1_token_layout", "e8p_packed_abs_grid",
     "expert_select", "gather_vqmm", "gather_vqmm_sorted_routes", "gather_vqmm_verify_rows", "half2_pairs",
-    "is_available", "moe_decode", "moe_layer", "moe_layer_supported", "pair_packed", "resident_bias", "route_plan",
+    "is_available", "moe_decode", "moe_layer", "moe_layer_supported", "moe_tiles_layer", "pair_packed", "resident_bias", "route_plan",
     "router_dual_topk", "trace_gather_vqmm_calls", "vq_qmm", "vq_qmv",
 ]

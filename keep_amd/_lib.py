@@ -41,6 +41,9 @@ _SIGS = {
     "keep_moe_tiles": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int,
                        c_int64, c_int64, _P, c_float, _P, _P, c_int64, _P, c_int, _P],
     "keep_moe_tiles_workspace_bytes": [c_int64, c_int64, c_int64, c_int64],
+    "keep_moe_tiles_layer": [_P, _P, _P, c_int, c_int, c_float, c_float, _P, c_int64, c_int64, c_int64, _P, c_int,
+                             c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float,
+                             _P, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int, _P],
     "keep_vq_grouped_gemm_q8_workspace_bytes": [c_int64, c_int64],
     "keep_route_combine": [_P, _P, c_int64, c_int64, c_int64, _P, c_int, _P],
     "keep_rht": [_P, c_int, _P, c_int, c_int64, c_int64, _P, c_int, _P],

@@ -29,6 +29,7 @@
 //     with a nonzero weight gives NaN), as the one-token layer combines.
 #include "common.h"
 #include "moe_dev.h"
+#include "plan_dev.h"
 #include "q8_dev.h"
 #include "route_dev.h"
 
@@ -54,14 +55,11 @@ struct MTArgs {
 
 // ------------------------------------------------------------------ x terms
 
-// Block t, wave s: the three int8 terms of x[t] * s_slice over K slice s (256
-// values) in the A-slot layout of q8_aword, and 1 / (4 s_slice).
+// Token t, K slice s (one wave): the three int8 terms of x[t] * s_slice over
+// the slice's 256 values in the A-slot layout of q8_aword, and 1 / (4 s_slice).
 template <bool XBF>
-__global__ __launch_bounds__(1024) void k_q8_xterms(const void* x, int H, uint4* xt, float* xinv) {
-  const int lane = threadIdx.x & 63;
-  const int s = threadIdx.x >> 6;
+__device__ __forceinline__ void mt_xterms(const void* x, int H, uint4* xt, float* xinv, int t, int s, int lane) {
   const int S = H >> 8;
-  const int t = blockIdx.x;
   const uint4 c = ldg16_q((const uint4*)x + ((size_t)t * H >> 3) + s * 32 + (lane >> 1));
   float v[4];
   q8_half4<XBF>(c, lane & 1, v);
@@ -74,6 +72,79 @@ __global__ __launch_bounds__(1024) void k_q8_xterms(const void* x, int H, uint4*
 #pragma unroll
   for (int n = 0; n < 3; ++n) base[q8_aword((uint32_t)n, lane >> 1, lane & 1)] = tw[n];
   if (lane == 0) xinv[(size_t)t * S + s] = inv4s;
+}
+
+// Block t, wave s: token t's terms of slice s.
+template <bool XBF>
+__global__ __launch_bounds__(1024) void k_q8_xterms(const void* x, int H, uint4* xt, float* xinv) {
+  mt_xterms<XBF>(x, H, xt, xinv, (int)blockIdx.x, (int)(threadIdx.x >> 6), (int)(threadIdx.x & 63));
+}
+
+// ------------------------------------------------------------------ fused prologue (few tokens)
+
+constexpr int MT_FUSED_MAX_T = 32;  // tokens the one-block router of the prologue takes
+
+struct MTPro {
+  const void* x;
+  int H;
+  uint4* xt;
+  float* xinv;
+  const float* logits;
+  const float *bias_s, *bias_d;
+  int func, renorm;
+  float route_scale, tau;
+  const int32_t* slot_map;
+  int T, E, S, k;  // S: pool rows (the plan's buckets)
+  int32_t* idx;
+  float* w;
+  int32_t* want;
+  float* want_score;
+  uint8_t* admit;
+  int32_t *order, *inverse, *counts, *offsets, *te, *to, *tc, *nt;
+  int max_tiles;
+};
+
+// One launch in place of the router, the x terms and the route plan: block
+// t < T builds token t's x terms (as k_q8_xterms); block T routes every token
+// (wave w takes tokens w, w + 16, ..., each as k_router does, with the same
+// outputs) and keeps the served slots in LDS, from which it runs the route
+// plan (plan_block, as k_route_plan over idx).
+template <int PER, bool XBF>
+__global__ __launch_bounds__(1024) void k_mt_prologue(MTPro p) {
+  __shared__ PlanLds L;
+  __shared__ int32_t s_r[MT_FUSED_MAX_T * 16];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if ((int)blockIdx.x < p.T) {
+    if (wv < (p.H >> 8)) mt_xterms<XBF>(p.x, p.H, p.xt, p.xinv, (int)blockIdx.x, wv, lane);
+    return;
+  }
+  for (int t = wv; t < p.T; t += 16) {
+    float z[PER], bs[PER], bd[PER];
+    rt_load<PER>(p.logits + (int64_t)t * p.E, p.bias_s, p.bias_d, p.E, lane, z, bs, bd);
+    const RouteLane r = rt_route<PER>(z, bs, bd, p.E, p.k, p.func, p.renorm, p.route_scale, p.tau,
+                                      p.bias_d == p.bias_s, lane);
+    int slot = r.expert;
+    if (p.slot_map) {
+      int sm[PER];
+      rt_load_slots<PER>(p.slot_map, p.E, lane, sm);
+      slot = rt_slot_of<PER>(sm, r.valid ? r.expert : -1, p.E, p.S);
+    }
+    if (lane < p.k) s_r[t * p.k + lane] = r.valid ? slot : -1;
+    if (r.valid) {
+      const int64_t o = (int64_t)t * p.k + (lane < 32 ? lane : lane - 32);
+      if (lane < 32) {
+        p.idx[o] = slot;
+        p.w[o] = r.value;
+      } else {
+        if (p.want) p.want[o] = r.expert;
+        if (p.want_score) p.want_score[o] = r.value;
+        if (p.admit) p.admit[o] = r.admit;
+      }
+    }
+  }
+  __syncthreads();
+  plan_block([&](int r) { return s_r[r]; }, p.T * p.k, p.S, MT_TILE, p.order, p.inverse, p.counts, p.offsets,
+             p.te, p.to, p.tc, p.max_tiles, p.nt, L);
 }
 
 // ------------------------------------------------------------------ gate/up
@@ -440,13 +511,12 @@ extern "C" int keep_moe_tiles_supported(int64_t T, int64_t num_experts, int64_t 
   return moe_tiles_supported(T, num_experts, H, I, k, group_size_h, group_size_i) ? 1 : 0;
 }
 
-extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, const int32_t* idx,
-                              const float* w, int64_t k, int64_t num_experts, const uint16_t* gate_codes,
-                              const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
-                              const uint16_t* down_codes, const void* down_scales, int scale_dtype,
-                              int64_t group_size_h, int64_t group_size_i, const void* prepared, float swiglu_limit,
-                              void* h_work, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
-                              void* stream) {
+// The checks both few-token entry points make on the expert side.
+static int mt_check(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t k, int64_t num_experts,
+                    const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
+                    const void* up_scales, const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                    int64_t group_size_h, int64_t group_size_i, const void* prepared, void* h_work, void* workspace,
+                    int64_t workspace_bytes, void* out, int out_dtype) {
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(group_size_h > 0 && H % group_size_h == 0 && group_size_i > 0 && I % group_size_i == 0,
@@ -454,8 +524,8 @@ extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, 
   KEEP_REQUIRE(moe_tiles_supported(T, num_experts, H, I, k, group_size_h, group_size_i),
                "shape not served by the tiled MoE kernels (T <= 256, k <= 16, E <= 1024, H a multiple of 256 up "
                "to 4096, I a multiple of 256 up to 2048, scale groups of 256-element multiples)");
-  KEEP_REQUIRE(x && idx && w && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
-                   prepared && h_work && workspace && out,
+  KEEP_REQUIRE(x && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales && prepared &&
+                   h_work && workspace && out,
                "null pointer argument");
   const MTWorkspace L = mt_layout(T, k, num_experts, H);
   KEEP_REQUIRE(workspace_bytes >= (int64_t)L.total, "workspace needs %lld bytes, got %lld", (long long)L.total,
@@ -463,8 +533,14 @@ extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, 
   KEEP_REQUIRE(aligned(x, 16) && aligned(h_work, 16) && aligned(prepared, 16) && aligned(workspace, 256),
                "x, h_work and prepared must be 16-byte aligned and the workspace 256-byte aligned");
   KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 16), "codes misaligned");
-  hipStream_t s = (hipStream_t)stream;
-  char* ws = (char*)workspace;
+  return KEEP_OK;
+}
+
+static MTArgs mt_args(int64_t H, int64_t I, int64_t k, int64_t num_experts, const uint16_t* gate_codes,
+                      const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
+                      const uint16_t* down_codes, const void* down_scales, int scale_dtype, int64_t group_size_h,
+                      int64_t group_size_i, const void* prepared, float swiglu_limit, void* h_work, char* ws,
+                      const MTWorkspace& L) {
   MTArgs a{};
   a.xt = (const uint4*)(ws + L.xt);
   a.xinv = (const float*)(ws + L.xinv);
@@ -482,8 +558,45 @@ extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, 
   a.limit = swiglu_limit;
   a.h = (uint16_t*)h_work;
   a.y = (float*)(ws + L.y);
-  const int64_t R = T * k;
+  return a;
+}
 
+// gate/up, down and the combine, once the x terms and the plan are in the workspace.
+static void mt_tail(const MTArgs& a, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t k, int64_t num_experts,
+                    const int32_t* idx, const float* w, const MTWorkspace& L, void* out, int out_dtype,
+                    hipStream_t s) {
+  const int64_t R = T * k;
+  const int64_t tiles_ub = std::min<int64_t>(R, L.max_tiles);
+  const unsigned g1 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (I / 16)));
+  const unsigned g2 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (H / 64)));
+  if (x_dtype == KEEP_BF16)
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<true>), dim3(g1), dim3(1024), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<false>), dim3(g1), dim3(1024), 0, s, a);
+  hipLaunchKernelGGL(k_moeq_down_tiles, dim3(g2), dim3(512), 0, s, a);
+  const int64_t n = T * H;
+  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.y, idx, w, (int)T, (int)k,
+                     (int)num_experts, (int)H, a.tq_bad, out, out_dtype);
+}
+
+extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, const int32_t* idx,
+                              const float* w, int64_t k, int64_t num_experts, const uint16_t* gate_codes,
+                              const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
+                              const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                              int64_t group_size_h, int64_t group_size_i, const void* prepared, float swiglu_limit,
+                              void* h_work, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
+                              void* stream) {
+  const int chk = mt_check(x, x_dtype, T, H, I, k, num_experts, gate_codes, gate_scales, up_codes, up_scales,
+                           down_codes, down_scales, scale_dtype, group_size_h, group_size_i, prepared, h_work,
+                           workspace, workspace_bytes, out, out_dtype);
+  if (chk != KEEP_OK) return chk;
+  KEEP_REQUIRE(idx && w, "null pointer argument");
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const MTWorkspace L = mt_layout(T, k, num_experts, H);
+  const MTArgs a = mt_args(H, I, k, num_experts, gate_codes, gate_scales, up_codes, up_scales, down_codes,
+                           down_scales, scale_dtype, group_size_h, group_size_i, prepared, swiglu_limit, h_work, ws, L);
+  const int64_t R = T * k;
   const dim3 xb((unsigned)(64 * (H / 256)));
   if (x_dtype == KEEP_BF16)
     hipLaunchKernelGGL((k_q8_xterms<true>), dim3((unsigned)T), xb, 0, s, x, (int)H, (uint4*)(ws + L.xt),
@@ -496,16 +609,74 @@ extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, 
                                  (int32_t*)(ws + L.to), (int32_t*)(ws + L.tc), L.max_tiles, (int32_t*)(ws + L.nt),
                                  stream);
   if (rc != KEEP_OK) return rc;
-  const int64_t tiles_ub = std::min<int64_t>(R, L.max_tiles);
-  const unsigned g1 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (I / 16)));
-  const unsigned g2 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (H / 64)));
-  if (x_dtype == KEEP_BF16)
-    hipLaunchKernelGGL((k_moeq_gateup_tiles<true>), dim3(g1), dim3(1024), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_moeq_gateup_tiles<false>), dim3(g1), dim3(1024), 0, s, a);
-  hipLaunchKernelGGL(k_moeq_down_tiles, dim3(g2), dim3(512), 0, s, a);
-  const int64_t n = T * H;
-  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const float*)(ws + L.y), idx,
-                     w, (int)T, (int)k, (int)num_experts, (int)H, a.tq_bad, out, out_dtype);
+  mt_tail(a, x_dtype, T, H, I, k, num_experts, idx, w, L, out, out_dtype, s);
   return launch_status("keep_moe_tiles");
+}
+
+// Router declaration (router.hip).
+extern "C" int keep_router_dual_topk(const float* logits, int64_t T, int64_t E, int64_t k, const float* bias_served,
+                                     const float* bias_demand, int score_func, int renormalize, float route_scale,
+                                     float tau, const int32_t* slot_map, int64_t num_slots, int32_t* idx, float* w,
+                                     int32_t* want, float* want_score, uint8_t* admit, void* stream);
+
+extern "C" int keep_moe_tiles_layer(const float* logits, const float* bias_served, const float* bias_demand,
+                                    int score_func, int renormalize, float route_scale, float tau,
+                                    const int32_t* slot_map, int64_t num_slots, int64_t num_experts, int64_t k,
+                                    const void* x, int x_dtype, int64_t T, int64_t H, int64_t I,
+                                    const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
+                                    const void* up_scales, const uint16_t* down_codes, const void* down_scales,
+                                    int scale_dtype, int64_t group_size_h, int64_t group_size_i,
+                                    const void* prepared, float swiglu_limit, int32_t* idx, float* w, int32_t* want,
+                                    float* want_score, uint8_t* admit, void* h_work, void* workspace,
+                                    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE(num_experts >= 1 && num_experts <= 64 * RT_MAX_PER_LANE, "num_experts must be in 1..%d",
+               64 * RT_MAX_PER_LANE);
+  KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);
+  KEEP_REQUIRE(!slot_map || (num_slots >= 1 && num_slots <= 1024), "num_slots must be in 1..1024");
+  const int64_t S = slot_map ? num_slots : num_experts;  // pool rows
+  const int chk = mt_check(x, x_dtype, T, H, I, k, S, gate_codes, gate_scales, up_codes, up_scales, down_codes,
+                           down_scales, scale_dtype, group_size_h, group_size_i, prepared, h_work, workspace,
+                           workspace_bytes, out, out_dtype);
+  if (chk != KEEP_OK) return chk;
+  KEEP_REQUIRE(k <= num_experts, "k must be <= num_experts");
+  KEEP_REQUIRE(logits && idx && w, "null pointer argument");
+  if (T > MT_FUSED_MAX_T) {  // the router on its own launch (one wave per token), then keep_moe_tiles
+    const int rc = keep_router_dual_topk(logits, T, num_experts, k, bias_served, bias_demand, score_func, renormalize,
+                                         route_scale, tau, slot_map, num_slots, idx, w, want, want_score, admit,
+                                         stream);
+    if (rc != KEEP_OK) return rc;
+    return keep_moe_tiles(x, x_dtype, T, H, I, idx, w, k, S, gate_codes, gate_scales, up_codes, up_scales,
+                          down_codes, down_scales, scale_dtype, group_size_h, group_size_i, prepared, swiglu_limit,
+                          h_work, workspace, workspace_bytes, out, out_dtype, stream);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const MTWorkspace L = mt_layout(T, k, S, H);
+  const MTArgs a = mt_args(H, I, k, S, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales,
+                           scale_dtype, group_size_h, group_size_i, prepared, swiglu_limit, h_work, ws, L);
+  MTPro p{};
+  p.x = x; p.H = (int)H; p.xt = (uint4*)(ws + L.xt); p.xinv = (float*)(ws + L.xinv);
+  p.logits = logits; p.bias_s = bias_served; p.bias_d = bias_demand; p.func = score_func; p.renorm = renormalize;
+  p.route_scale = route_scale; p.tau = tau; p.slot_map = slot_map;
+  p.T = (int)T; p.E = (int)num_experts; p.S = (int)S; p.k = (int)k;
+  p.idx = idx; p.w = w; p.want = want; p.want_score = want_score; p.admit = admit;
+  p.order = (int32_t*)(ws + L.order); p.inverse = (int32_t*)(ws + L.inverse); p.counts = (int32_t*)(ws + L.counts);
+  p.offsets = (int32_t*)(ws + L.offsets); p.te = (int32_t*)(ws + L.te); p.to = (int32_t*)(ws + L.to);
+  p.tc = (int32_t*)(ws + L.tc); p.nt = (int32_t*)(ws + L.nt); p.max_tiles = (int)L.max_tiles;
+  const int per = (int)((num_experts + 63) / 64);
+  const dim3 grid((unsigned)(T + 1)), blk(1024);
+#define MT_PRO(P)                                                                        \
+  do {                                                                                   \
+    if (x_dtype == KEEP_BF16) hipLaunchKernelGGL((k_mt_prologue<P, true>), grid, blk, 0, s, p); \
+    else hipLaunchKernelGGL((k_mt_prologue<P, false>), grid, blk, 0, s, p);             \
+  } while (0)
+  if (per <= 1) MT_PRO(1);
+  else if (per <= 2) MT_PRO(2);
+  else if (per <= 4) MT_PRO(4);
+  else if (per <= 6) MT_PRO(6);
+  else if (per <= 8) MT_PRO(8);
+  else MT_PRO(16);
+#undef MT_PRO
+  mt_tail(a, x_dtype, T, H, I, k, S, idx, w, L, out, out_dtype, s);
+  return launch_status("keep_moe_tiles_layer");
 }

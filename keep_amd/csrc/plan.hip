@@ -1,176 +1,15 @@
-// Device route plan: stable counting sort of routes by expert plus tile
-// descriptors, in one workgroup of 1024 threads (no host sync, no device
-// allocation). Routes with an expert outside [0, E) sort after every valid
-// route; their tiles follow the valid ones with tile_expert -1, so a GEMM
-// over every descriptor writes their rows (as NaN) instead of leaving them
-// unset. n_tiles_out counts the valid tiles only. With B <= E + 1 non-empty
-// buckets the descriptors fit in ceil(R / tile) + E entries, since
-// ceil(a / t) + ceil(b / t) <= ceil((a + b) / t) + 1.
-//
-// Stability: routes are taken in chunks of 1024 in route order. Inside a
-// chunk, a route's rank among same-expert routes is (routes of its expert in
-// earlier waves of the chunk, from per-wave histograms) + (earlier lanes of
-// its own wave with the same expert, by a 64-step shuffle scan).
-#include "common.h"
+// Device route plan kernel (the plan itself is plan_block in plan_dev.h).
+#include "plan_dev.h"
 
 namespace keep {
-
-constexpr int PLAN_THREADS = 1024;
-constexpr int PLAN_WAVES = PLAN_THREADS / 64;
-constexpr int PLAN_MAX_E = 1024;
-constexpr int PLAN_PER = 16;  // routes per thread held in registers (R <= 16384)
 
 __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs, int R, int E, int tile,
                                                              int32_t* order, int32_t* inverse, int32_t* counts,
                                                              int32_t* offsets, int32_t* te, int32_t* to, int32_t* tc,
                                                              int max_tiles, int32_t* n_tiles_out) {
-  __shared__ int cnt[PLAN_MAX_E + 1];
-  __shared__ int run[PLAN_MAX_E + 1];
-  __shared__ int tbase[PLAN_MAX_E + 1];
-  __shared__ int wh[PLAN_WAVES][PLAN_MAX_E + 1];
-  __shared__ int wtot[2][PLAN_WAVES];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int EB = E + 1;  // bucket E collects invalid expert ids
-  for (int e = tid; e < EB; e += PLAN_THREADS) cnt[e] = 0;
-  __syncthreads();
-  // up to PLAN_PER routes per thread stay in registers from here to the scatter
-  const bool held = R <= PLAN_THREADS * PLAN_PER;
-  int ev[PLAN_PER];
-  if (held) {
-#pragma unroll
-    for (int i = 0; i < PLAN_PER; ++i) {
-      const int r = i * PLAN_THREADS + tid;
-      int e = -1;
-      if (r < R) {
-        e = rhs[r];
-        if (e < 0 || e >= E) e = E;
-      }
-      ev[i] = e;
-    }
-#pragma unroll
-    for (int i = 0; i < PLAN_PER; ++i)
-      if (ev[i] >= 0) atomicAdd(&cnt[ev[i]], 1);
-  } else {
-    for (int r = tid; r < R; r += PLAN_THREADS) {
-      int e = rhs[r];
-      if (e < 0 || e >= E) e = E;
-      atomicAdd(&cnt[e], 1);
-    }
-  }
-  __syncthreads();
-  // Exclusive prefix sums of the bucket sizes (route bases) and of the tile
-  // counts (first tile of each expert): buckets 2 tid, 2 tid + 1 per thread,
-  // a shuffle scan inside each wave, then the 16 wave totals.
-  {
-    const int b0 = 2 * tid, b1 = 2 * tid + 1;
-    const int c0 = b0 < EB ? cnt[b0] : 0, c1 = b1 < EB ? cnt[b1] : 0;
-    const int t0 = b0 < E ? (c0 + tile - 1) / tile : 0, t1 = b1 < E ? (c1 + tile - 1) / tile : 0;
-    int vc = c0 + c1, vt = t0 + t1;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int oc = __shfl_up(vc, d, 64), ot = __shfl_up(vt, d, 64);
-      if (lane >= d) {
-        vc += oc;
-        vt += ot;
-      }
-    }
-    if (lane == 63) {
-      wtot[0][wv] = vc;
-      wtot[1][wv] = vt;
-    }
-    __syncthreads();
-    int bc = 0, bt = 0;
-    for (int w = 0; w < wv; ++w) {
-      bc += wtot[0][w];
-      bt += wtot[1][w];
-    }
-    const int ec = bc + vc - (c0 + c1), et = bt + vt - (t0 + t1);  // exclusive
-    if (b0 < EB) {
-      run[b0] = ec;
-      tbase[b0] = et;
-    }
-    if (b1 < EB) {
-      run[b1] = ec + c0;
-      tbase[b1] = et + t0;
-    }
-    if (b0 == E) n_tiles_out[0] = et;
-    if (b1 == E) n_tiles_out[0] = et + t0;
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += PLAN_THREADS) {
-    counts[e] = cnt[e];
-    offsets[e] = run[e];
-    const int nt = (cnt[e] + tile - 1) / tile;
-    for (int i = 0; i < nt; ++i) {
-      const int ti = tbase[e] + i;
-      if (ti < max_tiles) {
-        te[ti] = e;
-        to[ti] = run[e] + i * tile;
-        tc[ti] = min(tile, cnt[e] - i * tile);
-      }
-    }
-  }
-  {
-    const int nbad = (cnt[E] + tile - 1) / tile;  // the invalid routes' tiles, expert -1
-    for (int ti = tbase[E] + tid; ti < max_tiles; ti += PLAN_THREADS) {
-      const int i = ti - tbase[E];
-      const bool b = i < nbad;
-      te[ti] = b ? -1 : 0;
-      to[ti] = b ? run[E] + i * tile : 0;
-      tc[ti] = b ? min(tile, cnt[E] - i * tile) : 0;
-    }
-  }
-  // stable scatter, PLAN_THREADS routes per pass: a route's position is its
-  // bucket's running offset + the routes of that bucket in earlier waves of
-  // the pass + the lanes of its own wave below it with the same bucket
-  const int nbits = 32 - __builtin_clz((unsigned)E);  // bucket ids 0..E
-  auto pass = [&](int base, int e) {
-    for (int i = tid; i < PLAN_WAVES * EB; i += PLAN_THREADS) wh[i / EB][i % EB] = 0;
-    __syncthreads();
-    const int r = base + tid;
-    uint64_t peers = __ballot(e >= 0);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (e >> b) & 1;
-      const uint64_t m = __ballot(bit);
-      peers &= bit ? m : ~m;
-    }
-    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
-    if (e >= 0) atomicAdd(&wh[wv][e], 1);
-    __syncthreads();
-    for (int q = tid; q < EB; q += PLAN_THREADS) {
-      int acc = run[q];
-      for (int w = 0; w < PLAN_WAVES; ++w) {
-        const int c = wh[w][q];
-        wh[w][q] = acc;
-        acc += c;
-      }
-      run[q] = acc;
-    }
-    __syncthreads();
-    if (e >= 0) {
-      const int pos = wh[wv][e] + rank;
-      order[pos] = r;
-      inverse[r] = pos;
-    }
-    __syncthreads();
-  };
-  if (held) {
-#pragma unroll
-    for (int i = 0; i < PLAN_PER; ++i) {
-      if (i * PLAN_THREADS >= R) break;
-      pass(i * PLAN_THREADS, ev[i]);
-    }
-  } else {
-    for (int base = 0; base < R; base += PLAN_THREADS) {
-      const int r = base + tid;
-      int e = -1;
-      if (r < R) {
-        e = rhs[r];
-        if (e < 0 || e >= E) e = E;
-      }
-      pass(base, e);
-    }
-  }
+  __shared__ PlanLds L;
+  plan_block([&](int r) { return rhs[r]; }, R, E, tile, order, inverse, counts, offsets, te, to, tc, max_tiles,
+             n_tiles_out, L);
 }
 
 }  // namespace keep

@@ -502,6 +502,67 @@ def moe_decode(x: torch.Tensor, idx: torch.Tensor, weight: torch.Tensor, gate, u
     return out
 
 
+def moe_tiles_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, bias_served=None,
+                    bias_demand=None, score_func: str = "softmax", renormalize: bool = True,
+                    route_scale: float = 1.0, tau: float = float("inf"), limit: float = 0.0,
+                    codebook: torch.Tensor | None = None, out_dtype: torch.dtype | None = None, slot_map=None,
+                    h_work: torch.Tensor | None = None):
+    """A few tokens' whole MoE layer from the router logits (``keep_moe_tiles_layer``):
+    ``router_dual_topk``'s outputs and ``moe_decode``'s result on the tiles path, byte
+    for byte, with the router, the activation terms and the route plan in one launch
+    for up to 32 tokens. ``x [T, H]`` (fp16/bf16), ``logits [T, E]``; ``slot_map`` as
+    in ``moe_layer``. Returns ``(out [T, H], RouterOutput)``; float32 by default."""
+
+    device = x.device
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("moe_tiles_layer needs float16 or bfloat16 activations")
+    if score_func not in _lib.SCORE_FUNCS:
+        raise ValueError(f"score_func must be one of {sorted(_lib.SCORE_FUNCS)}")
+    (gc, gs), (uc, us), (dc, ds) = gate, up, down
+    S, I, Hc = gc.shape
+    H = Hc * 8
+    if x.ndim != 2 or x.shape[1] != H:
+        raise ValueError(f"x must be [tokens, {H}], found {tuple(x.shape)}")
+    if tuple(uc.shape) != (S, I, Hc) or tuple(dc.shape) != (S, H, I // 8):
+        raise ValueError("gate/up codes must be [E, I, H/8] and down codes [E, H, I/8]")
+    if not (gs.dtype == us.dtype == ds.dtype):
+        raise ValueError("gate/up/down scales must share a dtype")
+    T = x.shape[0]
+    z = logits.to(device=device, dtype=torch.float32).reshape(T, -1).contiguous()
+    E = z.shape[1]
+    if slot_map is None and E != S:
+        raise ValueError(f"logits must hold {S} experts, found {E}")
+    sm, ns = _slot_args(slot_map, S if slot_map is not None else None, E, device)
+    bs = None if bias_served is None else bias_served.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    bd = None if bias_demand is None else bias_demand.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    if bias_demand is bias_served:
+        bd = bs
+    for name, b in (("bias_served", bs), ("bias_demand", bd)):
+        if b is not None and b.numel() != E:
+            raise ValueError(f"{name} must have {E} entries, found {b.numel()}")
+    i32 = dict(dtype=torch.int32, device=device)
+    f32 = dict(dtype=torch.float32, device=device)
+    r = RouterOutput(torch.empty((T, k), **i32), torch.empty((T, k), **f32), torch.empty((T, k), **i32),
+                     torch.empty((T, k), **f32), torch.empty((T, k), dtype=torch.uint8, device=device))
+    od = out_dtype or torch.float32
+    out = torch.empty((T, H), dtype=od, device=device)
+    if h_work is None:
+        h_work = torch.empty((T * k * I,), dtype=torch.bfloat16, device=device)
+    elif h_work.numel() < T * k * I or h_work.dtype != torch.bfloat16:
+        raise ValueError("h_work must hold T*k*I bfloat16 elements")
+    cb = ops._codebook_tensor(codebook, 16, device)
+    prep = ops.prepared_table(cb)
+    gh, gi = H // gs.shape[-1], I // ds.shape[-1]
+    ws = torch.empty(int(_lib.load().keep_moe_tiles_workspace_bytes(T, k, S, H)), dtype=torch.uint8, device=device)
+    _lib.call("keep_moe_tiles_layer", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
+              int(bool(renormalize)), float(route_scale), float(tau), ops._ptr(sm), ns, E, k, x.data_ptr(),
+              ops._DT[x.dtype], T, H, I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(),
+              ds.data_ptr(), ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit), r.idx.data_ptr(),
+              r.weight.data_ptr(), r.want.data_ptr(), r.want_score.data_ptr(), r.admit.data_ptr(), h_work.data_ptr(),
+              ws.data_ptr(), ws.numel(), out.data_ptr(), ops._DT[od], ops._stream(device))
+    return out, r
+
+
 def moe_tiles_supported(T: int, num_experts: int, hidden: int, intermediate: int, k: int, group_size_h: int,
                         group_size_i: int) -> bool:
     """Whether the expert-grouped few-token path (``keep_moe_tiles``) serves this shape."""
@@ -732,10 +793,25 @@ class RoutedVQMoE:
                 moe_layer_supported(g.num_experts, g.input_dims, g.output_dims, self.top_k,
                                     g.input_dims // g.scales.shape[-1], d.input_dims // d.scales.shape[-1]))
 
+    def _tiles_layer_path(self, x: torch.Tensor) -> bool:
+        g, d = self.glu.gate_proj, self.glu.down_proj
+        T = x.shape[0]
+        return (2 <= T <= self.decode_max_tokens and x.dtype in (torch.float16, torch.bfloat16) and
+                self.glu._all_e8p() and self.glu.hot_tier is None and self.top_k <= 16 and
+                moe_tiles_supported(T, g.num_experts, g.input_dims, g.output_dims, self.top_k,
+                                    g.input_dims // g.scales.shape[-1], d.input_dims // d.scales.shape[-1]))
+
     def __call__(self, x: torch.Tensor, logits: torch.Tensor, *, residual: torch.Tensor | None = None):
         extra = self.shared_experts is not None or residual is not None
         od = torch.float32 if extra else self.out_dtype
-        if self._layer_path(x):
+        if self._tiles_layer_path(x):
+            g, u, d = self.glu.gate_proj, self.glu.up_proj, self.glu.down_proj
+            out, r = moe_tiles_layer(x, logits, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
+                                     k=self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
+                                     score_func=self.score_func, renormalize=self.renormalize,
+                                     route_scale=self.route_scale, tau=self.tau, limit=self.limit,
+                                     codebook=g.codebook, out_dtype=od, slot_map=self.slot_map)
+        elif self._layer_path(x):
             g, u, d = self.glu.gate_proj, self.glu.up_proj, self.glu.down_proj
             out, r = moe_layer(x, logits, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
                                k=self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,

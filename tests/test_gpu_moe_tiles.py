@@ -2,7 +2,9 @@
 identity with the one-token layer token by token (the verify-rows discipline
 of the reference, tests/test_gather_vqmm_verify_rows.py:1-33), the C oracle at
 the verify shapes of config 3, the float64 oracle with many routes per expert
-(several tiles and route chunks per expert), and the combine's edge cases."""
+(several tiles and route chunks per expert), the combine's edge cases, and the
+layer from the logits (keep_moe_tiles_layer: router, terms and plan in one
+launch up to 32 tokens) byte-identical to the router followed by the tiles."""
 
 import numpy as np
 import pytest
@@ -111,3 +113,61 @@ def test_tiles_zero_weight_and_bad_expert(dev):
     gw = np.array([[0.7, 0.0], [1.0, 0.0]], dtype=np.float32)
     want = ops.moe_layer(x[[0, 2]].float().cpu().numpy(), good, gw, gate, up, down, h_round="bfloat16")
     _check(out[[0, 2]], want)
+
+
+@pytest.fixture(scope="module")
+def small_pool(dev):
+    E, H, I = 1000, 1024, 512
+    return (synth.projection(E, I, H, seed=5, device=dev), synth.projection(E, I, H, seed=6, device=dev),
+            synth.projection(E, H, I, seed=7, device=dev))
+
+
+@pytest.mark.parametrize("T, E, xdt, biased", [(2, 384, torch.float16, False), (8, 384, torch.float16, False),
+                                              (16, 100, torch.bfloat16, True), (32, 1000, torch.float16, True),
+                                              (33, 384, torch.float16, False), (64, 300, torch.bfloat16, True)])
+def test_tiles_layer_equals_router_then_tiles(dev, small_pool, T, E, xdt, biased):
+    """keep_moe_tiles_layer: the router's five outputs and the tiles' result, bit for bit, on both sides of
+    the fused-prologue limit (32 tokens), every router lane width, with and without biases and admission."""
+    from keep_amd.router import resident_bias
+    H, I, k = 1024, 512, 6
+    pool = tuple((p.codes[:E], p.scales[:E]) for p in small_pool)
+    x = synth.rht_activations(T, H, seed=60 + T, device=dev).to(xdt)
+    z = synth.router_logits(T, E, seed=61 + T, device=dev)
+    kw = {}
+    if biased:
+        mask = torch.from_numpy(synth.resident_mask(E, frac=0.5, seed=62)).to(dev)
+        kw = dict(bias_served=resident_bias(mask), bias_demand=None, tau=0.3)
+    r = keep_amd.router_dual_topk(z, k, **kw)
+    want = keep_amd.moe_decode(x, r.idx, r.weight, *pool)
+    out, r2 = keep_amd.moe_tiles_layer(x, z, *pool, k=k, **kw)
+    for name in ("idx", "weight", "want", "want_score", "admit"):
+        assert torch.equal(getattr(r2, name), getattr(r, name)), f"router output {name} differs"
+    assert torch.equal(out, want), "layer output differs from the router followed by keep_moe_tiles"
+
+
+def test_tiles_layer_slot_map_and_module(dev, small_pool):
+    """A pool of 256 rows under a 1000-expert router (slot map), and RoutedVQMoE's few-token call."""
+    E, S, H, I, k, T = 1000, 256, 1024, 512, 6, 8
+    pool = tuple((p.codes[:S], p.scales[:S]) for p in small_pool)
+    rng = np.random.default_rng(70)
+    sm_np = np.full(E, -1, dtype=np.int32)
+    sm_np[rng.choice(E, S, replace=False)] = np.arange(S, dtype=np.int32)
+    sm = torch.from_numpy(sm_np).to(dev)
+    from keep_amd.router import resident_bias
+    bias = resident_bias(sm >= 0)
+    x = synth.rht_activations(T, H, seed=71, device=dev)
+    z = synth.router_logits(T, E, seed=72, device=dev)
+    r = keep_amd.router_dual_topk(z, k, bias_served=bias, slot_map=sm, num_slots=S)
+    want = keep_amd.moe_decode(x, r.idx, r.weight, *pool)
+    out, r2 = keep_amd.moe_tiles_layer(x, z, *pool, k=k, bias_served=bias, slot_map=sm)
+    assert torch.equal(r2.idx, r.idx) and torch.equal(r2.weight, r.weight)
+    assert torch.equal(out, want)
+    lin = lambda p, i, o: keep_amd.QuantizedVQSwitchLinear(  # noqa: E731
+        input_dims=i, output_dims=o, num_experts=S, codes=p.codes[:S], scales=p.scales[:S], group_size=i,
+        code_bits=16)
+    g, u, d = small_pool
+    moe = keep_amd.RoutedVQMoE(keep_amd.QuantizedVQSwitchGLU(gate_proj=lin(g, H, I), up_proj=lin(u, H, I),
+                                                             down_proj=lin(d, I, H)),
+                               top_k=k, bias_served=bias, slot_map=sm)
+    out_m, r_m = moe(x, z)
+    assert torch.equal(r_m.idx, r.idx) and torch.equal(out_m, want)
