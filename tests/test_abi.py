@@ -85,3 +85,27 @@ def test_other_entry_points_validate():
                                0.0, 16, 16, 1, None) == -1
     assert b"group_size_h" in lib.keep_last_error()
     assert lib.keep_e8p_decode(16, 10, 16, 16, 1, 3, 1, 16, None) == -1
+
+
+def _tiles_layer(**over):
+    args = dict(logits=16, bias_s=None, bias_d=None, func=0, renorm=1, route_scale=1.0, tau=0.3, slot_map=None,
+                num_slots=0, E=384, k=6, x=16, x_dtype=1, T=8, H=4096, I=2048, gc=16, gs=16, uc=16, us=16, dc=16,
+                ds=16, sdt=1, gsh=4096, gsi=2048, prep=16, limit=0.0, idx=16, w=16, want=None, want_score=None,
+                admit=None, h_work=16, ws=256, ws_bytes=1 << 40, out=16, out_dtype=1, stream=None)
+    args.update(over)
+    return _lib.load().keep_moe_tiles_layer(*args.values())
+
+
+@pytest.mark.parametrize("over, msg", [
+    (dict(E=2000), "num_experts must be"),
+    (dict(func=5), "score_func"),
+    (dict(slot_map=16, num_slots=0), "num_slots"),
+    (dict(k=17), "shape not served"),
+    (dict(T=300), "shape not served"),
+    (dict(x_dtype=3), "fp16 or bf16"),
+    (dict(logits=None), "null pointer"),
+    (dict(ws_bytes=1024), "workspace needs"),
+])
+def test_tiles_layer_argument_validation_before_launch(over, msg):
+    assert _tiles_layer(**over) == _lib.KEEP_EINVAL
+    assert msg in _lib.load().keep_last_error().decode()
