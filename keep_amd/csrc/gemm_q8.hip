@@ -39,7 +39,8 @@
 // item streams its K blocks with D blocks' code loads and A rows in flight in
 // registers (every load unconditional and clamped at the end), the A rows of
 // the next block staged into a second LDS buffer while the current one feeds
-// the MFMAs; each k-step's B operands are decoded during the one before.
+// the MFMAs; each k-step's image lookups are issued two k-steps ahead of its
+// MFMAs and converted to fp16 one k-step ahead.
 // Work items are spread XCD-aware (see the item loop).
 #include <cstdlib>
 #include <type_traits>
@@ -83,14 +84,6 @@ __device__ __forceinline__ h8 gq_f16_of_bytes(uint2 b) {
 // Natural-order bytes of a packed-nibble-order pair (dims 0, 2, 4, 6 | 1, 3, 5, 7).
 __device__ __forceinline__ uint2 gq_natural(uint2 v) {
   return make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x05010400u), __builtin_amdgcn_perm(v.y, v.x, 0x07030602u));
-}
-
-// E8P codeword (the low or high half of a code dword) -> its 8 bytes q + 128, from the LDS image.
-__device__ __forceinline__ uint2 gq_lookup(const char* img, const Q8Keys& k, uint32_t w, bool hi) {
-  const uint32_t a1 = __builtin_amdgcn_perm(w, k.base1, hi ? k.s1hi : k.s1lo);
-  const uint32_t a2 = __builtin_amdgcn_perm(w, k.base2, hi ? k.s2hi : k.s2lo);
-  const uint2 x1 = *(const uint2*)(img + a1), x2 = *(const uint2*)(img + a2);
-  return make_uint2(x1.x ^ x2.x, x1.y ^ x2.y);
 }
 
 // ------------------------------------------------------------------ row scales
@@ -208,17 +201,25 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
   // write 128 consecutive LDS bytes per store: no bank conflicts)
   const int sr = tid >> 3, sp = tid & 7;
   const uint32_t sbytes = a.sdt == KEEP_F32 ? 4u : 2u;
-  // B operand of k-step s of one n-tile from this lane's 8 codewords of the K block
-  auto bop = [&](const uint4& q, int s) -> h8 {
+  // B operand of k-step s of one n-tile from this lane's 8 codewords of the K
+  // block, in two halves: the LDS image lookups (look), then the bytes -> fp16
+  // (cvt), so that a k-step's lookups are issued two k-steps before its MFMAs.
+  auto look = [&](const uint4& q, int s) -> uint4 {
     if constexpr (RES) {  // code bytes: codeword s is byte s of q.x / q.y
       const uint32_t w = s < 4 ? q.x : q.y;
       const uint32_t byte = (w >> (8 * (s & 3))) & 0xffu;
-      return gq_f16_of_bytes(*(const uint2*)(img + byte * 128u + (uint32_t)(lane & 15) * 8u));
+      const uint2 x = *(const uint2*)(img + byte * 128u + (uint32_t)(lane & 15) * 8u);
+      return make_uint4(x.x, x.y, 0u, 0u);
     } else {
       const uint32_t w = s < 2 ? q.x : (s < 4 ? q.y : (s < 6 ? q.z : q.w));
-      return gq_f16_of_bytes(gq_lookup(img, lk, w, (s & 1) != 0));
+      const bool hi = (s & 1) != 0;
+      const uint32_t a1 = __builtin_amdgcn_perm(w, lk.base1, hi ? lk.s1hi : lk.s1lo);
+      const uint32_t a2 = __builtin_amdgcn_perm(w, lk.base2, hi ? lk.s2hi : lk.s2lo);
+      const uint2 x1 = *(const uint2*)(img + a1), x2 = *(const uint2*)(img + a2);
+      return make_uint4(x1.x, x1.y, x2.x, x2.y);
     }
   };
+  auto cvt = [&](const uint4& r) -> h8 { return gq_f16_of_bytes(make_uint2(r.x ^ r.z, r.y ^ r.w)); };
 
   // XCD-aware order: item w = column block x tiles + tile, each XCD running a
   // contiguous range of w, so the tiles of an expert at one column block (its
@@ -361,12 +362,18 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
       }
     };
     // NT live m-tiles. Unit u stages the A rows of block u + 1, runs the MFMAs
-    // of block u k-step by k-step, decoding each k-step's B operands during the
-    // one before (the last k-step decodes block u + 1's first), and issues the
-    // loads of block u + D.
+    // of block u k-step by k-step and issues the loads of block u + D. During
+    // k-step s it looks up the image for k-step s + 2 and converts the
+    // lookups of k-step s + 1 (issued one k-step earlier), so no lookup is
+    // waited on right after its issue; the last two k-steps look up block
+    // u + 1's first two.
     h8 Bc[NTW];
+    uint4 Lc[NTW];
 #pragma unroll
-    for (int jn = 0; jn < NTW; ++jn) Bc[jn] = bop(bb[0].q[jn], 0);
+    for (int jn = 0; jn < NTW; ++jn) {
+      Bc[jn] = cvt(look(bb[0].q[jn], 0));
+      Lc[jn] = look(bb[0].q[jn], 1);
+    }
     auto run = [&](auto nt_c) {
       constexpr int NT = decltype(nt_c)::value;
       auto unit = [&](int u, Buf& b, const Buf& bn) {
@@ -378,15 +385,22 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
             h8 A[NT];
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) A[mt] = *(const h8*)(abase + mt * 32 * GQ_ROW + 16 * s);
+            uint4 Ln[NTW];
             h8 Bn[NTW];
 #pragma unroll
-            for (int jn = 0; jn < NTW; ++jn) Bn[jn] = s < 7 ? bop(b.q[jn], s + 1) : bop(bn.q[jn], 0);
+            for (int jn = 0; jn < NTW; ++jn) {
+              Ln[jn] = s < 6 ? look(b.q[jn], s + 2) : look(bn.q[jn], s - 6);
+              Bn[jn] = cvt(Lc[jn]);
+            }
 #pragma unroll
             for (int jn = 0; jn < NTW; ++jn)
 #pragma unroll
               for (int mt = 0; mt < NT; ++mt) acc[mt][jn] = mfma32_f16(A[mt], Bc[jn], acc[mt][jn]);
 #pragma unroll
-            for (int jn = 0; jn < NTW; ++jn) Bc[jn] = Bn[jn];
+            for (int jn = 0; jn < NTW; ++jn) {
+              Bc[jn] = Bn[jn];
+              Lc[jn] = Ln[jn];
+            }
           }
           if constexpr (GROUPED) {
             if ((u + 1) % a.kpg == 0) fold(u / (int)a.kpg);
