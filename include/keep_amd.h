@@ -403,6 +403,44 @@ int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_rows, const 
                               int64_t I, int64_t H, int64_t group_size, float swiglu_limit, void* workspace,
                               int64_t workspace_bytes, void* h_out, void* stream);
 
+/* The nested 3-bit tier fused into the sorted-route prefill: as
+ * keep_vq_grouped_swiglu_q8 (per-row base scales, group_size = H), and on the
+ * tiles of an expert e with a residual row r = hot_row[e] (0 <= r < hot_rows;
+ * -1: none) gate and up each add that row's 8-bit E8 residual,
+ * R[r, n] . x * res_scale[r, n] (codes uint8 [hot_rows][I][H / 8], one scale per
+ * row, res_table the packed 8-bit E8 table, uint32[256]), before the SwiGLU. A
+ * hot_row entry outside [-1, hot_rows) makes that expert's h rows NaN. Replaces
+ * the base GEMMs, the residual GEMMs (keep_vq_grouped_gemm_q8 with
+ * code_bits = 8) and the activation of the tiered prefill, the serving
+ * step's base-plus-residual (scripts/v41_build/omlx_lattice.py:172-186,
+ * 358-370). */
+int keep_vq_grouped_swiglu_nested_q8(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
+                                     const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
+                                     const void* up_scales, int scale_dtype, const void* prepared,
+                                     const uint8_t* gate_res_codes, const void* gate_res_scales,
+                                     const uint8_t* up_res_codes, const void* up_res_scales, int res_scale_dtype,
+                                     const int32_t* hot_row, int64_t hot_rows, const uint32_t* res_table,
+                                     const int32_t* tile_expert, const int32_t* tile_offset,
+                                     const int32_t* tile_count, int64_t n_tiles, int64_t routes,
+                                     int64_t num_experts, int64_t I, int64_t H, float swiglu_limit, void* workspace,
+                                     int64_t workspace_bytes, void* h_out, void* stream);
+
+/* One projection with the nested tier fused in (the down projection of the
+ * tiered prefill): keep_vq_grouped_gemm_q8 on E8P codes with per-row scales
+ * (group_size = K), plus, on the tiles of a hot expert, its residual row's
+ * 8-bit E8 codes (uint8 [hot_rows][N][K / 8], one scale per row), added before
+ * the store. hot_row and res_table as keep_vq_grouped_swiglu_nested_q8.
+ * Replaces the tiered prefill's base GEMM plus residual GEMM of one projection
+ * (scripts/v41_build/omlx_lattice.py:172-186). */
+int keep_vq_grouped_gemm_nested_q8(const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs,
+                                   const int32_t* out_index, const uint16_t* codes, const void* scales,
+                                   int scale_dtype, const void* prepared, const uint8_t* res_codes,
+                                   const void* res_scales, int res_scale_dtype, const int32_t* hot_row,
+                                   int64_t hot_rows, const uint32_t* res_table, const int32_t* tile_expert,
+                                   const int32_t* tile_offset, const int32_t* tile_count, int64_t n_tiles,
+                                   int64_t routes, int64_t num_experts, int64_t N, int64_t K, void* workspace,
+                                   int64_t workspace_bytes, void* out, int out_dtype, void* stream);
+
 /* Weighted combine of per-route outputs: out[t, :] = sum over j < k, in
  * order, of w[t, j] * y[t k + j, :] with fp32 multiply-adds (a NaN route row
  * stays NaN whatever its weight). y fp32 [T k, H], w fp32 [T, k]. Replaces the

@@ -55,6 +55,12 @@ _SIGS = {
                                 c_int64, c_int64, c_int64, c_int64, _P, c_int64, _P, c_int, _P],
     "keep_vq_grouped_swiglu_q8": [_P, c_int, c_int64, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, c_int64, c_int64,
                                   c_int64, c_int64, c_int64, c_int64, c_float, _P, c_int64, _P, _P],
+    "keep_vq_grouped_swiglu_nested_q8": [_P, c_int, c_int64, _P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, c_int,
+                                         _P, c_int64, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                         c_float, _P, c_int64, _P, _P],
+    "keep_vq_grouped_gemm_nested_q8": [_P, c_int, c_int64, _P, _P, _P, _P, c_int, _P, _P, _P, c_int, _P, c_int64, _P,
+                                       _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, c_int64, _P,
+                                       c_int, _P],
     "keep_moe_tiles_supported": [c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64],
     "keep_moe_gateup": [_P, c_int, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, _P, _P, _P, _P, c_int,
                         c_int64, _P, _P, c_float, _P, _P],

@@ -151,44 +151,65 @@ struct GQArgs {
   void* out;
   int odt;
   int64_t ncb, total, per_xcd;  // column blocks, work items, items per XCD
+  // the fused residual (HOT)
+  const uint8_t *rc0, *rc1;  // residual codes [hot_rows][N][K / 8] (gate/up: gate, up)
+  const void *rs0, *rs1;     // residual scales [hot_rows][N], one per row
+  int rsdt;
+  const int32_t* hot;        // residual row of each expert (-1: none)
+  int64_t hot_rows;
+  const uint32_t* t8;        // the packed 8-bit E8 table (uint32[256])
 };
 
 // RES: the nested tier's 8-bit E8 residual instead of E8P base codes (one code
 // byte per codeword, one 8-byte lookup); the result is added to the fp32
-// output (the base projection's). XT: the A rows' element type.
+// output (the base projection's). HOT: E8P base codes and, on the tiles of an
+// expert with a residual row (hot[e] in [0, hot_rows)), that row's 8-bit E8
+// residual codes, decoded from a second LDS image and multiplied by the same A
+// operands into a second accumulator; base and residual are scaled and summed
+// before the epilogue (the SwiGLU of gate/up), as the nested tier's serving
+// step adds them (omlx_lattice.py:172-186). A hot tile runs as one pass per 32
+// routes (its second m-tile's accumulators hold the residual); a hot row out of
+// range other than -1 makes the tile's rows NaN. XT: the A rows' element type.
 // NTW: 32-column n-tiles per wave (2: items of 512 columns; 1: of 256, for
 // problems with too few items to spread over the CUs).
-template <bool GATEUP, bool GROUPED, typename XT, bool RES = false, int NTW = 2>
+template <bool GATEUP, bool GROUPED, typename XT, bool RES = false, int NTW = 2, bool HOT = false>
 __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
+  static_assert(!(HOT && (RES || GROUPED)), "the fused residual takes E8P base codes and per-row scales");
   constexpr int D = 2;                         // K blocks in flight
   constexpr int NCOL = GQ_WAVES * 32 * NTW;    // output columns per work item
   constexpr int XV = sizeof(XT) == 4 ? 4 : 2;           // 16-byte A loads per thread and K block
   __shared__ uint4 tqs[TQR_BYTES / 16];
+  __shared__ uint2 t8s[HOT ? T8R_BYTES / 8 : 1];  // HOT: the residual image
   __shared__ __attribute__((aligned(16))) uint8_t ash[2][GQ_M * GQ_ROW];
   __shared__ float s_ok[GQ_M];  // 1 / r of the row (NaN: no valid row)
   __shared__ int32_t s_orow[GQ_M];
   const char* img = (const char*)tqs;
+  const char* img8 = (const char*)t8s;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, h = lane >> 5;
   const Q8Keys lk = q8_keys(lane);
   const uint32_t tq_bad = GATEUP ? ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0] : 0u;
-  {  // the LDS image: entry tid / 2, copies 8 (tid & 1) .. + 7
+  {  // the LDS image(s): entry tid / 2, copies 8 (tid & 1) .. + 7
     const int e = tid >> 1;
-    if constexpr (RES) {  // row e: sixteen copies of the 8 bytes 2 (nibble d - 8) + 128, d = 0..7
-      const uint32_t p = ((const uint32_t*)a.tq)[e];
+    // residual row e: sixteen copies of the 8 bytes 2 (nibble d - 8) + 128, d = 0..7
+    auto e8_row = [&](uint32_t p, char* base) {
       uint32_t b[2] = {0u, 0u};
 #pragma unroll
       for (int d = 0; d < 8; ++d) b[d >> 2] |= ((uint32_t)(2 * ((int)((p >> (4 * d)) & 15u) - 8) + 128) & 0xffu) << (8 * (d & 3));
-      uint2* row = (uint2*)(img + e * 128 + (tid & 1) * 64);
+      uint2* row = (uint2*)(base + e * 128 + (tid & 1) * 64);
 #pragma unroll
       for (int i = 0; i < 8; ++i) row[i] = make_uint2(b[0], b[1]);
+    };
+    if constexpr (RES) {
+      e8_row(((const uint32_t*)a.tq)[e], (char*)tqs);
     } else {  // row e: sixteen copies of (T'[e], M[e]), T' = T ^ 0x80 per byte, natural dim order
       const uint2 t = gq_natural(((const uint2*)a.tq)[e]), m = gq_natural(((const uint2*)a.tq)[256 + e]);
       const uint4 v = make_uint4(t.x ^ 0x80808080u, t.y ^ 0x80808080u, m.x, m.y);
       uint4* row = tqs + e * 16 + (tid & 1) * 8;
 #pragma unroll
       for (int i = 0; i < 8; ++i) row[i] = v;
+      if constexpr (HOT) e8_row(a.t8[e], (char*)t8s);
     }
   }
   __syncthreads();
@@ -201,6 +222,7 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
   // write 128 consecutive LDS bytes per store: no bank conflicts)
   const int sr = tid >> 3, sp = tid & 7;
   const uint32_t sbytes = a.sdt == KEEP_F32 ? 4u : 2u;
+  const uint32_t rbytes = a.rsdt == KEEP_F32 ? 4u : 2u;
   // B operand of k-step s of one n-tile from this lane's 8 codewords of the K
   // block, in two halves: the LDS image lookups (look), then the bytes -> fp16
   // (cvt), so that a k-step's lookups are issued two k-steps before its MFMAs.
@@ -220,6 +242,12 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
     }
   };
   auto cvt = [&](const uint4& r) -> h8 { return gq_f16_of_bytes(make_uint2(r.x ^ r.z, r.y ^ r.w)); };
+  // HOT: the residual codeword s of this lane's 8 code bytes -> its 8 bytes q + 128
+  auto look_r = [&](const uint2& r, int s) -> uint2 {
+    const uint32_t w = s < 4 ? r.x : r.y;
+    const uint32_t byte = (w >> (8 * (s & 3))) & 0xffu;
+    return *(const uint2*)(img8 + byte * 128u + (uint32_t)(lane & 15) * 8u);
+  };
 
   // XCD-aware order: item w = column block x tiles + tile, each XCD running a
   // contiguous range of w, so the tiles of an expert at one column block (its
@@ -234,30 +262,48 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
     if (cnt_raw <= 0 || off < 0 || off + cnt > a.routes) continue;  // nothing can be written safely
     const int64_t e = a.te[tile];
     if (RES && e < 0) continue;  // routes off the residual tier (row -1): nothing to add
-    const bool bad = e < 0 || e >= a.E || cnt_raw > GQ_M;  // rows written as NaN
+    bool bad = e < 0 || e >= a.E || cnt_raw > GQ_M;  // rows written as NaN
+    int64_t hr = -1;  // HOT: the tile's residual row
+    if constexpr (HOT) {
+      if (!bad) {
+        const int32_t r = a.hot[e];
+        if (r >= 0 && r < a.hot_rows) hr = r;
+        else if (r != -1) bad = true;
+      }
+    }
     const bool two = cnt > 32;
 
-    // this lane's column of each n-tile: a code row and its scale row
-    int64_t n[NTW], crow[NTW];
+    // this lane's column of each n-tile: a code row and its scale row (HOT: and
+    // its residual code row)
+    int64_t n[NTW], crow[NTW], rrow[NTW];
     bool nv[NTW];
     const uint8_t* cp[NTW];
+    const uint8_t* rp[NTW];
     const void* sbase[NTW];
+    const void* rsbase[NTW];
 #pragma unroll
     for (int jn = 0; jn < NTW; ++jn) {
       const uint16_t* cbase;
+      const uint8_t* rbase;
       if constexpr (GATEUP) {
         n[jn] = cb * (NCOL / 2) + (wv * NTW + jn) * 16 + (c & 15);
         cbase = c < 16 ? a.c0 : a.c1;
         sbase[jn] = c < 16 ? a.s0 : a.s1;
+        rbase = c < 16 ? a.rc0 : a.rc1;
+        rsbase[jn] = c < 16 ? a.rs0 : a.rs1;
       } else {
         n[jn] = cb * NCOL + (wv * NTW + jn) * 32 + c;
         cbase = a.c0;
         sbase[jn] = a.s0;
+        rbase = a.rc0;
+        rsbase[jn] = a.rs0;
       }
       nv[jn] = n[jn] < a.N;
       crow[jn] = (bad || !nv[jn]) ? 0 : e * a.N + n[jn];
       // E8P: 16 bytes per K block (codewords 8 h ..); residual: 8 bytes (one byte per codeword)
       cp[jn] = RES ? (const uint8_t*)cbase + crow[jn] * C + 8 * h : (const uint8_t*)(cbase + crow[jn] * C + 8 * h);
+      rrow[jn] = (hr < 0 || !nv[jn]) ? 0 : hr * a.N + n[jn];
+      rp[jn] = HOT ? rbase + rrow[jn] * C + 8 * h : nullptr;
     }
     // A staging row of this thread
     int64_t xs = off + min(sr, cnt - 1);
@@ -278,8 +324,10 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
 
     struct Buf {
       uint4 q[NTW], ax[XV];  // codes of block u, A row elements of block u + 1
+      uint2 r[NTW];          // HOT: residual codes of block u
     };
-    auto issue = [&](int u, Buf& b) {
+    auto issue = [&](int u, Buf& b, auto ht_c) {
+      constexpr bool HT = decltype(ht_c)::value;
       const int kq = min(u, nkb - 1), ka = min(u + 1, nkb - 1);
 #pragma unroll
       for (int jn = 0; jn < NTW; ++jn) {
@@ -289,6 +337,7 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
         } else {
           b.q[jn] = ldg16_q(cp[jn] + kq * 32);
         }
+        if constexpr (HT) b.r[jn] = ldg8_q(rp[jn] + kq * 16);
       }
 #pragma unroll
       for (int i = 0; i < XV; ++i) b.ax[i] = ldg16_q(ap + ((int64_t)ka * GQ_KB + 64 * (i / (XV / 2))) * sizeof(XT) +
@@ -322,28 +371,9 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
       *(uint4*)d = o[0];
       *(uint4*)(d + 128) = o[1];
     };
-    {
-      uint4 ax0[XV];
-#pragma unroll
-      for (int i = 0; i < XV; ++i) ax0[i] = ldg16_q(ap + 64 * (i / (XV / 2)) * sizeof(XT) + 16 * (i % (XV / 2)));
-      wait_vm_q<0>();
-      stage(0, ax0);
-    }
-    Buf bb[D];
-#pragma unroll
-    for (int i = 0; i < D; ++i) issue(i, bb[i]);
-    __syncthreads();  // A block 0, s_ok, s_orow; the previous item's readers are done
 
     f32x16 acc[2][NTW];
     float accf[2][NTW][GROUPED ? 16 : 1];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int jn = 0; jn < NTW; ++jn) {
-        acc[mt][jn] = f32x16{};
-#pragma unroll
-        for (int v = 0; v < (GROUPED ? 16 : 1); ++v) accf[mt][jn][v] = 0.f;
-      }
     auto fold = [&](int g) {  // scale group g ends: add its partial sums
       if constexpr (GROUPED) {
 #pragma unroll
@@ -361,97 +391,159 @@ __global__ __launch_bounds__(GQ_THREADS) void k_gemm_e8(GQArgs a) {
         }
       }
     };
-    // NT live m-tiles. Unit u stages the A rows of block u + 1, runs the MFMAs
-    // of block u k-step by k-step and issues the loads of block u + D. During
-    // k-step s it looks up the image for k-step s + 2 and converts the
-    // lookups of k-step s + 1 (issued one k-step earlier), so no lookup is
-    // waited on right after its issue; the last two k-steps look up block
-    // u + 1's first two.
-    h8 Bc[NTW];
-    uint4 Lc[NTW];
-#pragma unroll
-    for (int jn = 0; jn < NTW; ++jn) {
-      Bc[jn] = cvt(look(bb[0].q[jn], 0));
-      Lc[jn] = look(bb[0].q[jn], 1);
-    }
-    auto run = [&](auto nt_c) {
+    // One pass over K. NT live m-tiles (from m-tile msel when NT = 1); HT: the
+    // residual into acc[1] beside the base of m-tile msel into acc[0]. The
+    // pass stages block 0's A rows and issues D blocks' loads, then unit u
+    // stages the A rows of block u + 1, runs the MFMAs of block u k-step by
+    // k-step and issues the loads of block u + D. During k-step s it looks up
+    // the image for k-step s + 2 and converts the lookups of k-step s + 1
+    // (issued one k-step earlier), so no lookup is waited on right after its
+    // issue; the last two k-steps look up block u + 1's first two.
+    auto pass = [&](auto nt_c, auto ht_c, int msel) {
       constexpr int NT = decltype(nt_c)::value;
+      constexpr bool HT = decltype(ht_c)::value;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int jn = 0; jn < NTW; ++jn) {
+          acc[mt][jn] = f32x16{};
+#pragma unroll
+          for (int v = 0; v < (GROUPED ? 16 : 1); ++v) accf[mt][jn][v] = 0.f;
+        }
+      {
+        uint4 ax0[XV];
+#pragma unroll
+        for (int i = 0; i < XV; ++i) ax0[i] = ldg16_q(ap + 64 * (i / (XV / 2)) * sizeof(XT) + 16 * (i % (XV / 2)));
+        wait_vm_q<0>();
+        stage(0, ax0);
+      }
+      Buf bb[D];
+#pragma unroll
+      for (int i = 0; i < D; ++i) issue(i, bb[i], ht_c);
+      __syncthreads();  // A block 0, s_ok, s_orow; the previous pass's readers are done
+
+      h8 Bc[NTW], Rc[NTW];
+      uint4 Lc[NTW];
+      uint2 Lr[NTW];
+#pragma unroll
+      for (int jn = 0; jn < NTW; ++jn) {
+        Bc[jn] = cvt(look(bb[0].q[jn], 0));
+        Lc[jn] = look(bb[0].q[jn], 1);
+        if constexpr (HT) {
+          Rc[jn] = gq_f16_of_bytes(look_r(bb[0].r[jn], 0));
+          Lr[jn] = look_r(bb[0].r[jn], 1);
+        }
+      }
       auto unit = [&](int u, Buf& b, const Buf& bn) {
         stage((u + 1) & 1, b.ax);
         if (u < nkb) {
-          const uint8_t* abase = &ash[u & 1][c * GQ_ROW + 128 * h];
+          const uint8_t* abase = &ash[u & 1][(c + 32 * msel) * GQ_ROW + 128 * h];
 #pragma unroll
           for (int s = 0; s < 8; ++s) {
             h8 A[NT];
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) A[mt] = *(const h8*)(abase + mt * 32 * GQ_ROW + 16 * s);
             uint4 Ln[NTW];
-            h8 Bn[NTW];
+            uint2 Lrn[NTW];
+            h8 Bn[NTW], Rn[NTW];
 #pragma unroll
             for (int jn = 0; jn < NTW; ++jn) {
               Ln[jn] = s < 6 ? look(b.q[jn], s + 2) : look(bn.q[jn], s - 6);
               Bn[jn] = cvt(Lc[jn]);
+              if constexpr (HT) {
+                Lrn[jn] = s < 6 ? look_r(b.r[jn], s + 2) : look_r(bn.r[jn], s - 6);
+                Rn[jn] = gq_f16_of_bytes(Lr[jn]);
+              }
             }
 #pragma unroll
-            for (int jn = 0; jn < NTW; ++jn)
+            for (int jn = 0; jn < NTW; ++jn) {
 #pragma unroll
               for (int mt = 0; mt < NT; ++mt) acc[mt][jn] = mfma32_f16(A[mt], Bc[jn], acc[mt][jn]);
+              if constexpr (HT) acc[1][jn] = mfma32_f16(A[0], Rc[jn], acc[1][jn]);
+            }
 #pragma unroll
             for (int jn = 0; jn < NTW; ++jn) {
               Bc[jn] = Bn[jn];
               Lc[jn] = Ln[jn];
+              if constexpr (HT) {
+                Rc[jn] = Rn[jn];
+                Lr[jn] = Lrn[jn];
+              }
             }
           }
           if constexpr (GROUPED) {
             if ((u + 1) % a.kpg == 0) fold(u / (int)a.kpg);
           }
         }
-        issue(u + D, b);
+        issue(u + D, b, ht_c);
         __syncthreads();
       };
       for (int u = 0; u < nkb; u += D) {  // every call unconditional: blocks past the end only reload
 #pragma unroll
         for (int i = 0; i < D; ++i) unit(u + i, bb[i], bb[(i + 1) % D]);
       }
+      wait_vm_q<0>();
     };
-    if (two) run(std::integral_constant<int, 2>{});
-    else run(std::integral_constant<int, 1>{});
-    wait_vm_q<0>();
 
-    // epilogue: D row m = 8 (v / 4) + 4 h + v % 4 of m-tile mt, column c of n-tile jn
+    // epilogue of a pass: D row m = 8 (v / 4) + 4 h + v % 4 of m-tile mt (HT:
+    // of m-tile msel, base in acc[0] and residual in acc[1]), column c of n-tile jn
+    auto emit = [&](auto ht_c, int msel) {
+      constexpr bool HT = decltype(ht_c)::value;
 #pragma unroll
-    for (int jn = 0; jn < NTW; ++jn) {
-      float sc = 0.25f;
-      if constexpr (!GROUPED) {
-        sc = nv[jn] && !bad ? 0.25f * scale_cvt(ldg4_q((const char*)sbase[jn] + ((crow[jn] * sbytes) & ~(int64_t)3)),
-                                                a.sdt, (uint32_t)crow[jn])
-                            : 0.f;
-      }
+      for (int jn = 0; jn < NTW; ++jn) {
+        float sc = 0.25f, scr = 0.f;
+        if constexpr (!GROUPED) {
+          sc = nv[jn] && !bad ? 0.25f * scale_cvt(ldg4_q((const char*)sbase[jn] + ((crow[jn] * sbytes) & ~(int64_t)3)),
+                                                  a.sdt, (uint32_t)crow[jn])
+                              : 0.f;
+        }
+        if constexpr (HT) {
+          scr = nv[jn] && !bad ? 0.25f * scale_cvt(ldg4_q((const char*)rsbase[jn] + ((rrow[jn] * rbytes) & ~(int64_t)3)),
+                                                   a.rsdt, (uint32_t)rrow[jn])
+                               : 0.f;
+        }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < (HT ? 1 : 2); ++mt) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int m = mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-          float val = (GROUPED ? accf[mt][jn][v] : acc[mt][jn][v]) * sc * s_ok[m];
-          if (bad) val = __builtin_nanf("");
-          if constexpr (GATEUP) {
-            const float other = __shfl_xor(val, 16, 64);
-            float hv = c < 16 ? silu_mul(val, other, a.limit) : silu_mul(other, val, a.limit);
-            if (tq_bad) hv = __builtin_nanf("");
-            const bool mine = (c < 16) == ((v & 1) == 0);
-            if (mine && m < cnt && nv[jn])
-              ((uint16_t*)a.out)[(off + m) * a.N + n[jn]] = from_float<bf16s>(hv).bits;
-          } else {
-            if (m < cnt && nv[jn]) {
-              const int64_t o = (int64_t)s_orow[m] * a.N + n[jn];
-              if constexpr (RES) ((float*)a.out)[o] += val;
-              else if (a.odt == KEEP_F32) ((float*)a.out)[o] = val;
-              else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[o] = from_float<bf16s>(val).bits;
-              else ((_Float16*)a.out)[o] = (_Float16)val;
+          for (int v = 0; v < 16; ++v) {
+            const int m = (HT ? msel : mt) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            float val;
+            if constexpr (HT) val = fmaf(acc[0][jn][v], sc, acc[1][jn][v] * scr) * s_ok[m];
+            else val = (GROUPED ? accf[mt][jn][v] : acc[mt][jn][v]) * sc * s_ok[m];
+            if (bad) val = __builtin_nanf("");
+            if constexpr (GATEUP) {
+              const float other = __shfl_xor(val, 16, 64);
+              float hv = c < 16 ? silu_mul(val, other, a.limit) : silu_mul(other, val, a.limit);
+              if (tq_bad) hv = __builtin_nanf("");
+              const bool mine = (c < 16) == ((v & 1) == 0);
+              if (mine && m < cnt && nv[jn])
+                ((uint16_t*)a.out)[(off + m) * a.N + n[jn]] = from_float<bf16s>(hv).bits;
+            } else {
+              if (m < cnt && nv[jn]) {
+                const int64_t o = (int64_t)s_orow[m] * a.N + n[jn];
+                if constexpr (RES) ((float*)a.out)[o] += val;
+                else if (a.odt == KEEP_F32) ((float*)a.out)[o] = val;
+                else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[o] = from_float<bf16s>(val).bits;
+                else ((_Float16*)a.out)[o] = (_Float16)val;
+              }
             }
           }
         }
       }
+    };
+
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using Cold = std::false_type;
+    if (HOT && hr >= 0) {
+      for (int ms = 0; ms < (two ? 2 : 1); ++ms) {
+        pass(I1{}, std::integral_constant<bool, HOT>{}, ms);
+        emit(std::integral_constant<bool, HOT>{}, ms);
+      }
+    } else {
+      if (two) pass(I2{}, Cold{}, 0);
+      else pass(I1{}, Cold{}, 0);
+      emit(Cold{}, 0);
     }
   }
 }
@@ -505,20 +597,22 @@ const float2* gq_rowscale(const void* x, int x_dtype, int64_t rows, int64_t K, v
   return rs;
 }
 
-template <bool GATEUP, bool RES, typename XT, int NTW>
+template <bool GATEUP, bool RES, typename XT, int NTW, bool HOT>
 void gq_launch_x(const GQArgs& a, dim3 grid, hipStream_t s) {
-  if (a.G > 1) hipLaunchKernelGGL((k_gemm_e8<GATEUP, true, XT, RES, NTW>), grid, dim3(GQ_THREADS), 0, s, a);
+  if constexpr (HOT) hipLaunchKernelGGL((k_gemm_e8<GATEUP, false, XT, false, NTW, true>), grid, dim3(GQ_THREADS), 0, s, a);
+  else if (a.G > 1) hipLaunchKernelGGL((k_gemm_e8<GATEUP, true, XT, RES, NTW>), grid, dim3(GQ_THREADS), 0, s, a);
   else hipLaunchKernelGGL((k_gemm_e8<GATEUP, false, XT, RES, NTW>), grid, dim3(GQ_THREADS), 0, s, a);
 }
 
-template <bool GATEUP, bool RES, int NTW>
+template <bool GATEUP, bool RES, int NTW, bool HOT = false>
 void gq_launch_t(const GQArgs& a, dim3 grid, hipStream_t s) {
-  if (a.xdt == KEEP_F16) gq_launch_x<GATEUP, RES, _Float16, NTW>(a, grid, s);
-  else if (a.xdt == KEEP_BF16) gq_launch_x<GATEUP, RES, bf16s, NTW>(a, grid, s);
-  else gq_launch_x<GATEUP, RES, float, NTW>(a, grid, s);
+  if (a.xdt == KEEP_F16) gq_launch_x<GATEUP, RES, _Float16, NTW, HOT>(a, grid, s);
+  else if (a.xdt == KEEP_BF16) gq_launch_x<GATEUP, RES, bf16s, NTW, HOT>(a, grid, s);
+  else gq_launch_x<GATEUP, RES, float, NTW, HOT>(a, grid, s);
 }
 
-void gq_launch(GQArgs& a, bool gateup, hipStream_t s, bool res = false) {
+// hot: the fused residual (a.hot, a.rc0 / a.rc1, ... set; per-row scales)
+void gq_launch(GQArgs& a, bool gateup, hipStream_t s, bool res = false, bool hot = false) {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -534,11 +628,13 @@ void gq_launch(GQArgs& a, bool gateup, hipStream_t s, bool res = false) {
   const int64_t per = std::max<int64_t>(1, std::min<int64_t>(a.per_xcd, cus / GQ_XCDS));
   const dim3 grid((unsigned)(per * GQ_XCDS));
   if (wide) {
-    if (res) gq_launch_t<false, true, 2>(a, grid, s);
+    if (hot) gateup ? gq_launch_t<true, false, 2, true>(a, grid, s) : gq_launch_t<false, false, 2, true>(a, grid, s);
+    else if (res) gq_launch_t<false, true, 2>(a, grid, s);
     else if (gateup) gq_launch_t<true, false, 2>(a, grid, s);
     else gq_launch_t<false, false, 2>(a, grid, s);
   } else {
-    if (res) gq_launch_t<false, true, 1>(a, grid, s);
+    if (hot) gateup ? gq_launch_t<true, false, 1, true>(a, grid, s) : gq_launch_t<false, false, 1, true>(a, grid, s);
+    else if (res) gq_launch_t<false, true, 1>(a, grid, s);
     else if (gateup) gq_launch_t<true, false, 1>(a, grid, s);
     else gq_launch_t<false, false, 1>(a, grid, s);
   }
@@ -640,6 +736,94 @@ extern "C" int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_r
   a.out = h_out; a.odt = KEEP_BF16;
   gq_launch(a, true, s);
   return launch_status("keep_vq_grouped_swiglu_q8");
+}
+
+// The nested tier's checks and fields shared by the two fused-residual entry points.
+static int gq_nested_args(GQArgs& a, const uint8_t* rc0, const void* rs0, const uint8_t* rc1, const void* rs1,
+                          int res_scale_dtype, const int32_t* hot_row, int64_t hot_rows,
+                          const uint32_t* res_table) {
+  KEEP_REQUIRE(dtype_ok(res_scale_dtype), "bad dtype enum");
+  KEEP_REQUIRE(hot_rows >= 0, "bad sizes");
+  KEEP_REQUIRE(hot_row && res_table && rc0 && rs0 && rc1 && rs1, "null pointer argument");
+  KEEP_REQUIRE(aligned(rc0, 8) && aligned(rc1, 8), "residual codes must be 8-byte aligned");
+  a.rc0 = rc0; a.rc1 = rc1; a.rs0 = rs0; a.rs1 = rs1; a.rsdt = res_scale_dtype;
+  a.hot = hot_row; a.hot_rows = hot_rows; a.t8 = res_table;
+  return KEEP_OK;
+}
+
+extern "C" int keep_vq_grouped_swiglu_nested_q8(
+    const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs, const uint16_t* gate_codes,
+    const void* gate_scales, const uint16_t* up_codes, const void* up_scales, int scale_dtype, const void* prepared,
+    const uint8_t* gate_res_codes, const void* gate_res_scales, const uint8_t* up_res_codes,
+    const void* up_res_scales, int res_scale_dtype, const int32_t* hot_row, int64_t hot_rows,
+    const uint32_t* res_table, const int32_t* tile_expert, const int32_t* tile_offset, const int32_t* tile_count,
+    int64_t n_tiles, int64_t routes, int64_t num_experts, int64_t I, int64_t H, float swiglu_limit,
+    void* workspace, int64_t workspace_bytes, void* h_out, void* stream) {
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
+  KEEP_REQUIRE(dtype_ok(scale_dtype), "bad dtype enum");
+  KEEP_REQUIRE(gq_shape_ok(H, H), "int8 grouped GEMM needs H a multiple of %d (H=%lld)", GQ_KB, (long long)H);
+  KEEP_REQUIRE(I > 0 && n_tiles >= 0 && routes >= 0 && num_experts > 0 && x_rows >= 0, "bad sizes");
+  if (n_tiles == 0 || routes == 0) return KEEP_OK;
+  KEEP_REQUIRE(x_rows > 0 && x && gate_codes && gate_scales && up_codes && up_scales && prepared && tile_expert &&
+                   tile_offset && tile_count && h_out,
+               "null pointer argument");
+  KEEP_REQUIRE(aligned(x, 16) && aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(prepared, 16),
+               "x, codes and prepared must be 16-byte aligned");
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || (workspace && aligned(workspace, 16) && workspace_bytes >= gq_ws_bytes(x_rows)),
+               "bf16 / fp32 input needs a 16-byte aligned workspace of %lld bytes, got %lld",
+               (long long)gq_ws_bytes(x_rows), (long long)workspace_bytes);
+  GQArgs a{};
+  const int rc = gq_nested_args(a, gate_res_codes, gate_res_scales, up_res_codes, up_res_scales, res_scale_dtype,
+                                hot_row, hot_rows, res_table);
+  if (rc != KEEP_OK) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  a.x = x; a.xdt = x_dtype; a.x_rows = x_rows; a.lhs = lhs;
+  a.rs = gq_rowscale(x, x_dtype, x_rows, H, workspace, s);
+  a.oidx = nullptr; a.c0 = gate_codes; a.c1 = up_codes; a.s0 = gate_scales; a.s1 = up_scales;
+  a.sdt = scale_dtype;
+  a.tq = (const char*)prepared + TQ_OFFSET;
+  a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
+  a.te = tile_expert; a.to = tile_offset; a.tc = tile_count; a.n_tiles = n_tiles; a.routes = routes;
+  a.E = num_experts; a.N = I; a.K = H; a.G = 1; a.kpg = H / GQ_KB; a.limit = swiglu_limit;
+  a.out = h_out; a.odt = KEEP_BF16;
+  gq_launch(a, true, s, false, true);
+  return launch_status("keep_vq_grouped_swiglu_nested_q8");
+}
+
+extern "C" int keep_vq_grouped_gemm_nested_q8(
+    const void* x, int x_dtype, int64_t x_rows, const int32_t* lhs, const int32_t* out_index, const uint16_t* codes,
+    const void* scales, int scale_dtype, const void* prepared, const uint8_t* res_codes, const void* res_scales,
+    int res_scale_dtype, const int32_t* hot_row, int64_t hot_rows, const uint32_t* res_table,
+    const int32_t* tile_expert, const int32_t* tile_offset, const int32_t* tile_count, int64_t n_tiles,
+    int64_t routes, int64_t num_experts, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* out,
+    int out_dtype, void* stream) {
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
+  KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
+  KEEP_REQUIRE(gq_shape_ok(K, K), "int8 grouped GEMM needs K a multiple of %d (K=%lld)", GQ_KB, (long long)K);
+  KEEP_REQUIRE(N > 0 && n_tiles >= 0 && routes >= 0 && num_experts > 0 && x_rows >= 0, "bad sizes");
+  if (n_tiles == 0 || routes == 0) return KEEP_OK;
+  KEEP_REQUIRE(x_rows > 0 && x && codes && scales && prepared && tile_expert && tile_offset && tile_count && out,
+               "null pointer argument");
+  KEEP_REQUIRE(aligned(x, 16) && aligned(codes, 16) && aligned(prepared, 16),
+               "x, codes and prepared must be 16-byte aligned");
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || (workspace && aligned(workspace, 16) && workspace_bytes >= gq_ws_bytes(x_rows)),
+               "bf16 / fp32 input needs a 16-byte aligned workspace of %lld bytes, got %lld",
+               (long long)gq_ws_bytes(x_rows), (long long)workspace_bytes);
+  GQArgs a{};
+  const int rc = gq_nested_args(a, res_codes, res_scales, res_codes, res_scales, res_scale_dtype, hot_row, hot_rows,
+                                res_table);
+  if (rc != KEEP_OK) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  a.x = x; a.xdt = x_dtype; a.x_rows = x_rows; a.lhs = lhs;
+  a.rs = gq_rowscale(x, x_dtype, x_rows, K, workspace, s);
+  a.oidx = out_index; a.c0 = a.c1 = codes; a.s0 = a.s1 = scales; a.sdt = scale_dtype;
+  a.tq = (const char*)prepared + TQ_OFFSET;
+  a.tq_bad = (const uint32_t*)((const char*)prepared + TQ_FLAG_OFFSET);
+  a.te = tile_expert; a.to = tile_offset; a.tc = tile_count; a.n_tiles = n_tiles; a.routes = routes;
+  a.E = num_experts; a.N = N; a.K = K; a.G = 1; a.kpg = K / GQ_KB; a.limit = 0.f;
+  a.out = out; a.odt = out_dtype;
+  gq_launch(a, false, s, false, true);
+  return launch_status("keep_vq_grouped_gemm_nested_q8");
 }
 
 extern "C" int keep_route_combine(const float* y, const float* w, int64_t T, int64_t k, int64_t H, void* out,

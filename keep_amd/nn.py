@@ -352,6 +352,19 @@ class QuantizedVQSwitchGLU:
             return self.activation.limit
         return None
 
+    def _nested_prefill_fused(self, limit: float | None) -> bool:
+        """Whether the tiered prefill runs on the fused base-plus-residual
+        kernels: a fused SwiGLU, one scale per row for every base and residual
+        projection, gate and up scales (and their residuals') of one dtype."""
+
+        ht, g, u, d = self.hot_tier, self.gate_proj, self.up_proj, self.down_proj
+        if limit is None or g.scales.dtype != u.scales.dtype:
+            return False
+        if any(p.group_size != p.input_dims for p in (g, u, d)):
+            return False
+        res = [ht.residual_arrays[n][1] for n in ("gate", "up", "down")]
+        return all(sc.shape[-1] == 1 for sc in res) and res[0].dtype == res[1].dtype
+
     def _shared_sorted_route_prefill(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """One device route plan shared by gate, up and down
         (``glm4_moe_adapter.py:274-353``): gate and up in one int8 grouped GEMM
@@ -369,6 +382,17 @@ class QuantizedVQSwitchGLU:
         f32 = torch.float32
         limit = self._fused_swiglu_limit()
         ht = self.hot_tier
+        if ht is not None and self._nested_prefill_fused(limit):
+            # base and residual in one pass per kernel: a hot expert's tiles add its residual row before
+            # the SwiGLU (gate/up) and before the store (down)
+            rg, ru, rd = (ht.residual_arrays[n] for n in ("gate", "up", "down"))
+            hidden = ops.grouped_swiglu_nested(flat_x, g.codes, g.scales, u.codes, u.scales, g.codebook, rg, ru,
+                                               ht._hot32, ht._table_packed, tiles, lhs=sorted_lhs, routes=R,
+                                               input_dims=g.input_dims, hidden_dims=g.output_dims, limit=limit)
+            y = ops.grouped_gemm_nested(hidden, d.codes, d.scales, d.codebook, rd, ht._hot32, ht._table_packed, tiles,
+                                        lhs=None, routes=R, input_dims=d.input_dims, output_dims=d.output_dims,
+                                        out_dtype=f32, out_index=order)
+            return y.reshape(lead + (k, d.output_dims))
         if ht is not None:  # base GEMMs, then the residual GEMMs over tiles of routes grouped by residual row
             rrows = ht.route_rows(flat_rhs)
             r_order, _, _, _, rte, rto, rtc, _ = ops.route_plan(rrows, ht.rows, ops.GEMM_ROUTE_TILE)

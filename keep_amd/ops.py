@@ -398,6 +398,76 @@ def grouped_swiglu(x: torch.Tensor, gate_codes: torch.Tensor, gate_scales: torch
     return h
 
 
+def _nested_residual(res, name: str, n: int, k: int):
+    codes, scales = res
+    if codes.dtype != torch.uint8 or tuple(codes.shape[1:]) != (n, k // 8) or not codes.is_contiguous():
+        raise ValueError(f"{name} residual codes must be contiguous uint8 [rows, {n}, {k // 8}]")
+    if scales.ndim != 3 or tuple(scales.shape) != (codes.shape[0], n, 1) or not scales.is_contiguous():
+        raise ValueError(f"{name} residual scales must be contiguous [rows, {n}, 1] (one scale per row)")
+    return codes, scales
+
+
+def grouped_swiglu_nested(x: torch.Tensor, gate_codes: torch.Tensor, gate_scales: torch.Tensor,
+                          up_codes: torch.Tensor, up_scales: torch.Tensor, codebook: torch.Tensor, gate_res, up_res,
+                          hot_row: torch.Tensor, res_table: torch.Tensor, tile_descriptors, *,
+                          lhs: torch.Tensor | None, routes: int, input_dims: int, hidden_dims: int,
+                          limit: float = 0.0) -> torch.Tensor:
+    """``keep_vq_grouped_swiglu_nested_q8``: ``grouped_swiglu`` (per-row base
+    scales) with the nested tier's 8-bit E8 residual of each hot expert added
+    to gate and up before the SwiGLU (``omlx_lattice.py:172-186``). ``gate_res``
+    / ``up_res`` = (uint8 codes ``[rows, I, H / 8]``, scales ``[rows, I, 1]``),
+    ``hot_row`` int32 ``[E]`` (-1: none), ``res_table`` the packed E8 table."""
+
+    device = x.device
+    h = torch.empty((routes, hidden_dims), dtype=torch.bfloat16, device=device)
+    if routes == 0:
+        return h
+    if gate_scales.dtype != up_scales.dtype:
+        raise ValueError("gate and up scales must share a dtype")
+    grc, grs = _nested_residual(gate_res, "gate", hidden_dims, input_dims)
+    urc, urs = _nested_residual(up_res, "up", hidden_dims, input_dims)
+    if grs.dtype != urs.dtype or grc.shape[0] != urc.shape[0]:
+        raise ValueError("gate and up residuals must share their rows and scale dtype")
+    te, to, tc = tile_descriptors
+    xc = x.contiguous()
+    ws = _q8_workspace(xc.shape[0], input_dims, device)
+    prep = prepared_table(codebook)
+    _lib.call("keep_vq_grouped_swiglu_nested_q8", xc.data_ptr(), _dtype_code(xc, "x"), xc.shape[0], _ptr(lhs),
+              gate_codes.data_ptr(), gate_scales.data_ptr(), up_codes.data_ptr(), up_scales.data_ptr(),
+              _dtype_code(gate_scales, "scales"), prep.data_ptr(), grc.data_ptr(), grs.data_ptr(), urc.data_ptr(),
+              urs.data_ptr(), _dtype_code(grs, "residual scales"), hot_row.data_ptr(), grc.shape[0],
+              res_table.data_ptr(), te.data_ptr(), to.data_ptr(), tc.data_ptr(), te.numel(), routes,
+              gate_codes.shape[0], hidden_dims, input_dims, float(limit), ws.data_ptr(), ws.numel(), h.data_ptr(),
+              _stream(device))
+    return h
+
+
+def grouped_gemm_nested(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor, codebook: torch.Tensor, res,
+                        hot_row: torch.Tensor, res_table: torch.Tensor, tile_descriptors, *,
+                        lhs: torch.Tensor | None, routes: int, input_dims: int, output_dims: int,
+                        out_dtype: torch.dtype | None = None, out_index: torch.Tensor | None = None) -> torch.Tensor:
+    """``keep_vq_grouped_gemm_nested_q8``: ``grouped_gemm`` (per-row base
+    scales) plus the nested tier's residual of each hot expert, added before
+    the store (row ``out_index[p]`` when given)."""
+
+    device = x.device
+    od = out_dtype or output_dtype(x.dtype)
+    out = torch.empty((routes, output_dims), dtype=od, device=device)
+    if routes == 0:
+        return out
+    rc, rs = _nested_residual(res, "down", output_dims, input_dims)
+    te, to, tc = tile_descriptors
+    xc = x.contiguous()
+    ws = _q8_workspace(xc.shape[0], input_dims, device)
+    prep = prepared_table(codebook)
+    _lib.call("keep_vq_grouped_gemm_nested_q8", xc.data_ptr(), _dtype_code(xc, "x"), xc.shape[0], _ptr(lhs),
+              _ptr(out_index), codes.data_ptr(), scales.data_ptr(), _dtype_code(scales, "scales"), prep.data_ptr(),
+              rc.data_ptr(), rs.data_ptr(), _dtype_code(rs, "residual scales"), hot_row.data_ptr(), rc.shape[0],
+              res_table.data_ptr(), te.data_ptr(), to.data_ptr(), tc.data_ptr(), te.numel(), routes, codes.shape[0],
+              output_dims, input_dims, ws.data_ptr(), ws.numel(), out.data_ptr(), _DT[od], _stream(device))
+    return out
+
+
 def route_combine(y: torch.Tensor, weight: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """``keep_route_combine``: ``sum_j w[t, j] * y[t, j, :]`` in fp32 for
     ``y [T, k, H]`` (``glm4_moe_adapter.py:367-372``)."""

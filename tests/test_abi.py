@@ -109,3 +109,31 @@ def _tiles_layer(**over):
 def test_tiles_layer_argument_validation_before_launch(over, msg):
     assert _tiles_layer(**over) == _lib.KEEP_EINVAL
     assert msg in _lib.load().keep_last_error().decode()
+
+
+def _nested_gemm(**over):
+    args = dict(x=16, x_dtype=1, x_rows=4, lhs=None, oidx=None, codes=16, scales=16, sdt=1, prep=16, rc=16, rs=16,
+                rsdt=1, hot=16, hot_rows=2, table=16, te=16, to=16, tc=16, n_tiles=1, routes=4, E=8, N=256, K=512,
+                ws=256, ws_bytes=1 << 20, out=16, odt=0, stream=None)
+    args.update(over)
+    return _lib.load().keep_vq_grouped_gemm_nested_q8(*args.values())
+
+
+@pytest.mark.parametrize("over, msg", [
+    (dict(K=500), "multiple of 128"),
+    (dict(hot=None), "null pointer"),
+    (dict(rc=4), "8-byte aligned"),
+    (dict(rsdt=7), "dtype enum"),
+    (dict(x_dtype=2, ws=None), "workspace"),
+])
+def test_nested_gemm_argument_validation_before_launch(over, msg):
+    assert _nested_gemm(**over) == _lib.KEEP_EINVAL
+    assert msg in _lib.load().keep_last_error().decode()
+
+
+def test_nested_swiglu_argument_validation_before_launch():
+    lib = _lib.load()
+    args = [16, 1, 4, None, 16, 16, 16, 16, 1, 16, 16, 16, 16, 16, 1, None, 2, 16, 16, 16, 16, 1, 4, 8, 256, 512,
+            0.0, None, 0, 16, None]
+    assert lib.keep_vq_grouped_swiglu_nested_q8(*args) == _lib.KEEP_EINVAL
+    assert b"null pointer" in lib.keep_last_error()

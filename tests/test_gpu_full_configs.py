@@ -161,33 +161,24 @@ def test_config5_prefill_with_tier_full_shape(dev):
     oi, *_ = ops.router_dual_topk(z.cpu().numpy(), keep_amd.resident_bias(torch.from_numpy(mask)).numpy()
                                   .astype(np.float64), np.zeros(E), k, tau=0.3)
     np.testing.assert_array_equal(idx, oi)
-    # the module's kernels one by one (the tiered sorted-route prefill): h in sorted order, y in route order
+    # the module's kernels one by one (the tiered sorted-route prefill, base and residual fused): h in
+    # sorted order, y in route order
     kops = keep_amd.ops
     R = T * k
     flat = r.idx.reshape(-1).to(torch.int32).contiguous()
     flat_lhs = (torch.arange(R, dtype=torch.int32, device=dev) // k).contiguous()
     order, inverse, _, _, te, to, tc, _ = kops.route_plan(flat, E, kops.GEMM_ROUTE_TILE)
     sorted_lhs = flat_lhs[order.long()].contiguous()
-    rrows = tier.route_rows(flat)
-    r_order, _, _, _, rte, rto, rtc, _ = kops.route_plan(rrows, tier.rows, kops.GEMM_ROUTE_TILE)
-    at_base = inverse[r_order.long()].to(torch.int32).contiguous()
     cb = glu.gate_proj.codebook
     f32 = torch.float32
-    gu = {}
-    for name, p in (("gate", gate), ("up", up)):
-        o = kops.grouped_gemm(x, p.codes, p.scales, cb, (te, to, tc), lhs=sorted_lhs, routes=R, input_dims=H,
-                              output_dims=I, group_size=H, out_dtype=f32)
-        rc, rs = tier.residual_arrays[name]
-        kops.grouped_residual_add(o, x, rc, rs, (rte, rto, rtc), lhs=flat_lhs[r_order.long()].contiguous(),
-                                  out_index=at_base, routes=R, input_dims=H, output_dims=I,
-                                  group_size=H // rs.shape[-1], table=tier._table_packed)
-        gu[name] = o
-    hidden = glu._apply_activation(gu["up"], gu["gate"]).to(torch.bfloat16).contiguous()
-    y = kops.grouped_gemm(hidden, down.codes, down.scales, cb, (te, to, tc), lhs=None, routes=R, input_dims=I,
-                          output_dims=H, group_size=I, out_dtype=f32, out_index=order)
-    rc, rs = tier.residual_arrays["down"]
-    kops.grouped_residual_add(y, hidden, rc, rs, (rte, rto, rtc), lhs=at_base, out_index=r_order, routes=R,
-                              input_dims=I, output_dims=H, group_size=I // rs.shape[-1], table=tier._table_packed)
+    assert glu._nested_prefill_fused(glu._fused_swiglu_limit())
+    rg, ru, rd = (tier.residual_arrays[n] for n in ("gate", "up", "down"))
+    hidden = kops.grouped_swiglu_nested(x, gate.codes, gate.scales, up.codes, up.scales, cb, rg, ru, tier._hot32,
+                                        tier._table_packed, (te, to, tc), lhs=sorted_lhs, routes=R, input_dims=H,
+                                        hidden_dims=I, limit=glu._fused_swiglu_limit())
+    y = kops.grouped_gemm_nested(hidden, down.codes, down.scales, cb, rd, tier._hot32, tier._table_packed,
+                                 (te, to, tc), lhs=None, routes=R, input_dims=I, output_dims=H, out_dtype=f32,
+                                 out_index=order)
     again = kops.route_combine(y.reshape(T, k, H), r.weight)
     assert torch.equal(again, out), "RoutedVQMoE differs from its own kernels run one by one"
     tab, t8 = e8p.e8p_packed_abs_grid(), e8p.e8_1bit_packed()

@@ -55,11 +55,12 @@ def _block(dev, E=32, H=512, I=256, n_hot=8):
     return glu, (gate, up, down), hot_of_slot, residual
 
 
-@pytest.mark.parametrize("T,k,hot", [(1, 8, True), (3, 6, True), (48, 6, True), (48, 6, False)])
+@pytest.mark.parametrize("T,k,hot", [(1, 8, True), (3, 6, True), (48, 6, True), (48, 6, False), (256, 6, True)])
 @pytest.mark.parametrize("limit", [10.0, 0.0])
 def test_hot_tier_block_vs_oracle(dev, T, k, hot, limit):
     """T = 1, 3: nested mat-vecs; T = 48 (288 routes): the prefill path, with
-    and without the tier. Unclamped (limit 0), h reaches thousands and one bf16
+    and without the tier; T = 256 (1536 routes, ~48 per expert): hot tiles of
+    more than 32 routes, which the fused prefill runs as two passes. Unclamped (limit 0), h reaches thousands and one bf16
     ulp of it (32 at 4096) moves an output by ~1% of the outputs' rms: the
     oracle's own bf16-h and exact-h forms differ by 8e-3 elementwise there,
     and any tie the two sides break differently shows up at that size. That
@@ -153,3 +154,40 @@ def test_hot_tier_fused_layer_off_tier_and_bad_row(dev):
     bad = keep_amd.HotTier(hot, glu.hot_tier.residual_arrays)
     out, _ = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0, hot_tier=bad)
     assert torch.isnan(out).all()
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_hot_tier_prefill_fused_kernels(dev, xdt, monkeypatch):
+    """The tiered prefill runs on the fused base-plus-residual kernels
+    (keep_vq_grouped_swiglu_nested_q8, keep_vq_grouped_gemm_nested_q8) and
+    matches the split form (base GEMMs, residual GEMMs over a second plan, torch
+    SwiGLU) to fp32 rounding before the bf16 h; an expert whose hot row is out
+    of range gives NaN for exactly the tokens routed to it."""
+    glu, (gate, up, down), hot_of_slot, residual = _block(dev)
+    glu.activation = keep_amd.LimitedSwiGLU(10.0, fp32=True)
+    moe = keep_amd.RoutedVQMoE(glu, top_k=6, swiglu_limit=10.0)
+    x = synth.rht_activations(256, 512, seed=350, device=dev).to(xdt)
+    z = synth.router_logits(256, 32, seed=351, device=dev)
+    calls = []
+    real = keep_amd.ops.grouped_swiglu_nested
+    monkeypatch.setattr(keep_amd.ops, "grouped_swiglu_nested", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    fused, r = moe(x, z)
+    assert calls, "the fused tier kernels did not run"
+    monkeypatch.setattr(type(glu), "_nested_prefill_fused", lambda self, limit: False)
+    split, r2 = moe(x, z)
+    assert torch.equal(r.idx, r2.idx)
+    f, sp = fused.float().cpu().numpy(), split.float().cpu().numpy()
+    assert ops.max_rel_err(f, sp) <= 1e-3
+    monkeypatch.undo()
+    idx = r.idx.cpu().numpy()
+    hot = hot_of_slot.copy()
+    victim = int(np.nonzero(hot != keep_amd.ops.NO_RESIDUAL)[0][0])
+    hot[victim] = 8  # rows 0..7 exist
+    glu.hot_tier = keep_amd.HotTier(hot, glu.hot_tier.residual_arrays)
+    out, _ = moe(x, z)
+    hit = (idx == victim).any(axis=1)
+    assert hit.any() and not hit.all()
+    o = out.float().cpu().numpy()
+    assert np.isnan(o[hit]).all(1).all()
+    assert np.isfinite(o[~hit]).all()
+    np.testing.assert_array_equal(o[~hit], f[~hit])
