@@ -367,16 +367,15 @@ class QuantizedVQSwitchGLU:
 
     def _shared_sorted_route_prefill(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """One device route plan shared by gate, up and down
-        (``glm4_moe_adapter.py:274-353``): gate and up in one int8 grouped GEMM
+        (``glm4_moe_adapter.py:274-353``): gate and up in one grouped GEMM
         with SwiGLU in its epilogue (h in bf16), down scattered straight back
         to route order; per-route outputs are float32."""
         lead, k = tuple(x.shape[:-1]), indices.shape[-1]
         flat_x = x.reshape(-1, self.input_dims).contiguous()
         flat_rhs = indices.reshape(-1).to(torch.int32).contiguous()
         R = flat_rhs.numel()
-        flat_lhs = torch.arange(R, dtype=torch.int32, device=x.device) // k
         order, inverse, _, _, te, to, tc, _ = ops.route_plan(flat_rhs, self.num_experts, ops.GEMM_ROUTE_TILE)
-        sorted_lhs = flat_lhs[order.long()].contiguous()
+        sorted_lhs = torch.div(order, k, rounding_mode="floor")  # route r is token r // k's
         tiles = (te, to, tc)
         g, u, d = self.gate_proj, self.up_proj, self.down_proj
         f32 = torch.float32
@@ -405,7 +404,7 @@ class QuantizedVQSwitchGLU:
             up = ops.grouped_gemm(flat_x, u.codes, u.scales, u.codebook, tiles, lhs=sorted_lhs, routes=R,
                                   input_dims=u.input_dims, output_dims=u.output_dims, group_size=u.group_size,
                                   out_dtype=f32)
-            x_lhs = flat_lhs[ro].contiguous()
+            x_lhs = torch.div(r_order, k, rounding_mode="floor")
             for out_t, name, proj in ((gate, "gate", g), (up, "up", u)):
                 rc, rs = ht.residual_arrays[name]
                 ops.grouped_residual_add(out_t, flat_x, rc, rs, r_tiles, lhs=x_lhs, out_index=at_base, routes=R,
