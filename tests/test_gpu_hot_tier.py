@@ -1,8 +1,9 @@
 """GPU parity of the nested 3-bit tier in the routed SwiGLU block (config 5's
 hot experts): E8P base plus an 8-bit E8 residual for the experts listed in
 hot_of_slot, through RoutedVQMoE on the decode-sized path (one-pass nested
-mat-vecs, omlx_lattice.py:358-370) and the prefill path (int8 grouped GEMMs
-plus the residual of every route, zero off the tier, omlx_lattice.py:172-186),
+mat-vecs, omlx_lattice.py:358-370) and the prefill path (grouped GEMMs on the
+fp16 matrix cores with each hot expert's residual added in the same pass, or
+the split form with separate residual GEMMs, omlx_lattice.py:172-186),
 against the float64 oracle with the same bf16 rounding of h."""
 
 import numpy as np
