@@ -9,10 +9,13 @@
 // buckets the descriptors fit in ceil(R / tile) + E entries, since
 // ceil(a / t) + ceil(b / t) <= ceil((a + b) / t) + 1.
 //
-// Stability: routes are taken in chunks of 1024 in route order. Inside a
-// chunk, a route's rank among same-expert routes is (routes of its expert in
-// earlier waves of the chunk, from per-wave histograms) + (earlier lanes of
-// its own wave with the same expert, by a 64-step shuffle scan).
+// Stability: wave w owns the contiguous route range [w P, (w + 1) P), P =
+// ceil(R / 16). A route's position is its bucket's base + the routes of that
+// bucket in earlier waves' ranges (per-wave histograms, scanned once) + the
+// earlier routes of its own range with the same bucket: each wave walks its
+// range 64 routes at a time, ranking a route among the same-bucket lanes below
+// it (ballots over the bucket bits) and advancing its per-bucket offset from
+// the last such lane, with no block barrier.
 #include "common.h"
 
 namespace keep {
@@ -20,7 +23,7 @@ namespace keep {
 constexpr int PLAN_THREADS = 1024;
 constexpr int PLAN_WAVES = PLAN_THREADS / 64;
 constexpr int PLAN_MAX_E = 1024;
-constexpr int PLAN_PER = 16;  // routes per thread held in registers (R <= 16384)
+constexpr int PLAN_PER = 16;  // routes per lane held in registers (R <= 16 x 64 x 16 = 16384)
 
 // The plan's LDS scratch (78 KiB).
 struct PlanLds {
@@ -44,31 +47,35 @@ __device__ __forceinline__ void plan_block(Route route, int R, int E, int tile, 
   int (*wtot)[PLAN_WAVES] = L.wtot;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int EB = E + 1;  // bucket E collects invalid expert ids
-  for (int e = tid; e < EB; e += PLAN_THREADS) cnt[e] = 0;
+  const int P = (R + PLAN_WAVES - 1) / PLAN_WAVES;
+  const int r0 = min(R, wv * P), r1 = min(R, r0 + P);  // this wave's routes
+  auto bucket = [&](int r) {
+    const int e = route(r);
+    return (e < 0 || e >= E) ? E : e;
+  };
+  for (int i = tid; i < PLAN_WAVES * EB; i += PLAN_THREADS) wh[i / EB][i % EB] = 0;
   __syncthreads();
-  // up to PLAN_PER routes per thread stay in registers from here to the scatter
-  const bool held = R <= PLAN_THREADS * PLAN_PER;
+  // up to PLAN_PER routes per lane stay in registers from here to the scatter
+  const bool held = P <= 64 * PLAN_PER;
   int ev[PLAN_PER];
   if (held) {
 #pragma unroll
     for (int i = 0; i < PLAN_PER; ++i) {
-      const int r = i * PLAN_THREADS + tid;
-      int e = -1;
-      if (r < R) {
-        e = route(r);
-        if (e < 0 || e >= E) e = E;
-      }
-      ev[i] = e;
+      const int r = r0 + i * 64 + lane;
+      ev[i] = r < r1 ? bucket(r) : -1;
     }
 #pragma unroll
     for (int i = 0; i < PLAN_PER; ++i)
-      if (ev[i] >= 0) atomicAdd(&cnt[ev[i]], 1);
+      if (ev[i] >= 0) atomicAdd(&wh[wv][ev[i]], 1);
   } else {
-    for (int r = tid; r < R; r += PLAN_THREADS) {
-      int e = route(r);
-      if (e < 0 || e >= E) e = E;
-      atomicAdd(&cnt[e], 1);
-    }
+    for (int r = r0 + lane; r < r1; r += 64) atomicAdd(&wh[wv][bucket(r)], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < EB; e += PLAN_THREADS) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < PLAN_WAVES; ++w) c += wh[w][e];
+    cnt[e] = c;
   }
   __syncthreads();
   // Exclusive prefix sums of the bucket sizes (route bases) and of the tile
@@ -114,6 +121,17 @@ __device__ __forceinline__ void plan_block(Route route, int R, int E, int tile, 
     if (b1 == E) n_tiles_out[0] = et + t0;
   }
   __syncthreads();
+  // each wave's first position in every bucket: the bucket's base plus the
+  // bucket's routes in earlier waves' ranges
+  for (int e = tid; e < EB; e += PLAN_THREADS) {
+    int acc = run[e];
+#pragma unroll
+    for (int w = 0; w < PLAN_WAVES; ++w) {
+      const int c = wh[w][e];
+      wh[w][e] = acc;
+      acc += c;
+    }
+  }
   for (int e = tid; e < E; e += PLAN_THREADS) {
     counts[e] = cnt[e];
     offsets[e] = run[e];
@@ -137,57 +155,37 @@ __device__ __forceinline__ void plan_block(Route route, int R, int E, int tile, 
       tc[ti] = b ? min(tile, cnt[E] - i * tile) : 0;
     }
   }
-  // stable scatter, PLAN_THREADS routes per pass: a route's position is its
-  // bucket's running offset + the routes of that bucket in earlier waves of
-  // the pass + the lanes of its own wave below it with the same bucket
+  __syncthreads();
+  // stable scatter, each wave over its own range (no block barrier): a route's
+  // rank among the same-bucket lanes below it, then the last of those lanes
+  // advances the wave's offset for the bucket (one wave's LDS operations run in
+  // order, and the offset write depends on the read before it)
   const int nbits = 32 - __builtin_clz((unsigned)E);  // bucket ids 0..E
-  auto pass = [&](int base, int e) {
-    const int nwp = min(PLAN_WAVES, (R - base + 63) >> 6);  // waves holding routes of this pass
-    for (int i = tid; i < nwp * EB; i += PLAN_THREADS) wh[i / EB][i % EB] = 0;
-    __syncthreads();
-    const int r = base + tid;
+  auto scatter = [&](int rb, int e) {  // routes rb + lane (e = -1: none)
+    const int r = rb + lane;
     uint64_t peers = __ballot(e >= 0);
     for (int b = 0; b < nbits; ++b) {
       const bool bit = (e >> b) & 1;
       const uint64_t m = __ballot(bit);
       peers &= bit ? m : ~m;
     }
-    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
-    if (e >= 0) atomicAdd(&wh[wv][e], 1);
-    __syncthreads();
-    for (int q = tid; q < EB; q += PLAN_THREADS) {
-      int acc = run[q];
-      for (int w = 0; w < nwp; ++w) {
-        const int c = wh[w][q];
-        wh[w][q] = acc;
-        acc += c;
-      }
-      run[q] = acc;
-    }
-    __syncthreads();
     if (e >= 0) {
+      const int rank = __popcll(peers & ((1ull << lane) - 1ull));
       const int pos = wh[wv][e] + rank;
+      const uint64_t above = lane == 63 ? 0ull : (peers >> (lane + 1));
+      if (above == 0ull) wh[wv][e] = pos + 1;
       order[pos] = r;
       inverse[r] = pos;
     }
-    __syncthreads();
   };
   if (held) {
 #pragma unroll
     for (int i = 0; i < PLAN_PER; ++i) {
-      if (i * PLAN_THREADS >= R) break;
-      pass(i * PLAN_THREADS, ev[i]);
+      if (r0 + i * 64 >= r1) break;
+      scatter(r0 + i * 64, ev[i]);
     }
   } else {
-    for (int base = 0; base < R; base += PLAN_THREADS) {
-      const int r = base + tid;
-      int e = -1;
-      if (r < R) {
-        e = route(r);
-        if (e < 0 || e >= E) e = E;
-      }
-      pass(base, e);
-    }
+    for (int rb = r0; rb < r1; rb += 64) scatter(rb, rb + lane < r1 ? bucket(rb + lane) : -1);
   }
 }
 
