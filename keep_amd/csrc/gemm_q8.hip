@@ -668,7 +668,7 @@ extern "C" int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_row
   KEEP_REQUIRE(code_bits == 16 || code_bits == 8, "code_bits must be 16 (E8P) or 8 (residual E8)");
   KEEP_REQUIRE(code_bits == 16 || out_dtype == KEEP_F32, "the residual form adds into an fp32 output");
   KEEP_REQUIRE(gq_shape_ok(K, group_size),
-               "int8 grouped GEMM needs K and the scale group multiples of %d, the group dividing K (K=%lld, "
+               "grouped GEMM needs K and the scale group multiples of %d, the group dividing K (K=%lld, "
                "group_size=%lld)",
                GQ_KB, (long long)K, (long long)group_size);
   KEEP_REQUIRE(N > 0 && n_tiles >= 0 && routes >= 0 && num_experts > 0 && x_rows >= 0, "bad sizes");
@@ -710,7 +710,7 @@ extern "C" int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_r
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
   KEEP_REQUIRE(dtype_ok(scale_dtype), "bad dtype enum");
   KEEP_REQUIRE(gq_shape_ok(H, group_size),
-               "int8 grouped GEMM needs H and the scale group multiples of %d, the group dividing H (H=%lld, "
+               "grouped GEMM needs H and the scale group multiples of %d, the group dividing H (H=%lld, "
                "group_size=%lld)",
                GQ_KB, (long long)H, (long long)group_size);
   KEEP_REQUIRE(I > 0 && n_tiles >= 0 && routes >= 0 && num_experts > 0 && x_rows >= 0, "bad sizes");
@@ -761,7 +761,7 @@ extern "C" int keep_vq_grouped_swiglu_nested_q8(
     void* workspace, int64_t workspace_bytes, void* h_out, void* stream) {
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
   KEEP_REQUIRE(dtype_ok(scale_dtype), "bad dtype enum");
-  KEEP_REQUIRE(gq_shape_ok(H, H), "int8 grouped GEMM needs H a multiple of %d (H=%lld)", GQ_KB, (long long)H);
+  KEEP_REQUIRE(gq_shape_ok(H, H), "grouped GEMM needs H a multiple of %d (H=%lld)", GQ_KB, (long long)H);
   KEEP_REQUIRE(I > 0 && n_tiles >= 0 && routes >= 0 && num_experts > 0 && x_rows >= 0, "bad sizes");
   if (n_tiles == 0 || routes == 0) return KEEP_OK;
   KEEP_REQUIRE(x_rows > 0 && x && gate_codes && gate_scales && up_codes && up_scales && prepared && tile_expert &&
@@ -799,7 +799,7 @@ extern "C" int keep_vq_grouped_gemm_nested_q8(
     int out_dtype, void* stream) {
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
-  KEEP_REQUIRE(gq_shape_ok(K, K), "int8 grouped GEMM needs K a multiple of %d (K=%lld)", GQ_KB, (long long)K);
+  KEEP_REQUIRE(gq_shape_ok(K, K), "grouped GEMM needs K a multiple of %d (K=%lld)", GQ_KB, (long long)K);
   KEEP_REQUIRE(N > 0 && n_tiles >= 0 && routes >= 0 && num_experts > 0 && x_rows >= 0, "bad sizes");
   if (n_tiles == 0 || routes == 0) return KEEP_OK;
   KEEP_REQUIRE(x_rows > 0 && x && codes && scales && prepared && tile_expert && tile_offset && tile_count && out,

@@ -101,8 +101,9 @@ _PREPARED: dict[tuple[int, str], tuple[torch.Tensor, torch.Tensor]] = {}
 
 
 def prepared_table(codebook: torch.Tensor) -> torch.Tensor:
-    """Expanded E8P table of ``codebook`` for the fused MoE decode kernels
-    (``keep_e8p_prepare``: 2 x 128 KiB, fp16 then bf16), cached per codebook tensor."""
+    """The prepared E8P table of ``codebook`` for the matrix-core kernels
+    (``keep_e8p_prepare``: T and M of the int8 decode, a check word and the
+    64 KiB LDS image, ``keep_e8p_prepared_bytes()`` bytes), cached per codebook tensor."""
 
     key = (codebook.data_ptr(), str(codebook.device))
     hit = _PREPARED.get(key)
@@ -484,7 +485,7 @@ def route_combine(y: torch.Tensor, weight: torch.Tensor, out_dtype: torch.dtype 
 
 
 def gemm_eligible(*, code_bits: int, x_dtype: torch.dtype, input_dims: int, group_size: int) -> bool:
-    """Whether the int8 grouped GEMM serves this call (E8P, fp16/bf16/fp32
+    """Whether the grouped GEMM (fp16 matrix cores) serves this call (E8P, fp16/bf16/fp32
     activations, K and the scale group multiples of 128)."""
 
     return (code_bits == 16 and x_dtype in (torch.float16, torch.bfloat16, torch.float32) and input_dims % 128 == 0
