@@ -192,3 +192,24 @@ def test_hot_tier_prefill_fused_kernels(dev, xdt, monkeypatch):
     assert np.isnan(o[hit]).all(1).all()
     assert np.isfinite(o[~hit]).all()
     np.testing.assert_array_equal(o[~hit], f[~hit])
+
+
+@pytest.mark.parametrize("xdt,rdt", [(torch.float32, torch.bfloat16), (torch.float32, torch.float32),
+                                     (torch.bfloat16, torch.bfloat16)])
+def test_hot_tier_prefill_fused_dtypes_vs_oracle(dev, xdt, rdt):
+    """The fused tiered prefill with fp32 / bf16 activations and bf16 / fp32
+    residual scales (the oracle takes the same rounded scale values)."""
+    glu, (gate, up, down), hot_of_slot, residual = _block(dev)
+    res = {n: (c, torch.from_numpy(s.astype(np.float32)).to(rdt)) for n, (c, s) in residual.items()}
+    glu.hot_tier = keep_amd.HotTier(hot_of_slot, {n: (_t(c, dev), s.to(dev)) for n, (c, s) in res.items()})
+    glu.activation = keep_amd.LimitedSwiGLU(10.0, fp32=True)
+    assert glu._nested_prefill_fused(glu._fused_swiglu_limit())
+    moe = keep_amd.RoutedVQMoE(glu, top_k=6, swiglu_limit=10.0)
+    x = synth.rht_activations(256, 512, seed=360, device=dev).to(xdt)
+    z = synth.router_logits(256, 32, seed=361, device=dev)
+    out, r = moe(x, z)
+    idx = r.idx.cpu().numpy()
+    want = ops.moe_layer(x.float().cpu().numpy(), idx, r.weight.cpu().numpy(), gate, up, down, limit=10.0,
+                         h_round="bfloat16", hot_of_slot=hot_of_slot,
+                         residual={n: (c, s.float().numpy()) for n, (c, s) in res.items()})
+    _check(out, want)
