@@ -124,7 +124,8 @@ def small_pool(dev):
 
 @pytest.mark.parametrize("T, E, xdt, biased", [(2, 384, torch.float16, False), (8, 384, torch.float16, False),
                                               (16, 100, torch.bfloat16, True), (32, 1000, torch.float16, True),
-                                              (33, 384, torch.float16, False), (64, 300, torch.bfloat16, True)])
+                                              (33, 384, torch.float16, False), (64, 300, torch.bfloat16, True),
+                                              (65, 384, torch.float16, False)])
 def test_tiles_layer_equals_router_then_tiles(dev, small_pool, T, E, xdt, biased):
     """keep_moe_tiles_layer: the router's five outputs and the tiles' result, bit for bit, on both sides of
     the fused-prologue limit (32 tokens), every router lane width, with and without biases and admission."""
