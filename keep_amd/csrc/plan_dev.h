@@ -10,7 +10,7 @@
 // ceil(a / t) + ceil(b / t) <= ceil((a + b) / t) + 1.
 //
 // Stability: wave w owns the contiguous route range [w P, (w + 1) P), P =
-// ceil(R / 16). A route's position is its bucket's base + the routes of that
+// max(64, ceil(R / 16)). A route's position is its bucket's base + the routes of that
 // bucket in earlier waves' ranges (per-wave histograms, scanned once) + the
 // earlier routes of its own range with the same bucket: each wave walks its
 // range 64 routes at a time, ranking a route among the same-bucket lanes below
@@ -47,13 +47,15 @@ __device__ __forceinline__ void plan_block(Route route, int R, int E, int tile, 
   int (*wtot)[PLAN_WAVES] = L.wtot;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int EB = E + 1;  // bucket E collects invalid expert ids
-  const int P = (R + PLAN_WAVES - 1) / PLAN_WAVES;
+  // at least 64 routes per wave, so that few routes occupy few waves
+  const int P = max(64, (R + PLAN_WAVES - 1) / PLAN_WAVES);
+  const int nwp = min(PLAN_WAVES, (R + P - 1) / P);     // waves holding routes
   const int r0 = min(R, wv * P), r1 = min(R, r0 + P);  // this wave's routes
   auto bucket = [&](int r) {
     const int e = route(r);
     return (e < 0 || e >= E) ? E : e;
   };
-  for (int i = tid; i < PLAN_WAVES * EB; i += PLAN_THREADS) wh[i / EB][i % EB] = 0;
+  for (int i = tid; i < nwp * EB; i += PLAN_THREADS) wh[i / EB][i % EB] = 0;
   __syncthreads();
   // up to PLAN_PER routes per lane stay in registers from here to the scatter
   const bool held = P <= 64 * PLAN_PER;
@@ -73,8 +75,7 @@ __device__ __forceinline__ void plan_block(Route route, int R, int E, int tile, 
   __syncthreads();
   for (int e = tid; e < EB; e += PLAN_THREADS) {
     int c = 0;
-#pragma unroll
-    for (int w = 0; w < PLAN_WAVES; ++w) c += wh[w][e];
+    for (int w = 0; w < nwp; ++w) c += wh[w][e];
     cnt[e] = c;
   }
   __syncthreads();
@@ -125,8 +126,7 @@ __device__ __forceinline__ void plan_block(Route route, int R, int E, int tile, 
   // bucket's routes in earlier waves' ranges
   for (int e = tid; e < EB; e += PLAN_THREADS) {
     int acc = run[e];
-#pragma unroll
-    for (int w = 0; w < PLAN_WAVES; ++w) {
+    for (int w = 0; w < nwp; ++w) {
       const int c = wh[w][e];
       wh[w][e] = acc;
       acc += c;
