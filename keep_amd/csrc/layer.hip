@@ -401,8 +401,9 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     if (gave_up && lane == 0) {
       __hip_atomic_fetch_or(hdr + 2, FL_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // A terms: rows 4 r and 4 r + 1 of route r's slice, the two int8 digits of
-    // h s with s the slice's power of two (a wave that gave up makes every
+    // A terms: rows 4 r and 4 r + 1 of route r's slice, the two int8 digits
+    // (base 256) of h s with s the slice's power of two, formed from the
+    // slice's largest |h| on the scalar unit (a wave that gave up makes every
     // route it holds NaN)
     float inv4d[RPW];
     uint32_t* aw = (uint32_t*)(dsh + wv * 256);
@@ -412,12 +413,13 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       const float v[4] = {__uint_as_float(w0 << 16), __uint_as_float(w0 & 0xffff0000u), __uint_as_float(w1 << 16),
                           __uint_as_float(w1 & 0xffff0000u)};
       // max |h| by the bits: a NaN outranks every number and makes inv4d NaN
-      const uint32_t m = max(max((w0 & 0x7fffu) << 16, w0 & 0x7fff0000u), max((w1 & 0x7fffu) << 16, w1 & 0x7fff0000u));
+      const uint32_t a0 = w0 & 0x7fff7fffu, a1 = w1 & 0x7fff7fffu;
+      const uint32_t m = max(max(a0 << 16, a0 & 0xffff0000u), max(a1 << 16, a1 & 0xffff0000u));
       float s;
-      q8_scale(rt_wave_max_abs(__uint_as_float(m)), s, inv4d[r]);
+      q8_scale(__uint_as_float(__builtin_amdgcn_readfirstlane(rt_wave_u32<true>(m))), s, inv4d[r]);
       if (gave_up) inv4d[r] = __builtin_nanf("");
       uint32_t tw[2];
-      q8_digits2(v, s, tw);
+      q8_digits2_b256(v, s * 256.f, tw);
 #pragma unroll
       for (int n = 0; n < 2; ++n) aw[q8_aword((uint32_t)(4 * r + n), lane >> 1, lane & 1)] = tw[n];
     }
@@ -445,7 +447,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       if ((int)g == r) {
         const int route = rg * RPW + r;
         const float wt = dlive[r] ? s_w[route] : 0.f;
-        const float d = (float)acc[0] + (float)acc[1] * 0.0078125f;
+        const float d = (float)acc[0] + (float)acc[1] * 0.00390625f;
         const float val = d * inv4d[r] * scale_cvt(srd[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + dgrp);
         c = wt == 0.f ? 0.f : dok[r] ? wt * val : __builtin_nanf("");
       }

@@ -28,8 +28,9 @@
 // remainder, so every |t| <= 64); A rows 0-2 are the three terms and the dot is
 // (D0 + D1 / 128 + D2 / 128^2) / (4 s). The residual is below 2^-21 of max |x|,
 // under the rounding of the fp32 sums. h (bf16) uses two terms (residual below
-// 2^-14 of its slice's max), so the down kernel puts route r's terms in rows
-// 2r and 2r + 1 (up to 8 routes). Each wave builds its terms once, in LDS.
+// 2^-14 of its slice's max; in base 128 in the two-launch kernels, base 256 in
+// the one-launch layer), so the down kernels put route r's terms in two rows
+// of A. Each wave builds its terms once, in LDS.
 //
 // K layout. Lane l of an MFMA holds row (A) / column (B) l % 16 and 16 bytes
 // of k-block l / 16. A wave's 256-wide K slice is 32 codewords; lane group g
@@ -183,6 +184,22 @@ __device__ __forceinline__ void q8_digits2(const float (&v)[4], float s, uint32_
   // the low byte of each half, values 0..3 in bytes 0..3
   out[0] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, h23), __builtin_bit_cast(uint32_t, h01), 0x06040200u);
   out[1] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, l23), __builtin_bit_cast(uint32_t, l01), 0x06040200u);
+}
+
+// The same two terms in base 256, t0 + t1 / 256 = rint(v s 256) / 256 of four
+// values (|v| s < 64), from s256 = s * 256 (a power of two): the FMA with
+// 1.5 * 2^23 + 128 leaves F + 128 = rint(v s 256) + 128 in the low 16 bits of
+// the float (two's complement); t0 is its high byte, floor((F + 128) / 256)
+// (|t0| <= 64), and t1 = F - 256 t0 is its low byte minus 128, i.e. the low
+// byte with bit 7 flipped. Four FMAs, four byte permutes and one XOR.
+__device__ __forceinline__ void q8_digits2_b256(const float (&v)[4], float s256, uint32_t (&out)[2]) {
+  uint32_t f[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) f[t] = __float_as_uint(fmaf(v[t], s256, 12583040.0f));
+  const uint32_t p01 = __builtin_amdgcn_perm(f[1], f[0], 0x05040100u);  // F + 128 of values 0, 1
+  const uint32_t p23 = __builtin_amdgcn_perm(f[3], f[2], 0x05040100u);  // of values 2, 3
+  out[0] = __builtin_amdgcn_perm(p23, p01, 0x07050301u);                // high bytes
+  out[1] = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;  // low bytes - 128
 }
 
 // Word index in an A-term buffer of 16-byte slots [row][g * 4 + i] for the
