@@ -272,6 +272,15 @@ int keep_moe_layer_noalloc(const float* logits, const float* bias_served, const 
  * scripts/v41_build/omlx_lattice.py:327-371 for batch 1. */
 int64_t keep_moe_layer1_workspace_bytes(int64_t k, int64_t I);
 int keep_moe_layer1_status(const void* workspace, uint32_t* status, void* stream);
+/* The give-up budget of every later keep_moe_layer1 launch in this process,
+ * in ticks of the GPU's 100 MHz real-time counter (default 20000 = 200 us,
+ * at most 1e8 = 1 s); *previous (if not null) receives the old value. A
+ * launch whose wait for another block's h outlasts it writes NaN for the
+ * routes that wave holds and sets status bit 1: callers check
+ * keep_moe_layer1_status() where a NaN output must not pass unnoticed. Tests
+ * use a budget of 0 to drive the give-up path. No counterpart in the
+ * reference (its decode step has no cross-block wait). */
+int keep_moe_layer1_set_spin_ticks(uint32_t ticks, uint32_t* previous);
 int keep_moe_layer1(const float* logits, const float* bias_served, const float* bias_demand,
                     int score_func, int renormalize, float route_scale, float tau,
                     const int32_t* slot_map, int64_t num_slots,

@@ -27,6 +27,8 @@
 // every route), and the workspace's status word records it.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "common.h"
 #include "moe_dev.h"
 #include "q8_dev.h"
@@ -38,6 +40,8 @@ constexpr int FL_BLOCKS = 256;       // H / 16 down row tiles, one block per CU
 constexpr int FL_WAVES = 16;         // H / 256 gate/up K slices
 constexpr uint32_t FL_HDR_BYTES = 256;  // epoch, arrivals, status
 constexpr uint32_t FL_TIMEOUT = 1u;     // status bit: a wait gave up
+constexpr uint32_t FL_SPIN_TICKS_DEFAULT = 20000u;   // 200 us of the 100 MHz counter
+constexpr uint32_t FL_SPIN_TICKS_MAX = 100000000u;   // 1 s
 
 // The arguments the first loads need: the kernel's leading arguments,
 // preloaded into SGPRs by the dispatcher (-amdgpu-kernarg-preload-count).
@@ -586,6 +590,16 @@ extern "C" int64_t keep_moe_layer1_workspace_bytes(int64_t k, int64_t I) {
   return fl_workspace_bytes(k, I);
 }
 
+// the give-up budget of every later launch, in ticks of the 100 MHz real-time counter
+static std::atomic<uint32_t> g_spin_ticks{FL_SPIN_TICKS_DEFAULT};
+
+extern "C" int keep_moe_layer1_set_spin_ticks(uint32_t ticks, uint32_t* previous) {
+  KEEP_REQUIRE(ticks <= FL_SPIN_TICKS_MAX, "spin budget above %u ticks (one second)", FL_SPIN_TICKS_MAX);
+  const uint32_t old = g_spin_ticks.exchange(ticks);
+  if (previous) *previous = old;
+  return KEEP_OK;
+}
+
 extern "C" int keep_moe_layer1_status(const void* workspace, uint32_t* status, void* stream) {
   KEEP_REQUIRE(workspace && status, "null pointer argument");
   if (hipMemcpyAsync(status, (const char*)workspace + 8, 4, hipMemcpyDeviceToHost, (hipStream_t)stream) !=
@@ -625,7 +639,8 @@ extern "C" int keep_moe_layer1(const float* logits, const float* bias_served, co
   KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 16), "codes misaligned");
   fl_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, slot_map, num_slots, E, k, x,
             x_dtype, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
-            group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, workspace, 20000u,
+            group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, workspace,
+            g_spin_ticks.load(std::memory_order_relaxed),
             out, out_dtype, (hipStream_t)stream);
   return launch_status("keep_moe_layer1");
 }

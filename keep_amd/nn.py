@@ -148,7 +148,7 @@ class QuantizedVQSwitchLinear:
                  scales: torch.Tensor, codebook: torch.Tensor | None = None, bias: torch.Tensor | None = None,
                  group_size: int = 512, code_bits: int = 8, use_gather_vqmm: bool = True,
                  route_strategy: str = "auto", gather_codebook_duplication: int = 8,
-                 rht_signs: torch.Tensor | None = None, **sidecars):
+                 rht_signs: torch.Tensor | None = None, rotation_matrix: torch.Tensor | None = None, **sidecars):
         if input_dims <= 0 or output_dims <= 0 or num_experts <= 0:
             raise ValueError("input_dims, output_dims, and num_experts must be positive")
         if input_dims % CODEWORD_DIM != 0:
@@ -174,6 +174,11 @@ class QuantizedVQSwitchLinear:
             raise ValueError(f"bias must have shape ({num_experts}, {output_dims}), found {tuple(bias.shape)}")
         if rht_signs is not None and tuple(rht_signs.shape) != (input_dims,):
             raise ValueError(f"rht_signs must have shape ({input_dims},), found {tuple(rht_signs.shape)}")
+        if rht_signs is not None and rotation_matrix is not None:
+            raise ValueError("rht_signs and rotation_matrix are mutually exclusive")
+        if rotation_matrix is not None and tuple(rotation_matrix.shape) != (input_dims, input_dims):
+            raise ValueError(f"rotation_matrix must have shape ({input_dims}, {input_dims}), "
+                             f"found {tuple(rotation_matrix.shape)}")
         device = codes.device if isinstance(codes, torch.Tensor) and codes.is_cuda else ops._device_of(codes)
         self.input_dims, self.output_dims, self.num_experts = input_dims, output_dims, num_experts
         self.group_size, self.code_bits = group_size, code_bits
@@ -187,11 +192,53 @@ class QuantizedVQSwitchLinear:
         if self.rht_signs is not None:
             from keep_amd.rht import check_signs
             check_signs(self.rht_signs)
+        self.rotation_matrix = None if rotation_matrix is None else ops._to_dev(rotation_matrix, device,
+                                                                                torch.float32)
+
+    @classmethod
+    def from_weights(cls, weight, bias=None, *, group_size: int = 512, code_bits: int = 8,
+                     use_gather_vqmm: bool = True, route_strategy: str = "auto",
+                     gather_codebook_duplication: int = 8, rht_signs=None,
+                     rotation_matrix=None) -> "QuantizedVQSwitchLinear":
+        """Quantise stacked dense expert weights ``[E, out, in]`` on the GPU
+        (``switch_linear.py:527-571``): the RHT (or rotation) of every expert's
+        rows, as the inputs will get it, then each expert's data-free RTN. The
+        RTN's scales belong to one (row, group), so the E experts quantise as one
+        ``[E * out, in]`` matrix in a single pass."""
+
+        from keep_amd.encode import quantize_weight_rtn
+
+        if rht_signs is not None and rotation_matrix is not None:
+            raise ValueError("rht_signs and rotation_matrix are mutually exclusive")
+        w = weight if isinstance(weight, torch.Tensor) else torch.from_numpy(np.asarray(weight, dtype=np.float32))
+        if w.ndim != 3:
+            raise ValueError(f"weight must be 3D [experts, out, in], found {tuple(w.shape)}")
+        device = w.device if w.is_cuda else torch.device("cuda", torch.cuda.current_device())
+        w = w.to(device=device, dtype=torch.float32).contiguous()
+        num_experts, out_dim, in_dim = w.shape
+        if rht_signs is not None:
+            from keep_amd.rht import apply_rht
+            w = apply_rht(w, torch.as_tensor(rht_signs).to(device))
+        if rotation_matrix is not None:
+            w = w @ torch.as_tensor(rotation_matrix).to(device=device, dtype=torch.float32)
+        q = quantize_weight_rtn(w.reshape(num_experts * out_dim, in_dim), group_size=group_size, code_bits=code_bits)
+        return cls(input_dims=in_dim, output_dims=out_dim, num_experts=num_experts,
+                   codes=q.codes.reshape(num_experts, out_dim, in_dim // CODEWORD_DIM),
+                   scales=q.scales.reshape(num_experts, out_dim, in_dim // q.group_size),
+                   codebook=torch.from_numpy(q.codebook.view(np.int32)).to(device), bias=bias,
+                   group_size=q.group_size, code_bits=q.code_bits, use_gather_vqmm=use_gather_vqmm,
+                   route_strategy=route_strategy, gather_codebook_duplication=gather_codebook_duplication,
+                   rht_signs=None if rht_signs is None else torch.as_tensor(rht_signs).to(device),
+                   rotation_matrix=None if rotation_matrix is None else torch.as_tensor(rotation_matrix))
 
     def effective_scales(self) -> torch.Tensor:
         return self.scales
 
     def _rht(self, x: torch.Tensor) -> torch.Tensor:
+        """The input transform the weights were quantised under: RHT, or
+        ``x @ rotation_matrix`` in ``x``'s dtype (``switch_linear.py:318-325``)."""
+        if self.rotation_matrix is not None:
+            return x @ self.rotation_matrix.to(x.dtype)
         if self.rht_signs is None:
             return x
         from keep_amd.rht import apply_rht
@@ -246,7 +293,32 @@ class HotTier:
         ops._unpaired_table(self._table)
         hot = self.hot_of_slot.to(torch.int64) & 0xFFFFFFFF
         self._hot32 = torch.where(hot == ops.NO_RESIDUAL, torch.full_like(hot, -1), hot).to(torch.int32)
+        self._rows = self._hot32.cpu().numpy().astype(np.int64)  # host copy of the slot rows (-1: none)
+        self._dirty = False
         self._image = None
+
+    def route_slot(self, slot: int, row: int | None) -> None:
+        """Pool row ``slot`` now holds an expert whose residual row is ``row``
+        (None: an expert without one). The device rows change at the next
+        ``publish()``, in the current stream's order, as a residency cache
+        moves experts between slots (``omlx_lattice.py:274-278``)."""
+        if not 0 <= slot < self._rows.size:
+            raise ValueError(f"slot {slot} out of range for {self._rows.size} pool rows")
+        if row is not None and not 0 <= row < self.rows:
+            raise ValueError(f"residual row {row} out of range for a tier of {self.rows} rows")
+        v = -1 if row is None else int(row)
+        if self._rows[slot] != v:
+            self._rows[slot], self._dirty = v, True
+
+    def publish(self) -> None:
+        """Queue the slot rows changed by ``route_slot`` on the current stream
+        (pinned staging: the host may change them again at once)."""
+        if not self._dirty:
+            return
+        rows = torch.from_numpy(self._rows.astype(np.int32)).pin_memory()
+        self._hot32.copy_(rows, non_blocking=True)
+        self.hot_of_slot.view(torch.int32).copy_(rows, non_blocking=True)  # -1 is NO_RESIDUAL's bits
+        self._dirty = False
 
     def image(self) -> torch.Tensor:
         """The residual table's LDS image for the fused decode layer (built once, on the tier's device)."""
@@ -332,7 +404,7 @@ class QuantizedVQSwitchGLU:
         return self.activation(up, gate)
 
     def _all_e8p(self) -> bool:
-        return all(p.code_bits == 16 and p.bias is None and p.rht_signs is None
+        return all(p.code_bits == 16 and p.bias is None and p.rht_signs is None and p.rotation_matrix is None
                    for p in (self.gate_proj, self.up_proj, self.down_proj))
 
     def _can_use_shared_sorted_route_prefill(self, x: torch.Tensor, indices: torch.Tensor) -> bool:
@@ -625,6 +697,19 @@ def layer_status(workspace: torch.Tensor) -> int:
     out = (_lib.c_uint32 * 1)()
     _lib.call("keep_moe_layer1_status", workspace.data_ptr(), out, ops._stream(workspace.device))
     return int(out[0])
+
+
+def layer_spin_ticks(ticks: int) -> int:
+    """Set the give-up budget of every later one-launch layer call in this
+    process, in ticks of the GPU's 100 MHz real-time counter (default 20000:
+    200 us); returns the previous budget. A call whose wait for another
+    block's SwiGLU output outlasts it returns NaN for the routes that wait
+    held and sets bit 1 of ``layer_status`` (zero the workspace before the
+    next call)."""
+
+    prev = (_lib.c_uint32 * 1)()
+    _lib.call("keep_moe_layer1_set_spin_ticks", int(ticks), prev)
+    return int(prev[0])
 
 
 def _one_launch_ok(device: torch.device, E: int, H: int, I: int, k: int) -> bool:

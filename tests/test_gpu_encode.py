@@ -113,3 +113,52 @@ def test_quantized_vq_linear_from_weights(dev):
     deq = e8p.decode_weight_matrix(codes, scales.astype(np.float32), code_bits=16, dtype=np.float64)
     want = orht.apply_rht(x.cpu().numpy(), signs) @ deq.T
     assert np.abs(y - want).max() <= 2e-3 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("code_bits,transform", [(8, None), (16, None), (16, "rht"), (8, "rotation")])
+def test_quantized_vq_switch_linear_from_weights(dev, code_bits, transform):
+    """Stacked experts ``[E, out, in]`` (switch_linear.py:527-571), with an
+    all-zero row and an all-zero group: codes and fp16 scales bit for bit
+    against the oracle RTN run per expert on the same transformed weights,
+    then a routed forward against the float64 dequantised product."""
+    print(f"switch from_weights: code_bits={code_bits} transform={transform}", flush=True)
+    rng = np.random.default_rng(21 + code_bits)
+    E, N, K, g = 5, 48, 512, 128
+    w = (rng.standard_normal((E, N, K)) * 0.05).astype(np.float32)
+    w[1, 3] = 0.0
+    w[2, 5, :g] = 0.0
+    kw, xform = {}, (lambda a: a)
+    if transform == "rht":
+        signs = np.where(rng.integers(0, 2, K) == 1, 1.0, -1.0).astype(np.float32)
+        kw["rht_signs"] = torch.from_numpy(signs).to(dev)
+        wt = orht.apply_rht_f32(w, signs)  # the GPU RHT is this float32 transform, bit for bit
+        xform = lambda a: orht.apply_rht(a, signs)  # noqa: E731
+    elif transform == "rotation":
+        rot = np.linalg.qr(rng.standard_normal((K, K)))[0].astype(np.float32)
+        kw["rotation_matrix"] = torch.from_numpy(rot).to(dev)
+        # the product's rounding is the GPU GEMM's: take it from there, and pin it to float64 separately
+        wt = (torch.from_numpy(w).to(dev) @ torch.from_numpy(rot).to(dev)).cpu().numpy()
+        assert np.abs(wt - w.astype(np.float64) @ rot.astype(np.float64)).max() <= 1e-5
+        xform = lambda a: a @ rot.astype(np.float64)  # noqa: E731
+    else:
+        wt = w
+    layer = keep_amd.QuantizedVQSwitchLinear.from_weights(torch.from_numpy(w).to(dev), group_size=g,
+                                                          code_bits=code_bits, **kw)
+    assert tuple(layer.codes.shape) == (E, N, K // 8) and tuple(layer.scales.shape) == (E, N, K // g)
+    ref = [oenc.quantize_weight_rtn(wt[e], group_size=g, code_bits=code_bits) for e in range(E)]
+    for e, (codes, scales) in enumerate(ref):
+        np.testing.assert_array_equal(_u(layer.codes[e]), codes, err_msg=f"expert {e}")
+        np.testing.assert_array_equal(layer.scales[e].cpu().numpy(), scales, err_msg=f"expert {e}")
+    assert (ref[1][1][3] == 0).all()  # the zero row stays zero under any transform
+    assert transform is not None or ref[2][1][5, 0] == 0  # the zero group only untransformed (RHT mixes a row)
+    T, k = 4, 3
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    idx = rng.integers(0, E, (T, k)).astype(np.int32)
+    y = layer(torch.from_numpy(x).to(dev), torch.from_numpy(idx).to(dev)).cpu().numpy().astype(np.float64)
+    deq = [e8p.decode_weight_matrix(c, s.astype(np.float32), code_bits=code_bits, dtype=np.float64) for c, s in ref]
+    xt = xform(x.astype(np.float64))
+    want = np.stack([np.stack([deq[idx[t, j]] @ xt[t] for j in range(k)]) for t in range(T)])
+    assert y.shape == want.shape
+    assert np.abs(y - want).max() <= 2e-3 * np.abs(want).max()
+    with pytest.raises(ValueError, match="3D"):
+        keep_amd.QuantizedVQSwitchLinear.from_weights(torch.from_numpy(w[0]).to(dev), group_size=g)

@@ -173,6 +173,44 @@ def test_layer1_graph_replays_match_eager(dev):
         torch.cuda.synchronize()
 
 
+def test_layer1_give_up_path_and_recovery(dev):
+    """A host-set spin budget of 0 ticks: a wave whose first poll finds another
+    block's h not yet written gives up at once (every wait ends), writes NaN
+    for the routes it holds and sets status bit 1; the router's outputs and
+    every finite output equal a normal call's. With the default budget back
+    and the workspace zeroed, the next call equals the normal call bit for bit."""
+    E, I, k = 384, 2048, 6
+    pool = _pool(E, I, None, None, 41)
+    x = synth.rht_activations(1, 4096, seed=42, device=dev)
+    z = synth.router_logits(1, E, seed=43, device=dev)
+    ref, r_ref = keep_amd.moe_layer(x, z, *_pairs(pool), k=k, one_launch=True, workspace=_workspace(dev, k, I))
+    ws = _workspace(dev, k, I)
+    gave_up = False
+    prev = knn.layer_spin_ticks(0)
+    try:
+        for attempt in range(3):
+            print(f"layer1 give-up: budget 0, call {attempt}", flush=True)
+            out, r = keep_amd.moe_layer(x, z, *_pairs(pool), k=k, one_launch=True, workspace=ws)
+            torch.cuda.synchronize()
+            for a, b in zip(r, r_ref):
+                assert torch.equal(a, b)
+            nan = torch.isnan(out)
+            status = knn.layer_status(ws)
+            assert bool(nan.any()) == bool(status & 1), "NaN outputs exactly when a wait gave up"
+            assert torch.equal(out[~nan], ref[~nan])
+            if status & 1:
+                gave_up = True
+                break
+    finally:
+        assert knn.layer_spin_ticks(prev) == 0
+    assert prev == 20000 and gave_up, "no wait gave up under a budget of 0 ticks"
+    ws.zero_()
+    out, r = keep_amd.moe_layer(x, z, *_pairs(pool), k=k, one_launch=True, workspace=ws)
+    assert knn.layer_status(ws) == 0 and torch.equal(out, ref)
+    with pytest.raises(ValueError, match="spin budget"):
+        knn.layer_spin_ticks(100000001)
+
+
 def test_layer1_rejects_unserved(dev):
     E, I, k = 384, 2048, 6
     pool = _pool(E, I, None, None, 1)

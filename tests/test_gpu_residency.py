@@ -15,7 +15,7 @@ import torch
 
 import keep_amd
 from keep_amd import loaders, synth
-from keep_amd.residency import ResidencyCache
+from keep_amd.residency import ROUTED, ResidencyCache, ResidencyPolicy
 from oracle import cpu, e8p, ops
 
 pytestmark = pytest.mark.gpu
@@ -56,7 +56,7 @@ def test_pool_smaller_than_experts_serves_residents_and_installs(dev, tmp_path, 
     for step in range(12):
         cache.begin()
         torch.cuda.synchronize()
-        slot_expert = cache.slot_expert.copy()
+        slot_expert = cache.table().slot_expert()
         resident = cache.resident_mask()
         for s, e in enumerate(slot_expert):  # every routed row holds its expert's file bytes
             if e >= 0:
@@ -66,7 +66,7 @@ def test_pool_smaller_than_experts_serves_residents_and_installs(dev, tmp_path, 
         z_np[0, hot] += 6.0
         z = torch.from_numpy(z_np).to(dev)
         out, r = keep_amd.moe_layer(x, z, pools["w1"], pools["w3"], pools["w2"], k=K,
-                                    bias_served=cache.bias_served, tau=cache.tau, slot_map=cache.slot_map,
+                                    bias_served=cache.bias(), tau=cache.tau, slot_map=cache.slots(),
                                     one_launch=one_launch,
                                     workspace=None if not one_launch else keep_amd.nn.layer_workspace(dev, K, I))
         cache.observe(r)
@@ -90,7 +90,8 @@ def test_pool_smaller_than_experts_serves_residents_and_installs(dev, tmp_path, 
         err = ops.max_rel_err(out.cpu().numpy(), want)
         assert err <= 2e-3, f"step {step}: max rel err {err:.3e}"
     assert cache.stats["installed"] >= 2 and cache.stats["evicted"] >= 2
-    assert all(h in cache.slot_of for h in hot), "strongly demanded experts are resident by now"
+    assert all(h in cache.table().assignment() for h in hot), "strongly demanded experts are resident by now"
+    assert cache.mismatched() == 0
     assert served_hot, "an installed expert was served"
 
 
@@ -113,15 +114,15 @@ def test_route_only_after_copy_event(dev, tmp_path):
     score = np.array([[5.0, 0.1, 0.1, 0.1]], np.float32)
     for _ in range(4):
         cache.begin()
-        cache.pending.setdefault(cache.step, []).append((want, score))
-    assert 30 in cache.reading and 30 not in cache.slot_of
-    assert cache.bias_served[30].item() <= ops.MASKED_BIAS
+        ResidencyPolicy.observe(cache, want, score)  # host demand, as a finished call's
+    assert cache.table().read_at[30] >= 0 and 30 not in cache.table().assignment()
+    assert cache.bias()[30].item() <= ops.MASKED_BIAS
     cache.hold = False
     torch.cuda.synchronize()
     cache.begin()
     torch.cuda.synchronize()
-    slot = cache.slot_of[30]
-    assert cache.bias_served[30].item() == 0.0 and cache.slot_map[30].item() == slot
+    slot = cache.table().assignment()[30]
+    assert cache.bias()[30].item() == 0.0 and cache.slots()[30].item() == slot
     np.testing.assert_array_equal(pools["w3"][0][slot].cpu().numpy().view(np.uint16), layer.read("w3_codes", [30])[0])
 
 
@@ -141,13 +142,13 @@ def test_routed_moe_over_slots_all_paths(dev, tmp_path, T):
                                                 scales=pools[p][1], group_size=K, code_bits=16)
     glu = keep_amd.QuantizedVQSwitchGLU(gate_proj=lin("w1", H, I), up_proj=lin("w3", H, I),
                                         down_proj=lin("w2", I, H))
-    moe = keep_amd.RoutedVQMoE(glu, top_k=K, bias_served=cache.bias_served, slot_map=cache.slot_map)
+    moe = keep_amd.RoutedVQMoE(glu, top_k=K, bias_served=cache.bias(), slot_map=cache.slots())
     x = synth.rht_activations(T, H, seed=T, device=dev)
     z = synth.router_logits(T, E, seed=T + 1, device=dev)
     out, r = moe(x, z)
     bias = np.where(cache.resident_mask(), 0.0, ops.MASKED_BIAS)
     oi, ow, *_ = ops.router_dual_topk(z.cpu().numpy(), bias, np.zeros(E), K)
-    np.testing.assert_array_equal(r.idx.cpu().numpy(), np.vectorize(cache.slot_of.get)(oi))
+    np.testing.assert_array_equal(r.idx.cpu().numpy(), np.vectorize(cache.table().assignment().get)(oi))
     used = np.unique(oi)
     local = np.searchsorted(used, oi).astype(np.int32)
     pick = lambda p: (arrays[f"{p}_codes"][used], arrays[f"{p}_scales"][used].astype(np.float32))  # noqa: E731
@@ -155,3 +156,162 @@ def test_routed_moe_over_slots_all_paths(dev, tmp_path, T):
                           e8p.e8p_packed_abs_grid())
     err = ops.max_rel_err(out.cpu().numpy(), want)
     assert err <= 2e-3, f"max rel err {err:.3e}"
+
+
+def _residual(rng, n_hot):
+    def res(N, Kd):
+        c = rng.integers(0, 256, (n_hot, N, Kd // 8), dtype=np.uint8)
+        s = (np.exp(rng.normal(0, 0.3, (n_hot, N, 1))) * 0.1).astype(np.float16)
+        return c, s
+    return {"gate": res(I, H), "up": res(I, H), "down": res(H, I)}
+
+
+def _check(out, want, tol=2e-3):
+    g = out.float().cpu().numpy()
+    err = ops.max_rel_err(g, want)
+    assert err <= tol, f"max rel err {err:.3e}"
+    assert ops.elementwise_ok(g, want, rtol=tol), "elementwise bound violated"
+
+
+def test_hot_tier_rows_follow_the_residents(dev, tmp_path):
+    """The nested tier over an 8-row pool: the cache's route hook rewrites the
+    tier's slot rows as experts move (omlx_lattice.py:274-278). Hot experts 20
+    and 27 start absent and are installed, one of them into the slot that hot
+    expert 2 (never demanded, the coldest resident) held; expert 5 keeps its
+    row throughout. Every call: each routed slot's tier row is its expert's row, and
+    the fused nested layer matches the float64 oracle in expert space."""
+    print("residency: hot tier rows follow the residents", flush=True)
+    arrays = _write_layer(tmp_path / "layer-00.npz")
+    layer = loaders.LayerFile(tmp_path / "layer-00.npz")
+    pools = _pools(dev)
+    rng = np.random.default_rng(40)
+    hot_row_of = {2: 0, 20: 1, 27: 2, 5: 3}
+    residual = _residual(rng, len(hot_row_of))
+    tier = keep_amd.HotTier(np.full(S, keep_amd.ops.NO_RESIDUAL, np.uint32),
+                            {n: (torch.from_numpy(c).to(dev), torch.from_numpy(s).to(dev))
+                             for n, (c, s) in residual.items()})
+    order = [0, 1, 3, 4, 5, 6, 7, 2] + list(range(8, E))  # 2 in slot 7, the coldest: evicted first
+    cache = ResidencyCache(loaders.ExpertInstaller(layer, pools, dev), E, order, tau=0.2, spare=1, lag=1,
+                           hot_tier=tier, hot_row_of=hot_row_of)
+    assert tier._hot32.cpu().tolist() == [-1, -1, -1, -1, 3, -1, -1, 0]
+    hot_by_expert = np.full(E, keep_amd.ops.NO_RESIDUAL, np.uint32)
+    for e, row in hot_row_of.items():
+        hot_by_expert[e] = row
+    proj = {p: (arrays[f"{p}_codes"], arrays[f"{p}_scales"]) for p in ("w1", "w3", "w2")}
+    x = synth.rht_activations(1, H, seed=41, device=dev)
+    served = set()
+    for step in range(10):
+        cache.begin()
+        torch.cuda.synchronize()
+        slot_expert = cache.table().slot_expert()
+        rows, bits = tier._hot32.cpu().numpy(), tier.hot_of_slot.cpu().numpy().view(np.uint32)
+        for s in cache.table().slots_in(ROUTED):
+            want_row = hot_row_of.get(int(slot_expert[s]), -1)
+            assert rows[s] == want_row and bits[s] == np.uint32(want_row & 0xFFFFFFFF), f"step {step} slot {s}"
+        z_np = rng.standard_normal((1, E)).astype(np.float32)
+        z_np[0, [20, 27]] += 6.0
+        z_np[0, 2] -= 6.0
+        z = torch.from_numpy(z_np).to(dev)
+        out, r = keep_amd.moe_layer(x, z, pools["w1"], pools["w3"], pools["w2"], k=K, bias_served=cache.bias(),
+                                    tau=cache.tau, slot_map=cache.slots(), hot_tier=tier, limit=7.0)
+        cache.observe(r)
+        experts = slot_expert[r.idx.cpu().numpy()]
+        assert (experts >= 0).all()
+        served |= set(experts.ravel().tolist())
+        want = ops.moe_layer(x.float().cpu().numpy(), experts, r.weight.cpu().numpy(), proj["w1"], proj["w3"],
+                             proj["w2"], limit=7.0, h_round="bfloat16", hot_of_slot=hot_by_expert, residual=residual)
+        _check(out, want)
+    assert {20, 27} <= served and 2 not in cache.table().assignment()
+    assert cache.mismatched() == 0
+
+
+def test_prefill_in_pieces_over_the_slots(dev, tmp_path):
+    """Prefill under the wait rule (omlx_lattice.py:427-449) over an 8-row
+    pool: 24 tokens whose demand spans more experts than slots run in pieces;
+    each piece fetches its demand (wait_min 0: every route), then RoutedVQMoE
+    serves exactly that demand from the slots, against the C oracle on the
+    piece's tokens. The next piece's copies queue behind the last run."""
+    print("residency: prefill in pieces", flush=True)
+    arrays = _write_layer(tmp_path / "layer-00.npz")
+    layer = loaders.LayerFile(tmp_path / "layer-00.npz")
+    pools = _pools(dev)
+    cache = ResidencyCache(loaders.ExpertInstaller(layer, pools, dev), E, list(range(E)), tau=float("inf"), lag=1)
+
+    def lin(p, Kd, N):
+        return keep_amd.QuantizedVQSwitchLinear(input_dims=Kd, output_dims=N, num_experts=S, codes=pools[p][0],
+                                                scales=pools[p][1], group_size=Kd, code_bits=16)
+    glu = keep_amd.QuantizedVQSwitchGLU(gate_proj=lin("w1", H, I), up_proj=lin("w3", H, I),
+                                        down_proj=lin("w2", I, H))
+    moe = keep_amd.RoutedVQMoE(glu, top_k=K, bias_served=cache.bias(), slot_map=cache.slots())
+    T = 24
+    x = synth.rht_activations(T, H, seed=51, device=dev)
+    z = synth.router_logits(T, E, seed=52, device=dev)
+    demand = keep_amd.router_dual_topk(z, K)
+    want, score = demand.want.cpu().numpy(), demand.want_score.cpu().numpy()
+    host = {p: (arrays[f"{p}_codes"], arrays[f"{p}_scales"].astype(np.float32)) for p in ("w1", "w3", "w2")}
+    ran = []
+
+    def run(a, b):
+        slot_expert = cache.table().slot_expert()
+        out, r = moe(x[a:b], z[a:b])
+        experts = slot_expert[r.idx.cpu().numpy()]
+        np.testing.assert_array_equal(np.sort(experts, 1), np.sort(want[a:b], 1))
+        used = np.unique(experts)
+        local = np.searchsorted(used, experts).astype(np.int32)
+        pick = lambda p: (host[p][0][used], host[p][1][used])  # noqa: E731
+        ref = cpu.moe_decode(x[a:b].float().cpu().numpy(), local, r.weight.cpu().numpy(), pick("w1"), pick("w3"),
+                             pick("w2"), e8p.e8p_packed_abs_grid())
+        err = ops.max_rel_err(out.float().cpu().numpy(), ref)
+        assert err <= 2e-3, f"piece {a}:{b}: max rel err {err:.3e}"
+        ran.append((a, b))
+    n = cache.run_pieces(want, score, 0.0, run)
+    assert n >= 3 and ran[0][0] == 0 and ran[-1][1] == T and all(p[1] == q[0] for p, q in zip(ran, ran[1:]))
+    assert cache.stats["waits"] >= n - 1 and cache.mismatched() == 0
+
+
+def test_slot_bytes_check_and_stats_log(dev, tmp_path):
+    """The stats log's byte check (omlx_routed.py:138-145,249-260): a routed
+    slot whose device bytes differ from its expert's stored bytes counts."""
+    _write_layer(tmp_path / "layer-00.npz")
+    layer = loaders.LayerFile(tmp_path / "layer-00.npz")
+    pools = _pools(dev)
+    cache = ResidencyCache(loaders.ExpertInstaller(layer, pools, dev), E, list(range(E)), tau=0.2, spare=1, lag=1)
+    assert cache.mismatched() == 0
+    pools["w2"][1][3, 7, 0] += 1.0  # one scale of slot 3
+    assert cache.differing(0, 3) == 1 and cache.differing(0, 2) == 0
+    row = cache.write_log(tmp_path / "stats.jsonl", verify=True)
+    assert row["mismatched"] == 1 and row["step"] == 0
+
+
+def test_one_policy_over_two_layers(dev, tmp_path):
+    """One clock over two layers' pools: begin() once per forward, each
+    layer's demand observed after its call; each layer installs its own
+    strongly demanded expert into its own pool, and the routed layers serve
+    from their own slot maps."""
+    print("residency: two layers", flush=True)
+    files, pools = [], []
+    for li in range(2):
+        _write_layer(tmp_path / f"layer-{li:02d}.npz")
+        files.append(loaders.LayerFile(tmp_path / f"layer-{li:02d}.npz"))
+        pools.append(_pools(dev))
+    cache = ResidencyCache.for_layers(
+        [(loaders.ExpertInstaller(files[li], pools[li], dev), E, list(range(E)) if li == 0 else list(range(E))[::-1])
+         for li in range(2)], tau=0.2, spare=1, lag=1)
+    hot = {0: 25, 1: 3}  # absent at first in each layer (layer 1 starts with 31..24)
+    rng = np.random.default_rng(60)
+    x = synth.rht_activations(1, H, seed=61, device=dev)
+    for _ in range(6):
+        cache.begin()
+        for li in range(2):
+            z_np = rng.standard_normal((1, E)).astype(np.float32)
+            z_np[0, hot[li]] += 6.0
+            _, r = keep_amd.moe_layer(x, torch.from_numpy(z_np).to(dev), pools[li]["w1"], pools[li]["w3"],
+                                      pools[li]["w2"], k=K, bias_served=cache.bias(li), tau=cache.tau,
+                                      slot_map=cache.slots(li))
+            cache.observe(r, li)
+    torch.cuda.synchronize()
+    for li in range(2):
+        assert hot[li] in cache.table(li).assignment()
+        assert cache.bias(li)[hot[li]].item() == 0.0
+        assert cache.slots(li)[hot[li]].item() == cache.table(li).assignment()[hot[li]]
+    assert cache.mismatched() == 0
