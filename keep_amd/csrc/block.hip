@@ -52,6 +52,7 @@ using namespace keep;
 
 extern "C" int keep_moe_combine_add(const float* routed, const void* shared, int shared_dtype, const void* residual,
                                     int residual_dtype, int64_t n, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(n);
   KEEP_REQUIRE(dtype_ok(out_dtype) && (!shared || dtype_ok(shared_dtype)) && (!residual || dtype_ok(residual_dtype)),
                "bad dtype enum");
   KEEP_REQUIRE(n >= 0, "n must be >= 0");

@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "../../include/keep_amd.h"
 
 namespace keep {
@@ -40,6 +42,16 @@ int launch_status(const char* what);
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 inline int dtype_size(int dt) { return dt == KEEP_F32 ? 4 : 2; }
 inline bool dtype_ok(int dt) { return dt == KEEP_F32 || dt == KEEP_F16 || dt == KEEP_BF16; }
+// Every size an entry point takes lies in [0, 2^31) (the kernels index in 32
+// bits). Checked first, so that the products later checks form (two sizes, or
+// a size and a small constant) cannot overflow int64.
+constexpr int64_t KEEP_DIM_LIMIT = int64_t(1) << 31;
+inline bool dims_ok(std::initializer_list<int64_t> dims) {
+  for (int64_t d : dims)
+    if (d < 0 || d >= KEEP_DIM_LIMIT) return false;
+  return true;
+}
+#define KEEP_REQUIRE_DIMS(...) KEEP_REQUIRE(::keep::dims_ok({__VA_ARGS__}), "every size must be in [0, 2^31)")
 
 // ---------------------------------------------------------------- element types
 struct bf16s {

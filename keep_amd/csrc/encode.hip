@@ -190,6 +190,7 @@ using namespace keep;
 extern "C" int keep_vq_encode(const float* vectors, int64_t n, int code_bits, const float* diagonal, int diag_mode,
                               const uint32_t* table, const float* scales, int64_t vectors_per_scale, void* codes,
                               void* stream) {
+  KEEP_REQUIRE_DIMS(n, vectors_per_scale);
   KEEP_REQUIRE(code_bits == 8 || code_bits == 16, "code_bits must be 8 or 16, got %d", code_bits);
   KEEP_REQUIRE(diag_mode >= 0 && diag_mode <= 2, "diag_mode must be 0 (none), 1 (shared [8]) or 2 (per vector)");
   KEEP_REQUIRE(n >= 0, "n must be >= 0");
@@ -207,6 +208,7 @@ extern "C" int keep_vq_encode(const float* vectors, int64_t n, int code_bits, co
 
 extern "C" int keep_group_absmax(const float* x, int64_t groups_total, int64_t group_size, float divisor,
                                  float* scales, void* stream) {
+  KEEP_REQUIRE_DIMS(groups_total, group_size);
   KEEP_REQUIRE(groups_total >= 0 && group_size >= 1, "bad group sizes");
   KEEP_REQUIRE(divisor > 0.f, "divisor must be positive");
   if (groups_total == 0) return KEEP_OK;

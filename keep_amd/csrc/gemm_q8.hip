@@ -652,6 +652,7 @@ using namespace keep;
 // Workspace of the grouped GEMMs: one (r, 1 / r) pair per row of bf16 / fp32 input
 // (fp16 input uses none).
 extern "C" int64_t keep_vq_grouped_gemm_q8_workspace_bytes(int64_t x_rows, int64_t K) {
+  if (!::keep::dims_ok({x_rows, K})) return -1;
   if (x_rows < 0 || K <= 0) return -1;
   return gq_ws_bytes(x_rows);
 }
@@ -663,6 +664,7 @@ extern "C" int keep_vq_grouped_gemm_q8(const void* x, int x_dtype, int64_t x_row
                                        int64_t routes, int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
                                        void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
                                        void* stream) {
+  KEEP_REQUIRE_DIMS(x_rows, n_tiles, routes, num_experts, N, K, group_size);
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(code_bits == 16 || code_bits == 8, "code_bits must be 16 (E8P) or 8 (residual E8)");
@@ -707,6 +709,7 @@ extern "C" int keep_vq_grouped_swiglu_q8(const void* x, int x_dtype, int64_t x_r
                                          int64_t routes, int64_t num_experts, int64_t I, int64_t H,
                                          int64_t group_size, float swiglu_limit, void* workspace,
                                          int64_t workspace_bytes, void* h_out, void* stream) {
+  KEEP_REQUIRE_DIMS(x_rows, n_tiles, routes, num_experts, I, H, group_size);
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
   KEEP_REQUIRE(dtype_ok(scale_dtype), "bad dtype enum");
   KEEP_REQUIRE(gq_shape_ok(H, group_size),
@@ -759,6 +762,7 @@ extern "C" int keep_vq_grouped_swiglu_nested_q8(
     const uint32_t* res_table, const int32_t* tile_expert, const int32_t* tile_offset, const int32_t* tile_count,
     int64_t n_tiles, int64_t routes, int64_t num_experts, int64_t I, int64_t H, float swiglu_limit,
     void* workspace, int64_t workspace_bytes, void* h_out, void* stream) {
+  KEEP_REQUIRE_DIMS(x_rows, hot_rows, n_tiles, routes, num_experts, I, H);
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
   KEEP_REQUIRE(dtype_ok(scale_dtype), "bad dtype enum");
   KEEP_REQUIRE(gq_shape_ok(H, H), "grouped GEMM needs H a multiple of %d (H=%lld)", GQ_KB, (long long)H);
@@ -797,6 +801,7 @@ extern "C" int keep_vq_grouped_gemm_nested_q8(
     const int32_t* tile_expert, const int32_t* tile_offset, const int32_t* tile_count, int64_t n_tiles,
     int64_t routes, int64_t num_experts, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* out,
     int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(x_rows, hot_rows, n_tiles, routes, num_experts, N, K);
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16 || x_dtype == KEEP_F32, "bad activation dtype");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(gq_shape_ok(K, K), "grouped GEMM needs K a multiple of %d (K=%lld)", GQ_KB, (long long)K);
@@ -828,6 +833,7 @@ extern "C" int keep_vq_grouped_gemm_nested_q8(
 
 extern "C" int keep_route_combine(const float* y, const float* w, int64_t T, int64_t k, int64_t H, void* out,
                                   int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(T, k, H);
   KEEP_REQUIRE(dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(T >= 0 && k >= 1 && H >= 4 && H % 4 == 0, "need k >= 1 and H a multiple of 4");
   if (T == 0) return KEEP_OK;

@@ -496,10 +496,11 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
 int64_t fl_workspace_bytes(int64_t k, int64_t I) { return FL_HDR_BYTES + k * I * 4; }
 
 bool fl_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
+  if (!(H == 4096 && I % 512 == 0 && I >= 512 && I <= 2048 && k >= 1 && k <= 8 && k <= E && E <= 1024))
+    return false;  // bounds first: the products below stay small
   const int64_t qtiles = k * I / 16;
-  return H == 4096 && I % 512 == 0 && I >= 512 && I <= 2048 && k >= 1 && k <= 8 && k <= E && E <= 1024 &&
-         (qtiles + FL_BLOCKS - 1) / FL_BLOCKS <= 4 && group_h % 256 == 0 && group_i % 256 == 0 &&
-         k <= 4 * (FL_WAVES / (I / 256));
+  return (qtiles + FL_BLOCKS - 1) / FL_BLOCKS <= 4 && group_h >= 256 && group_h % 256 == 0 && group_i >= 256 &&
+         group_i % 256 == 0 && k <= 4 * (FL_WAVES / (I / 256));
 }
 
 // All FL_BLOCKS blocks must be resident together: one block per CU.
@@ -586,6 +587,7 @@ void fl_launch(const float* logits, const float* bias_s, const float* bias_d, in
 using namespace keep;
 
 extern "C" int64_t keep_moe_layer1_workspace_bytes(int64_t k, int64_t I) {
+  if (!::keep::dims_ok({k, I})) return -1;
   if (k < 1 || I < 1) return -1;
   return fl_workspace_bytes(k, I);
 }
@@ -618,6 +620,7 @@ extern "C" int keep_moe_layer1(const float* logits, const float* bias_served, co
                                int64_t group_size_h, int64_t group_size_i, const void* prepared, float swiglu_limit,
                                int32_t* idx, float* w, int32_t* want, float* want_score, uint8_t* admit,
                                void* workspace, int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(num_slots, E, k, H, I, group_size_h, group_size_i);
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);

@@ -528,6 +528,7 @@ using namespace keep;
 extern "C" int keep_e8p_decode(const uint16_t* codes, int64_t n, const uint32_t* table, const void* scales,
                                int scale_dtype, int64_t codewords_per_row, int64_t group_codewords, float* out,
                                void* stream) {
+  KEEP_REQUIRE_DIMS(n, codewords_per_row, group_codewords);
   KEEP_REQUIRE(n >= 0, "n must be >= 0");
   if (n == 0) return KEEP_OK;
   KEEP_REQUIRE(codes && table && out, "codes, table and out must be non-null");
@@ -548,6 +549,7 @@ extern "C" int keep_e8p_decode(const uint16_t* codes, int64_t n, const uint32_t*
 extern "C" int keep_e8_1bit_decode(const uint8_t* codes, int64_t n, const uint32_t* table, const void* scales,
                                    int scale_dtype, int64_t codewords_per_row, int64_t group_codewords, float* out,
                                    void* stream) {
+  KEEP_REQUIRE_DIMS(n, codewords_per_row, group_codewords);
   KEEP_REQUIRE(n >= 0, "n must be >= 0");
   if (n == 0) return KEEP_OK;
   KEEP_REQUIRE(codes && table && out, "codes, table and out must be non-null");
@@ -571,6 +573,7 @@ extern "C" int keep_vq_matvec(const void* x, int x_dtype, int64_t x_rows, const 
                               int64_t K, int64_t group_size, const uint8_t* res_codes, const void* res_scales,
                               int64_t res_group_size, const uint32_t* res_table, const uint32_t* hot_of_slot,
                               int64_t num_hot, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(x_rows, routes, x_div, num_experts, N, K, group_size, res_group_size, num_hot);
   KEEP_REQUIRE(code_bits == 8 || code_bits == 16, "code_bits must be 8 or 16, got %d", code_bits);
   KEEP_REQUIRE(dtype_ok(x_dtype) && dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(N > 0 && K > 0 && K % 8 == 0, "need N > 0 and K > 0 divisible by 8 (N=%lld K=%lld)", (long long)N,
@@ -634,6 +637,7 @@ extern "C" int keep_vq_matvec_tiles(const void* x, int x_dtype, int64_t x_rows, 
                                     const int32_t* tile_offset, const int32_t* tile_count, int64_t n_tiles,
                                     int64_t m_rows, int64_t num_experts, int64_t N, int64_t K, int64_t group_size,
                                     void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(x_rows, routes, n_tiles, m_rows, num_experts, N, K, group_size);
   KEEP_REQUIRE(dtype_ok(x_dtype) && dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(code_bits == 8 || code_bits == 16, "code_bits must be 8 or 16, got %d", code_bits);
   KEEP_REQUIRE(N > 0 && K > 0 && K % 8 == 0, "need N > 0 and K divisible by 8");
@@ -715,7 +719,8 @@ static int moe_common(bool gateup, bool down, const char* what, const void* x, i
   a.cpg_i = group_size_i / 8; a.table = table; a.limit = swiglu_limit; a.h = h_work; a.out = out; a.odt = out_dtype;
   a.rb_gu = (I + MV_WAVES * MV_ROWS - 1) / (MV_WAVES * MV_ROWS);
   a.rb_d = (H + MV_WAVES * MV_ROWS - 1) / (MV_WAVES * MV_ROWS);
-  KEEP_REQUIRE(a.rb_gu * T * k <= 0x7fffffffLL && a.rb_d * T <= 0x7fffffffLL, "too many blocks");
+  KEEP_REQUIRE(T * k <= 0x7fffffffLL && a.rb_gu * (T * k) <= 0x7fffffffLL && a.rb_d * T <= 0x7fffffffLL,
+               "too many blocks");
   hipStream_t s = (hipStream_t)stream;
   if (x_dtype == KEEP_F16) launch_moe<_Float16>(ch_h, ch_i, gateup, down, s, a);
   else launch_moe<bf16s>(ch_h, ch_i, gateup, down, s, a);
@@ -729,6 +734,7 @@ extern "C" int keep_moe_decode(const void* x, int x_dtype, int64_t T, int64_t H,
                                int64_t group_size_h, int64_t group_size_i, const uint32_t* table,
                                const void* prepared, float swiglu_limit, void* h_work, void* out, int out_dtype,
                                void* stream) {
+  KEEP_REQUIRE_DIMS(T, H, I, k, num_experts, group_size_h, group_size_i);
   return moe_common(true, true, "keep_moe_decode", x, x_dtype, T, H, I, idx, w, k, num_experts, gate_codes,
                     gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype, group_size_h,
                     group_size_i, table, prepared, swiglu_limit, h_work, out, out_dtype, stream);
@@ -739,6 +745,7 @@ extern "C" int keep_moe_gateup(const void* x, int x_dtype, int64_t T, int64_t H,
                                const void* gate_scales, const uint16_t* up_codes, const void* up_scales,
                                int scale_dtype, int64_t group_size_h, const uint32_t* table, const void* prepared,
                                float swiglu_limit, void* h_work, void* stream) {
+  KEEP_REQUIRE_DIMS(T, H, I, k, num_experts, group_size_h);
   return moe_common(true, false, "keep_moe_gateup", x, x_dtype, T, H, I, idx, w, k, num_experts, gate_codes,
                     gate_scales, up_codes, up_scales, nullptr, nullptr, scale_dtype, group_size_h, I, table,
                     prepared, swiglu_limit, h_work, nullptr, KEEP_F32, stream);
@@ -748,6 +755,7 @@ extern "C" int keep_moe_down(int h_dtype, int64_t T, int64_t H, int64_t I, const
                              int64_t k, int64_t num_experts, const uint16_t* down_codes, const void* down_scales,
                              int scale_dtype, int64_t group_size_i, const uint32_t* table, const void* prepared,
                              const void* h_work, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(T, H, I, k, num_experts, group_size_i);
   return moe_common(false, true, "keep_moe_down", nullptr, h_dtype, T, H, I, idx, w, k, num_experts, nullptr,
                     nullptr, nullptr, nullptr, down_codes, down_scales, scale_dtype, H, group_size_i, table,
                     prepared, 0.f, const_cast<void*>(h_work), out, out_dtype, stream);
@@ -757,6 +765,7 @@ extern "C" int keep_e8_1bit_matvec(const void* x, int x_dtype, int64_t x_rows, c
                                    const void* scales, int scale_dtype, const uint32_t* table, const uint32_t* rhs,
                                    int64_t routes, int64_t x_div, int64_t num_experts, int64_t N, int64_t K,
                                    int64_t group_size, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(x_rows, routes, x_div, num_experts, N, K, group_size);
   KEEP_REQUIRE(dtype_ok(x_dtype) && dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(N > 0 && K > 0 && K % 8 == 0, "need N > 0 and K > 0 divisible by 8 (N=%lld K=%lld)", (long long)N,
                (long long)K);

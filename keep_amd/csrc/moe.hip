@@ -38,6 +38,7 @@ extern "C" int keep_e8p_prepared_bytes(void) { return PREPARED_TOTAL; }
 
 extern "C" int keep_moe_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_size_h,
                                         int64_t group_size_i) {
+  if (!::keep::dims_ok({E, H, I, k, group_size_h, group_size_i})) return 0;
   return moe_q_layer_supported(E, H, I, k, group_size_h, group_size_i) ? 1 : 0;
 }
 
@@ -50,6 +51,7 @@ extern "C" int keep_moe_layer(const float* logits, const float* bias_served, con
                               const void* prepared, float swiglu_limit, int32_t* idx, float* w, int32_t* want,
                               float* want_score, uint8_t* admit, void* h_work, void* out, int out_dtype,
                               void* stream) {
+  KEEP_REQUIRE_DIMS(num_slots, E, k, H, I, group_size_h, group_size_i);
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);
@@ -118,6 +120,7 @@ extern "C" int keep_moe_layer_noalloc(const float* logits, const float* bias_ser
                                       const void* prepared, float swiglu_limit, int32_t* idx, float* w,
                                       int32_t* want, float* want_score, uint8_t* admit, void* out, int out_dtype,
                                       void* stream) {
+  KEEP_REQUIRE_DIMS(num_slots, E, k, H, I, group_size_h, group_size_i);
   KEEP_REQUIRE(k >= 1 && I >= 1 && k * I <= NOALLOC_H_ELEMS,
                "keep_moe_layer_noalloc holds at most %lld SwiGLU values (k * I) in its static scratch, got %lld",
                (long long)NOALLOC_H_ELEMS, (long long)(k * I));

@@ -537,9 +537,11 @@ void tq_build(const uint32_t* table, void* prepared, hipStream_t s) {
 }
 
 bool moe_q_layer_supported(int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
+  if (!(H == 4096 && I >= 512 && I % 512 == 0 && I <= 2048 && k >= 1 && k <= 8 && k <= E && E <= 1024))
+    return false;  // bounds first: the products below stay small
   const int64_t qtiles = k * I / 16;
-  return H == 4096 && I % 512 == 0 && I <= 2048 && k >= 1 && k <= 8 && k <= E && E <= 1024 &&
-         (qtiles + 255) / 256 <= 3 && group_h % 256 == 0 && group_i % 256 == 0;
+  return (qtiles + 255) / 256 <= 3 && group_h >= 256 && group_h % 256 == 0 && group_i >= 256 &&
+         group_i % 256 == 0;
 }
 
 void moe_q_down_launch(const int32_t* idx, const float* w, int64_t k, int64_t E, int64_t H, int64_t I,
@@ -647,6 +649,7 @@ extern "C" int keep_moe_layer_nested(
     const uint8_t* res_gate_codes, const void* res_gate_scales, const uint8_t* res_up_codes,
     const void* res_up_scales, const uint8_t* res_down_codes, const void* res_down_scales, int res_scale_dtype,
     int64_t res_group_size_h, int64_t res_group_size_i, const void* res_image, int32_t* hot_route, void* stream) {
+  KEEP_REQUIRE_DIMS(num_slots, E, k, H, I, group_size_h, group_size_i, num_hot, res_group_size_h, res_group_size_i);
   KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
   KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype) && dtype_ok(res_scale_dtype), "bad dtype enum");
   KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);

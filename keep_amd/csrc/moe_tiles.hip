@@ -502,12 +502,14 @@ extern "C" int keep_route_plan(const int32_t* rhs, int64_t R, int64_t E, int64_t
                                void* stream);
 
 extern "C" int64_t keep_moe_tiles_workspace_bytes(int64_t T, int64_t k, int64_t num_experts, int64_t H) {
+  if (!::keep::dims_ok({T, k, num_experts, H})) return -1;
   if (T < 0 || k < 1 || num_experts < 1 || H < 256) return -1;
   return (int64_t)mt_layout(T, k, num_experts, H).total;
 }
 
 extern "C" int keep_moe_tiles_supported(int64_t T, int64_t num_experts, int64_t H, int64_t I, int64_t k,
                                         int64_t group_size_h, int64_t group_size_i) {
+  if (!::keep::dims_ok({T, num_experts, H, I, k, group_size_h, group_size_i})) return 0;
   return moe_tiles_supported(T, num_experts, H, I, k, group_size_h, group_size_i) ? 1 : 0;
 }
 
@@ -586,6 +588,7 @@ extern "C" int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, 
                               int64_t group_size_h, int64_t group_size_i, const void* prepared, float swiglu_limit,
                               void* h_work, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
                               void* stream) {
+  KEEP_REQUIRE_DIMS(T, H, I, k, num_experts, group_size_h, group_size_i);
   const int chk = mt_check(x, x_dtype, T, H, I, k, num_experts, gate_codes, gate_scales, up_codes, up_scales,
                            down_codes, down_scales, scale_dtype, group_size_h, group_size_i, prepared, h_work,
                            workspace, workspace_bytes, out, out_dtype);
@@ -629,6 +632,7 @@ extern "C" int keep_moe_tiles_layer(const float* logits, const float* bias_serve
                                     const void* prepared, float swiglu_limit, int32_t* idx, float* w, int32_t* want,
                                     float* want_score, uint8_t* admit, void* h_work, void* workspace,
                                     int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(num_slots, num_experts, k, T, H, I, group_size_h, group_size_i);
   KEEP_REQUIRE(num_experts >= 1 && num_experts <= 64 * RT_MAX_PER_LANE, "num_experts must be in 1..%d",
                64 * RT_MAX_PER_LANE);
   KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);

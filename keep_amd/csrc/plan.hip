@@ -20,6 +20,7 @@ extern "C" int keep_route_plan(const int32_t* rhs, int64_t R, int64_t E, int64_t
                                int32_t* inverse, int32_t* counts, int32_t* offsets, int32_t* tile_expert,
                                int32_t* tile_offset, int32_t* tile_count, int64_t max_tiles, int32_t* n_tiles_out,
                                void* stream) {
+  KEEP_REQUIRE_DIMS(R, E, tile, max_tiles);
   KEEP_REQUIRE(R >= 0 && R <= 0x7fffffffLL, "bad route count");
   KEEP_REQUIRE(E >= 1 && E <= PLAN_MAX_E, "E must be in 1..%d", PLAN_MAX_E);
   KEEP_REQUIRE(tile >= 1 && tile <= 4096, "tile must be in 1..4096");

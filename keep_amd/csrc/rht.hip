@@ -242,6 +242,7 @@ void launch_rht(const void* x, int xdt, const float* signs, int inverse, int64_t
 
 extern "C" int keep_rht(const void* x, int x_dtype, const float* signs, int inverse, int64_t T, int64_t n, void* out,
                         int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(T, n);
   KEEP_REQUIRE(dtype_ok(x_dtype) && dtype_ok(out_dtype), "bad dtype enum");
   KEEP_REQUIRE(n > 0 && (n & (n - 1)) == 0, "RHT dimension must be a positive power of two");
   KEEP_REQUIRE(T >= 0 && T <= 0x7FFFFFFF, "row count out of range");
@@ -291,6 +292,7 @@ void launch_norm_quant(const void* x, int xdt, const void* gamma, int gdt, float
 extern "C" int keep_rmsnorm_quant_rht(const void* x, int x_dtype, int64_t T, int64_t n, const void* gamma,
                                       int gamma_dtype, float eps, int64_t quant_block, int pow2_scales,
                                       const float* signs, void* normed, void* out, int out_dtype, void* stream) {
+  KEEP_REQUIRE_DIMS(T, n, quant_block);
   KEEP_REQUIRE(dtype_ok(x_dtype) && dtype_ok(out_dtype) && (!gamma || dtype_ok(gamma_dtype)), "bad dtype enum");
   KEEP_REQUIRE(n >= 64 && n <= (1 << RHT_MAX_LOG) && (n & (n - 1)) == 0,
                "keep_rmsnorm_quant_rht serves power-of-two rows of 64..8192 values, got %lld", (long long)n);

@@ -49,6 +49,7 @@ extern "C" int keep_router_dual_topk(const float* logits, int64_t T, int64_t E, 
                                      const float* bias_demand, int score_func, int renormalize, float route_scale,
                                      float tau, const int32_t* slot_map, int64_t num_slots, int32_t* idx, float* w,
                                      int32_t* want, float* want_score, uint8_t* admit, void* stream) {
+  KEEP_REQUIRE_DIMS(T, E, k, num_slots);
   KEEP_REQUIRE(T >= 0, "T must be >= 0");
   KEEP_REQUIRE(E >= 1 && E <= 64 * RT_MAX_PER_LANE, "E must be in 1..%d, got %lld", 64 * RT_MAX_PER_LANE,
                (long long)E);

@@ -182,14 +182,23 @@ def swiglu(gate, up, limit: float = 0.0) -> np.ndarray:
     return g / (1.0 + np.exp(-g)) * u
 
 
-def round_bf16(a) -> np.ndarray:
-    """Round to bfloat16 (nearest even) and back to float64."""
+BF16_MAX = (2.0 - 2.0 ** -7) * 2.0 ** 127
 
-    f = np.asarray(a, dtype=np.float32)
-    u = f.view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
-    out = u.astype(np.uint32).view(np.float32).astype(np.float64)
-    return np.where(np.isnan(f), np.nan, out)
+
+def round_bf16(a) -> np.ndarray:
+    """Round float32 or float64 values once to bfloat16 (nearest, ties to even;
+    beyond the largest finite value to +-inf; subnormals on the 2^-133 grid),
+    returned as float64. The step is 2^(e - 7) for |a| in [2^e, 2^(e+1)), and
+    ``np.round`` of the exact quotient by it rounds half to even."""
+
+    with np.errstate(invalid="ignore"):  # NaN payloads widen quietly
+        x = np.asarray(a, dtype=np.float64)
+    _, ex = np.frexp(x)  # |x| in [2^(ex-1), 2^ex)
+    step = np.ldexp(1.0, np.maximum(ex - 8, -133))
+    with np.errstate(invalid="ignore", over="ignore"):
+        r = np.round(x / step) * step
+        r = np.where(np.abs(r) > BF16_MAX, np.copysign(np.inf, x), r)
+    return np.where(np.isfinite(x), r, x)
 
 
 def moe_layer(x, idx, w, gate, up, down, *, limit=0.0, h_round=None, hot_of_slot=None,

@@ -78,9 +78,9 @@ def test_router_fewer_resident_than_k(dev):
                                                 (1025, 1, 4, False, 0), (12288, 384, 64, True, 0),
                                                 (300, 16, 8, False, 21), (20000, 384, 64, False, 130)])
 def test_route_plan_exact(dev, R, E, tile, skew, bad):
-    # each of the plan's 16 waves ranks a contiguous range of ceil(R / 16) routes (R = 6: most
-    # waves hold none); `bad` routes get expert ids outside [0, E): they sort last, in tiles of
-    # expert -1
+    # each of the plan's 16 waves ranks a contiguous range of max(64, ceil(R / 16)) routes (R = 6:
+    # one wave holds them all); `bad` routes get expert ids outside [0, E): they sort last, in tiles
+    # of expert -1
     rng = np.random.default_rng(R + E)
     rhs = rng.integers(0, E, size=R).astype(np.int32)
     if skew:  # a few hot experts: long same-expert runs inside each wave

@@ -58,3 +58,45 @@ def test_quantize_scale_divisor_is_the_grids_largest_magnitude():
     codes, scales = oenc.quantize_weight_rtn(w, group_size=16, code_bits=16)
     assert scales.tolist() == [[0.0], [1.0]]  # a zero group keeps scale 0 (it divided by 1)
     np.testing.assert_array_equal(codes, oenc.nearest(w.reshape(-1, 8), 16).reshape(2, 2))
+
+
+def _rtn_vectors(n, code_bits, seed, group=512):
+    """Vectors as the RTN feeds them to the search: Gaussian rows divided by max |w| / the grid's largest value."""
+    w = np.random.default_rng(seed).standard_normal((n * 8 // group, group)).astype(np.float32)
+    div = np.float32(np.abs(oenc.grid(code_bits)).max())
+    s = (np.abs(w).max(axis=1) / div).astype(np.float32)
+    return (w / s[:, None]).astype(np.float32).reshape(-1, 8)
+
+
+@pytest.mark.parametrize("code_bits", [8, 16])
+def test_float32_search_restatement_pins(code_bits):
+    """The float32 restatement of the reference's searches returns every
+    codeword's own code, and on dyadic inputs (exact in float32) without a tie
+    the exact scan's code."""
+    g = oenc.grid(code_bits)
+    np.testing.assert_array_equal(oenc.nearest_f32(g, code_bits), np.arange(len(g)))
+    rng = np.random.default_rng(3)
+    v = (rng.integers(-24, 25, (4000 if code_bits == 8 else 800, 8)) / 8.0).astype(np.float32)
+    v64, g64 = v.astype(np.float64), g.astype(np.float64)
+    # exact in float64: every term is a multiple of 1/32 below 2^10
+    d = (v64 * v64).sum(1)[:, None] + (g64 * g64).sum(1)[None, :] - 2 * v64 @ g64.T
+    part = np.partition(d, 1, axis=1)
+    clear = part[:, 1] > part[:, 0]
+    assert clear.sum() > len(v) // 4
+    np.testing.assert_array_equal(oenc.nearest_f32(v[clear], code_bits), d[clear].argmin(1))
+
+
+@pytest.mark.parametrize("code_bits,n", [(8, 1_000_000), (16, 65536)])
+def test_float32_search_agrees_with_the_exact_scan(code_bits, n):
+    """Agreement of the reference's float32 search with the exact scan on RTN
+    inputs: 8-bit, 0 of 1e6 differ; E8P, 2 of 1e6 differ (measured once over
+    1e6; this test takes 65,536). Every difference is a near-tie: the float32
+    pick is farther by at most 1e-6 (|v|^2 + 1) in exact distance."""
+    v = _rtn_vectors(n, code_bits, seed=11)
+    ex, f = oenc.nearest(v, code_bits), oenc.nearest_f32(v, code_bits)
+    dis = np.flatnonzero(ex != f)
+    assert dis.size <= max(2, n // 10000)
+    g = oenc.grid(code_bits).astype(np.float64)
+    vv = v[dis].astype(np.float64)
+    gap = ((vv - g[f[dis]]) ** 2).sum(1) - ((vv - g[ex[dis]]) ** 2).sum(1)
+    assert ((gap >= 0) & (gap <= 1e-6 * ((vv ** 2).sum(1) + 1))).all()
