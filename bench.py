@@ -23,7 +23,14 @@ and the median and minimum per layer over those samples are reported beside it.
 events on the stream it is launched on. ``cpu_baseline`` times the C/OpenMP restatement
 of the same layer (``oracle/cpu_ref.c``) on the host.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--config {1,2,3,4,5}]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-extra-configs]
+[--config {1,2,3,4,5}]
+
+The default line also carries ``config3_verify`` (8, 16 and 64 tokens through
+the same layer, each with its HBM roofline over the distinct experts read) and
+``config4_prefill`` (2048 tokens, the grouped GEMMs, with the fp16
+matrix-core roofline and the matrix-core busy share from the committed
+counter summary), measured on the same expert pool after the headline.
 
 ``--config`` other than 2 measures the BASELINE's other configurations, one
 JSON line per workload, with the same fields (they are parity-test shapes of
@@ -51,6 +58,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16 matrix-core peak of the MI355X
 # the arithmetic of the int8 matrix-core paths (decode layer, few-token tiles): decoded E8P weights x 4 are exact int8; activations are split
 # exactly into int8 terms under a power-of-two scale (residual below the fp32 rounding of the sums)
 DTYPE_Q8 = ("fp16 activations x E8P-2bit (uint16) codes on the int8 matrix cores: x as 3 int8 terms per "
@@ -76,6 +84,20 @@ TWO_LAUNCH_KERNELS = ("k_moeq_route_gateup", "k_moeq_down")  # keep_moe_layer, t
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_layer_config2_counters.md")
 PROFILE_C4 = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "grouped_gemm_config4_kernel_trace.md")
 PREFILL_KERNELS = ("k_gemm_e8_gateup", "k_gemm_e8_down")  # the two grouped GEMMs of a config-4 layer
+
+
+def mfma_busy(kernels, profile):
+    """Matrix-core busy % of each of `kernels` from the committed counter summary (None if absent)."""
+    found = {}
+    try:
+        with open(profile) as f:
+            for line in f:
+                m = re.match(r"mfma_busy_pct\[(\w+)\] = ([0-9.]+)", line.strip())
+                if m:
+                    found[m.group(1)] = float(m.group(2))
+    except OSError:
+        return None
+    return {k: found[k] for k in kernels if k in found} or None
 
 
 def measured_traffic(kernels, profile=PROFILE):
@@ -108,6 +130,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
                     help="BASELINE configuration to measure (2: the headline decode layer)")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="skip the config-3 (verify) and config-4 (prefill) keys of the default line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy kernel (torch.neg, fp16) 8 times, the known-size "
                          "reference that scales FETCH_SIZE / WRITE_SIZE counter readings to bytes")
@@ -336,10 +360,41 @@ def main() -> int:
                                        "profiles/moe_layer_config2_counters.md"},
         "cpu_baseline": None,
     }
+    if not args.no_extra_configs:
+        result.update(extra_configs(torch, stream, gate, up, down, table))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, gate, up, down, x, idx, w, table, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def extra_configs(torch, stream, gate, up, down, table) -> dict:
+    """Configs 3 and 4 on the config-2 pool (the same 384 x 4096 / 2048 experts): speculative verify at
+    8, 16 and 64 tokens (the whole layer from the logits; HBM roofline over the distinct experts read)
+    and prefill at 2048 tokens (the experts' grouped GEMMs; fp16 matrix-core roofline)."""
+
+    from keep_amd.nn import QuantizedVQSwitchGLU, QuantizedVQSwitchLinear, RoutedVQMoE
+
+    def lin(pj, K, Nn):
+        return QuantizedVQSwitchLinear(input_dims=K, output_dims=Nn, num_experts=E, codes=pj.codes, scales=pj.scales,
+                                       codebook=table, group_size=K, code_bits=16)
+
+    glu = QuantizedVQSwitchGLU(gate_proj=lin(gate, H, I), up_proj=lin(up, H, I), down_proj=lin(down, I, H))
+    moe = RoutedVQMoE(glu, top_k=K_TOP)
+    expert_b = 2 * projection_bytes(I, H) + projection_bytes(H, I)
+    fpr = 2 * 3 * H * I
+    c3 = {}
+    for T in (8, 16, 64):
+        log(f"bench: config 3, {T} tokens")
+        c3[f"T{T}"] = verify_point(torch, stream, moe, E, K_TOP, H, I, T, expert_b, fpr)
+    log("bench: config 4, 2048 tokens")
+    c4 = prefill_point(torch, stream, moe, E, K_TOP, H, I, 2048, expert_b, fpr)
+    log("bench: config 3 " + ", ".join(f"T={v['tokens']} {v['us_per_layer']} us" for v in c3.values())
+        + f" | config 4 {c4['us_per_layer']} us, {c4['tflops']} TFLOP/s")
+    return {"config3_verify": {"workload": "config 3: speculative verify through the config-2 layer (router + fused "
+                                           "gate/up/SwiGLU + down/combine), fresh logits per call",
+                               "metric_unit": "GB/s over the distinct experts read", **c3},
+            "config4_prefill": c4}
 
 
 def measure_component(args) -> int:
@@ -606,75 +661,100 @@ def other_config(args) -> int:
     moe = RoutedVQMoE(glu, top_k=k, bias_served=bias, bias_demand=None if cfg == 5 else bias,
                       tau=0.3 if cfg == 5 else float("inf"))
     sizes = {3: [8, 16, 64], 4: [2048], 5: [1, 512]}[cfg]
-    n_sets = 16
     for T in sizes:
-        x = synth.rht_activations(T, H, seed=30 + T, device=dev)
         if cfg == 4:
-            idx_np = [synth.zipf_routes(T, E, k, s=1.1, seed=40 + i) for i in range(4)]
-            idx = [torch.from_numpy(a).to(dev) for a in idx_np]
-            wts = [torch.softmax(torch.randn(T, k, device=dev), -1) for _ in range(4)]
-            distinct = float(np.mean([len(np.unique(a)) for a in idx_np]))
-
-            def fn(i):
-                return moe.experts(x, idx[i % 4], wts[i % 4])
-
-            us = _timed_eager(torch, stream, fn, 4, 8)
-            flops = T * k * flops_per_route
-            tf = flops / (us * 1e-6) / 1e12
-            gbps = distinct * expert_b / (us * 1e-6) / 1e9
-            _line(tf, "TFLOP/s", us, "config 4: prefill, 2048 tokens, Zipf(1.1) routing over 384 experts, top-6 "
-                  "(route plan + 3 MFMA grouped GEMMs + SwiGLU + combine)",
+            pt = prefill_point(torch, stream, moe, E, k, H, I, T, expert_b, flops_per_route)
+            _line(pt["tflops"], "TFLOP/s", pt["us_per_layer"], pt["workload"],
                   {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I,
-                   "distinct_experts": distinct, "hbm_gbps_distinct": round(gbps, 1),
-                   "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2)},
-                  DTYPE_F16,
-                  roofline={"bound": "mfma", "kernel": "k_gemm_e8 (gate/up + SwiGLU, then down) with k_gq_rowscale "
-                                                       "(h), k_route_plan, k_route_combine", "achieved": round(tf, 2),
-                            "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4),
-                            "flops_per_layer": flops, "us_per_layer": round(us, 1),
-                            "traffic": measured_traffic(PREFILL_KERNELS, PROFILE_C4),
-                            "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated), "
-                                              "profiles/grouped_gemm_config4_kernel_trace.md"})
+                   "distinct_experts": pt["distinct_experts"], "hbm_gbps_distinct": pt["hbm_gbps_distinct"],
+                   "pct_of_8TBps": pt["pct_of_8TBps"]}, DTYPE_F16, roofline=pt["roofline"])
             continue
-        logits = synth.router_logits(n_sets * T, E, seed=50 + T, device=dev).reshape(n_sets, T, E).contiguous()
-        with torch.no_grad():
-            r0 = [moe(x, logits[i])[1] for i in range(n_sets)] if T > 1 else None
-        torch.cuda.synchronize()
-        if r0 is not None:
-            sets = [np.unique(r.idx.cpu().numpy()) for r in r0]
-        else:
-            with torch.no_grad():
-                sets = [np.unique(moe(x, logits[i])[1].idx.cpu().numpy()) for i in range(n_sets)]
-        distinct = float(np.mean([len(u) for u in sets]))
-        distinct_hot = float(np.mean([int((hot_rows[u] != 0xFFFFFFFF).sum()) for u in sets])) if tier else 0.0
-        layer_b = distinct * expert_b + distinct_hot * res_b
-        outs = []
-
-        def fn(i):
-            o = moe(x, logits[i])
-            outs.append(o)  # keep graph outputs alive
-
-        if T <= 64:
-            us = _timed_graph(torch, stream, fn, n_sets, reps)
-        else:
-            us = _timed_eager(torch, stream, fn, n_sets, 8)
-        gbps = layer_b / (us * 1e-6) / 1e9
+        pt = verify_point(torch, stream, moe, E, k, H, I, T, expert_b, flops_per_route, hot_rows=hot_rows,
+                          res_b=res_b)
         name = {3: f"config 3: speculative verify, {T} tokens through the 384-expert top-6 layer "
                    "(router + fused gate/up/SwiGLU + down/combine)",
                 5: f"config 5: 288 experts, top-8, 4096/1536, 50% resident (-inf bias), tau 0.3, 3-bit tier "
                    f"(E8P + 8-bit E8 residual) on 29 experts, {'decode batch 1' if T == 1 else f'prefill {T} tokens'}"
                 }[cfg]
-        extra = {"distinct_hot_experts": distinct_hot} if tier else {}
-        _line(gbps, "GB/s", us, name,
-              {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I, "distinct_experts": distinct,
-               **extra,
-               "tok_per_s": round(T / (us * 1e-6), 1), "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2),
-               "tflops": round(T * k * flops_per_route / (us * 1e-6) / 1e12, 2)},
-              DTYPE_Q8 if T <= 64 else DTYPE_F16,
-              roofline={"bound": "hbm", "kernel": "layer", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
-                        "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                        "bytes_per_layer": int(layer_b), "us_per_layer": round(us, 2), "traffic": None})
+        extra = {"distinct_hot_experts": pt["distinct_hot_experts"]} if tier else {}
+        _line(pt["gbps"], "GB/s", pt["us_per_layer"], name,
+              {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I,
+               "distinct_experts": pt["distinct_experts"], **extra, "tok_per_s": pt["tok_per_s"],
+               "pct_of_8TBps": pt["pct_of_8TBps"], "tflops": pt["tflops"]},
+              DTYPE_Q8 if T <= 64 else DTYPE_F16, roofline=pt["roofline"])
     return 0
+
+
+def verify_point(torch, stream, moe, E, k, H, I, T, expert_b, flops_per_route, *, hot_rows=None, res_b=0,
+                 n_sets=16, reps=4) -> dict:
+    """One layer call of `moe` on T tokens (fresh router logits per call, 16 sets): us per layer, and the
+    HBM roofline over the bytes of the distinct experts each call reads (codes + row scales, plus the
+    residual tier's rows for its hot experts). Graph-replayed up to 64 tokens, eager above."""
+
+    from keep_amd import synth
+
+    x = synth.rht_activations(T, H, seed=30 + T, device=torch.device("cuda", 0))
+    logits = synth.router_logits(n_sets * T, E, seed=50 + T, device=x.device).reshape(n_sets, T, E).contiguous()
+    with torch.no_grad():
+        sets = [np.unique(moe(x, logits[i])[1].idx.cpu().numpy()) for i in range(n_sets)]
+    torch.cuda.synchronize()
+    distinct = float(np.mean([len(u) for u in sets]))
+    distinct_hot = float(np.mean([int((hot_rows[u] != 0xFFFFFFFF).sum()) for u in sets])) if hot_rows is not None \
+        else 0.0
+    layer_b = distinct * expert_b + distinct_hot * res_b
+    outs = []
+
+    def fn(i):
+        outs.append(moe(x, logits[i]))  # keep graph outputs alive
+
+    us = _timed_graph(torch, stream, fn, n_sets, reps) if T <= 64 else _timed_eager(torch, stream, fn, n_sets, 8)
+    gbps = layer_b / (us * 1e-6) / 1e9
+    return {"tokens": T, "us_per_layer": round(us, 2), "tok_per_s": round(T / (us * 1e-6), 1),
+            "distinct_experts": distinct, "distinct_hot_experts": distinct_hot, "gbps": round(gbps, 2),
+            "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2),
+            "tflops": round(T * k * flops_per_route / (us * 1e-6) / 1e12, 2),
+            "roofline": {"bound": "hbm", "kernel": "layer", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes_per_layer": int(layer_b),
+                         "us_per_layer": round(us, 2), "traffic": None}}
+
+
+def prefill_point(torch, stream, moe, E, k, H, I, T, expert_b, flops_per_route) -> dict:
+    """The experts of one prefill layer on T tokens with Zipf(1.1) routing (4 route sets, eager: the
+    plan sizes its work on the host): us per layer, TFLOP/s against the fp16 matrix-core peak, and the
+    HBM rate over the distinct experts read."""
+
+    from keep_amd import synth
+
+    dev = torch.device("cuda", 0)
+    x = synth.rht_activations(T, H, seed=30 + T, device=dev)
+    idx_np = [synth.zipf_routes(T, E, k, s=1.1, seed=40 + i) for i in range(4)]
+    idx = [torch.from_numpy(a).to(dev) for a in idx_np]
+    gen = torch.Generator(device=dev).manual_seed(7)
+    wts = [torch.softmax(torch.randn(T, k, device=dev, generator=gen), -1) for _ in range(4)]
+    distinct = float(np.mean([len(np.unique(a)) for a in idx_np]))
+
+    def fn(i):
+        return moe.experts(x, idx[i % 4], wts[i % 4])
+
+    us = _timed_eager(torch, stream, fn, 4, 8)
+    flops = T * k * flops_per_route
+    tf = flops / (us * 1e-6) / 1e12
+    gbps = distinct * expert_b / (us * 1e-6) / 1e9
+    busy = mfma_busy(PREFILL_KERNELS, PROFILE_C4)
+    return {"tokens": T, "us_per_layer": round(us, 1), "tflops": round(tf, 2), "tok_per_s": round(T / (us * 1e-6), 1),
+            "distinct_experts": distinct, "hbm_gbps_distinct": round(gbps, 1),
+            "pct_of_8TBps": round(100 * gbps / HBM_PEAK_GBPS, 2),
+            "workload": f"config 4: prefill, {T} tokens, Zipf(1.1) routing over {E} experts, top-{k} "
+                        "(route plan + 3 MFMA grouped GEMMs + SwiGLU + combine)",
+            "roofline": {"bound": "mfma", "kernel": "k_gemm_e8 (gate/up + SwiGLU, then down) with k_gq_rowscale "
+                                                    "(h), k_route_plan, k_route_combine", "achieved": round(tf, 2),
+                         "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                         "flops_per_layer": flops, "us_per_layer": round(us, 1),
+                         "mfma_busy_pct": busy,
+                         "traffic": measured_traffic(PREFILL_KERNELS, PROFILE_C4),
+                         "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated) and "
+                                           "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 256 CUs x 4 SIMDs), "
+                                           "profiles/grouped_gemm_config4_kernel_trace.md"}}
 
 
 def _cpu_projection(torch, p, x, table, seconds):
