@@ -671,12 +671,23 @@ def other_config(args) -> int:
             continue
         pt = verify_point(torch, stream, moe, E, k, H, I, T, expert_b, flops_per_route, hot_rows=hot_rows,
                           res_b=res_b)
+        one = None
+        if cfg == 5 and T == 1:  # the same decode layer in one launch (keep_moe_layer1_nested)
+            moe.one_launch = True
+            one = verify_point(torch, stream, moe, E, k, H, I, T, expert_b, flops_per_route, hot_rows=hot_rows,
+                               res_b=res_b)
+            moe.one_launch = False
+            log(f"bench: config 5 decode, two launches {pt['us_per_layer']} us, one launch {one['us_per_layer']} us")
         name = {3: f"config 3: speculative verify, {T} tokens through the 384-expert top-6 layer "
                    "(router + fused gate/up/SwiGLU + down/combine)",
                 5: f"config 5: 288 experts, top-8, 4096/1536, 50% resident (-inf bias), tau 0.3, 3-bit tier "
                    f"(E8P + 8-bit E8 residual) on 29 experts, {'decode batch 1' if T == 1 else f'prefill {T} tokens'}"
                 }[cfg]
         extra = {"distinct_hot_experts": pt["distinct_hot_experts"]} if tier else {}
+        if one is not None:
+            extra["one_launch"] = {"us_per_layer": one["us_per_layer"], "gbps": one["gbps"],
+                                   "pct_of_8TBps": one["pct_of_8TBps"],
+                                   "path": "keep_moe_layer1_nested (RoutedVQMoE(one_launch=True))"}
         _line(pt["gbps"], "GB/s", pt["us_per_layer"], name,
               {"tokens": T, "experts": E, "top_k": k, "hidden": H, "intermediate": I,
                "distinct_experts": pt["distinct_experts"], **extra, "tok_per_s": pt["tok_per_s"],

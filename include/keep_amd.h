@@ -293,6 +293,33 @@ int keep_moe_layer1(const float* logits, const float* bias_served, const float* 
                     uint8_t* admit, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
                     void* stream);
 
+/* keep_moe_layer1 with the nested 3-bit tier: an expert's pool row with a
+ * residual row (hot_of_slot[row] < num_hot; 0xFFFFFFFF = none; any other value
+ * makes that route's output NaN) adds R[row] . x to gate and up and R[row] . h
+ * to down, R the 8-bit E8 residual (codes uint8 [num_hot, N, K/8] indexing
+ * res_table, the packed E8 table uint32[256], value (nibble - 8) / 2 per
+ * dimension, times scales [num_hot, N, K/group] of res_scale_dtype; residual
+ * groups of 256-element multiples). Same workspace, give-up budget and status
+ * as keep_moe_layer1; with a slot map, num_slots <= num_experts. Replaces the
+ * decode step with the tier, scripts/v41_build/omlx_lattice.py:327-371
+ * (nested mat-vecs 358-370, e8p_nested_m1.py:90-112), in one launch. */
+int keep_moe_layer1_nested(const float* logits, const float* bias_served, const float* bias_demand,
+                           int score_func, int renormalize, float route_scale, float tau,
+                           const int32_t* slot_map, int64_t num_slots, int64_t num_experts, int64_t k,
+                           const void* x, int x_dtype, int64_t H, int64_t I,
+                           const uint16_t* gate_codes, const void* gate_scales,
+                           const uint16_t* up_codes, const void* up_scales,
+                           const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+                           int64_t group_size_h, int64_t group_size_i, const void* prepared,
+                           float swiglu_limit, int32_t* idx, float* w, int32_t* want, float* want_score,
+                           uint8_t* admit, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
+                           const uint32_t* hot_of_slot, int64_t num_hot,
+                           const uint8_t* res_gate_codes, const void* res_gate_scales,
+                           const uint8_t* res_up_codes, const void* res_up_scales,
+                           const uint8_t* res_down_codes, const void* res_down_scales, int res_scale_dtype,
+                           int64_t res_group_size_h, int64_t res_group_size_i, const uint32_t* res_table,
+                           void* stream);
+
 /* keep_moe_layer with the nested 3-bit tier: an expert e with a residual row
  * (hot_of_slot[e] < num_hot; 0xFFFFFFFF = none; any other value makes that
  * route's output NaN) adds R[row] . x to gate, up and down, R the 8-bit E8

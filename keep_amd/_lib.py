@@ -74,6 +74,10 @@ _SIGS = {
     "keep_moe_layer1": [_P, _P, _P, c_int, c_int, c_float, c_float, _P, c_int64, c_int64, c_int64, _P, c_int, c_int64,
                         c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P, _P, _P, _P, _P,
                         c_int64, _P, c_int, _P],
+    "keep_moe_layer1_nested": [_P, _P, _P, c_int, c_int, c_float, c_float, _P, c_int64, c_int64, c_int64, _P, c_int,
+                               c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, _P, c_float, _P, _P,
+                               _P, _P, _P, _P, c_int64, _P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P, c_int,
+                               c_int64, c_int64, _P, _P],
     "keep_moe_layer1_workspace_bytes": [c_int64, c_int64],
     "keep_moe_layer1_status": [_P, _P, _P],
     "keep_moe_layer1_set_spin_ticks": [c_uint32, _P],

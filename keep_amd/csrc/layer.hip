@@ -25,6 +25,15 @@
 // outlasts spin_ticks of the 100 MHz real-time counter gives up: the routes
 // of the waiting wave are NaN, and so are the outputs of its block (each sums
 // every route), and the workspace's status word records it.
+//
+// The nested 3-bit tier (RES): a pool row with a residual row r (hot[row] in
+// [0, nhot); -1 none, anything else makes its routes NaN) adds the 8-bit E8
+// residual r of gate, up and down (codes uint8 [nhot, N, K / 8], one byte per
+// codeword indexing the packed E8 table; weight x 4 = 2 (nibble - 8), exact in
+// int8) to its base: multiplied by the same A operands into a second
+// accumulator and added, each with its own scale, before the SwiGLU and
+// before the weighted sum (omlx_lattice.py:172-186, 358-370). Every block
+// builds a 4-copy LDS image of the table (8 KiB; lane l reads copy l % 4).
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -79,7 +88,32 @@ struct FLArgs {
   uint32_t spin_ticks;
   void* out;
   int odt;
+  // the nested tier (RES)
+  const int32_t* hot;  // [S] residual row of each pool row
+  int32_t nhot;
+  const uint8_t *rgc, *ruc, *rdc;  // residual codes [nhot][N][K / 8]
+  const void *rgs, *rus, *rds;
+  int rsdt;
+  int32_t rGh, rgsz_h, rGi, rgsz_i;
+  const uint32_t* t8;  // the packed 8-bit E8 table, uint32[256]
 };
+
+// The residual image: entry n (the 8 bytes 2 (nibble d - 8), packed-nibble
+// order) in four copies, copy c at n * 32 + 8 c; lane l reads copy l % 4.
+constexpr int FL_T8_BYTES = 256 * 32;
+__device__ __forceinline__ q8v4 fl_t8_decode2(const char* img, uint32_t lane, uint32_t w) {
+  const uint32_t c8 = (lane & 3u) * 8u;
+  const uint2 x0 = *(const uint2*)(img + (w & 0xffu) * 32u + c8);
+  const uint2 x1 = *(const uint2*)(img + ((w >> 8) & 0xffu) * 32u + c8);
+  return q8v4{(int)x0.x, (int)x0.y, (int)x1.x, (int)x1.y};
+}
+// B operands of 8 residual code bytes (codewords 2i, 2i + 1 -> R[i]).
+__device__ __forceinline__ void fl_t8_decode8(const char* img, uint32_t lane, uint2 q, q8v4 (&R)[4]) {
+  R[0] = fl_t8_decode2(img, lane, q.x);
+  R[1] = fl_t8_decode2(img, lane, q.x >> 16);
+  R[2] = fl_t8_decode2(img, lane, q.y);
+  R[3] = fl_t8_decode2(img, lane, q.y >> 16);
+}
 
 __device__ __forceinline__ uint64_t fl_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -100,19 +134,21 @@ __device__ __forceinline__ uint32_t fl_pos(uint32_t d) { return (d & 1u) * 4u + 
 //
 // LDS is one array with the decode image at address 0, so a lookup address
 // is exactly the byte permute of q8_decode2 (no base to add).
-template <int NT, int PER, int NSL, int RPW, bool G1>
+template <int NT, int PER, int NSL, int RPW, bool G1, bool RES>
 __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const float* bias_s, const float* bias_d,
                                                      const uint2* tqe, const void* xin, uint32_t* hdr, int32_t E,
                                                      FLArgs a) {
   constexpr int QT = NT / 2;
   constexpr int RG = FL_WAVES / NSL;
   static_assert(RPW * 4 <= 16, "at most four routes per down wave (A rows 4 r + t)");
+  static_assert(!(RES && G1), "the nested tier scales every slice's partials (no per-row fold)");
   constexpr int O_DSH = TQR_BYTES;                      // down terms [wave][row 4 r + t][g * 4 + i]
   constexpr int O_ASH = O_DSH + FL_WAVES * 16 * 256;    // x terms [slice][term][g * 4 + i]
   constexpr int O_GRED = O_ASH + 16 * 3 * 256;          // gate/up partials [wave][tile][row]
   constexpr int O_RED = O_GRED + 16 * NT * 16 * 4;      // down partials [row][wave]
-  constexpr int O_SMALL = O_RED + 16 * 16 * 4;         // s_inv4s[16], s_idx[8], s_w[8]
-  constexpr int LDS_BYTES = O_SMALL + 256;
+  constexpr int O_SMALL = O_RED + 16 * 16 * 4;         // s_inv4s[16], s_idx[8], s_w[8], s_hr[8]
+  constexpr int O_T8 = O_SMALL + 256;                   // RES: the residual image
+  constexpr int LDS_BYTES = O_T8 + (RES ? FL_T8_BYTES : 0);
   __shared__ uint4 smem[LDS_BYTES / 16];
   char* lds = (char*)smem;
   uint4* tqs = smem;
@@ -123,6 +159,8 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   float* s_inv4s = (float*)(lds + O_SMALL);
   int32_t* s_idx = (int32_t*)(lds + O_SMALL + 64);
   float* s_w = (float*)(lds + O_SMALL + 96);
+  int32_t* s_hr = (int32_t*)(lds + O_SMALL + 128);  // RES: each route's residual row (-1 none, -2 invalid)
+  const char* t8i = lds + O_T8;
   const char* tq = (const char*)tqs;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -148,6 +186,12 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
   if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, E, lane, sm);
+  int hv[PER];  // RES: the residual rows of pool rows lane + 64 i (wave 0)
+  uint32_t t8w = 0u;
+  if constexpr (RES) {
+    if (wv == 0) rt_load_slots<PER>(a.hot, a.S, lane, hv);
+    t8w = a.t8[threadIdx.x >> 2];
+  }
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t ep = __builtin_amdgcn_readfirstlane(ep_word);
   {
@@ -157,7 +201,20 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     row[1] = v;
     row[2] = v;
     row[3] = v;
+    if constexpr (RES) *(uint2*)(lds + O_T8 + (threadIdx.x >> 2) * 32 + (threadIdx.x & 3) * 8) = t8_entry(t8w);
   }
+  // RES: the residual row of pool row `slot` (wave 0, every lane takes part): -1 none, -2 invalid
+  auto hot_of = [&](int slot) -> int {
+    const bool in = slot >= 0 && slot < a.S;
+    const int ss = in ? slot : 0, owner = ss & 63, i0 = ss >> 6;
+    int v = -1;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int x = __shfl(hv[i], owner, 64);
+      v = i == i0 ? x : v;
+    }
+    return !in || v == -1 ? -1 : (v >= 0 && v < a.nhot ? v : -2);
+  };
 
   // 1. served routing (wave 0) | A terms: rows 0-2 of slice w are the three
   //    int8 terms of x s, s the slice's power of two
@@ -191,6 +248,10 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     e_sel = sel.mine;
     sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, E, a.S) : (e_sel >= 0 && e_sel < E ? e_sel : -1);
     if (lane < kneed) s_idx[lane] = sl;
+    if constexpr (RES) {
+      const int hr = hot_of(sl);
+      if (lane < kneed) s_hr[lane] = hr;
+    }
   } else if (wv >= 2) {
     build(xc, wv);
     if (wv < 4) build(xc2, wv - 2);
@@ -234,6 +295,33 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
 #pragma unroll
   for (int t = 0; t < NT; ++t)
     q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + (size_t)(rbase[t >> 1] + j) * C + kc0);
+  // RES: each hot tile's residual codes (8 bytes per lane: codewords kc0 ..) and slice scales
+  int hrt[QT];
+  uint32_t rrow[QT];
+  uint2 qr[NT];
+  ScaleRaw srr[NT];
+  const uint32_t rgrp = RES ? (uint32_t)(wv * 256) / (uint32_t)a.rgsz_h : 0u;
+  if constexpr (RES) {
+#pragma unroll
+    for (int u = 0; u < QT; ++u) {
+      const uint32_t qt = b * QT + u;
+      const bool valid = qt < (uint32_t)a.qtiles;
+      const uint32_t q0 = (valid ? qt : 0u) * 16u;
+      const uint32_t route = q0 / (uint32_t)a.I;
+      hrt[u] = valid ? s_hr[route] : -1;
+      rrow[u] = (hrt[u] >= 0 ? (uint32_t)hrt[u] * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (hrt[t >> 1] >= 0) {  // block-uniform
+        qr[t] = ldg8_q(((t & 1) ? a.ruc : a.rgc) + (size_t)(rrow[t >> 1] + j) * C + kc0);
+        srr[t] = scale_raw((t & 1) ? a.rus : a.rgs, a.rsdt, (rrow[t >> 1] + j) * (uint32_t)a.rGh + rgrp);
+      } else {
+        qr[t] = make_uint2(0u, 0u);
+        srr[t] = 0u;
+      }
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // the remaining routes (wave 0) while the codes are in flight: every wave
@@ -244,6 +332,10 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       e_sel = sel.mine;
       sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, E, a.S) : (e_sel >= 0 && e_sel < E ? e_sel : -1);
       if (lane >= kneed && lane < a.k) s_idx[lane] = sl;
+      if constexpr (RES) {
+        const int hr = hot_of(sl);
+        if (lane >= kneed && lane < a.k) s_hr[lane] = hr;
+      }
     }
     rt_lds_barrier();
   }
@@ -276,13 +368,25 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
+    float vres = 0.f;  // RES: the residual's scaled partial
+    if constexpr (RES) {
+      if (hrt[t >> 1] >= 0) {  // block-uniform
+        q8v4 R[4];
+        fl_t8_decode8(t8i, (uint32_t)lane, qr[t], R);
+        q8v4 accr = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) accr = mfma_i8(A[i], R[i], accr);
+        const float dr = ((float)accr[0] + (float)accr[1] * 0.0078125f) + (float)accr[2] * 0.00006103515625f;
+        vres = dr * inv4s * scale_cvt(srr[t], a.rsdt, (rrow[t >> 1] + j) * (uint32_t)a.rGh + rgrp);
+      }
+    }
     if (lane < 16) {
       const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
       if constexpr (G1) {
         gred[(wv * NT + t) * 16 + j] = d * inv4s;
       } else {
         const uint32_t si = (rbase[t >> 1] + j) * (uint32_t)a.Gh + grp;
-        gred[(wv * NT + t) * 16 + j] = d * inv4s * scale_cvt(sr[t], a.sdt, si);
+        gred[(wv * NT + t) * 16 + j] = d * inv4s * scale_cvt(sr[t], a.sdt, si) + vres;
       }
     }
   }
@@ -309,6 +413,27 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   uint4 qd[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) qd[r] = ldg16_q(a.dc + (size_t)(dbase[r] + j) * CI + sd * 32 + g * 8);
+  // RES: each hot route's residual down codes and slice scale
+  int hrd[RPW];
+  uint32_t drow[RPW];
+  uint2 qrd[RPW];
+  ScaleRaw srrd[RPW];
+  const uint32_t rdgrp = RES ? (uint32_t)(sd * 256) / (uint32_t)a.rgsz_i : 0u;
+  if constexpr (RES) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int route = rg * RPW + r;
+      hrd[r] = dok[r] ? s_hr[route] : -1;  // wave-uniform
+      drow[r] = (hrd[r] >= 0 ? (uint32_t)hrd[r] * 4096u : 0u) + b * 16u;
+      if (hrd[r] >= 0) {
+        qrd[r] = ldg8_q(a.rdc + (size_t)(drow[r] + j) * CI + sd * 32 + g * 8);
+        srrd[r] = scale_raw(a.rds, a.rsdt, (drow[r] + j) * (uint32_t)a.rGi + rdgrp);
+      } else {
+        qrd[r] = make_uint2(0u, 0u);
+        srrd[r] = 0u;
+      }
+    }
+  }
   // this block counts itself in (it has read the epoch); the last block in advances it after the exchange
   uint32_t arrived = 0u;
   if (threadIdx.x == 0)
@@ -339,6 +464,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     }
     float hv = silu_mul(gsum, usum, a.limit);
     if (tq_bad || e < 0 || e >= a.S) hv = __builtin_nanf("");
+    if (RES && s_hr[q0 / (uint32_t)a.I] == -2) hv = __builtin_nanf("");
     const uint32_t hb = from_float<bf16s>(hv).bits;
     const uint32_t hb2 = (uint32_t)__shfl((int)hb, lane ^ 2, 64);
     if (valid && (jj & 2u) == 0u) {
@@ -448,12 +574,26 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc = mfma_i8(AD[i], BD[r][i], acc);
+      float vres = 0.f;
+      bool rbad = false;
+      if constexpr (RES) {
+        rbad = hrd[r] == -2;
+        if (hrd[r] >= 0) {  // wave-uniform
+          q8v4 R[4];
+          fl_t8_decode8(t8i, (uint32_t)lane, qrd[r], R);
+          q8v4 accr = {0, 0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) accr = mfma_i8(AD[i], R[i], accr);
+          const float dr = (float)accr[0] + (float)accr[1] * 0.00390625f;
+          vres = dr * inv4d[r] * scale_cvt(srrd[r], a.rsdt, (drow[r] + j) * (uint32_t)a.rGi + rdgrp);
+        }
+      }
       if ((int)g == r) {
         const int route = rg * RPW + r;
         const float wt = dlive[r] ? s_w[route] : 0.f;
         const float d = (float)acc[0] + (float)acc[1] * 0.00390625f;
-        const float val = d * inv4d[r] * scale_cvt(srd[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + dgrp);
-        c = wt == 0.f ? 0.f : dok[r] ? wt * val : __builtin_nanf("");
+        const float val = d * inv4d[r] * scale_cvt(srd[r], a.sdt, (dbase[r] + j) * (uint32_t)a.Gi + dgrp) + vres;
+        c = wt == 0.f ? 0.f : (dok[r] && !rbad) ? wt * val : __builtin_nanf("");
       }
     }
     // the sum over the wave's routes (lane rows 0 + 1, then + rows 2 + 3)
@@ -511,15 +651,26 @@ bool fl_device_ok() {
   return cus >= FL_BLOCKS;
 }
 
+// The nested tier's host-side arguments (keep_moe_layer1_nested).
+struct FLNest {
+  const int32_t* hot;
+  int32_t nhot;
+  const uint8_t *gc, *uc, *dc;
+  const void *gs, *us, *ds;
+  int sdt;
+  int64_t group_h, group_i;
+  const uint32_t* t8;
+};
+
 // The (tiles per block, slices, routes per down wave) of each served (I, k):
 // gate/up q-tiles per block ceil(k I / 16 / 256), down route groups
 // RG = 16 / (I / 256) of ceil(k / RG) routes.
-template <int PER, bool G1>
+template <int PER, bool G1, bool RES>
 static bool fl_dispatch(const FLHead& h, const FLArgs& a, hipStream_t s) {
   const dim3 grid(FL_BLOCKS), blk(1024);
-#define FL_K(NT, NSL, RPW)                                                                                  \
-  hipLaunchKernelGGL((k_moe_layer1<NT, PER, NSL, RPW, G1>), grid, blk, 0, s, h.logits, h.bias_s, h.bias_d, h.tq, \
-                     h.x, h.hdr, h.E, a)
+#define FL_K(NT, NSL, RPW)                                                                                 \
+  hipLaunchKernelGGL((k_moe_layer1<NT, PER, NSL, RPW, G1, RES>), grid, blk, 0, s, h.logits, h.bias_s, h.bias_d, \
+                     h.tq, h.x, h.hdr, h.E, a)
   const int k = a.k;
   switch (a.I) {
     case 2048:
@@ -553,7 +704,7 @@ void fl_launch(const float* logits, const float* bias_s, const float* bias_d, in
                const void* gs, const uint16_t* uc, const void* us, const uint16_t* dc, const void* ds, int sdt,
                int64_t group_h, int64_t group_i, const void* prepared, float limit, int32_t* idx, float* w,
                int32_t* want, float* want_score, uint8_t* admit, void* workspace, uint32_t spin_ticks, void* out,
-               int odt, hipStream_t s) {
+               int odt, hipStream_t s, const FLNest* nest) {
   FLHead h{};
   h.logits = logits; h.bias_s = bias_s; h.bias_d = bias_d; h.E = (int32_t)E;
   h.x = x; h.tq = (const uint2*)((const char*)prepared + TQ_OFFSET); h.hdr = (uint32_t*)workspace;
@@ -572,13 +723,24 @@ void fl_launch(const float* logits, const float* bias_s, const float* bias_d, in
   a.spin_ticks = spin_ticks;
   a.out = out; a.odt = odt;
   a.xbf = x_dtype == KEEP_BF16;
+  if (nest) {  // every slice's partials scaled in place (no per-row fold)
+    a.hot = nest->hot; a.nhot = nest->nhot;
+    a.rgc = nest->gc; a.ruc = nest->uc; a.rdc = nest->dc;
+    a.rgs = nest->gs; a.rus = nest->us; a.rds = nest->ds; a.rsdt = nest->sdt;
+    a.rGh = (int32_t)(4096 / nest->group_h); a.rgsz_h = (int32_t)nest->group_h;
+    a.rGi = (int32_t)(I / nest->group_i); a.rgsz_i = (int32_t)nest->group_i;
+    a.t8 = nest->t8;
+    if (E <= 384) fl_dispatch<6, false, true>(h, a, s);
+    else fl_dispatch<16, false, true>(h, a, s);
+    return;
+  }
   const bool g1 = group_h == 4096;
   if (g1) {
-    if (E <= 384) fl_dispatch<6, true>(h, a, s);
-    else fl_dispatch<16, true>(h, a, s);
+    if (E <= 384) fl_dispatch<6, true, false>(h, a, s);
+    else fl_dispatch<16, true, false>(h, a, s);
   } else {
-    if (E <= 384) fl_dispatch<6, false>(h, a, s);
-    else fl_dispatch<16, false>(h, a, s);
+    if (E <= 384) fl_dispatch<6, false, false>(h, a, s);
+    else fl_dispatch<16, false, false>(h, a, s);
   }
 }
 
@@ -644,6 +806,58 @@ extern "C" int keep_moe_layer1(const float* logits, const float* bias_served, co
             x_dtype, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
             group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, workspace,
             g_spin_ticks.load(std::memory_order_relaxed),
-            out, out_dtype, (hipStream_t)stream);
+            out, out_dtype, (hipStream_t)stream, nullptr);
   return launch_status("keep_moe_layer1");
+}
+
+extern "C" int keep_moe_layer1_nested(
+    const float* logits, const float* bias_served, const float* bias_demand, int score_func, int renormalize,
+    float route_scale, float tau, const int32_t* slot_map, int64_t num_slots, int64_t E, int64_t k, const void* x,
+    int x_dtype, int64_t H, int64_t I, const uint16_t* gate_codes, const void* gate_scales, const uint16_t* up_codes,
+    const void* up_scales, const uint16_t* down_codes, const void* down_scales, int scale_dtype,
+    int64_t group_size_h, int64_t group_size_i, const void* prepared, float swiglu_limit, int32_t* idx, float* w,
+    int32_t* want, float* want_score, uint8_t* admit, void* workspace, int64_t workspace_bytes, void* out,
+    int out_dtype, const uint32_t* hot_of_slot, int64_t num_hot, const uint8_t* res_gate_codes,
+    const void* res_gate_scales, const uint8_t* res_up_codes, const void* res_up_scales,
+    const uint8_t* res_down_codes, const void* res_down_scales, int res_scale_dtype, int64_t res_group_size_h,
+    int64_t res_group_size_i, const uint32_t* res_table, void* stream) {
+  KEEP_REQUIRE_DIMS(num_slots, E, k, H, I, group_size_h, group_size_i, num_hot, res_group_size_h, res_group_size_i);
+  KEEP_REQUIRE(x_dtype == KEEP_F16 || x_dtype == KEEP_BF16, "activations must be fp16 or bf16");
+  KEEP_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(out_dtype) && dtype_ok(res_scale_dtype), "bad dtype enum");
+  KEEP_REQUIRE(score_func >= 0 && score_func <= 2, "bad score_func %d", score_func);
+  KEEP_REQUIRE(group_size_h > 0 && H % group_size_h == 0 && group_size_i > 0 && I % group_size_i == 0,
+               "bad group sizes");
+  KEEP_REQUIRE(fl_supported(E, H, I, k, group_size_h, group_size_i),
+               "shape not served by the one-launch decode layer (needs H = 4096, I a multiple of 512 up to 2048, "
+               "k <= 8, E <= 1024, scale groups of 256-element multiples)");
+  KEEP_REQUIRE(res_group_size_h >= 256 && H % res_group_size_h == 0 && res_group_size_h % 256 == 0 &&
+                   res_group_size_i >= 256 && I % res_group_size_i == 0 && res_group_size_i % 256 == 0,
+               "residual scale groups must divide H and I and be multiples of 256");
+  KEEP_REQUIRE(num_hot >= 1 && num_hot * I * H < (int64_t(1) << 31), "bad residual row count %lld",
+               (long long)num_hot);
+  KEEP_REQUIRE(fl_device_ok(), "the one-launch decode layer needs %d compute units", FL_BLOCKS);
+  // the residual rows of the pool rows are read as E entries at most (the router's lanes)
+  KEEP_REQUIRE(!slot_map || (num_slots >= 1 && num_slots <= E), "num_slots must be in 1..E with the nested tier");
+  KEEP_REQUIRE(logits && x && gate_codes && gate_scales && up_codes && up_scales && down_codes && down_scales &&
+                   prepared && idx && w && workspace && out && hot_of_slot && res_gate_codes && res_gate_scales &&
+                   res_up_codes && res_up_scales && res_down_codes && res_down_scales && res_table,
+               "null pointer argument");
+  KEEP_REQUIRE(workspace_bytes >= fl_workspace_bytes(k, I), "workspace needs %lld bytes, got %lld",
+               (long long)fl_workspace_bytes(k, I), (long long)workspace_bytes);
+  KEEP_REQUIRE(aligned(x, 16) && aligned(workspace, 256) && aligned(prepared, 16),
+               "x and prepared must be 16-byte aligned, the workspace 256-byte aligned");
+  KEEP_REQUIRE(aligned(gate_codes, 16) && aligned(up_codes, 16) && aligned(down_codes, 16), "codes misaligned");
+  KEEP_REQUIRE(aligned(res_gate_codes, 8) && aligned(res_up_codes, 8) && aligned(res_down_codes, 8) &&
+                   aligned(hot_of_slot, 4) && aligned(res_table, 4),
+               "residual codes must be 8-byte aligned");
+  FLNest n{};
+  n.hot = (const int32_t*)hot_of_slot; n.nhot = (int32_t)num_hot;
+  n.gc = res_gate_codes; n.uc = res_up_codes; n.dc = res_down_codes;
+  n.gs = res_gate_scales; n.us = res_up_scales; n.ds = res_down_scales; n.sdt = res_scale_dtype;
+  n.group_h = res_group_size_h; n.group_i = res_group_size_i; n.t8 = res_table;
+  fl_launch(logits, bias_served, bias_demand, score_func, renormalize, route_scale, tau, slot_map, num_slots, E, k, x,
+            x_dtype, I, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales, scale_dtype,
+            group_size_h, group_size_i, prepared, swiglu_limit, idx, w, want, want_score, admit, workspace,
+            g_spin_ticks.load(std::memory_order_relaxed), out, out_dtype, (hipStream_t)stream, &n);
+  return launch_status("keep_moe_layer1_nested");
 }

@@ -729,10 +729,11 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
     weighted combine. ``x [1, H]`` (fp16/bf16), ``logits [1, E]``. With
     ``hot_tier`` (``keep_moe_layer_nested``) the routes of experts on the
     nested tier add their 8-bit E8 residual to all three projections. With
-    ``one_launch`` (``keep_moe_layer1``) the same layer runs as one launch of
-    256 co-resident blocks that pass h through ``workspace`` (by default
+    ``one_launch`` (``keep_moe_layer1``, with ``hot_tier``
+    ``keep_moe_layer1_nested``) the same layer runs as one launch of 256
+    co-resident blocks that pass h through ``workspace`` (by default
     ``layer_workspace(device, k, I)`` of the current stream); it serves
-    H = 4096, I in {512, 1024, 1536, 2048}, k <= 8, no hot tier. With
+    H = 4096, I in {512, 1024, 1536, 2048}, k <= 8. With
     ``slot_map`` (int32 ``[E]``, expert -> pool row) the pools hold fewer rows
     than the router has experts (a residency cache's slots); ``RouterOutput.idx``
     then holds rows. Returns ``(out [1, H], RouterOutput)``; the output is
@@ -778,8 +779,6 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
     cb = ops._codebook_tensor(codebook, 16, device)
     prep = ops.prepared_table(cb)
     if one_launch:
-        if hot_tier is not None:
-            raise ValueError("the one-launch layer has no hot tier; use one_launch=False")
         if not _one_launch_ok(device, E, H, I, k):
             raise ValueError("shape or device not served by the one-launch layer (H = 4096, I in {512, 1024, 1536, "
                              "2048}, k <= 8, E <= 1024, 256 compute units)")
@@ -787,6 +786,23 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, 
         ws = layer_workspace(device, k, I) if workspace is None else workspace
         if ws.dtype != torch.uint8 or ws.device != device or ws.numel() < need or not ws.is_contiguous():
             raise ValueError(f"workspace must be a contiguous uint8 tensor of at least {need} bytes on {device}")
+        if hot_tier is not None:
+            if hot_tier.hot_of_slot.numel() != S:
+                raise ValueError(f"hot_of_slot must have {S} entries (one per pool row)")
+            groups = hot_tier.layer_groups(H, I)
+            if groups is None:
+                raise ValueError("residual scale groups must be 256-element multiples (one dtype) for the decode layer")
+            (rgc, rgs), (ruc, rus), (rdc, rds) = (hot_tier.residual_arrays[n] for n in ("gate", "up", "down"))
+            _lib.call("keep_moe_layer1_nested", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
+                      int(bool(renormalize)), float(route_scale), float(tau), ops._ptr(sm), ns, E, k, x.data_ptr(),
+                      ops._DT[x.dtype], H, I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(),
+                      dc.data_ptr(), ds.data_ptr(), ops._DT[gs.dtype], gh, gi, prep.data_ptr(), float(limit),
+                      r.idx.data_ptr(), r.weight.data_ptr(), r.want.data_ptr(), r.want_score.data_ptr(),
+                      r.admit.data_ptr(), ws.data_ptr(), ws.numel(), out.data_ptr(), ops._DT[od],
+                      hot_tier._hot32.data_ptr(), hot_tier.rows, rgc.data_ptr(), rgs.data_ptr(), ruc.data_ptr(),
+                      rus.data_ptr(), rdc.data_ptr(), rds.data_ptr(), ops._DT[rgs.dtype], groups[0], groups[1],
+                      hot_tier._table_packed.data_ptr(), ops._stream(device))
+            return out, r
         _lib.call("keep_moe_layer1", z.data_ptr(), ops._ptr(bs), ops._ptr(bd), _lib.SCORE_FUNCS[score_func],
                   int(bool(renormalize)), float(route_scale), float(tau), ops._ptr(sm), ns, E, k, x.data_ptr(),
                   ops._DT[x.dtype], H, I, gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), dc.data_ptr(),
@@ -842,14 +858,24 @@ class RoutedVQMoE:
     ``__call__(..., residual=h)`` adds the residual stream, both in fp32 and
     rounded once to ``out_dtype`` (``DeepseekV4FlashVQMoE.__call__``,
     ``deepseek_v4_flash_adapter.py:1777-1784``; ``omlx_lattice.py:374-388``).
+
+    One token runs the fused two-launch layer (``keep_moe_layer``, or
+    ``keep_moe_layer_nested`` with a hot tier). ``one_launch=True`` runs it as
+    the one-launch layer where that serves the shape (``keep_moe_layer1`` /
+    ``keep_moe_layer1_nested``, the current stream's ``layer_workspace``):
+    faster, but it assumes all 256 of its blocks are resident together, so a
+    caller sharing the GPU with other work checks ``layer_status`` for a wait
+    that gave up (NaN output).
     """
 
     def __init__(self, glu: QuantizedVQSwitchGLU, *, top_k: int, score_func: str = "softmax",
                  renormalize: bool = True, route_scale: float = 1.0, swiglu_limit: float = 0.0,
                  bias_served: torch.Tensor | None = None, bias_demand: torch.Tensor | None = None,
                  tau: float = float("inf"), decode_max_tokens: int = 64, out_dtype=torch.float32,
-                 shared_experts: QuantizedVQSwitchGLU | None = None, slot_map: torch.Tensor | None = None):
+                 shared_experts: QuantizedVQSwitchGLU | None = None, slot_map: torch.Tensor | None = None,
+                 one_launch: bool = False):
         self.glu, self.top_k, self.score_func = glu, top_k, score_func
+        self.one_launch = bool(one_launch)
         self.renormalize, self.route_scale, self.limit = renormalize, route_scale, float(swiglu_limit)
         self.bias_served, self.bias_demand, self.tau = bias_served, bias_demand, tau
         self.decode_max_tokens = decode_max_tokens
@@ -921,11 +947,13 @@ class RoutedVQMoE:
                                      codebook=g.codebook, out_dtype=od, slot_map=self.slot_map)
         elif self._layer_path(x):
             g, u, d = self.glu.gate_proj, self.glu.up_proj, self.glu.down_proj
+            one = self.one_launch and _one_launch_ok(x.device, logits.shape[-1], g.input_dims, g.output_dims,
+                                                     self.top_k)
             out, r = moe_layer(x, logits, (g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales),
                                k=self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
                                score_func=self.score_func, renormalize=self.renormalize,
                                route_scale=self.route_scale, tau=self.tau, limit=self.limit, codebook=g.codebook,
-                               out_dtype=od, hot_tier=self.glu.hot_tier, slot_map=self.slot_map)
+                               out_dtype=od, hot_tier=self.glu.hot_tier, slot_map=self.slot_map, one_launch=one)
         else:
             r = router_dual_topk(logits, self.top_k, bias_served=self.bias_served, bias_demand=self.bias_demand,
                                  score_func=self.score_func, renormalize=self.renormalize,

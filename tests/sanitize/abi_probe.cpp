@@ -63,6 +63,7 @@ int main() {
   PROBE(keep_moe_layer1_workspace_bytes);
   PROBE(keep_moe_layer1_status);
   PROBE(keep_moe_layer1);
+  PROBE(keep_moe_layer1_nested);
   PROBE(keep_e8_1bit_image);
   PROBE(keep_moe_layer_nested);
   PROBE(keep_moe_tiles_workspace_bytes);

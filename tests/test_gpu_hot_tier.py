@@ -134,6 +134,63 @@ def test_hot_tier_fused_decode_layer_vs_oracle(dev, k, I, gh, gi, rgh, rgi, xdt)
     _check(out, split.double().cpu().numpy())
 
 
+@pytest.mark.parametrize("k,I,gh,gi,rgh,rgi,xdt", [(8, 512, 4096, 512, 4096, 512, torch.float16),
+                                                    (6, 1024, 1024, 256, 256, 512, torch.bfloat16),
+                                                    (8, 1536, 4096, 1536, 4096, 1536, torch.float16)])
+def test_hot_tier_one_launch_layer_vs_oracle(dev, k, I, gh, gi, rgh, rgi, xdt):
+    """One token through the one-launch layer with the tier
+    (keep_moe_layer1_nested): half the pool on the tier, per-row and grouped
+    base and residual scales, fp16 and bf16 activations, the clamped SwiGLU;
+    against the float64 oracle, and its router outputs equal to the two-launch
+    nested layer's on the same call."""
+    E, H = 32, 4096
+    print(f"one-launch nested: k={k} I={I} groups {gh}/{gi} res {rgh}/{rgi}", flush=True)
+    glu, (gate, up, down), hot_of_slot, residual = _layer_block(dev, E, I, 16, gh, gi, rgh, rgi, seed=400 + k + I)
+    x = synth.rht_activations(1, H, seed=410 + k, device=dev, dtype=xdt)
+    z = synth.router_logits(1, E, seed=420 + k, device=dev)
+    g, u, d = glu.gate_proj, glu.up_proj, glu.down_proj
+    args = ((g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales))
+    ws = torch.zeros(int(keep_amd._lib.load().keep_moe_layer1_workspace_bytes(k, I)), dtype=torch.uint8, device=dev)
+    out, r = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0, hot_tier=glu.hot_tier, one_launch=True, workspace=ws)
+    two, r2 = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0, hot_tier=glu.hot_tier)
+    for a_, b_ in zip(r, r2):
+        assert torch.equal(a_, b_)
+    idx = r.idx.cpu().numpy()
+    on = hot_of_slot[idx] != keep_amd.ops.NO_RESIDUAL
+    assert on.any() and (~on).any(), "want routes on and off the tier"
+    want = ops.moe_layer(x.float().cpu().numpy(), idx, r.weight.cpu().numpy(), gate, up, down, limit=7.0,
+                         h_round="bfloat16", hot_of_slot=hot_of_slot, residual=residual)
+    _check(out, want)
+    _check(out, two.double().cpu().numpy())
+    assert keep_amd.nn.layer_status(ws) == 0
+
+
+def test_hot_tier_one_launch_off_tier_and_bad_row(dev):
+    """The one-launch layer with a tier that holds none of the selected
+    experts equals the plain one-launch layer bit for bit; a selected expert
+    whose residual row is out of range makes the output NaN (every output row
+    sums every route)."""
+    E, I, k = 32, 512, 4
+    glu, (gate, up, down), hot_of_slot, residual = _layer_block(dev, E, I, 8, 4096, 512, 4096, 512, seed=430)
+    x = synth.rht_activations(1, 4096, seed=431, device=dev)
+    z = synth.router_logits(1, E, seed=432, device=dev)
+    g, u, d = glu.gate_proj, glu.up_proj, glu.down_proj
+    args = ((g.codes, g.scales), (u.codes, u.scales), (d.codes, d.scales))
+    ws = lambda: torch.zeros(1 << 16, dtype=torch.uint8, device=dev)  # noqa: E731
+    plain, r = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0, one_launch=True, workspace=ws())
+    sel = r.idx.cpu().numpy().ravel()
+    hot = hot_of_slot.copy()
+    hot[sel] = keep_amd.ops.NO_RESIDUAL
+    off = keep_amd.HotTier(hot, glu.hot_tier.residual_arrays)
+    nested, r2 = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0, hot_tier=off, one_launch=True, workspace=ws())
+    assert torch.equal(r.idx, r2.idx)
+    assert torch.equal(plain, nested)
+    hot[sel[1]] = 8  # rows 0..7 exist
+    bad = keep_amd.HotTier(hot, glu.hot_tier.residual_arrays)
+    out, _ = keep_amd.moe_layer(x, z, *args, k=k, limit=7.0, hot_tier=bad, one_launch=True, workspace=ws())
+    assert torch.isnan(out).all()
+
+
 def test_hot_tier_fused_layer_off_tier_and_bad_row(dev):
     """Routes all off the tier: byte-identical to keep_moe_layer. A selected
     expert whose hot_of_slot row is out of range: NaN output."""

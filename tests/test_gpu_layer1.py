@@ -218,6 +218,6 @@ def test_layer1_rejects_unserved(dev):
     z = synth.router_logits(1, E, seed=5, device=dev)
     with pytest.raises(ValueError, match="workspace"):
         keep_amd.moe_layer(x, z, *_pairs(pool), k=k, one_launch=True, workspace=_workspace(dev, k, 1024))
-    with pytest.raises(ValueError, match="one-launch"):
-        keep_amd.moe_layer(x, z, *_pairs(pool), k=k, one_launch=True,
-                           hot_tier=object())
+    with pytest.raises(ValueError, match="one-launch"):  # fewer than k experts
+        keep_amd.moe_layer(x, z[:, :4], *_pairs(pool), k=k, one_launch=True, slot_map=torch.zeros(4, dtype=torch.int32,
+                                                                                               device=dev))

@@ -173,14 +173,15 @@ def _check(out, want, tol=2e-3):
     assert ops.elementwise_ok(g, want, rtol=tol), "elementwise bound violated"
 
 
-def test_hot_tier_rows_follow_the_residents(dev, tmp_path):
+@pytest.mark.parametrize("one_launch", [False, True])
+def test_hot_tier_rows_follow_the_residents(dev, tmp_path, one_launch):
     """The nested tier over an 8-row pool: the cache's route hook rewrites the
     tier's slot rows as experts move (omlx_lattice.py:274-278). Hot experts 20
     and 27 start absent and are installed, one of them into the slot that hot
     expert 2 (never demanded, the coldest resident) held; expert 5 keeps its
     row throughout. Every call: each routed slot's tier row is its expert's row, and
     the fused nested layer matches the float64 oracle in expert space."""
-    print("residency: hot tier rows follow the residents", flush=True)
+    print(f"residency: hot tier rows follow the residents, one_launch={one_launch}", flush=True)
     arrays = _write_layer(tmp_path / "layer-00.npz")
     layer = loaders.LayerFile(tmp_path / "layer-00.npz")
     pools = _pools(dev)
@@ -213,7 +214,9 @@ def test_hot_tier_rows_follow_the_residents(dev, tmp_path):
         z_np[0, 2] -= 6.0
         z = torch.from_numpy(z_np).to(dev)
         out, r = keep_amd.moe_layer(x, z, pools["w1"], pools["w3"], pools["w2"], k=K, bias_served=cache.bias(),
-                                    tau=cache.tau, slot_map=cache.slots(), hot_tier=tier, limit=7.0)
+                                    tau=cache.tau, slot_map=cache.slots(), hot_tier=tier, limit=7.0,
+                                    one_launch=one_launch,
+                                    workspace=keep_amd.nn.layer_workspace(dev, K, I) if one_launch else None)
         cache.observe(r)
         experts = slot_expert[r.idx.cpu().numpy()]
         assert (experts >= 0).all()
