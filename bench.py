@@ -764,7 +764,7 @@ def prefill_point(torch, stream, moe, E, k, H, I, T, expert_b, flops_per_route) 
                          "mfma_busy_pct": busy,
                          "traffic": measured_traffic(PREFILL_KERNELS, PROFILE_C4),
                          "traffic_source": "rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-calibrated) and "
-                                           "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 256 CUs x 4 SIMDs), "
+                                           "SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / (GRBM_GUI_ACTIVE / 8 XCDs), "
                                            "profiles/grouped_gemm_config4_kernel_trace.md"}}
 
 
