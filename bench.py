@@ -60,10 +60,11 @@ import numpy as np
 HBM_PEAK_GBPS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16 matrix-core peak of the MI355X
 # the arithmetic of the int8 matrix-core paths (decode layer, few-token tiles): decoded E8P weights x 4 are exact int8; activations are split
-# exactly into int8 terms under a power-of-two scale (residual below the fp32 rounding of the sums)
+# into int8 terms under a power-of-two scale per 256-wide slice
 DTYPE_Q8 = ("fp16 activations x E8P-2bit (uint16) codes on the int8 matrix cores: x as 3 int8 terms per "
-            "256-wide slice (residual < 2^-21 of the slice max), SwiGLU output h in bf16 as 2 int8 terms "
-            "(residual < 2^-14), exact int32 MFMA sums, fp32 scaling, SwiGLU and route combine")
+            "256-wide slice (residual <= 2^-20 of the slice max), SwiGLU output h in bf16 as 2 int8 terms "
+            "(residual <= 2^-13 of the slice max; 2^-14 in the one-launch layer), exact int32 MFMA sums, fp32 "
+            "scaling, SwiGLU and route combine")
 # the prefill grouped GEMMs (configs 4 and 5 prefill): fp16 matrix cores, as the reference's fp16 sorted matmul
 DTYPE_F16 = ("fp16 activations (bf16 h times a power of two per row, then fp16) x E8P-2bit (uint16) codes "
              "decoded to exact fp16 on the fp16 matrix cores (v_mfma_f32_32x32x16_f16): exact products, fp32 sums, "

@@ -151,17 +151,44 @@ __global__ __launch_bounds__(1024) void k_mt_prologue(MTPro p) {
 
 // The two persistent kernels share one schedule. Tiles hold at most
 // MT_TILE routes, so every unit of every tile is one pass over its codes and
-// costs about the same: an even split of the units balances the blocks. A
-// block's units form segments (the units of one tile, at most SEG of them):
-// per segment the tile's A operands go to registers, then the units run
-// with the next two units' codes and scale words in flight while one is
-// decoded, unrolled by two over two register buffers. Inside a segment every
-// load is unconditional (past its end the last unit is loaded again and
-// stores nothing) and no global store is issued -- outputs are staged in LDS
-// and written when the segment ends -- so each wait the compiler inserts
-// counts exactly the loads before it. The cross-wave partial sums are
+// costs about the same: an even split of the units balances the blocks (an
+// even count per block). A block's units form segments (the units of one
+// tile, at most SEG of them), and run as one pipeline across them: the next
+// two units' codes and scale words are in flight while one is decoded, in
+// pairs over two register buffers, and those loads cross into the next
+// segment, and the next tile, before the current one ends; tile and SEG
+// bounds are even, so only a block's last segment can end on an odd unit.
+// Loads past the block's last unit read that unit again. Wave 0 reads the
+// descriptors of every tile the block touches (expert row, routes) into an
+// LDS table when the kernel starts, and every wave reads its first tile
+// itself, all with vector loads: a scalar load in flight would make each LDS
+// wait of the decode wait for it as well. The first units' codes are issued
+// after the block's small loads, as every block then is, so that no block's
+// descriptor loads queue behind the grid's code stream; a switch to a new
+// segment waits only for that segment's A operands. Outputs are staged in LDS
+// and written when their segment ends. The cross-wave partial sums are
 // double-buffered by unit parity: a wave writes a unit's partials only after
 // the barrier that the previous reader of that buffer has passed.
+
+// A tile's first code row (expert x rows per expert), route count and routes
+// (order[off + min(i, nr - 1)]).
+struct MTTile {
+  uint32_t row;
+  int nr;
+  int r[MT_TILE];
+};
+
+// Tiles a block touches, at most: ceil(units per block / units per tile) + 1,
+// at most 10 for the shapes the kernels serve (checked on the host).
+constexpr int MT_TPB = 16;
+
+// Route i of the tile whose routes lanes 0-3 hold (lane i: route i), for a
+// lane-dependent i: a cross-lane read, no memory. A tile's routes are never
+// held in an array indexed by a lane value: the compiler would keep such an
+// array per thread in LDS.
+__device__ __forceinline__ int mt_route_of_lanes(int rr, uint32_t i) {
+  return __builtin_amdgcn_ds_bpermute((int)(i << 2), rr);
+}
 
 // Gate/up: a unit is 16 rows of gate and of up (two code loads per wave, 32
 // KiB per block). One MFMA chain per projection serves all the tile's
@@ -174,6 +201,7 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
   __shared__ uint4 tqs[TQR_BYTES / 16];
   __shared__ float gred[2][16][2][MT_TILE][16];  // [parity][wave][gate, up][route][row]
   __shared__ uint16_t hst[MT_TILE][SEG * 16];    // the segment's h rows
+  __shared__ MTTile s_td[MT_TPB];                // the block's tiles
   const char* tq = (const char*)tqs;
   const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
   const Q8Keys lk = q8_keys(threadIdx.x & 63);
@@ -182,10 +210,10 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
   const uint32_t j = lane & 15, g = lane >> 4;
   const bool dec = wv < a.S;  // this wave owns a K slice
   const int sl = dec ? wv : 0;
-  const int rg_n = a.I >> 4;
+  const int rg_n = a.I >> 4;  // units per tile (>= 16)
   const int nt = __builtin_amdgcn_readfirstlane(*a.ntiles);
   const int U = nt * rg_n;
-  const int per = (U + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int per = ((U + (int)gridDim.x - 1) / (int)gridDim.x + 1) & ~1;  // even: see the unit loop
   const int u0 = (int)blockIdx.x * per, u1 = min(U, u0 + per);
 #pragma unroll
   for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
@@ -201,88 +229,157 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
     uint4 q[2];
     uint32_t s[2];
   };
-  for (int us = u0; us < u1;) {
-    const int tic = us / rg_n;
-    const int ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
-    const uint32_t ebase = (uint32_t)a.te[tic] * (uint32_t)a.I;
-    const uint32_t row0 = (uint32_t)(us - tic * rg_n) * 16u;
-    const int off = a.to[tic], nr = a.tc[tic];  // 1 <= nr <= MT_TILE
-    // a unit's codes and its rows' scale words (the aligned word holding each)
-    auto load_unit = [&](int u, Buf& b) {
-      const uint32_t row = ebase + (uint32_t)(min(u, ue - 1) - tic * rg_n) * 16u + j;
+  const int tic0 = u0 / rg_n, ntb = (u1 - 1) / rg_n - tic0 + 1;  // the block's tiles (<= MT_TPB)
+  int tic = tic0;
+  // the first tile (every wave) and the next tile's row; wave 0, lane l < ntb: tile tic0 + l for the table
+  int zv = 0;
+  asm volatile("" : "+v"(zv));  // a lane value: these loads go through the vector unit
+  const int te0 = a.te[tic0 + zv], te1 = a.te[min(tic0 + 1, nt - 1) + zv];
+  const int off0 = a.to[tic0 + zv], nr0 = a.tc[tic0 + zv];
+  const bool tl = wv == 0 && lane < ntb;
+  int tte = 0, tto = 0, ttc = 1;
+  if (tl) {
+    tte = a.te[tic0 + lane];
+    tto = a.to[tic0 + lane];
+    ttc = a.tc[tic0 + lane];
+  }
+  // the current and the next tile: first row and route count in scalar registers, routes from the table
+  uint32_t cur_row = (uint32_t)__builtin_amdgcn_readfirstlane(te0) * (uint32_t)a.I;
+  uint32_t nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane(te1) * (uint32_t)a.I;
+  int cur_nr = __builtin_amdgcn_readfirstlane(nr0), nxt_nr = cur_nr;
+  const int rr = a.order[__builtin_amdgcn_readfirstlane(off0) + min((int)(lane & 3u), cur_nr - 1)];
+  int tr[MT_TILE] = {0, 0, 0, 0};
+  if (tl) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        b.q[t] = ldg16_q((t ? a.uc : a.gc) + (size_t)row * C + kc0);
-        b.s[t] = ldg4_q((const char*)(t ? a.us : a.gs) + ((row * (uint32_t)a.Gh + grp) * sbytes & ~3u));
-      }
-    };
-    // A row j = 4i + t: term t of route i (routes past nr repeat the last one; their D rows are unused)
-    const int tok_a = a.order[off + min((int)(j >> 2), nr - 1)] / a.k;
-    const int tok_d = a.order[off + min((int)g, nr - 1)] / a.k;  // the route of this lane's D rows
+    for (int i = 0; i < MT_TILE; ++i) tr[i] = a.order[tto + min(i, ttc - 1)];
+  }
+  // the first row of unit u (past the block's end: its last unit); u is at most two units past the
+  // segment, so in tile tic or tic + 1
+  auto unit_row = [&](int u) -> uint32_t {
+    const int uu = min(u, u1 - 1);
+    const bool n = uu >= (tic + 1) * rg_n;
+    return (n ? nxt_row : cur_row) + (uint32_t)(uu - (n ? tic + 1 : tic) * rg_n) * 16u;
+  };
+  // a unit's codes and its rows' scale words (the aligned word holding each)
+  auto load_unit = [&](int u, Buf& b) {
+    const uint32_t row = unit_row(u) + j;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      b.q[t] = ldg16_q((t ? a.uc : a.gc) + (size_t)row * C + kc0);
+      b.s[t] = ldg4_q((const char*)(t ? a.us : a.gs) + ((row * (uint32_t)a.Gh + grp) * sbytes & ~3u));
+    }
+  };
+  if (tl) s_td[lane] = MTTile{(uint32_t)tte * (uint32_t)a.I, ttc, {tr[0], tr[1], tr[2], tr[3]}};
+  int us = u0, ue = min(min(u1, (tic + 1) * rg_n), u0 + SEG);
+  // the segment's A operands: row j = 4i + t is term t of route i (routes past nr repeat the last one;
+  // their D rows are unused), and 1 / (4 s) of the token of this lane's D rows
+  q8v4 A[4];
+  float inv;
+  uint4 araw[4];
+  auto issue_a = [&](int route_a, int route_d) {  // the routes of A row j and of this lane's D rows
+    const int tok_a = route_a / a.k, tok_d = route_d / a.k;
     const uint4* asrc = a.xt + ((size_t)tok_a * a.S + sl) * 48 + min(j & 3u, 2u) * 16 + g * 4;
-    uint4 araw[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) araw[m] = ldg16_q(asrc + m);
-    const float inv = a.xinv[(size_t)tok_d * a.S + sl];
-    Buf b0, b1;
-    load_unit(us, b0);
-    load_unit(us + 1, b1);
-    wait_vm_q<0>();
-    rt_lds_barrier();  // the table image (first segment); the previous flush has read hst
-    q8v4 A[4];
+    inv = a.xinv[(size_t)tok_d * a.S + sl];
+  };
+  auto build_a = [&]() {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const bool z = (j & 3u) == 3u;
       A[m] = q8v4{z ? 0 : (int)araw[m].x, z ? 0 : (int)araw[m].y, z ? 0 : (int)araw[m].z, z ? 0 : (int)araw[m].w};
     }
-    auto unit = [&](int u, Buf& b, int par) {
-      const uint32_t rowc = (uint32_t)(min(u, ue - 1) - tic * rg_n) * 16u;
-      q8v4 B[2][4];
+  };
+  // the segment's staged h rows to their routes' rows
+  auto flush = [&]() {
+    const int rows = (ue - us) * 16;
+    const uint32_t row0 = (uint32_t)(us - tic * rg_n) * 16u;
+    const MTTile* td = s_td + (tic - tic0);
+    for (int x = threadIdx.x; x < cur_nr * rows; x += 1024) {
+      const int i = x / rows, r = x - i * rows;
+      a.h[(size_t)td->r[i] * a.I + row0 + (uint32_t)r] = hst[i][r];
+    }
+  };
+  // the first units' codes only after every block's small loads: issued earlier, they queue other blocks'
+  // descriptor and image loads behind the whole grid's code stream
+  issue_a(mt_route_of_lanes(rr, j >> 2), mt_route_of_lanes(rr, g));
+  Buf b0, b1;
+  load_unit(u0, b0);
+  load_unit(u0 + 1, b1);
+  wait_vm_q<0>();
+  build_a();
+  rt_lds_barrier();  // the table image and the tile table
+  if (ntb > 1) {
+    nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_td[1].row);
+    nxt_nr = __builtin_amdgcn_readfirstlane(s_td[1].nr);
+  }
+  auto unit = [&](int u, Buf& b, int par) {
+    const uint32_t rowc = unit_row(u);
+    q8v4 B[2][4];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) q8_decode8(tq, lk, b.q[t], B[t]);
-      float scl[2];
+    for (int t = 0; t < 2; ++t) q8_decode8(tq, lk, b.q[t], B[t]);
+    float scl[2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) scl[t] = scale_cvt(b.s[t], a.sdt, (ebase + rowc + j) * (uint32_t)a.Gh + grp);
+    for (int t = 0; t < 2; ++t) scl[t] = scale_cvt(b.s[t], a.sdt, (rowc + j) * (uint32_t)a.Gh + grp);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(scl[t]));  // converted before b.s is reloaded
-      load_unit(u + 2, b);
-      __builtin_amdgcn_sched_barrier(0);
-      if (dec) {
+    for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(scl[t]));  // converted before b.s is reloaded
+    load_unit(u + 2, b);
+    __builtin_amdgcn_sched_barrier(0);
+    if (dec) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          q8v4 acc = {0, 0, 0, 0};
+      for (int t = 0; t < 2; ++t) {
+        q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
-          for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[t][m], acc);
-          const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
-          if ((int)g < nr) gred[par][wv][t][g][j] = d * inv * scl[t];
-        }
+        for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[t][m], acc);
+        const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
+        if ((int)g < cur_nr) gred[par][wv][t][g][j] = d * inv * scl[t];
       }
-      rt_lds_barrier();
-      // SwiGLU: thread (route i, row jj) -> the staged h rows
-      if ((int)threadIdx.x < nr * 16 && u < ue) {
-        const int i = threadIdx.x >> 4, jj = threadIdx.x & 15;
-        float gsum = 0.f, usum = 0.f;
-        for (int w = 0; w < a.S; ++w) {
-          gsum += gred[par][w][0][i][jj];
-          usum += gred[par][w][1][i][jj];
-        }
-        float hv = silu_mul(gsum, usum, a.limit);
-        if (tq_bad) hv = __builtin_nanf("");
-        hst[i][(u - us) * 16 + jj] = from_float<bf16s>(hv).bits;
-      }
-    };
-    for (int u = us; u < ue; u += 2) {  // both calls unconditional: a unit past the end stores nothing
-      unit(u, b0, 0);
-      unit(u + 1, b1, 1);
     }
     rt_lds_barrier();
-    const int rows = (ue - us) * 16;
-    for (int x = threadIdx.x; x < nr * rows; x += 1024) {
-      const int i = x / rows, r = x - i * rows;
-      a.h[(size_t)a.order[off + i] * a.I + row0 + (uint32_t)r] = hst[i][r];
+    // SwiGLU: thread (route i, row jj) -> the staged h rows
+    if ((int)threadIdx.x < cur_nr * 16 && u < ue) {
+      // the LDS address is rebuilt here, not kept across the unit loop: held, it is spilled, and a
+      // reload from scratch waits for every code load in flight
+      int tid = (int)threadIdx.x;
+      asm volatile("" : "+v"(tid));
+      const int i = tid >> 4, jj = tid & 15;
+      float gsum = 0.f, usum = 0.f;
+      for (int w = 0; w < a.S; ++w) {
+        gsum += gred[par][w][0][i][jj];
+        usum += gred[par][w][1][i][jj];
+      }
+      float hv = silu_mul(gsum, usum, a.limit);
+      if (tq_bad) hv = __builtin_nanf("");
+      hst[i][(u - us) * 16 + jj] = from_float<bf16s>(hv).bits;
     }
-    us = ue;
+  };
+  // u0 and every tile and SEG bound are even, so a segment starts on a pair and only the block's last unit
+  // can be a pair's second past the end (loaded again, nothing stored)
+  for (int u = u0; u < u1; u += 2) {
+    if (u == ue) {      // the next segment
+      rt_lds_barrier();  // every h row of this one staged
+      flush();
+      us = ue;
+      if (us == (tic + 1) * rg_n) {
+        ++tic;
+        cur_row = nxt_row;
+        cur_nr = nxt_nr;
+        if (tic + 1 - tic0 < ntb) {
+          nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_td[tic + 1 - tic0].row);
+          nxt_nr = __builtin_amdgcn_readfirstlane(s_td[tic + 1 - tic0].nr);
+        }
+      }
+      ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
+      const MTTile* td = s_td + (tic - tic0);
+      issue_a(td->r[j >> 2], td->r[g]);
+      build_a();
+      wait_vm_q<0>();  // nothing of the switch stays in flight: the units' waits count their own loads
+    }
+    unit(u, b0, 0);
+    unit(u + 1, b1, 1);
   }
+  rt_lds_barrier();
+  flush();
   wait_vm_q<0>();
 }
 
@@ -299,6 +396,7 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
   __shared__ float s_inv[8][MT_TILE];
   __shared__ float red[2][8][RT][MT_TILE][16];       // [parity][wave][row-tile][route][row]
   __shared__ float yst[MT_TILE][SEG * 16 * RT];      // the segment's y rows
+  __shared__ MTTile s_td[MT_TPB];                    // the block's tiles
   const char* tq = (const char*)tqs;
   const Q8Keys lk = q8_keys(threadIdx.x & 63);
   const int lane = threadIdx.x & 63;
@@ -306,10 +404,10 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
   const uint32_t j = lane & 15, g = lane >> 4;
   const int nsl = a.I >> 8;
   const bool dec = wv < nsl;
-  const int rg_n = a.H / (16 * RT);
+  const int rg_n = a.H / (16 * RT);  // units per tile (>= 4)
   const int nt = __builtin_amdgcn_readfirstlane(*a.ntiles);
   const int U = nt * rg_n;
-  const int per = (U + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int per = ((U + (int)gridDim.x - 1) / (int)gridDim.x + 1) & ~1;  // even: see the unit loop
   const int u0 = (int)blockIdx.x * per, u1 = min(U, u0 + per);
 #pragma unroll
   for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
@@ -325,28 +423,59 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
     uint4 q[RT];
     uint32_t s[RT];
   };
-  for (int us = u0; us < u1;) {
-    const int tic = us / rg_n;
-    const int ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
-    const uint32_t ebase = (uint32_t)a.te[tic] * (uint32_t)a.H;
-    const uint32_t row0 = (uint32_t)(us - tic * rg_n) * (16u * RT);
-    const int off = a.to[tic], nr = a.tc[tic];  // 1 <= nr <= MT_TILE
-    // a unit's codes and its rows' scale words (the aligned word holding each)
-    auto load_unit = [&](int u, Buf& b) {
-      const uint32_t rbase = ebase + (uint32_t)(min(u, ue - 1) - tic * rg_n) * (16u * RT) + j;
+  const int tic0 = u0 / rg_n, ntb = (u1 - 1) / rg_n - tic0 + 1;  // the block's tiles (<= MT_TPB)
+  int tic = tic0;
+  // the first tile (every wave) and the next tile's row; wave 0, lane l < ntb: tile tic0 + l for the table
+  int zv = 0;
+  asm volatile("" : "+v"(zv));  // a lane value: these loads go through the vector unit
+  const int te0 = a.te[tic0 + zv], te1 = a.te[min(tic0 + 1, nt - 1) + zv];
+  const int off0 = a.to[tic0 + zv], nr0 = a.tc[tic0 + zv];
+  const bool tl = wv == 0 && lane < ntb;
+  int tte = 0, tto = 0, ttc = 1;
+  if (tl) {
+    tte = a.te[tic0 + lane];
+    tto = a.to[tic0 + lane];
+    ttc = a.tc[tic0 + lane];
+  }
+  // the current and the next tile: first row and route count in scalar registers, routes from the table
+  uint32_t cur_row = (uint32_t)__builtin_amdgcn_readfirstlane(te0) * (uint32_t)a.H;
+  uint32_t nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane(te1) * (uint32_t)a.H;
+  int cur_nr = __builtin_amdgcn_readfirstlane(nr0), nxt_nr = cur_nr;
+  const int rr = a.order[__builtin_amdgcn_readfirstlane(off0) + min((int)(lane & 3u), cur_nr - 1)];
+  int tr[MT_TILE] = {0, 0, 0, 0};
+  if (tl) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        b.q[rt] = ldg16_q(a.dc + (size_t)(rbase + (uint32_t)rt * 16u) * C + kc0);
-        b.s[rt] = ldg4_q((const char*)a.ds + (((rbase + (uint32_t)rt * 16u) * (uint32_t)a.Gi + grp) * sbytes & ~3u));
-      }
-    };
-    if (dec) {  // the tile's h slices -> A operands (this wave's own LDS rows)
+    for (int i = 0; i < MT_TILE; ++i) tr[i] = a.order[tto + min(i, ttc - 1)];
+  }
+  // the first row of unit u (past the block's end: its last unit); u is at most two units past the
+  // segment, so in tile tic or tic + 1
+  auto unit_row = [&](int u) -> uint32_t {
+    const int uu = min(u, u1 - 1);
+    const bool n = uu >= (tic + 1) * rg_n;
+    return (n ? nxt_row : cur_row) + (uint32_t)(uu - (n ? tic + 1 : tic) * rg_n) * (16u * RT);
+  };
+  // a unit's codes and its rows' scale words (the aligned word holding each)
+  auto load_unit = [&](int u, Buf& b) {
+    const uint32_t rbase = unit_row(u) + j;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      b.q[rt] = ldg16_q(a.dc + (size_t)(rbase + (uint32_t)rt * 16u) * C + kc0);
+      b.s[rt] = ldg4_q((const char*)a.ds + (((rbase + (uint32_t)rt * 16u) * (uint32_t)a.Gi + grp) * sbytes & ~3u));
+    }
+  };
+  if (tl) s_td[lane] = MTTile{(uint32_t)tte * (uint32_t)a.H, ttc, {tr[0], tr[1], tr[2], tr[3]}};
+  int us = u0, ue = min(min(u1, (tic + 1) * rg_n), u0 + SEG);
+  // the segment's A operands: the tile's h slices as two int8 terms per route (this wave's own LDS
+  // rows), then the wave's A fragments and the 1 / (4 s) of its D rows
+  q8v4 A[4];
+  float inv[2];
+  auto load_a = [&](int r0, int r1, int r2, int r3) {  // the tile's routes (past nr: the last one again)
+    if (dec) {
+      const int rt4[MT_TILE] = {r0, r1, r2, r3};
       uint4 hq[MT_TILE];
 #pragma unroll
-      for (int i = 0; i < MT_TILE; ++i) {
-        const int route = a.order[off + min(i, nr - 1)];
-        hq[i] = ldg16_q((const uint4*)(a.h + (size_t)route * a.I) + wv * 32 + (lane >> 1));
-      }
+      for (int i = 0; i < MT_TILE; ++i)
+        hq[i] = ldg16_q((const uint4*)(a.h + (size_t)rt4[i] * a.I) + wv * 32 + (lane >> 1));
       uint32_t* aw = (uint32_t*)ash[wv];
 #pragma unroll
       for (int i = 0; i < MT_TILE; ++i) {
@@ -361,75 +490,104 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
         aw[q8_aword((uint32_t)(2 * i + 1), lane >> 1, lane & 1)] = tw[1];
         if (lane == 0) s_inv[wv][i] = inv4s;
       }
-    }
-    Buf b0, b1;
-    load_unit(us, b0);
-    load_unit(us + 1, b1);
-    wait_vm_q<0>();
-    rt_lds_barrier();  // the table image (first segment); the previous flush has read yst
-    q8v4 A[4];
-    {
       const q8v4* as = (const q8v4*)ash[wv] + (j & (2 * MT_TILE - 1)) * 16 + g * 4;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const q8v4 v = as[m];
-        const bool z = (int)j >= 2 * nr;  // rows past the tile's routes
+        const bool z = (int)j >= 2 * cur_nr;  // rows past the tile's routes
         A[m] = q8v4{z ? 0 : v[0], z ? 0 : v[1], z ? 0 : v[2], z ? 0 : v[3]};
       }
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) inv[h2] = s_inv[wv][min(2 * (int)g + h2, MT_TILE - 1)];
     }
-    float inv[2];
+  };
+  // the segment's staged y rows to their routes' rows
+  auto flush = [&]() {
+    const int rows = (ue - us) * 16 * RT;
+    const uint32_t row0 = (uint32_t)(us - tic * rg_n) * (16u * RT);
+    const MTTile* td = s_td + (tic - tic0);
+    for (int x = threadIdx.x; x < cur_nr * rows; x += 512) {
+      const int i = x / rows, r = x - i * rows;
+      a.y[(size_t)td->r[i] * a.H + row0 + (uint32_t)r] = yst[i][r];
+    }
+  };
+  // the first units' codes only after every block's small loads: issued earlier, they queue other blocks'
+  // descriptor and image loads behind the whole grid's code stream
+  load_a(__builtin_amdgcn_readlane(rr, 0), __builtin_amdgcn_readlane(rr, 1), __builtin_amdgcn_readlane(rr, 2),
+         __builtin_amdgcn_readlane(rr, 3));
+  Buf b0, b1;
+  load_unit(u0, b0);
+  load_unit(u0 + 1, b1);
+  wait_vm_q<0>();
+  rt_lds_barrier();  // the table image and the tile table
+  if (ntb > 1) {
+    nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_td[1].row);
+    nxt_nr = __builtin_amdgcn_readfirstlane(s_td[1].nr);
+  }
+  auto unit = [&](int u, Buf& b, int par) {
+    const uint32_t rowc = unit_row(u);
+    q8v4 B[RT][4];
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) inv[h2] = s_inv[dec ? wv : 0][min(2 * (int)g + h2, MT_TILE - 1)];
-    auto unit = [&](int u, Buf& b, int par) {
-      const uint32_t rowc = (uint32_t)(min(u, ue - 1) - tic * rg_n) * (16u * RT);
-      q8v4 B[RT][4];
+    for (int rt = 0; rt < RT; ++rt) q8_decode8(tq, lk, b.q[rt], B[rt]);
+    float scl[RT];
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) q8_decode8(tq, lk, b.q[rt], B[rt]);
-      float scl[RT];
+    for (int rt = 0; rt < RT; ++rt)
+      scl[rt] = scale_cvt(b.s[rt], a.sdt, (rowc + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-        scl[rt] = scale_cvt(b.s[rt], a.sdt, (ebase + rowc + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
+    for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(scl[rt]));  // converted before b.s is reloaded
+    load_unit(u + 2, b);
+    __builtin_amdgcn_sched_barrier(0);
+    if (dec) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(scl[rt]));  // converted before b.s is reloaded
-      load_unit(u + 2, b);
-      __builtin_amdgcn_sched_barrier(0);
-      if (dec) {
+      for (int rt = 0; rt < RT; ++rt) {
+        q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          q8v4 acc = {0, 0, 0, 0};
+        for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[rt][m], acc);
+        // route r: rows 2r, 2r + 1 = lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
 #pragma unroll
-          for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[rt][m], acc);
-          // route r: rows 2r, 2r + 1 = lanes 16 (r / 2) + j, registers 2 (r % 2), 2 (r % 2) + 1
-#pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2) {
-            const int r = 2 * (int)g + h2;
-            if (r < nr) {
-              const float d = h2 ? (float)acc[2] + (float)acc[3] * 0.0078125f : (float)acc[0] + (float)acc[1] * 0.0078125f;
-              red[par][wv][rt][r][j] = d * inv[h2] * scl[rt];
-            }
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int r = 2 * (int)g + h2;
+          if (r < cur_nr) {
+            const float d = h2 ? (float)acc[2] + (float)acc[3] * 0.0078125f : (float)acc[0] + (float)acc[1] * 0.0078125f;
+            red[par][wv][rt][r][j] = d * inv[h2] * scl[rt];
           }
         }
       }
-      rt_lds_barrier();
-      if ((int)threadIdx.x < nr * 16 * RT && u < ue) {
-        const int i = threadIdx.x / (16 * RT), rt = (threadIdx.x >> 4) % RT, jj = threadIdx.x & 15;
-        float v = 0.f;
-        for (int w = 0; w < nsl; ++w) v += red[par][w][rt][i][jj];
-        yst[i][(u - us) * 16 * RT + rt * 16 + jj] = v;
-      }
-    };
-    for (int u = us; u < ue; u += 2) {  // both calls unconditional: a unit past the end stores nothing
-      unit(u, b0, 0);
-      unit(u + 1, b1, 1);
     }
     rt_lds_barrier();
-    const int rows = (ue - us) * 16 * RT;
-    for (int x = threadIdx.x; x < nr * rows; x += 512) {
-      const int i = x / rows, r = x - i * rows;
-      a.y[(size_t)a.order[off + i] * a.H + row0 + (uint32_t)r] = yst[i][r];
+    if ((int)threadIdx.x < cur_nr * 16 * RT && u < ue) {
+      const int i = threadIdx.x / (16 * RT), rt = (threadIdx.x >> 4) % RT, jj = threadIdx.x & 15;
+      float v = 0.f;
+      for (int w = 0; w < nsl; ++w) v += red[par][w][rt][i][jj];
+      yst[i][(u - us) * 16 * RT + rt * 16 + jj] = v;
     }
-    us = ue;
+  };
+  // u0 and every tile and SEG bound are even, so a segment starts on a pair and only the block's last unit
+  // can be a pair's second past the end (loaded again, nothing stored)
+  for (int u = u0; u < u1; u += 2) {
+    if (u == ue) {      // the next segment
+      rt_lds_barrier();  // every y row of this one staged
+      flush();
+      us = ue;
+      if (us == (tic + 1) * rg_n) {
+        ++tic;
+        cur_row = nxt_row;
+        cur_nr = nxt_nr;
+        if (tic + 1 - tic0 < ntb) {
+          nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_td[tic + 1 - tic0].row);
+          nxt_nr = __builtin_amdgcn_readfirstlane(s_td[tic + 1 - tic0].nr);
+        }
+      }
+      ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
+      const MTTile* td = s_td + (tic - tic0);
+      load_a(__builtin_amdgcn_readfirstlane(td->r[0]), __builtin_amdgcn_readfirstlane(td->r[1]),
+             __builtin_amdgcn_readfirstlane(td->r[2]), __builtin_amdgcn_readfirstlane(td->r[3]));
+    }
+    unit(u, b0, 0);
+    unit(u + 1, b1, 1);
   }
+  rt_lds_barrier();
+  flush();
   wait_vm_q<0>();
 }
 
@@ -485,10 +643,28 @@ static MTWorkspace mt_layout(int64_t T, int64_t k, int64_t E, int64_t H) {
   return w;
 }
 
+// Grid of a persistent expert kernel over tiles of `units` units each (mt_tail), and the most tiles one
+// of its blocks can touch: its units (ceil(tiles x units / grid), rounded up to even) may start at a
+// tile's last unit.
+static int64_t mt_grid(int64_t tiles_ub, int64_t units) {
+  return std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * units));
+}
+static int64_t mt_tiles_per_block(int64_t tiles_ub, int64_t units) {
+  const int64_t per = ((tiles_ub * units + mt_grid(tiles_ub, units) - 1) / mt_grid(tiles_ub, units) + 1) & ~1LL;
+  return (per + units - 1) / units + 1;
+}
+
+// Tiles of one layer, at most: each holds at least one route.
+static int64_t mt_tiles_ub(int64_t T, int64_t k, int64_t E) {
+  const int64_t R = T * k;
+  return std::min<int64_t>(R, (R + MT_TILE - 1) / MT_TILE + E);
+}
+
 bool moe_tiles_supported(int64_t T, int64_t E, int64_t H, int64_t I, int64_t k, int64_t group_h, int64_t group_i) {
   return T >= 1 && T <= 256 && k >= 1 && k <= 16 && k <= E && E >= 1 && E <= 1024 && H % 256 == 0 && H <= 4096 &&
          I % 256 == 0 && I <= 2048 && group_h % 256 == 0 && group_i % 256 == 0 && (int64_t)E * I <= 0x7fffffffLL &&
-         (int64_t)E * H <= 0x7fffffffLL;
+         (int64_t)E * H <= 0x7fffffffLL && mt_tiles_per_block(mt_tiles_ub(T, k, E), I / 16) <= MT_TPB &&
+         mt_tiles_per_block(mt_tiles_ub(T, k, E), H / 64) <= MT_TPB;
 }
 
 }  // namespace keep
@@ -567,10 +743,9 @@ static MTArgs mt_args(int64_t H, int64_t I, int64_t k, int64_t num_experts, cons
 static void mt_tail(const MTArgs& a, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t k, int64_t num_experts,
                     const int32_t* idx, const float* w, const MTWorkspace& L, void* out, int out_dtype,
                     hipStream_t s) {
-  const int64_t R = T * k;
-  const int64_t tiles_ub = std::min<int64_t>(R, L.max_tiles);
-  const unsigned g1 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (I / 16)));
-  const unsigned g2 = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, tiles_ub * (H / 64)));
+  const int64_t tiles_ub = mt_tiles_ub(T, k, num_experts);
+  const unsigned g1 = (unsigned)mt_grid(tiles_ub, I / 16);
+  const unsigned g2 = (unsigned)mt_grid(tiles_ub, H / 64);
   if (x_dtype == KEEP_BF16)
     hipLaunchKernelGGL((k_moeq_gateup_tiles<true>), dim3(g1), dim3(1024), 0, s, a);
   else

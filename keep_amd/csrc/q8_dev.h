@@ -26,10 +26,11 @@
 // power of two s so that max |x| s lies in [32, 64), then split into int8
 // terms t0 + t1 / 128 + t2 / 128^2 (each a round-to-nearest of the scaled
 // remainder, so every |t| <= 64); A rows 0-2 are the three terms and the dot is
-// (D0 + D1 / 128 + D2 / 128^2) / (4 s). The residual is below 2^-21 of max |x|,
-// under the rounding of the fp32 sums. h (bf16) uses two terms (residual below
-// 2^-14 of its slice's max; in base 128 in the two-launch kernels, base 256 in
-// the one-launch layer), so the down kernels put route r's terms in two rows
+// (D0 + D1 / 128 + D2 / 128^2) / (4 s). The residual is at most 2^-20 of
+// max |x| (half a unit of the last term, 1 / (2 s 128^2), with s >= 32 / max |x|).
+// h (bf16) uses two terms, with the residual at most 2^-13 of its slice's max
+// in base 128 (the two-launch and few-token kernels) and 2^-14 in base 256
+// (the one-launch layer), so the down kernels put route r's terms in two rows
 // of A. Each wave builds its terms once, in LDS.
 //
 // K layout. Lane l of an MFMA holds row (A) / column (B) l % 16 and 16 bytes

@@ -96,6 +96,50 @@ def test_tiles_many_routes_per_expert_vs_oracle(dev, xdt):
     _check(out, want)
 
 
+def test_tiles_blocks_across_three_tiles_vs_oracle(dev):
+    """256 tokens x 8 routes over 16 experts (512 tiles of 4 routes): a gate/up block takes 32 units of
+    16-unit tiles and a down block 8 units of 4-unit tiles, so blocks start mid-tile and run through up to
+    three tiles, their code loads crossing each tile boundary two units ahead.
+
+    Each stage is checked on its own: every stored h (bf16, the route's row of h_work) lies within one bf16
+    ulp of the float64 SwiGLU (plus 1e-4 of the row's rms where the dots cancel), and the output lies within
+    the bound of the down kernel's arithmetic around the float64 down and combine of the stored h: each h
+    element enters as two int8 terms under a power of two per 256-wide slice, 2^(e - 6) with
+    2^(e - 1) <= max |h| < 2^e, so it is off by at most 2^(e - 14); the rest is exact int32 sums and fp32
+    scaling. With I = 256 and one heavy-tailed slice per route, an end-to-end bound against the float64
+    layer would measure bf16 ties and that split, not the schedule."""
+    E, H, I, k, T = 16, 256, 256, 8, 256
+    gate = synth.projection_np(E, I, H, seed=71)
+    up = synth.projection_np(E, I, H, seed=72)
+    down = synth.projection_np(E, H, I, seed=73)
+    x = synth.rht_activations(T, H, seed=74, device=dev)
+    z = synth.router_logits(T, E, seed=75, device=dev)
+    r = keep_amd.router_dual_topk(z, k)
+    assert keep_amd.nn.moe_tiles_supported(T, E, H, I, k, H, I)
+    tt = lambda p: (_t(p[0], dev), _t(p[1], dev))  # noqa: E731
+    h_work = torch.empty((T * k * I,), dtype=torch.bfloat16, device=dev)
+    out = keep_amd.moe_decode(x, r.idx, r.weight, tt(gate), tt(up), tt(down), h_work=h_work)
+    h = h_work.float().cpu().numpy().reshape(T, k, I).astype(np.float64)
+    xs = x.float().cpu().numpy().astype(np.float64)
+    idx, w = r.idx.cpu().numpy(), r.weight.cpu().numpy().astype(np.float64)
+    wg, wu, wd = ops.dense(*gate), ops.dense(*up), ops.dense(*down)
+    want, bound = np.zeros((T, H)), np.zeros((T, H))
+    for t in range(T):
+        for j in range(k):
+            e = idx[t, j]
+            h64 = ops.swiglu(wg[e] @ xs[t], wu[e] @ xs[t])
+            ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(h64), 2.0 ** -126))) - 7)
+            hb = ulp + 1e-4 * np.sqrt(np.mean(h64 * h64))
+            assert np.all(np.abs(h[t, j] - h64) <= hb), f"h of token {t} route {j} (expert {e})"
+            want[t] += w[t, j] * (wd[e] @ h[t, j])
+            mx = np.abs(h[t, j]).reshape(-1, 256).max(axis=1)
+            step = np.where(mx > 0, 2.0 ** (np.floor(np.log2(np.maximum(mx, 2.0 ** -126))) + 1 - 14), 0.0)
+            bound[t] += abs(w[t, j]) * (np.abs(wd[e]) @ (np.repeat(step, 256) + 1e-6 * np.abs(h[t, j])))
+    g = out.float().cpu().numpy()
+    assert ops.max_rel_err(g, want) <= TOL
+    assert np.all(np.abs(g - want) <= bound), f"worst excess {np.max(np.abs(g - want) - bound):.3g}"
+
+
 def test_tiles_zero_weight_and_bad_expert(dev):
     """A zero-weight route adds nothing; an out-of-range expert with a weight
     makes its token's row NaN and leaves the others intact."""
