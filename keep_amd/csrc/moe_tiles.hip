@@ -108,7 +108,8 @@ struct MTPro {
 // t < T builds token t's x terms (as k_q8_xterms); block T routes every token
 // (wave w takes tokens w, w + 16, ..., each as k_router does, with the same
 // outputs) and keeps the served slots in LDS, from which it runs the route
-// plan (plan_block, as k_route_plan over idx).
+// plan (as k_route_plan over idx: plan_small up to 128 routes, else
+// plan_block).
 template <int PER, bool XBF>
 __global__ __launch_bounds__(1024) void k_mt_prologue(MTPro p) {
   __shared__ PlanLds L;
@@ -143,8 +144,13 @@ __global__ __launch_bounds__(1024) void k_mt_prologue(MTPro p) {
     }
   }
   __syncthreads();
-  plan_block([&](int r) { return s_r[r]; }, p.T * p.k, p.S, MT_TILE, p.order, p.inverse, p.counts, p.offsets,
-             p.te, p.to, p.tc, p.max_tiles, p.nt, L);
+  auto route = [&](int r) { return s_r[r]; };
+  if (p.T * p.k <= PLAN_SMALL_R)
+    plan_small(route, p.T * p.k, p.S, MT_TILE, p.order, p.inverse, p.counts, p.offsets, p.te, p.to, p.tc,
+               p.max_tiles, p.nt, L);
+  else
+    plan_block(route, p.T * p.k, p.S, MT_TILE, p.order, p.inverse, p.counts, p.offsets, p.te, p.to, p.tc,
+               p.max_tiles, p.nt, L);
 }
 
 // ------------------------------------------------------------------ gate/up
@@ -306,7 +312,7 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
   Buf b0, b1;
   load_unit(u0, b0);
   load_unit(u0 + 1, b1);
-  wait_vm_q<0>();
+  wait_vm_q<4>();  // all but the second unit's four loads: the image, A and the first unit (loads retire in order)
   build_a();
   rt_lds_barrier();  // the table image and the tile table
   if (ntb > 1) {
@@ -518,7 +524,7 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
   Buf b0, b1;
   load_unit(u0, b0);
   load_unit(u0 + 1, b1);
-  wait_vm_q<0>();
+  wait_vm_q<2 * RT>();  // all but the second unit's loads: the image, h and the first unit (loads retire in order)
   rt_lds_barrier();  // the table image and the tile table
   if (ntb > 1) {
     nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_td[1].row);

@@ -1,4 +1,4 @@
-// Device route plan kernel (the plan itself is plan_block in plan_dev.h).
+// Device route plan kernel (the plan itself is plan_small / plan_block in plan_dev.h).
 #include "plan_dev.h"
 
 namespace keep {
@@ -8,8 +8,11 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_route_plan(const int32_t* rhs,
                                                              int32_t* offsets, int32_t* te, int32_t* to, int32_t* tc,
                                                              int max_tiles, int32_t* n_tiles_out) {
   __shared__ PlanLds L;
-  plan_block([&](int r) { return rhs[r]; }, R, E, tile, order, inverse, counts, offsets, te, to, tc, max_tiles,
-             n_tiles_out, L);
+  auto route = [&](int r) { return rhs[r]; };
+  if (R <= PLAN_SMALL_R)
+    plan_small(route, R, E, tile, order, inverse, counts, offsets, te, to, tc, max_tiles, n_tiles_out, L);
+  else
+    plan_block(route, R, E, tile, order, inverse, counts, offsets, te, to, tc, max_tiles, n_tiles_out, L);
 }
 
 }  // namespace keep

@@ -189,4 +189,134 @@ __device__ __forceinline__ void plan_block(Route route, int R, int E, int tile, 
   }
 }
 
+constexpr int PLAN_SMALL_R = 128;  // routes plan_small takes: two per lane of one wave
+
+// plan_block's outputs for R <= PLAN_SMALL_R, with one block barrier. Wave 0
+// holds routes lane and lane + 64 and ranks each against all of them with
+// ballots over the bucket bits (most significant first: a lane below on a
+// higher bit is less, and the equal set narrows), which gives the stable
+// position; it writes order and inverse, scatters the buckets into LDS in
+// sorted order, finds the first position of each bucket's run there (the
+// leaders), and writes each run's tiles at the exclusive scan of the tile
+// counts over the sorted positions. After the barrier every thread writes the
+// counts and offsets of its experts (two binary searches of the sorted
+// buckets) and zero-fills the descriptors past the last tile.
+template <typename Route>
+__device__ __forceinline__ void plan_small(Route route, int R, int E, int tile, int32_t* order, int32_t* inverse,
+                                           int32_t* counts, int32_t* offsets, int32_t* te, int32_t* to, int32_t* tc,
+                                           int max_tiles, int32_t* n_tiles_out, PlanLds& L) {
+  int* sb = L.cnt;         // the buckets in sorted order (R <= 128 <= PLAN_MAX_E + 1 entries)
+  int* ntot = L.wtot[0];   // [0]: the number of tiles
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (wv == 0) {
+    const bool v0 = lane < R, v1 = lane + 64 < R;
+    int k0 = 0, k1 = 0;  // buckets: E collects invalid expert ids
+    if (v0) {
+      const int e = route(lane);
+      k0 = (e < 0 || e >= E) ? E : e;
+    }
+    if (v1) {
+      const int e = route(lane + 64);
+      k1 = (e < 0 || e >= E) ? E : e;
+    }
+    const int nbits = 32 - __builtin_clz((unsigned)E);  // bucket ids 0..E
+    const uint64_t in0 = __ballot(v0), in1 = __ballot(v1);
+    uint64_t eq00 = in0, eq01 = in1, eq10 = in0, eq11 = in1;  // eqAB: routes of half B equal so far to my A key
+    uint64_t lt00 = 0, lt01 = 0, lt10 = 0, lt11 = 0;          // ... and below it
+    for (int b = nbits - 1; b >= 0; --b) {
+      const uint64_t m0 = __ballot((k0 >> b) & 1), m1 = __ballot((k1 >> b) & 1);
+      const uint64_t s0 = ((k0 >> b) & 1) ? ~0ull : 0ull, s1 = ((k1 >> b) & 1) ? ~0ull : 0ull;
+      lt00 |= eq00 & ~m0 & s0;
+      lt01 |= eq01 & ~m1 & s0;
+      lt10 |= eq10 & ~m0 & s1;
+      lt11 |= eq11 & ~m1 & s1;
+      eq00 &= ~(m0 ^ s0);
+      eq01 &= ~(m1 ^ s0);
+      eq10 &= ~(m0 ^ s1);
+      eq11 &= ~(m1 ^ s1);
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    const int p0 = __popcll(lt00) + __popcll(lt01) + __popcll(eq00 & below);
+    const int p1 = __popcll(lt10) + __popcll(lt11) + __popcll(eq10) + __popcll(eq11 & below);
+    if (v0) {
+      order[p0] = lane;
+      inverse[lane] = p0;
+      sb[p0] = k0;
+    }
+    if (v1) {
+      order[p1] = lane + 64;
+      inverse[lane + 64] = p1;
+      sb[p1] = k1;
+    }
+    // the sorted view: lane q holds positions q and q + 64
+    const int b0 = v0 ? sb[lane] : -1, b1 = v1 ? sb[lane + 64] : -1;
+    const int pb0 = sb[lane > 0 ? lane - 1 : 0], pb1 = sb[lane + 63];
+    const bool l0 = v0 && (lane == 0 || pb0 != b0), l1 = v1 && pb1 != b1;  // first position of a run
+    const uint64_t L0 = __ballot(l0), L1 = __ballot(l1);
+    auto run_end = [&](int q) {  // the next leader after position q, or R
+      if (q < 64) {
+        const uint64_t m = q < 63 ? L0 >> (q + 1) : 0ull;
+        if (m) return q + 1 + __builtin_ctzll(m);
+        return L1 ? 64 + __builtin_ctzll(L1) : R;
+      }
+      const int t = q - 64;
+      const uint64_t m = t < 63 ? L1 >> (t + 1) : 0ull;
+      return m ? q + 1 + __builtin_ctzll(m) : R;
+    };
+    const int c0 = l0 ? run_end(lane) - lane : 0, c1 = l1 ? run_end(lane + 64) - (lane + 64) : 0;
+    const int n0 = (c0 + tile - 1) / tile, n1 = (c1 + tile - 1) / tile;
+    int x0 = n0, x1 = n1;  // inclusive scans over the lanes
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y0 = __shfl_up(x0, d, 64), y1 = __shfl_up(x1, d, 64);
+      if (lane >= d) {
+        x0 += y0;
+        x1 += y1;
+      }
+    }
+    const int tot0 = __shfl(x0, 63, 64), total = tot0 + __shfl(x1, 63, 64);
+    const int tb0 = x0 - n0, tb1 = tot0 + x1 - n1;
+    for (int i = 0; i < n0; ++i) {
+      te[tb0 + i] = b0 < E ? b0 : -1;
+      to[tb0 + i] = lane + i * tile;
+      tc[tb0 + i] = min(tile, c0 - i * tile);
+    }
+    for (int i = 0; i < n1; ++i) {
+      te[tb1 + i] = b1 < E ? b1 : -1;
+      to[tb1 + i] = lane + 64 + i * tile;
+      tc[tb1 + i] = min(tile, c1 - i * tile);
+    }
+    // the invalid routes' run sorts last: its tiles are not counted
+    const uint64_t bad0 = __ballot(l0 && b0 == E), bad1 = __ballot(l1 && b1 == E);
+    const int nbad = bad1 ? __shfl(n1, __builtin_ctzll(bad1), 64) : bad0 ? __shfl(n0, __builtin_ctzll(bad0), 64) : 0;
+    if (lane == 0) {
+      n_tiles_out[0] = total - nbad;
+      ntot[0] = total;
+    }
+  }
+  __syncthreads();
+  const int total = ntot[0];
+  for (int e = tid; e < E; e += PLAN_THREADS) {
+    int lo = 0, hi = R;  // the first sorted position with bucket >= e
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sb[mid] < e) lo = mid + 1;
+      else hi = mid;
+    }
+    int lo2 = lo, hi2 = R;  // ... and > e
+    while (lo2 < hi2) {
+      const int mid = (lo2 + hi2) >> 1;
+      if (sb[mid] <= e) lo2 = mid + 1;
+      else hi2 = mid;
+    }
+    offsets[e] = lo;
+    counts[e] = lo2 - lo;
+  }
+  for (int ti = total + tid; ti < max_tiles; ti += PLAN_THREADS) {
+    te[ti] = 0;
+    to[ti] = 0;
+    tc[ti] = 0;
+  }
+}
+
 }  // namespace keep

@@ -76,11 +76,15 @@ def test_router_fewer_resident_than_k(dev):
                                                 (0, 5, 8, False, 0), (16384, 384, 64, False, 0),
                                                 (20000, 384, 64, False, 0), (5000, 1024, 32, False, 0),
                                                 (1025, 1, 4, False, 0), (12288, 384, 64, True, 0),
-                                                (300, 16, 8, False, 21), (20000, 384, 64, False, 130)])
+                                                (300, 16, 8, False, 21), (20000, 384, 64, False, 130),
+                                                (48, 384, 4, False, 0), (96, 384, 4, True, 0),
+                                                (128, 16, 4, False, 9), (127, 1024, 3, True, 5),
+                                                (64, 1, 4, False, 0), (65, 2, 64, False, 3), (1, 384, 4, False, 0),
+                                                (100, 7, 3, True, 100), (128, 384, 128, False, 0)])
 def test_route_plan_exact(dev, R, E, tile, skew, bad):
-    # each of the plan's 16 waves ranks a contiguous range of max(64, ceil(R / 16)) routes (R = 6:
-    # one wave holds them all); `bad` routes get expert ids outside [0, E): they sort last, in tiles
-    # of expert -1
+    # up to 128 routes one wave ranks them all (two per lane, across both halves); beyond, each of the
+    # plan's 16 waves ranks a contiguous range of max(64, ceil(R / 16)) routes; `bad` routes get expert
+    # ids outside [0, E): they sort last, in tiles of expert -1
     rng = np.random.default_rng(R + E)
     rhs = rng.integers(0, E, size=R).astype(np.int32)
     if skew:  # a few hot experts: long same-expert runs inside each wave
