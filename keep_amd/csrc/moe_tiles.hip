@@ -169,9 +169,8 @@ __global__ __launch_bounds__(1024) void k_mt_prologue(MTPro p) {
 // LDS table when the kernel starts, and every wave reads its first tile
 // itself, all with vector loads: a scalar load in flight would make each LDS
 // wait of the decode wait for it as well. The first units' codes are issued
-// after the block's small loads, as every block then is, so that no block's
-// descriptor loads queue behind the grid's code stream; a switch to a new
-// segment waits only for that segment's A operands. Outputs are staged in LDS
+// after the block's small loads; a switch to a new segment waits only for
+// that segment's A operands. Outputs are staged in LDS
 // and written when their segment ends. The cross-wave partial sums are
 // double-buffered by unit parity: a wave writes a unit's partials only after
 // the barrier that the previous reader of that buffer has passed.
@@ -306,8 +305,8 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
       a.h[(size_t)td->r[i] * a.I + row0 + (uint32_t)r] = hst[i][r];
     }
   };
-  // the first units' codes only after every block's small loads: issued earlier, they queue other blocks'
-  // descriptor and image loads behind the whole grid's code stream
+  // the first units' codes after the block's small loads (issued before the route and A loads, they
+  // measured no faster)
   issue_a(mt_route_of_lanes(rr, j >> 2), mt_route_of_lanes(rr, g));
   Buf b0, b1;
   load_unit(u0, b0);
@@ -517,8 +516,8 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
       a.y[(size_t)td->r[i] * a.H + row0 + (uint32_t)r] = yst[i][r];
     }
   };
-  // the first units' codes only after every block's small loads: issued earlier, they queue other blocks'
-  // descriptor and image loads behind the whole grid's code stream
+  // the first units' codes after the block's small loads (issued before the route and A loads, they
+  // measured no faster)
   load_a(__builtin_amdgcn_readlane(rr, 0), __builtin_amdgcn_readlane(rr, 1), __builtin_amdgcn_readlane(rr, 2),
          __builtin_amdgcn_readlane(rr, 3));
   Buf b0, b1;
