@@ -389,17 +389,20 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
 }
 
 // Down: a unit is 64 rows (four 16-row tiles, 32 KiB of codes per block);
-// wave w < I / 256 owns K slice w. The A operand holds two int8 terms of h
-// for each of the tile's routes (rows 2r, 2r + 1; rows past them zero),
-// built from h when the block enters a segment; route r's dot is D rows 2r,
-// 2r + 1.
-__global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
-  constexpr int RT = 4;
+// K slice s (I / 256 of them) has two waves, s and s + I / 256, taking row
+// tiles 0-1 and 2-3. The A operand holds two int8 terms of h for each of the
+// tile's routes (rows 2r, 2r + 1; rows past them zero), built in LDS by the
+// slice's first wave when the block enters a segment and read by both; route
+// r's dot is D rows 2r, 2r + 1. The partial sums are kept per slice and row
+// tile and summed over the slices in slice order.
+__global__ __launch_bounds__(1024) void k_moeq_down_tiles(MTArgs a) {
+  constexpr int RT = 4;   // row tiles per unit
+  constexpr int RW = 2;   // row tiles per wave
   constexpr int SEG = 48;  // units per segment (y staging capacity)
   __shared__ uint4 tqs[TQR_BYTES / 16];
-  __shared__ uint4 ash[8][2 * MT_TILE * 16];         // [wave][row * 16 + slot]
+  __shared__ uint4 ash[8][2 * MT_TILE * 16];         // [slice][row * 16 + slot]
   __shared__ float s_inv[8][MT_TILE];
-  __shared__ float red[2][8][RT][MT_TILE][16];       // [parity][wave][row-tile][route][row]
+  __shared__ float red[2][8][RT][MT_TILE][16];       // [parity][slice][row-tile][route][row]
   __shared__ float yst[MT_TILE][SEG * 16 * RT];      // the segment's y rows
   __shared__ MTTile s_td[MT_TPB];                    // the block's tiles
   const char* tq = (const char*)tqs;
@@ -408,25 +411,26 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t j = lane & 15, g = lane >> 4;
   const int nsl = a.I >> 8;
-  const bool dec = wv < nsl;
+  const bool dec = wv < 2 * nsl;  // this wave owns half of a K slice's row tiles
+  const int sl = dec ? wv % nsl : 0, hf = dec ? wv / nsl : 0;
   const int rg_n = a.H / (16 * RT);  // units per tile (>= 4)
   const int nt = __builtin_amdgcn_readfirstlane(*a.ntiles);
   const int U = nt * rg_n;
   const int per = ((U + (int)gridDim.x - 1) / (int)gridDim.x + 1) & ~1;  // even: see the unit loop
   const int u0 = (int)blockIdx.x * per, u1 = min(U, u0 + per);
 #pragma unroll
-  for (int u = 0; u < 8; ++u) dma16_q(a.tq + (wv * 8 + u) * 64 + lane, tqs + (wv * 8 + u) * 64);
+  for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
   if (u0 >= u1) {
     wait_vm_q<0>();
     return;
   }
   const uint32_t C = (uint32_t)a.I >> 3;
-  const uint32_t kc0 = (dec ? wv : 0) * 32 + g * 8;
-  const uint32_t grp = (uint32_t)((dec ? wv : 0) * 256) / (uint32_t)a.gsz_i;
+  const uint32_t kc0 = (uint32_t)sl * 32 + g * 8;
+  const uint32_t grp = (uint32_t)(sl * 256) / (uint32_t)a.gsz_i;
   const uint32_t sbytes = a.sdt == KEEP_F32 ? 4u : 2u;
   struct Buf {
-    uint4 q[RT];
-    uint32_t s[RT];
+    uint4 q[RW];
+    uint32_t s[RW];
   };
   const int tic0 = u0 / rg_n, ntb = (u1 - 1) / rg_n - tic0 + 1;  // the block's tiles (<= MT_TPB)
   int tic = tic0;
@@ -460,28 +464,29 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
     return (n ? nxt_row : cur_row) + (uint32_t)(uu - (n ? tic + 1 : tic) * rg_n) * (16u * RT);
   };
   // a unit's codes and its rows' scale words (the aligned word holding each)
-  auto load_unit = [&](int u, Buf& b) {
-    const uint32_t rbase = unit_row(u) + j;
+  auto load_unit = [&](int u, Buf& b) {  // this wave's row tiles 2 hf, 2 hf + 1
+    const uint32_t rbase = unit_row(u) + (uint32_t)hf * (16u * RW) + j;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
+    for (int rt = 0; rt < RW; ++rt) {
       b.q[rt] = ldg16_q(a.dc + (size_t)(rbase + (uint32_t)rt * 16u) * C + kc0);
       b.s[rt] = ldg4_q((const char*)a.ds + (((rbase + (uint32_t)rt * 16u) * (uint32_t)a.Gi + grp) * sbytes & ~3u));
     }
   };
   if (tl) s_td[lane] = MTTile{(uint32_t)tte * (uint32_t)a.H, ttc, {tr[0], tr[1], tr[2], tr[3]}};
   int us = u0, ue = min(min(u1, (tic + 1) * rg_n), u0 + SEG);
-  // the segment's A operands: the tile's h slices as two int8 terms per route (this wave's own LDS
-  // rows), then the wave's A fragments and the 1 / (4 s) of its D rows
+  // the segment's A operands: the slice's first wave writes the tile's h slices as two int8 terms per
+  // route into the slice's LDS rows; after a block barrier both waves of the slice read their A
+  // fragments and the 1 / (4 s) of their D rows
   q8v4 A[4];
   float inv[2];
-  auto load_a = [&](int r0, int r1, int r2, int r3) {  // the tile's routes (past nr: the last one again)
-    if (dec) {
+  auto build_a = [&](int r0, int r1, int r2, int r3) {  // the tile's routes (past nr: the last one again)
+    if (dec && hf == 0) {
       const int rt4[MT_TILE] = {r0, r1, r2, r3};
       uint4 hq[MT_TILE];
 #pragma unroll
       for (int i = 0; i < MT_TILE; ++i)
-        hq[i] = ldg16_q((const uint4*)(a.h + (size_t)rt4[i] * a.I) + wv * 32 + (lane >> 1));
-      uint32_t* aw = (uint32_t*)ash[wv];
+        hq[i] = ldg16_q((const uint4*)(a.h + (size_t)rt4[i] * a.I) + sl * 32 + (lane >> 1));
+      uint32_t* aw = (uint32_t*)ash[sl];
 #pragma unroll
       for (int i = 0; i < MT_TILE; ++i) {
         float v[4];
@@ -493,9 +498,13 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
         q8_digits2(v, sc, tw);
         aw[q8_aword((uint32_t)(2 * i), lane >> 1, lane & 1)] = tw[0];
         aw[q8_aword((uint32_t)(2 * i + 1), lane >> 1, lane & 1)] = tw[1];
-        if (lane == 0) s_inv[wv][i] = inv4s;
+        if (lane == 0) s_inv[sl][i] = inv4s;
       }
-      const q8v4* as = (const q8v4*)ash[wv] + (j & (2 * MT_TILE - 1)) * 16 + g * 4;
+    }
+  };
+  auto read_a = [&]() {  // after the barrier that follows build_a
+    if (dec) {
+      const q8v4* as = (const q8v4*)ash[sl] + (j & (2 * MT_TILE - 1)) * 16 + g * 4;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const q8v4 v = as[m];
@@ -503,7 +512,7 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
         A[m] = q8v4{z ? 0 : v[0], z ? 0 : v[1], z ? 0 : v[2], z ? 0 : v[3]};
       }
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) inv[h2] = s_inv[wv][min(2 * (int)g + h2, MT_TILE - 1)];
+      for (int h2 = 0; h2 < 2; ++h2) inv[h2] = s_inv[sl][min(2 * (int)g + h2, MT_TILE - 1)];
     }
   };
   // the segment's staged y rows to their routes' rows
@@ -511,40 +520,42 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
     const int rows = (ue - us) * 16 * RT;
     const uint32_t row0 = (uint32_t)(us - tic * rg_n) * (16u * RT);
     const MTTile* td = s_td + (tic - tic0);
-    for (int x = threadIdx.x; x < cur_nr * rows; x += 512) {
+    for (int x = threadIdx.x; x < cur_nr * rows; x += 1024) {
       const int i = x / rows, r = x - i * rows;
       a.y[(size_t)td->r[i] * a.H + row0 + (uint32_t)r] = yst[i][r];
     }
   };
   // the first units' codes after the block's small loads (issued before the route and A loads, they
   // measured no faster)
-  load_a(__builtin_amdgcn_readlane(rr, 0), __builtin_amdgcn_readlane(rr, 1), __builtin_amdgcn_readlane(rr, 2),
-         __builtin_amdgcn_readlane(rr, 3));
+  build_a(__builtin_amdgcn_readlane(rr, 0), __builtin_amdgcn_readlane(rr, 1), __builtin_amdgcn_readlane(rr, 2),
+          __builtin_amdgcn_readlane(rr, 3));
   Buf b0, b1;
   load_unit(u0, b0);
   load_unit(u0 + 1, b1);
-  wait_vm_q<2 * RT>();  // all but the second unit's loads: the image, h and the first unit (loads retire in order)
-  rt_lds_barrier();  // the table image and the tile table
+  wait_vm_q<2 * RW>();  // all but the second unit's loads: the image, h and the first unit (loads retire in order)
+  rt_lds_barrier();  // the table image, the tile table and the A terms
+  read_a();
   if (ntb > 1) {
     nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_td[1].row);
     nxt_nr = __builtin_amdgcn_readfirstlane(s_td[1].nr);
   }
   auto unit = [&](int u, Buf& b, int par) {
     const uint32_t rowc = unit_row(u);
-    q8v4 B[RT][4];
+    const uint32_t rowh = rowc + (uint32_t)hf * (16u * RW);
+    q8v4 B[RW][4];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) q8_decode8(tq, lk, b.q[rt], B[rt]);
-    float scl[RT];
+    for (int rt = 0; rt < RW; ++rt) q8_decode8(tq, lk, b.q[rt], B[rt]);
+    float scl[RW];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-      scl[rt] = scale_cvt(b.s[rt], a.sdt, (rowc + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
+    for (int rt = 0; rt < RW; ++rt)
+      scl[rt] = scale_cvt(b.s[rt], a.sdt, (rowh + (uint32_t)rt * 16u + j) * (uint32_t)a.Gi + grp);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(scl[rt]));  // converted before b.s is reloaded
+    for (int rt = 0; rt < RW; ++rt) asm volatile("" : "+v"(scl[rt]));  // converted before b.s is reloaded
     load_unit(u + 2, b);
     __builtin_amdgcn_sched_barrier(0);
     if (dec) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
+      for (int rt = 0; rt < RW; ++rt) {
         q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
         for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[rt][m], acc);
@@ -554,7 +565,7 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
           const int r = 2 * (int)g + h2;
           if (r < cur_nr) {
             const float d = h2 ? (float)acc[2] + (float)acc[3] * 0.0078125f : (float)acc[0] + (float)acc[1] * 0.0078125f;
-            red[par][wv][rt][r][j] = d * inv[h2] * scl[rt];
+            red[par][sl][hf * RW + rt][r][j] = d * inv[h2] * scl[rt];
           }
         }
       }
@@ -585,8 +596,10 @@ __global__ __launch_bounds__(512) void k_moeq_down_tiles(MTArgs a) {
       }
       ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
       const MTTile* td = s_td + (tic - tic0);
-      load_a(__builtin_amdgcn_readfirstlane(td->r[0]), __builtin_amdgcn_readfirstlane(td->r[1]),
-             __builtin_amdgcn_readfirstlane(td->r[2]), __builtin_amdgcn_readfirstlane(td->r[3]));
+      build_a(__builtin_amdgcn_readfirstlane(td->r[0]), __builtin_amdgcn_readfirstlane(td->r[1]),
+              __builtin_amdgcn_readfirstlane(td->r[2]), __builtin_amdgcn_readfirstlane(td->r[3]));
+      rt_lds_barrier();  // the segment's A terms
+      read_a();
     }
     unit(u, b0, 0);
     unit(u + 1, b1, 1);
@@ -755,7 +768,7 @@ static void mt_tail(const MTArgs& a, int x_dtype, int64_t T, int64_t H, int64_t 
     hipLaunchKernelGGL((k_moeq_gateup_tiles<true>), dim3(g1), dim3(1024), 0, s, a);
   else
     hipLaunchKernelGGL((k_moeq_gateup_tiles<false>), dim3(g1), dim3(1024), 0, s, a);
-  hipLaunchKernelGGL(k_moeq_down_tiles, dim3(g2), dim3(512), 0, s, a);
+  hipLaunchKernelGGL(k_moeq_down_tiles, dim3(g2), dim3(1024), 0, s, a);
   const int64_t n = T * H;
   hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.y, idx, w, (int)T, (int)k,
                      (int)num_experts, (int)H, a.tq_bad, out, out_dtype);
