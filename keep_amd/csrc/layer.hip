@@ -49,6 +49,7 @@ constexpr int FL_BLOCKS = 256;       // H / 16 down row tiles, one block per CU
 constexpr int FL_WAVES = 16;         // H / 256 gate/up K slices
 constexpr uint32_t FL_HDR_BYTES = 256;  // epoch, arrivals, status
 constexpr uint32_t FL_TIMEOUT = 1u;     // status bit: a wait gave up
+constexpr uint32_t FL_CERT = 2u;        // status bit: a certified early route differed from the exact one
 constexpr uint32_t FL_SPIN_TICKS_DEFAULT = 20000u;   // 200 us of the 100 MHz counter
 constexpr uint32_t FL_SPIN_TICKS_MAX = 100000000u;   // 1 s
 
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   constexpr int O_ASH = O_DSH + FL_WAVES * 16 * 256;    // x terms [slice][term][g * 4 + i]
   constexpr int O_GRED = O_ASH + 16 * 3 * 256;          // gate/up partials [wave][tile][row]
   constexpr int O_RED = O_GRED + 16 * NT * 16 * 4;      // down partials [row][wave]
-  constexpr int O_SMALL = O_RED + 16 * 16 * 4;         // s_inv4s[16], s_idx[8], s_w[8], s_hr[8]
+  constexpr int O_SMALL = O_RED + 16 * 16 * 4;         // s_inv4s[16], s_idx[8], s_w[8], s_hr[8], s_cert, s_chk
   constexpr int O_T8 = O_SMALL + 256;                   // RES: the residual image
   constexpr int LDS_BYTES = O_T8 + (RES ? FL_T8_BYTES : 0);
   __shared__ uint4 smem[LDS_BYTES / 16];
@@ -160,6 +161,8 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   int32_t* s_idx = (int32_t*)(lds + O_SMALL + 64);
   float* s_w = (float*)(lds + O_SMALL + 96);
   int32_t* s_hr = (int32_t*)(lds + O_SMALL + 128);  // RES: each route's residual row (-1 none, -2 invalid)
+  int32_t* s_cert = (int32_t*)(lds + O_SMALL + 160);  // the block's routing state (lds_flag)
+  int32_t* s_chk = (int32_t*)(lds + O_SMALL + 164);
   const char* t8i = lds + O_T8;
   const char* tq = (const char*)tqs;
   const int lane = threadIdx.x & 63;
@@ -170,40 +173,43 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   const uint32_t CI = (uint32_t)a.I >> 3;
   const uint32_t b = blockIdx.x;
 
-  // 0. the call's epoch; the router's inputs (wave 0); T and M for the image
-  //    (every thread builds four copies of one entry); the token slices this
-  //    wave builds terms for (wave w >= 2 slice w; waves 2 and 3 also slices
-  //    0 and 1), all from the preloaded arguments; then the table flag and the
-  //    slot map, which need the others
+  // 0. the call's epoch; the router's inputs (waves 0 and 1); T and M for the
+  //    image (every thread builds four copies of one entry); the token slices
+  //    this wave builds terms for (wave w >= 2 slice w; waves 2 and 3 also
+  //    slices 0 and 1), all from the preloaded arguments; then the table flag
+  //    and the slot map, which need the others
   const uint32_t ep_word = __hip_atomic_load(hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   float z[PER], bsv[PER], bdv[PER];
   int sm[PER];
-  if (wv == 0) rt_load<PER>(logits, bias_s, bias_d, E, lane, z, bsv, bdv);
+  if (wv < 2) rt_load<PER>(logits, bias_s, bias_d, E, lane, z, bsv, bdv);
   const uint32_t te = threadIdx.x >> 2;
   const uint2 tv = tqe[te], mv = tqe[256 + te];
   const uint4 xc = ldg16_q((const uint4*)xin + (wv < 2 ? 0 : wv) * 32 + (lane >> 1));
   const uint4 xc2 = ldg16_q((const uint4*)xin + (wv < 4 ? (wv & 1) : 0) * 32 + (lane >> 1));
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
-  if (wv == 0 && a.slot_map) rt_load_slots<PER>(a.slot_map, E, lane, sm);
-  int hv[PER];  // RES: the residual rows of pool rows lane + 64 i (wave 0)
+  if (wv < 2 && a.slot_map) rt_load_slots<PER>(a.slot_map, E, lane, sm);
+  int hv[PER];  // RES: the residual rows of pool rows lane + 64 i (waves 0 and 1)
   uint32_t t8w = 0u;
   if constexpr (RES) {
-    if (wv == 0) rt_load_slots<PER>(a.hot, a.S, lane, hv);
+    if (wv < 2) rt_load_slots<PER>(a.hot, a.S, lane, hv);
     t8w = a.t8[threadIdx.x >> 2];
   }
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t ep = __builtin_amdgcn_readfirstlane(ep_word);
   {
+    // the four threads of entry te write its sixteen copies; store k of thread
+    // (te, c) takes copy (4 c + te + k) & 15, so the sixteen lanes of an LDS
+    // pass (four entries x four threads) write sixteen different copies, each
+    // a distinct group of four banks
     const uint4 v = make_uint4(tv.x, tv.y, mv.x, mv.y);
-    uint4* row = tqs + te * 16 + (threadIdx.x & 3) * 4;
-    row[0] = v;
-    row[1] = v;
-    row[2] = v;
-    row[3] = v;
+    uint4* row = tqs + te * 16;
+    const uint32_t c0 = (threadIdx.x & 3) * 4 + te;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) row[(c0 + k) & 15u] = v;
     if constexpr (RES) *(uint2*)(lds + O_T8 + (threadIdx.x >> 2) * 32 + (threadIdx.x & 3) * 8) = t8_entry(t8w);
   }
-  // RES: the residual row of pool row `slot` (wave 0, every lane takes part): -1 none, -2 invalid
+  // RES: the residual row of pool row `slot` (a routing wave, every lane takes part): -1 none, -2 invalid
   auto hot_of = [&](int slot) -> int {
     const bool in = slot >= 0 && slot < a.S;
     const int ss = in ? slot : 0, owner = ss & 63, i0 = ss >> 6;
@@ -216,15 +222,31 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     return !in || v == -1 ? -1 : (v >= 0 && v < a.nhot ? v : -2);
   };
 
-  // 1. served routing (wave 0) | A terms: rows 0-2 of slice w are the three
-  //    int8 terms of x s, s the slice's power of two
+  // 1. routing. The selection order is "larger key, then lower index" over the
+  //    keys score + bias. Every score function is increasing in the logit, so
+  //    where each bias is 0 or at most RT_MASKED (no bias, or the residency
+  //    mask) the logits order the unmasked experts as the keys do and the bias
+  //    values order the masked ones, except where the score rounding makes two
+  //    keys equal whose logits differ. Wave 0 selects the routes of this
+  //    block's gate/up tiles (0 .. kneed - 1) on those logit keys, without the
+  //    score function, and the tiles' loads issue on them. For the softmax it
+  //    also certifies them: with every logit finite and each selected route's
+  //    logit at least 2^-16 above the next one's, within 60 of the largest
+  //    logit, the softmax keys are strictly ordered the same way (the
+  //    difference z - m rounds by at most 2^-17, the exponential then differs
+  //    by a factor above 1 + 2^-18 and the division keeps that order). Wave 1
+  //    forms the exact selection of all k routes meanwhile (the later routes,
+  //    the weights and the outputs); when wave 0 could not certify, every wave
+  //    waits for it before its first decode and reloads its tiles if an early
+  //    route differed. With other biases wave 0 selects on the exact keys.
+  //    A terms: rows 0-2 of slice w are the three int8 terms of x s, s the
+  //    slice's power of two (waves >= 2, meanwhile).
   float sc[PER];
   int e_sel = -1, sl = -1;
-  // the routes this block's gate/up tiles belong to: 0 .. kneed - 1 (the
-  // later selection rounds run while the codes are in flight)
   const int qlast = min((int)(b * QT + QT - 1), a.qtiles - 1);
   const int kneed = qlast < (int)(b * QT) ? 1 : min(a.k, qlast * 16 / a.I + 1);
   RtSel<PER> sel;
+  bool certify = false;  // wave 0: the softmax of finite logits under plain biases
   auto build = [&](uint4 c, int slice) {
     float v[4];
     if (a.xbf) q8_half4<true>(c, lane & 1, v);
@@ -239,113 +261,178 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     for (int n = 0; n < 3; ++n) aw[q8_aword((uint32_t)(slice * 3 + n), lane >> 1, lane & 1)] = tw[n];
     if (lane == 0) s_inv4s[slice] = inv4s;
   };
+  // the block's routing state in LDS, read wave-uniform: s_cert (wave 0) 1 the
+  // early routes are certified, 2 not; s_chk (wave 1) bit 1 every route is in
+  // s_idx / s_hr, bit 0 an early route differed from the exact one. Both are
+  // zeroed before the first barrier and set after it.
+  auto lds_flag = [&](int32_t* f) -> int {
+    return __builtin_amdgcn_readfirstlane(__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+  };
+  auto slot_of = [&](int e) -> int {
+    return a.slot_map ? rt_slot_of<PER>(sm, e, E, a.S) : (e >= 0 && e < E ? e : -1);
+  };
   if (wv == 0) {
-    rt_scores<PER>(z, E, a.func, lane, sc);
+    bool plain = true, finite = true;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      plain = plain && (bsv[i] == 0.f || bsv[i] <= RT_MASKED);
+      finite = finite && (lane + 64 * i >= E || fabsf(z[i]) < __builtin_inff());
+    }
     uint32_t kk[PER];
-    rt_keys<PER>(sc, bsv, E, lane, kk);
+    const bool proxy = __all(plain);
+    if (proxy) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) kk[i] = lane + 64 * i < E ? rt_sortable(bsv[i] != 0.f ? bsv[i] : z[i]) : 0u;
+    } else {
+      rt_scores<PER>(z, E, a.func, lane, sc);
+      rt_keys<PER>(sc, bsv, E, lane, kk);
+    }
     sel.init(kk, lane);
     sel.rounds(0, kneed, lane, 0);
-    e_sel = sel.mine;
-    sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, E, a.S) : (e_sel >= 0 && e_sel < E ? e_sel : -1);
+    sl = slot_of(sel.mine);
     if (lane < kneed) s_idx[lane] = sl;
     if constexpr (RES) {
       const int hr = hot_of(sl);
       if (lane < kneed) s_hr[lane] = hr;
     }
-  } else if (wv >= 2) {
+    certify = proxy && a.func == KEEP_SCORE_SOFTMAX && __all(finite);
+    if (lane == 0) *s_cert = 0;
+  } else if (wv == 1) {
+    rt_scores<PER>(z, E, a.func, lane, sc);
+    if (lane == 0) *s_chk = 0;
+  } else {
     build(xc, wv);
     if (wv < 4) build(xc2, wv - 2);
   }
-  rt_lds_barrier();  // this block's routes in s_idx, the image and every slice's A terms visible
+  rt_lds_barrier();  // the routes of the tiles' loads in s_idx, the image and every slice's A terms
 
   // 2. the gate/up loads of the block: scales and codes
   uint32_t rbase[QT];
-#pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const uint32_t qt = b * QT + u;
-    const bool valid = qt < (uint32_t)a.qtiles;
-    const uint32_t q0 = (valid ? qt : 0u) * 16u;
-    const uint32_t route = q0 / (uint32_t)a.I;
-    const int32_t e = s_idx[route];
-    const bool ok = valid && e >= 0 && e < a.S;
-    rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
-  }
   const uint32_t grp = G1 ? 0u : (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
-  // G1: the row scales of the reducing lanes (wave 0, lane 16 u + jj: row jj of q-tile u); else every
-  // wave's slice scales
-  ScaleRaw sr[NT];
-  if constexpr (G1) {
-    uint32_t rb = rbase[0];
-#pragma unroll
-    for (int u = 1; u < QT; ++u) rb = (lane >> 4) == (uint32_t)u ? rbase[u] : rb;
-    const uint32_t si = rb + j;
-    sr[0] = wv == 0 && lane < QT * 16 ? scale_raw(a.gs, a.sdt, si) : 0u;
-    sr[1] = wv == 0 && lane < QT * 16 ? scale_raw(a.us, a.sdt, si) : 0u;
-  } else {
-#pragma unroll
-    for (int u = 0; u < QT; ++u) {
-      const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
-      sr[2 * u] = scale_raw(a.gs, a.sdt, si);
-      sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
-    }
-  }
-  // the codes: every tile's 16 B per lane issued before any is needed
   const uint32_t kc0 = wv * 32 + g * 8;
+  ScaleRaw sr[NT];
   uint4 q[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-    q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + (size_t)(rbase[t >> 1] + j) * C + kc0);
-  // RES: each hot tile's residual codes (8 bytes per lane: codewords kc0 ..) and slice scales
   int hrt[QT];
   uint32_t rrow[QT];
   uint2 qr[NT];
   ScaleRaw srr[NT];
   const uint32_t rgrp = RES ? (uint32_t)(wv * 256) / (uint32_t)a.rgsz_h : 0u;
-  if constexpr (RES) {
+  auto issue = [&]() {
 #pragma unroll
     for (int u = 0; u < QT; ++u) {
       const uint32_t qt = b * QT + u;
       const bool valid = qt < (uint32_t)a.qtiles;
       const uint32_t q0 = (valid ? qt : 0u) * 16u;
       const uint32_t route = q0 / (uint32_t)a.I;
-      hrt[u] = valid ? s_hr[route] : -1;
-      rrow[u] = (hrt[u] >= 0 ? (uint32_t)hrt[u] * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
+      const int32_t e = s_idx[route];
+      const bool ok = valid && e >= 0 && e < a.S;
+      rbase[u] = (ok ? (uint32_t)e * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
     }
+    // G1: the row scales of the reducing lanes (wave 0, lane 16 u + jj: row jj of q-tile u); else every
+    // wave's slice scales
+    if constexpr (G1) {
+      uint32_t rb = rbase[0];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      if (hrt[t >> 1] >= 0) {  // block-uniform
-        qr[t] = ldg8_q(((t & 1) ? a.ruc : a.rgc) + (size_t)(rrow[t >> 1] + j) * C + kc0);
-        srr[t] = scale_raw((t & 1) ? a.rus : a.rgs, a.rsdt, (rrow[t >> 1] + j) * (uint32_t)a.rGh + rgrp);
-      } else {
-        qr[t] = make_uint2(0u, 0u);
-        srr[t] = 0u;
+      for (int u = 1; u < QT; ++u) rb = (lane >> 4) == (uint32_t)u ? rbase[u] : rb;
+      const uint32_t si = rb + j;
+      sr[0] = wv == 0 && lane < QT * 16 ? scale_raw(a.gs, a.sdt, si) : 0u;
+      sr[1] = wv == 0 && lane < QT * 16 ? scale_raw(a.us, a.sdt, si) : 0u;
+    } else {
+#pragma unroll
+      for (int u = 0; u < QT; ++u) {
+        const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
+        sr[2 * u] = scale_raw(a.gs, a.sdt, si);
+        sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
       }
     }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // the remaining routes (wave 0) while the codes are in flight: every wave
-  // waits for them here, ahead of the data it would otherwise wait for
-  if (kneed < a.k) {
-    if (wv == 0) {
-      sel.rounds(kneed, a.k, lane, 0);
-      e_sel = sel.mine;
-      sl = a.slot_map ? rt_slot_of<PER>(sm, e_sel, E, a.S) : (e_sel >= 0 && e_sel < E ? e_sel : -1);
-      if (lane >= kneed && lane < a.k) s_idx[lane] = sl;
-      if constexpr (RES) {
-        const int hr = hot_of(sl);
-        if (lane >= kneed && lane < a.k) s_hr[lane] = hr;
+    // the codes: every tile's 16 B per lane issued before any is needed
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      q[t] = ldg16_q(((t & 1) ? a.uc : a.gc) + (size_t)(rbase[t >> 1] + j) * C + kc0);
+    // RES: each hot tile's residual codes (8 bytes per lane: codewords kc0 ..) and slice scales
+    if constexpr (RES) {
+#pragma unroll
+      for (int u = 0; u < QT; ++u) {
+        const uint32_t qt = b * QT + u;
+        const bool valid = qt < (uint32_t)a.qtiles;
+        const uint32_t q0 = (valid ? qt : 0u) * 16u;
+        const uint32_t route = q0 / (uint32_t)a.I;
+        hrt[u] = valid ? s_hr[route] : -1;
+        rrow[u] = (hrt[u] >= 0 ? (uint32_t)hrt[u] * (uint32_t)a.I : 0u) + (q0 - route * (uint32_t)a.I);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (hrt[t >> 1] >= 0) {  // block-uniform
+          qr[t] = ldg8_q(((t & 1) ? a.ruc : a.rgc) + (size_t)(rrow[t >> 1] + j) * C + kc0);
+          srr[t] = scale_raw((t & 1) ? a.rus : a.rgs, a.rsdt, (rrow[t >> 1] + j) * (uint32_t)a.rGh + rgrp);
+        } else {
+          qr[t] = make_uint2(0u, 0u);
+          srr[t] = 0u;
+        }
       }
     }
-    rt_lds_barrier();
-  }
-  // the served weights and outputs (wave 0), while the codes are in flight
+  };
   if (wv == 0) {
+    // the certificate: lane j < kneed compares its winner with winner j + 1
+    // (a masked winner's key is its bias, <= RT_MASKED: no logit below it)
+    bool sure = false;
+    if (certify) {
+      sel.rounds(kneed, min(kneed + 1, E), lane, 0);
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int i = 0; i < PER; ++i) m = fmaxf(m, z[i]);
+      m = rt_wave_reduce(m, true);
+      const float zj = rt_unsortable(sel.mine_key);
+      const uint32_t kn = (uint32_t)__builtin_amdgcn_mov_dpp((int)sel.mine_key, 0x101, 0xF, 0xF, false);  // row_shl:1
+      const float zn = rt_unsortable(kn);
+      const bool next_masked = kn == 0u || zn <= RT_MASKED;
+      const bool ok = next_masked || (zj - zn >= 0x1p-16f && zn >= m - 60.f);
+      sure = __all(lane >= kneed || ok);
+    }
+    if (lane == 0) *s_cert = sure ? 1 : 2;
+  }
+  issue();
+  __builtin_amdgcn_sched_barrier(0);
+  if (wv == 1) {
+    // the exact selection of every route, its check against wave 0's, the
+    // residual rows, the served weights and outputs (a certified route equals
+    // the exact one, so rewriting it changes nothing)
+    uint32_t kk[PER];
+    rt_keys<PER>(sc, bsv, E, lane, kk);
+    sel.init(kk, lane);
+    sel.rounds(0, a.k, lane, 0);
+    e_sel = sel.mine;
+    sl = slot_of(e_sel);
+    const int early = lane < kneed ? s_idx[lane] : sl;
+    const bool differ = __any(early != sl);
+    if (lane < a.k) s_idx[lane] = sl;
+    if constexpr (RES) {
+      const int hr = hot_of(sl);
+      if (lane < a.k) s_hr[lane] = hr;
+    }
+    if (lane == 0) *s_chk = differ ? 3 : 2;  // bit 1: every route is in s_idx / s_hr; bit 0: an early one differed
     const RouteLane r = rt_finish<PER>(e_sel, true, sc, bsv, E, a.k, lane, 0, a.renorm, a.route_scale, a.tau);
     if (lane < a.k) s_w[lane] = r.valid ? r.value : 0.f;
     if (b == 0 && r.valid) {
       a.idx_out[lane] = sl;  // the pool row (the expert itself without a slot map)
       a.w_out[lane] = r.value;
+    }
+  }
+  {
+    // the early routes are certified, or wave 1 has checked them (rare)
+    int c = lds_flag(s_cert);
+    while (c == 0) {
+      __builtin_amdgcn_s_sleep(1);
+      c = lds_flag(s_cert);
+    }
+    int f = c == 1 ? 0 : lds_flag(s_chk);
+    while (c != 1 && !(f & 2)) {
+      __builtin_amdgcn_s_sleep(1);
+      f = lds_flag(s_chk);
+    }
+    if (f & 1) {  // block-uniform: an early route differed from the exact one
+      issue();
+      wait_vm_q<0>();  // every tile in before the decode, so the common path keeps exact wait counts
     }
   }
 
@@ -393,7 +480,8 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   // down's loads, once this wave's gate/up codes are in (requested together
   // they would share the memory system with gate/up, which gates the exchange)
   __builtin_amdgcn_sched_barrier(0);
-  // down: this wave's slice sd and routes rg * RPW + r'
+  // down: this wave's slice sd and routes rg * RPW + r' (every route written by wave 1 first)
+  while (!(lds_flag(s_chk) & 2)) __builtin_amdgcn_s_sleep(1);
   const bool dwave = wv < NSL * RG;  // wave-uniform
   const int sd = dwave ? wv % NSL : 0, rg = dwave ? wv / NSL : 0;
   uint32_t dbase[RPW];
@@ -611,7 +699,12 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   }
   rt_lds_barrier();
 
-  // 6. the sum of the waves' weighted partials, in wave order
+  // 6. the sum of the waves' weighted partials, in wave order (a certified
+  //    block whose exact routes differ would be a broken certificate: its
+  //    outputs are NaN and the status word records it; never expected)
+  const bool bad_cert = *s_cert == 1 && (*s_chk & 1);
+  if (bad_cert && threadIdx.x == 0)
+    __hip_atomic_fetch_or(hdr + 2, FL_CERT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (threadIdx.x < 16) {
     const float4* rp = (const float4*)(red + threadIdx.x * 16);
     float o = 0.f;
@@ -623,7 +716,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       o += v.z;
       o += v.w;
     }
-    if (tq_bad) o = __builtin_nanf("");
+    if (tq_bad || bad_cert) o = __builtin_nanf("");
     const size_t oi = b * 16u + threadIdx.x;
     if (a.odt == KEEP_F16) ((_Float16*)a.out)[oi] = (_Float16)o;
     else if (a.odt == KEEP_BF16) ((uint16_t*)a.out)[oi] = from_float<bf16s>(o).bits;

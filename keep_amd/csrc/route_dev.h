@@ -41,6 +41,11 @@ __device__ __forceinline__ uint32_t rt_sortable(float key) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// The float of a sortable key (rt_sortable's inverse for every non-NaN key).
+__device__ __forceinline__ float rt_unsortable(uint32_t s) {
+  return __uint_as_float((s & 0x80000000u) ? (s & 0x7fffffffu) : ~s);
+}
+
 // ---------------------------------------------------------------- wave reductions
 //
 // Inside each 16-lane row: quad_perm [1,0,3,2], quad_perm [2,3,0,1],
@@ -174,6 +179,7 @@ template <int PER>
 struct RtSel {
   uint32_t lo[PER], hi[PER];  // the sorted words as bit fields, popped with bitfield selects
   int mine;
+  uint32_t mine_key;  // the sortable key of this lane's winner (0: none)
 
   __device__ __forceinline__ void init(const uint32_t (&kk)[PER], int lane) {
     double d[PER];
@@ -195,6 +201,7 @@ struct RtSel {
       hi[i] = (uint32_t)(u >> 32);
     }
     mine = -1;
+    mine_key = 0u;
   }
 
   __device__ __forceinline__ void rounds(int j0, int j1, int lane, int slot0) {
@@ -210,6 +217,7 @@ struct RtSel {
       hi[PER - 1] &= ~pm;
       const int e = m ? (int)(0x3FFFFFFFu - (uint32_t)(m & 0x3FFFFFFFu)) : -1;
       mine = lane == slot0 + j ? e : mine;
+      mine_key = lane == slot0 + j ? (uint32_t)(m >> 30) : mine_key;
     }
   }
 };

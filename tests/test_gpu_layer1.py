@@ -139,6 +139,61 @@ def test_layer1_fewer_residents_than_k(dev):
     _check(out, _oracle(x, r, *pool))
 
 
+@pytest.mark.parametrize("place", [0, 5])
+def test_layer1_early_route_tie_reloads(dev, place):
+    """The tiles' loads issue on routes picked from the logits; they are used
+    unchecked only when each selected logit is at least 2^-16 above the next.
+    Here two logits differ by FLT_MIN (0 at expert 40, FLT_MIN at expert 300):
+    both softmax scores are exp(0) / sum exactly, so the exact selection takes
+    the lower index (40) and the logit order the higher (300). At place 0
+    every block's first route differs; at place 5 (the sixth route) only the
+    blocks holding tiles of route 5 do. Those blocks must reload their tiles:
+    the router outputs equal the standalone router's, the output the oracle's,
+    and no certified route differed (status 0)."""
+    E, I, k = 384, 2048, 6
+    pool = _pool(E, I, None, None, 51)
+    x = synth.rht_activations(1, 4096, seed=52, device=dev)
+    rng = np.random.default_rng(53)
+    z = -1.0 - rng.random(E).astype(np.float32)  # every other logit below -1
+    top = rng.choice([e for e in range(E) if e not in (40, 300)], size=place, replace=False)
+    z[top] = np.float32(3.0) - np.arange(place, dtype=np.float32) * np.float32(0.5)
+    z[40] = np.float32(0.0)
+    z[300] = np.finfo(np.float32).tiny
+    zt = torch.from_numpy(z.reshape(1, E)).to(dev)
+    ref = keep_amd.router_dual_topk(zt, k)
+    idx = ref.idx.cpu().numpy()[0]
+    assert idx[place] == 40 and (place + 1 >= k or idx[place + 1] == 300), \
+        "the exact selection breaks the score tie by index"
+    ws = _workspace(dev, k, I)
+    out, r = keep_amd.moe_layer(x, zt, *_pairs(pool), k=k, one_launch=True, workspace=ws)
+    for a, b in zip(r, ref):
+        assert torch.equal(a, b), "the one-launch router differs from the standalone router"
+    assert knn.layer_status(ws) == 0
+    _check(out, _oracle(x, r, *pool))
+    two, _ = keep_amd.moe_layer(x, zt, *_pairs(pool), k=k)
+    _check(out, two.double().cpu().numpy())
+
+
+def test_layer1_finite_biases(dev):
+    """Served biases that are neither 0 nor the residency mask (a score
+    correction bias beside it): the tile routes come from the exact keys, and
+    the outputs equal the standalone router's and the oracle's."""
+    E, I, k = 384, 2048, 6
+    pool = _pool(E, I, None, None, 61)
+    x = synth.rht_activations(1, 4096, seed=62, device=dev)
+    z = synth.router_logits(1, E, seed=63, device=dev)
+    corr = torch.from_numpy(np.random.default_rng(64).normal(0.0, 0.05, E).astype(np.float32)).to(dev)
+    mask = torch.from_numpy(synth.resident_mask(E, frac=0.5, seed=65)).to(dev)
+    for bias in (corr, keep_amd.resident_bias(mask, corr)):
+        ws = _workspace(dev, k, I)
+        out, r = keep_amd.moe_layer(x, z, *_pairs(pool), k=k, bias_served=bias, one_launch=True, workspace=ws)
+        ref = keep_amd.router_dual_topk(z, k, bias_served=bias)
+        for a, b in zip(r, ref):
+            assert torch.equal(a, b), "the one-launch router differs from the standalone router"
+        assert knn.layer_status(ws) == 0
+        _check(out, _oracle(x, r, *pool))
+
+
 def test_layer1_graph_replays_match_eager(dev):
     """Four layers captured in one graph on a side stream (the workspace of that
     stream); three replays with eager work between them, each equal to the
