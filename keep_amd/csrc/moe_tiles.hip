@@ -617,14 +617,30 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* y, const int32
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)T * H) return;
   const int t = (int)(i / H), n = (int)(i - (int64_t)t * H);
+  // every route's expert, weight and row value in flight together (the rows
+  // of y are always readable; an absent route's is simply not used): one
+  // memory round trip, then the sum in route order
+  constexpr int KC = 8;
   float o = 0.f;
   bool bad = false;
-  for (int r = 0; r < k; ++r) {
-    const int e = idx[t * k + r];
-    const float wt = w[t * k + r];
-    const bool ok = e >= 0 && e < E;
-    bad |= wt != 0.f && !ok;
-    if (ok && wt != 0.f) o = fmaf(wt, y[(int64_t)(t * k + r) * H + n], o);
+  for (int r0 = 0; r0 < k; r0 += KC) {
+    int e[KC];
+    float wt[KC], yv[KC];
+#pragma unroll
+    for (int r = 0; r < KC; ++r) {
+      const int rr = min(r0 + r, k - 1);
+      e[r] = idx[t * k + rr];
+      wt[r] = w[t * k + rr];
+      yv[r] = y[(int64_t)(t * k + rr) * H + n];
+    }
+#pragma unroll
+    for (int r = 0; r < KC; ++r) {
+      if (r0 + r < k) {
+        const bool ok = e[r] >= 0 && e[r] < E;
+        bad |= wt[r] != 0.f && !ok;
+        if (ok && wt[r] != 0.f) o = fmaf(wt[r], yv[r], o);
+      }
+    }
   }
   if (bad || *tq_bad) o = __builtin_nanf("");
   if (odt == KEEP_F16) ((_Float16*)out)[i] = (_Float16)o;
