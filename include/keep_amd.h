@@ -265,7 +265,11 @@ int keep_moe_layer_noalloc(const float* logits, const float* bias_served, const 
  * overlap on one workspace race). A wait on another block that outlasts
  * ~200 us gives up: the outputs of the blocks that waited are NaN and
  * keep_moe_layer1_status() reports bit 1 (zero the workspace before the next
- * call). Needs a device of at least 256 compute units. h is split into two
+ * call). Each block issues its gate/up loads on routes chosen from the logit
+ * order, certified equal to the exact selection or checked against it (and
+ * reloaded) before use; a certified route found different would make that
+ * block's outputs NaN and set status value 2 (never expected: a broken
+ * certificate). Needs a device of at least 256 compute units. h is split into two
  * int8 terms per 256-wide slice, as in keep_moe_layer. Serves H = 4096, I
  * in {512, 1024, 1536, 2048}, k <= 8, E <= 1024, scale groups of
  * 256-element multiples. Replaces the serving decode step of

@@ -692,7 +692,8 @@ def layer_workspace(device: torch.device, k: int, intermediate: int) -> torch.Te
 
 
 def layer_status(workspace: torch.Tensor) -> int:
-    """Status word of a one-launch layer workspace (bit 1: a wait gave up)."""
+    """Status word of a one-launch layer workspace (value 1: a wait gave up; value 2: a block's
+    certified early routes differed from the exact selection, never expected)."""
 
     out = (_lib.c_uint32 * 1)()
     _lib.call("keep_moe_layer1_status", workspace.data_ptr(), out, ops._stream(workspace.device))
