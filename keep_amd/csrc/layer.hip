@@ -580,13 +580,12 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   //    (lane & 1) of codeword lane / 2), waiting word by word for this call's tag
   if (dwave) {
     // down's B operands do not depend on h: decode them while h is awaited
-    // (with four routes per wave they would not fit in the registers)
-    constexpr bool PRE = RPW <= 3;
+    // (with four routes per wave all four would not fit in the registers:
+    // the first two then, the other two once h is in)
+    constexpr int NPRE = RPW <= 3 ? RPW : 2;
     q8v4 BD[RPW][4];
-    if constexpr (PRE) {
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) q8_decode8(tq, lk, qd[r], BD[r]);
-    }
+    for (int r = 0; r < NPRE; ++r) q8_decode8(tq, lk, qd[r], BD[r]);
     // every pass issues all of the wave's loads before it waits (a route
     // past k reads route 0's words and ignores them)
     const uint64_t* hp[RPW];
@@ -658,7 +657,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     float c = 0.f;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      if constexpr (!PRE) q8_decode8(tq, lk, qd[r], BD[r]);
+      if (r >= NPRE) q8_decode8(tq, lk, qd[r], BD[r]);
       q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc = mfma_i8(AD[i], BD[r][i], acc);
