@@ -379,11 +379,14 @@ int keep_moe_tiles(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, 
 
 /* The few-token layer from the router logits: keep_router_dual_topk's outputs
  * (idx, w, want, want_score, admit; same contract, k <= 16) and
- * keep_moe_tiles' result, byte for byte. For T <= 32 the router, the
- * activation terms and the route plan run as ONE launch (one block routes
- * every token, one wave each, and plans from the routes it holds in LDS,
- * while the other blocks build the tokens' terms), so the layer is four
- * launches; larger T runs the router and then keep_moe_tiles. With slot_map
+ * keep_moe_tiles' result, byte for byte. Up to T k = 128 routes and 512
+ * experts the gate/up launch routes and plans itself (every block routes
+ * every token, one wave each, plans in LDS, and forms the x terms of the
+ * tiles it takes; block 0 writes the router outputs and the plan), so the
+ * layer is three launches. Otherwise, for T <= 32, the router, the
+ * activation terms and the route plan run as one prologue launch before
+ * them (four launches); larger T runs the router and then keep_moe_tiles.
+ * With slot_map
  * the pools hold num_slots rows (the plan's buckets). `workspace` holds
  * keep_moe_tiles_workspace_bytes(T, k, pool rows, H) bytes. Replaces the
  * speculative-verify decode step of scripts/v41_build/omlx_lattice.py:327-371

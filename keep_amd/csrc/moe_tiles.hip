@@ -27,6 +27,14 @@
 //  5. k_moe_combine: out[t] = sum over the token's routes, in route order,
 //     of w * y (a zero weight contributes nothing; an out-of-range expert
 //     with a nonzero weight gives NaN), as the one-token layer combines.
+//
+// From the router logits (keep_moe_tiles_layer) with at most 128 routes and
+// 512 experts, launches 1 and 2 and the router fold into launch 3: every
+// gate/up block routes every token and plans the routes in LDS (block 0 also
+// writes the router's outputs and the plan for launches 4 and 5), and each
+// wave forms its K slice's x terms for the tile it enters. Up to 32 tokens
+// otherwise, one prologue launch routes, plans and builds the terms; beyond,
+// the router runs on its own launch.
 #include "common.h"
 #include "moe_dev.h"
 #include "plan_dev.h"
@@ -155,6 +163,91 @@ __global__ __launch_bounds__(1024) void k_mt_prologue(MTPro p) {
 
 // ------------------------------------------------------------------ gate/up
 
+// ------------------------------------------------------------------ routed gate/up (few routes)
+
+// The routing inputs and outputs of a layer whose gate/up kernel routes its
+// tokens itself (k_moeq_gateup_tiles with RPER > 0, up to PLAN_SMALL_R
+// routes): every block finds every token's served routes and plans them in
+// LDS. A token's served routes alone are found by rt_served_winners (no
+// scores or weights where the logits certify the order); block t < T routes
+// token t as k_router does and writes its router outputs, block 0 writes the
+// plan's order and tiles and the last block its per-expert counts and
+// offsets, for the down kernel and the combine.
+struct MTRoute {
+  const void* x;  // [T, H] fp16 / bf16
+  const float* logits;
+  const float *bias_s, *bias_d;
+  int func, renorm;
+  float route_scale, tau;
+  const int32_t* slot_map;
+  int T, E;  // tokens, router experts (the plan's buckets are the pool rows, MTArgs::E)
+  int32_t* idx;
+  float* w;
+  int32_t* want;
+  float* want_score;
+  uint8_t* admit;
+  int32_t *order, *inverse, *counts, *offsets, *te, *to, *tc, *nt;
+  int max_tiles;
+};
+
+// The routed kernel's LDS: the served slots, the block's copy of the plan,
+// and per wave the three x terms of its K slice for the current tile's four
+// routes (the A-term layout of the workspace's x terms) with their 1 / (4 s).
+// The unrouted kernel holds a one-entry stand-in.
+template <bool ON>
+struct MTRouteLds {
+  static constexpr int R = ON ? PLAN_SMALL_R : 1;
+  static constexpr int W = ON ? 16 : 1;
+  int32_t sr[R], sb[R], order[R], te[R], to[R], tc[R];
+  int32_t ntot[2];
+  uint4 xl[W][MT_TILE][ON ? 48 : 1];
+  float xinv[W][MT_TILE];
+};
+
+// Every wave takes tokens wv, wv + 16, ... (the served routes alone, but
+// token t fully, with its router outputs, in block t); then wave 0 plans the
+// block's copy (plan_small_to, with the workspace's parts as above). Every
+// thread of the block calls it.
+template <int PER, typename RLds>
+__device__ __forceinline__ void mt_route_and_plan(const MTArgs& a, const MTRoute& p, RLds& RL) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int t = wv; t < p.T; t += 16) {
+    const bool first = t == (int)blockIdx.x;
+    float z[PER], bs[PER], bd[PER];
+    rt_load<PER>(p.logits + (int64_t)t * p.E, p.bias_s, p.bias_d, p.E, lane, z, bs, bd);
+    int sm[PER];
+    if (p.slot_map) rt_load_slots<PER>(p.slot_map, p.E, lane, sm);
+    int e = -1;  // lane j < k: served route j's expert
+    RouteLane r{};
+    if (first) {
+      r = rt_route<PER>(z, bs, bd, p.E, a.k, p.func, p.renorm, p.route_scale, p.tau, p.bias_d == p.bias_s, lane);
+      e = r.valid ? r.expert : -1;
+    } else {
+      e = rt_served_winners<PER>(z, bs, p.E, a.k, p.func, lane);
+    }
+    int slot = e >= 0 && e < p.E ? e : -1;
+    if (p.slot_map) slot = rt_slot_of<PER>(sm, slot, p.E, a.E);
+    if (lane < a.k) RL.sr[t * a.k + lane] = slot;
+    if (first && r.valid) {
+      const int64_t o = (int64_t)t * a.k + (lane < 32 ? lane : lane - 32);
+      if (lane < 32) {
+        p.idx[o] = slot;
+        p.w[o] = r.value;
+      } else {
+        if (p.want) p.want[o] = r.expert;
+        if (p.want_score) p.want_score[o] = r.value;
+        if (p.admit) p.admit[o] = r.admit;
+      }
+    }
+  }
+  rt_lds_barrier();  // the routes in LDS (the router outputs are for later launches: not waited for)
+  const bool b0 = blockIdx.x == 0, bl = blockIdx.x == gridDim.x - 1;
+  const PlanSmallOut o{b0 ? p.order : nullptr, b0 ? p.inverse : nullptr, bl ? p.counts : nullptr,
+                       bl ? p.offsets : nullptr, b0 ? p.te : nullptr, b0 ? p.to : nullptr,
+                       b0 ? p.tc : nullptr, b0 ? p.nt : nullptr, p.max_tiles, RL.order, RL.te, RL.to, RL.tc};
+  plan_small_to([&](int r) { return RL.sr[r]; }, p.T * a.k, a.E, MT_TILE, o, RL.sb, RL.ntot);
+}
+
 // The two persistent kernels share one schedule. Tiles hold at most
 // MT_TILE routes, so every unit of every tile is one pass over its codes and
 // costs about the same: an even split of the units balances the blocks (an
@@ -200,13 +293,15 @@ __device__ __forceinline__ int mt_route_of_lanes(int rr, uint32_t i) {
 // routes: A row 4i + t is term t of route i's token (t < 3; row 4i + 3 is
 // zero), so D rows 4i .. 4i + 2 of column j, in lane 16 i + j, are route i's
 // three partial dots with weight row j.
-template <bool XBF>
-__global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
+template <bool XBF, int RPER>
+__global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a, MTRoute p) {
   constexpr int SEG = 128;  // units per segment (h staging capacity)
+  constexpr bool ROUTE = RPER > 0;
   __shared__ uint4 tqs[TQR_BYTES / 16];
   __shared__ float gred[2][16][2][MT_TILE][16];  // [parity][wave][gate, up][route][row]
   __shared__ uint16_t hst[MT_TILE][SEG * 16];    // the segment's h rows
   __shared__ MTTile s_td[MT_TPB];                // the block's tiles
+  __shared__ MTRouteLds<ROUTE> RL;
   const char* tq = (const char*)tqs;
   const uint32_t tq_bad = ((const __attribute__((address_space(4))) uint32_t*)a.tq_bad)[0];
   const Q8Keys lk = q8_keys(threadIdx.x & 63);
@@ -216,12 +311,19 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
   const bool dec = wv < a.S;  // this wave owns a K slice
   const int sl = dec ? wv : 0;
   const int rg_n = a.I >> 4;  // units per tile (>= 16)
-  const int nt = __builtin_amdgcn_readfirstlane(*a.ntiles);
+  int nt_ = 0;
+  if constexpr (!ROUTE) nt_ = __builtin_amdgcn_readfirstlane(*a.ntiles);
+  // routed: the image DMA after the routing (a DMA in flight makes every wait of the routing wait for it)
+  if constexpr (ROUTE) {
+    mt_route_and_plan<RPER>(a, p, RL);
+    nt_ = __builtin_amdgcn_readfirstlane(RL.ntot[1]);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
+  const int nt = nt_;
   const int U = nt * rg_n;
   const int per = ((U + (int)gridDim.x - 1) / (int)gridDim.x + 1) & ~1;  // even: see the unit loop
   const int u0 = (int)blockIdx.x * per, u1 = min(U, u0 + per);
-#pragma unroll
-  for (int u = 0; u < 4; ++u) dma16_q(a.tq + (wv * 4 + u) * 64 + lane, tqs + (wv * 4 + u) * 64);
   if (u0 >= u1) {
     wait_vm_q<0>();
     return;
@@ -239,24 +341,29 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
   // the first tile (every wave) and the next tile's row; wave 0, lane l < ntb: tile tic0 + l for the table
   int zv = 0;
   asm volatile("" : "+v"(zv));  // a lane value: these loads go through the vector unit
-  const int te0 = a.te[tic0 + zv], te1 = a.te[min(tic0 + 1, nt - 1) + zv];
-  const int off0 = a.to[tic0 + zv], nr0 = a.tc[tic0 + zv];
+  // the plan's descriptors and sorted routes: the workspace's, or the block's own copy in LDS
+  const int32_t* pte = ROUTE ? RL.te : a.te;
+  const int32_t* pto = ROUTE ? RL.to : a.to;
+  const int32_t* ptc = ROUTE ? RL.tc : a.tc;
+  const int32_t* pord = ROUTE ? RL.order : a.order;
+  const int te0 = pte[tic0 + zv], te1 = pte[min(tic0 + 1, nt - 1) + zv];
+  const int off0 = pto[tic0 + zv], nr0 = ptc[tic0 + zv];
   const bool tl = wv == 0 && lane < ntb;
   int tte = 0, tto = 0, ttc = 1;
   if (tl) {
-    tte = a.te[tic0 + lane];
-    tto = a.to[tic0 + lane];
-    ttc = a.tc[tic0 + lane];
+    tte = pte[tic0 + lane];
+    tto = pto[tic0 + lane];
+    ttc = ptc[tic0 + lane];
   }
   // the current and the next tile: first row and route count in scalar registers, routes from the table
   uint32_t cur_row = (uint32_t)__builtin_amdgcn_readfirstlane(te0) * (uint32_t)a.I;
   uint32_t nxt_row = (uint32_t)__builtin_amdgcn_readfirstlane(te1) * (uint32_t)a.I;
   int cur_nr = __builtin_amdgcn_readfirstlane(nr0), nxt_nr = cur_nr;
-  const int rr = a.order[__builtin_amdgcn_readfirstlane(off0) + min((int)(lane & 3u), cur_nr - 1)];
+  const int rr = pord[__builtin_amdgcn_readfirstlane(off0) + min((int)(lane & 3u), cur_nr - 1)];
   int tr[MT_TILE] = {0, 0, 0, 0};
   if (tl) {
 #pragma unroll
-    for (int i = 0; i < MT_TILE; ++i) tr[i] = a.order[tto + min(i, ttc - 1)];
+    for (int i = 0; i < MT_TILE; ++i) tr[i] = pord[tto + min(i, ttc - 1)];
   }
   // the first row of unit u (past the block's end: its last unit); u is at most two units past the
   // segment, so in tile tic or tic + 1
@@ -288,6 +395,43 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
     for (int m = 0; m < 4; ++m) araw[m] = ldg16_q(asrc + m);
     inv = a.xinv[(size_t)tok_d * a.S + sl];
   };
+  // routed: the wave forms the terms of its K slice itself, for the tile's four routes (routes past its
+  // count repeat the last one), from its x chunks (issue_x), into its LDS rows; then A and 1 / (4 s)
+  // read back from them as issue_a reads the workspace's
+  uint4 xc[MT_TILE];
+  auto issue_x = [&](int r0, int r1, int r2, int r3) {
+    const int rt[MT_TILE] = {r0, r1, r2, r3};
+#pragma unroll
+    for (int i = 0; i < MT_TILE; ++i)
+      xc[i] = ldg16_q((const uint4*)p.x + ((size_t)(rt[i] / a.k) * (uint32_t)a.H >> 3) + sl * 32 + (lane >> 1));
+  };
+  auto build_x = [&]() {
+    if constexpr (ROUTE) {
+#pragma unroll
+      for (int i = 0; i < MT_TILE; ++i) {
+        float v[4];
+        q8_half4<XBF>(xc[i], lane & 1, v);
+        const float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        float sc, inv4s;
+        q8_scale(rt_wave_reduce(mx, true), sc, inv4s);
+        uint32_t tw[3];
+        q8_terms<3>(v, sc, tw);
+        uint32_t* base = (uint32_t*)RL.xl[wv][i];
+#pragma unroll
+        for (int n = 0; n < 3; ++n) base[q8_aword((uint32_t)n, lane >> 1, lane & 1)] = tw[n];
+        if (lane == 0) RL.xinv[wv][i] = inv4s;
+      }
+      // the wave reads what its other lanes wrote: one wave's LDS operations run in order, and the
+      // compiler must not move the reads above the writes
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("" ::: "memory");
+      const uint4* asrc = RL.xl[wv][j >> 2] + min(j & 3u, 2u) * 16 + g * 4;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) araw[m] = asrc[m];
+      inv = RL.xinv[wv][g];
+    }
+  };
   auto build_a = [&]() {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -300,18 +444,31 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
     const int rows = (ue - us) * 16;
     const uint32_t row0 = (uint32_t)(us - tic * rg_n) * 16u;
     const MTTile* td = s_td + (tic - tic0);
-    for (int x = threadIdx.x; x < cur_nr * rows; x += 1024) {
+    int x0 = threadIdx.x;
+    if constexpr (ROUTE) asm volatile("" : "+v"(x0));  // the staging address rebuilt here (held, it is spilled)
+    for (int x = x0; x < cur_nr * rows; x += 1024) {
       const int i = x / rows, r = x - i * rows;
       a.h[(size_t)td->r[i] * a.I + row0 + (uint32_t)r] = hst[i][r];
     }
   };
   // the first units' codes after the block's small loads (issued before the route and A loads, they
   // measured no faster)
-  issue_a(mt_route_of_lanes(rr, j >> 2), mt_route_of_lanes(rr, g));
   Buf b0, b1;
-  load_unit(u0, b0);
-  load_unit(u0 + 1, b1);
-  wait_vm_q<4>();  // all but the second unit's four loads: the image, A and the first unit (loads retire in order)
+  if constexpr (ROUTE) {
+    // the codes first (they need only the tile's row), then the x chunks of its routes; the compiler waits
+    // for every load before the terms are formed (the image DMA in flight makes it count them all)
+    load_unit(u0, b0);
+    load_unit(u0 + 1, b1);
+    issue_x(__builtin_amdgcn_readfirstlane(mt_route_of_lanes(rr, 0)), __builtin_amdgcn_readfirstlane(mt_route_of_lanes(rr, 1)),
+            __builtin_amdgcn_readfirstlane(mt_route_of_lanes(rr, 2)), __builtin_amdgcn_readfirstlane(mt_route_of_lanes(rr, 3)));
+    wait_vm_q<0>();
+    build_x();
+  } else {
+    issue_a(mt_route_of_lanes(rr, j >> 2), mt_route_of_lanes(rr, g));
+    load_unit(u0, b0);
+    load_unit(u0 + 1, b1);
+    wait_vm_q<4>();  // all but the second unit's four loads: the image, A and the first unit (loads retire in order)
+  }
   build_a();
   rt_lds_barrier();  // the table image and the tile table
   if (ntb > 1) {
@@ -376,9 +533,17 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a) {
       }
       ue = min(min(u1, (tic + 1) * rg_n), us + SEG);
       const MTTile* td = s_td + (tic - tic0);
-      issue_a(td->r[j >> 2], td->r[g]);
-      build_a();
-      wait_vm_q<0>();  // nothing of the switch stays in flight: the units' waits count their own loads
+      if constexpr (ROUTE) {
+        issue_x(__builtin_amdgcn_readfirstlane(td->r[0]), __builtin_amdgcn_readfirstlane(td->r[1]),
+                __builtin_amdgcn_readfirstlane(td->r[2]), __builtin_amdgcn_readfirstlane(td->r[3]));
+        wait_vm_q<0>();  // nothing of the switch stays in flight: the units' waits count their own loads
+        build_x();
+        build_a();
+      } else {
+        issue_a(td->r[j >> 2], td->r[g]);
+        build_a();
+        wait_vm_q<0>();  // nothing of the switch stays in flight: the units' waits count their own loads
+      }
     }
     unit(u, b0, 0);
     unit(u + 1, b1, 1);
@@ -773,17 +938,33 @@ static MTArgs mt_args(int64_t H, int64_t I, int64_t k, int64_t num_experts, cons
   return a;
 }
 
-// gate/up, down and the combine, once the x terms and the plan are in the workspace.
+// The gate/up launch: unrouted (rp null: x terms and plan in the workspace) or routing its tokens itself
+// with `per` (<= 8) logits per router lane.
+template <bool XBF>
+static void mt_launch_gateup(const MTArgs& a, const MTRoute* rp, int per, unsigned g1, hipStream_t s) {
+  if (!rp) {
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<XBF, 0>), dim3(g1), dim3(1024), 0, s, a, MTRoute{});
+  } else if (per <= 2) {
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<XBF, 2>), dim3(g1), dim3(1024), 0, s, a, *rp);
+  } else if (per <= 4) {
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<XBF, 4>), dim3(g1), dim3(1024), 0, s, a, *rp);
+  } else if (per <= 6) {
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<XBF, 6>), dim3(g1), dim3(1024), 0, s, a, *rp);
+  } else {
+    hipLaunchKernelGGL((k_moeq_gateup_tiles<XBF, 8>), dim3(g1), dim3(1024), 0, s, a, *rp);
+  }
+}
+
+// gate/up, down and the combine, once the x terms and the plan are in the workspace (rp null), or with
+// the gate/up kernel routing and planning (rp: its routing arguments, per: logits per router lane).
 static void mt_tail(const MTArgs& a, int x_dtype, int64_t T, int64_t H, int64_t I, int64_t k, int64_t num_experts,
                     const int32_t* idx, const float* w, const MTWorkspace& L, void* out, int out_dtype,
-                    hipStream_t s) {
+                    hipStream_t s, const MTRoute* rp = nullptr, int per = 0) {
   const int64_t tiles_ub = mt_tiles_ub(T, k, num_experts);
   const unsigned g1 = (unsigned)mt_grid(tiles_ub, I / 16);
   const unsigned g2 = (unsigned)mt_grid(tiles_ub, H / 64);
-  if (x_dtype == KEEP_BF16)
-    hipLaunchKernelGGL((k_moeq_gateup_tiles<true>), dim3(g1), dim3(1024), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_moeq_gateup_tiles<false>), dim3(g1), dim3(1024), 0, s, a);
+  if (x_dtype == KEEP_BF16) mt_launch_gateup<true>(a, rp, per, g1, s);
+  else mt_launch_gateup<false>(a, rp, per, g1, s);
   hipLaunchKernelGGL(k_moeq_down_tiles, dim3(g2), dim3(1024), 0, s, a);
   const int64_t n = T * H;
   hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.y, idx, w, (int)T, (int)k,
@@ -867,6 +1048,22 @@ extern "C" int keep_moe_tiles_layer(const float* logits, const float* bias_serve
   const MTWorkspace L = mt_layout(T, k, S, H);
   const MTArgs a = mt_args(H, I, k, S, gate_codes, gate_scales, up_codes, up_scales, down_codes, down_scales,
                            scale_dtype, group_size_h, group_size_i, prepared, swiglu_limit, h_work, ws, L);
+  const int per = (int)((num_experts + 63) / 64);
+  // up to 128 routes and 512 experts the gate/up kernel routes and plans in every block (no prologue launch;
+  // a router lane holding 16 logits would spill inside it); every block of it routes a token fully
+  if (T * k <= PLAN_SMALL_R && per <= 8 && T <= mt_grid(mt_tiles_ub(T, k, S), I / 16)) {
+    MTRoute rp{};
+    rp.x = x; rp.logits = logits; rp.bias_s = bias_served; rp.bias_d = bias_demand; rp.func = score_func;
+    rp.renorm = renormalize; rp.route_scale = route_scale; rp.tau = tau; rp.slot_map = slot_map;
+    rp.T = (int)T; rp.E = (int)num_experts;
+    rp.idx = idx; rp.w = w; rp.want = want; rp.want_score = want_score; rp.admit = admit;
+    rp.order = (int32_t*)(ws + L.order); rp.inverse = (int32_t*)(ws + L.inverse);
+    rp.counts = (int32_t*)(ws + L.counts); rp.offsets = (int32_t*)(ws + L.offsets); rp.te = (int32_t*)(ws + L.te);
+    rp.to = (int32_t*)(ws + L.to); rp.tc = (int32_t*)(ws + L.tc); rp.nt = (int32_t*)(ws + L.nt);
+    rp.max_tiles = (int)L.max_tiles;
+    mt_tail(a, x_dtype, T, H, I, k, S, idx, w, L, out, out_dtype, s, &rp, per);
+    return launch_status("keep_moe_tiles_layer");
+  }
   MTPro p{};
   p.x = x; p.H = (int)H; p.xt = (uint4*)(ws + L.xt); p.xinv = (float*)(ws + L.xinv);
   p.logits = logits; p.bias_s = bias_served; p.bias_d = bias_demand; p.func = score_func; p.renorm = renormalize;
@@ -876,7 +1073,6 @@ extern "C" int keep_moe_tiles_layer(const float* logits, const float* bias_serve
   p.order = (int32_t*)(ws + L.order); p.inverse = (int32_t*)(ws + L.inverse); p.counts = (int32_t*)(ws + L.counts);
   p.offsets = (int32_t*)(ws + L.offsets); p.te = (int32_t*)(ws + L.te); p.to = (int32_t*)(ws + L.to);
   p.tc = (int32_t*)(ws + L.tc); p.nt = (int32_t*)(ws + L.nt); p.max_tiles = (int)L.max_tiles;
-  const int per = (int)((num_experts + 63) / 64);
   const dim3 grid((unsigned)(T + 1)), blk(1024);
 #define MT_PRO(P)                                                                        \
   do {                                                                                   \

@@ -191,6 +191,15 @@ __device__ __forceinline__ void plan_block(Route route, int R, int E, int tile, 
 
 constexpr int PLAN_SMALL_R = 128;  // routes plan_small takes: two per lane of one wave
 
+// Where plan_small_to writes. Every global pointer may be null (not written);
+// l_order / l_te / l_to / l_tc, when not null, receive LDS copies of order and
+// of the tile descriptors (at most R tiles).
+struct PlanSmallOut {
+  int32_t *order, *inverse, *counts, *offsets, *te, *to, *tc, *n_tiles;
+  int max_tiles;
+  int32_t *l_order, *l_te, *l_to, *l_tc;
+};
+
 // plan_block's outputs for R <= PLAN_SMALL_R, with one block barrier. Wave 0
 // holds routes lane and lane + 64 and ranks each against all of them with
 // ballots over the bucket bits (most significant first: a lane below on a
@@ -200,13 +209,13 @@ constexpr int PLAN_SMALL_R = 128;  // routes plan_small takes: two per lane of o
 // leaders), and writes each run's tiles at the exclusive scan of the tile
 // counts over the sorted positions. After the barrier every thread writes the
 // counts and offsets of its experts (two binary searches of the sorted
-// buckets) and zero-fills the descriptors past the last tile.
+// buckets) and zero-fills the descriptors past the last tile. The barrier
+// orders LDS only. sb: R ints of
+// LDS scratch; ntot: two ints of LDS, [0] the tiles written, [1] the valid
+// ones (n_tiles), both readable by every thread on return.
 template <typename Route>
-__device__ __forceinline__ void plan_small(Route route, int R, int E, int tile, int32_t* order, int32_t* inverse,
-                                           int32_t* counts, int32_t* offsets, int32_t* te, int32_t* to, int32_t* tc,
-                                           int max_tiles, int32_t* n_tiles_out, PlanLds& L) {
-  int* sb = L.cnt;         // the buckets in sorted order (R <= 128 <= PLAN_MAX_E + 1 entries)
-  int* ntot = L.wtot[0];   // [0]: the number of tiles
+__device__ __forceinline__ void plan_small_to(Route route, int R, int E, int tile, const PlanSmallOut& o, int* sb,
+                                              int* ntot) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   if (wv == 0) {
     const bool v0 = lane < R, v1 = lane + 64 < R;
@@ -223,29 +232,36 @@ __device__ __forceinline__ void plan_small(Route route, int R, int E, int tile, 
     const uint64_t in0 = __ballot(v0), in1 = __ballot(v1);
     uint64_t eq00 = in0, eq01 = in1, eq10 = in0, eq11 = in1;  // eqAB: routes of half B equal so far to my A key
     uint64_t lt00 = 0, lt01 = 0, lt10 = 0, lt11 = 0;          // ... and below it
+    const bool two = R > 64;  // the second half holds routes (else its masks stay 0: skipped)
     for (int b = nbits - 1; b >= 0; --b) {
-      const uint64_t m0 = __ballot((k0 >> b) & 1), m1 = __ballot((k1 >> b) & 1);
-      const uint64_t s0 = ((k0 >> b) & 1) ? ~0ull : 0ull, s1 = ((k1 >> b) & 1) ? ~0ull : 0ull;
+      const uint64_t m0 = __ballot((k0 >> b) & 1);
+      const uint64_t s0 = ((k0 >> b) & 1) ? ~0ull : 0ull;
       lt00 |= eq00 & ~m0 & s0;
-      lt01 |= eq01 & ~m1 & s0;
-      lt10 |= eq10 & ~m0 & s1;
-      lt11 |= eq11 & ~m1 & s1;
       eq00 &= ~(m0 ^ s0);
-      eq01 &= ~(m1 ^ s0);
-      eq10 &= ~(m0 ^ s1);
-      eq11 &= ~(m1 ^ s1);
+      if (two) {
+        const uint64_t m1 = __ballot((k1 >> b) & 1);
+        const uint64_t s1 = ((k1 >> b) & 1) ? ~0ull : 0ull;
+        lt01 |= eq01 & ~m1 & s0;
+        lt10 |= eq10 & ~m0 & s1;
+        lt11 |= eq11 & ~m1 & s1;
+        eq01 &= ~(m1 ^ s0);
+        eq10 &= ~(m0 ^ s1);
+        eq11 &= ~(m1 ^ s1);
+      }
     }
     const uint64_t below = (1ull << lane) - 1ull;
     const int p0 = __popcll(lt00) + __popcll(lt01) + __popcll(eq00 & below);
     const int p1 = __popcll(lt10) + __popcll(lt11) + __popcll(eq10) + __popcll(eq11 & below);
     if (v0) {
-      order[p0] = lane;
-      inverse[lane] = p0;
+      if (o.order) o.order[p0] = lane;
+      if (o.l_order) o.l_order[p0] = lane;
+      if (o.inverse) o.inverse[lane] = p0;
       sb[p0] = k0;
     }
     if (v1) {
-      order[p1] = lane + 64;
-      inverse[lane + 64] = p1;
+      if (o.order) o.order[p1] = lane + 64;
+      if (o.l_order) o.l_order[p1] = lane + 64;
+      if (o.inverse) o.inverse[lane + 64] = p1;
       sb[p1] = k1;
     }
     // the sorted view: lane q holds positions q and q + 64
@@ -276,47 +292,70 @@ __device__ __forceinline__ void plan_small(Route route, int R, int E, int tile, 
     }
     const int tot0 = __shfl(x0, 63, 64), total = tot0 + __shfl(x1, 63, 64);
     const int tb0 = x0 - n0, tb1 = tot0 + x1 - n1;
-    for (int i = 0; i < n0; ++i) {
-      te[tb0 + i] = b0 < E ? b0 : -1;
-      to[tb0 + i] = lane + i * tile;
-      tc[tb0 + i] = min(tile, c0 - i * tile);
-    }
-    for (int i = 0; i < n1; ++i) {
-      te[tb1 + i] = b1 < E ? b1 : -1;
-      to[tb1 + i] = lane + 64 + i * tile;
-      tc[tb1 + i] = min(tile, c1 - i * tile);
-    }
+    auto put = [&](int ti, int e, int off, int cnt) {
+      if (o.te) {
+        o.te[ti] = e;
+        o.to[ti] = off;
+        o.tc[ti] = cnt;
+      }
+      if (o.l_te) {
+        o.l_te[ti] = e;
+        o.l_to[ti] = off;
+        o.l_tc[ti] = cnt;
+      }
+    };
+    for (int i = 0; i < n0; ++i) put(tb0 + i, b0 < E ? b0 : -1, lane + i * tile, min(tile, c0 - i * tile));
+    for (int i = 0; i < n1; ++i) put(tb1 + i, b1 < E ? b1 : -1, lane + 64 + i * tile, min(tile, c1 - i * tile));
     // the invalid routes' run sorts last: its tiles are not counted
     const uint64_t bad0 = __ballot(l0 && b0 == E), bad1 = __ballot(l1 && b1 == E);
     const int nbad = bad1 ? __shfl(n1, __builtin_ctzll(bad1), 64) : bad0 ? __shfl(n0, __builtin_ctzll(bad0), 64) : 0;
     if (lane == 0) {
-      n_tiles_out[0] = total - nbad;
+      if (o.n_tiles) o.n_tiles[0] = total - nbad;
       ntot[0] = total;
+      ntot[1] = total - nbad;
     }
   }
-  __syncthreads();
+  // LDS only: the global writes are for later launches, so no wave waits here for their completion
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
   const int total = ntot[0];
-  for (int e = tid; e < E; e += PLAN_THREADS) {
-    int lo = 0, hi = R;  // the first sorted position with bucket >= e
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (sb[mid] < e) lo = mid + 1;
-      else hi = mid;
+  if (o.counts) {
+    for (int e = tid; e < E; e += PLAN_THREADS) {
+      int lo = 0, hi = R;  // the first sorted position with bucket >= e
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sb[mid] < e) lo = mid + 1;
+        else hi = mid;
+      }
+      int lo2 = lo, hi2 = R;  // ... and > e
+      while (lo2 < hi2) {
+        const int mid = (lo2 + hi2) >> 1;
+        if (sb[mid] <= e) lo2 = mid + 1;
+        else hi2 = mid;
+      }
+      o.offsets[e] = lo;
+      o.counts[e] = lo2 - lo;
     }
-    int lo2 = lo, hi2 = R;  // ... and > e
-    while (lo2 < hi2) {
-      const int mid = (lo2 + hi2) >> 1;
-      if (sb[mid] <= e) lo2 = mid + 1;
-      else hi2 = mid;
+  }
+  if (o.te) {
+    for (int ti = total + tid; ti < o.max_tiles; ti += PLAN_THREADS) {
+      o.te[ti] = 0;
+      o.to[ti] = 0;
+      o.tc[ti] = 0;
     }
-    offsets[e] = lo;
-    counts[e] = lo2 - lo;
   }
-  for (int ti = total + tid; ti < max_tiles; ti += PLAN_THREADS) {
-    te[ti] = 0;
-    to[ti] = 0;
-    tc[ti] = 0;
-  }
+}
+
+// plan_small_to with every output in global memory and PlanLds as scratch.
+template <typename Route>
+__device__ __forceinline__ void plan_small(Route route, int R, int E, int tile, int32_t* order, int32_t* inverse,
+                                           int32_t* counts, int32_t* offsets, int32_t* te, int32_t* to, int32_t* tc,
+                                           int max_tiles, int32_t* n_tiles_out, PlanLds& L) {
+  const PlanSmallOut o{order, inverse, counts, offsets, te, to, tc, n_tiles_out, max_tiles,
+                       nullptr, nullptr, nullptr, nullptr};
+  plan_small_to(route, R, E, tile, o, L.cnt, L.wtot[0]);
 }
 
 }  // namespace keep

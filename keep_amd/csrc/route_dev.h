@@ -335,6 +335,51 @@ __device__ __forceinline__ RouteLane rt_route(const float (&z)[PER], const float
   return lane < 32 ? rs : rd;
 }
 
+// The served winners alone (lane j < k: the expert of served route j, -1 for
+// none; other lanes -1), equal to rt_route's served lanes. The selection
+// order is "larger score + bias, then lower index"; every score function is
+// increasing in the logit, so where each bias is 0 or at most RT_MASKED (no
+// bias, or the residency mask) the logits order the unmasked experts as the
+// keys do and the bias values order the masked ones (score + bias rounds to
+// the bias there), except where score rounding makes two keys equal whose
+// logits differ. For the softmax of finite logits the winners are found on
+// those logit keys and certified: each winner's logit at least 2^-16 above
+// the next winner's, that one within 60 of the largest logit (the difference
+// z - m rounds by at most 2^-17, the exponential then differs by a factor above
+// 1 + 2^-18 and the division keeps the order), or the next winner masked.
+// Otherwise, or when the certificate fails, the winners come from the exact
+// keys as rt_route forms them.
+template <int PER>
+__device__ __forceinline__ int rt_served_winners(const float (&z)[PER], const float (&bs)[PER], int E, int k,
+                                                 int func, int lane) {
+  bool plain = true;
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    plain = plain && (bs[i] == 0.f || bs[i] <= RT_MASKED) && (lane + 64 * i >= E || fabsf(z[i]) < __builtin_inff());
+  if (func == KEEP_SCORE_SOFTMAX && __all(plain)) {
+    uint32_t kk[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) kk[i] = lane + 64 * i < E ? rt_sortable(bs[i] != 0.f ? bs[i] : z[i]) : 0u;
+    RtSel<PER> sel;
+    sel.init(kk, lane);
+    sel.rounds(0, min(k + 1, E), lane, 0);
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < PER; ++i) m = fmaxf(m, z[i]);
+    m = rt_wave_reduce(m, true);
+    const uint32_t kn = (uint32_t)__shfl_down((int)sel.mine_key, 1, 64);  // winner j + 1's key (0: none)
+    const float zj = rt_unsortable(sel.mine_key), zn = rt_unsortable(kn);
+    const bool next_masked = kn == 0u || zn <= RT_MASKED;
+    const bool ok = next_masked || (zj - zn >= 0x1p-16f && zn >= m - 60.f);
+    if (__all(lane >= k || ok)) return lane < k ? sel.mine : -1;
+  }
+  float s[PER];
+  rt_scores<PER>(z, E, func, lane, s);
+  uint32_t kk[PER];
+  rt_keys<PER>(s, bs, E, lane, kk);
+  return rt_topk<PER>(kk, k, lane, 0);
+}
+
 // Loads the lane's logits and biases (missing bias pointers read as 0).
 template <int PER>
 __device__ __forceinline__ void rt_load(const float* lrow, const float* bias_s, const float* bias_d, int E, int lane,

@@ -604,8 +604,10 @@ def moe_tiles_layer(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k:
                     h_work: torch.Tensor | None = None):
     """A few tokens' whole MoE layer from the router logits (``keep_moe_tiles_layer``):
     ``router_dual_topk``'s outputs and ``moe_decode``'s result on the tiles path, byte
-    for byte, with the router, the activation terms and the route plan in one launch
-    for up to 32 tokens. ``x [T, H]`` (fp16/bf16), ``logits [T, E]``; ``slot_map`` as
+    for byte: up to 128 routes (``T * k``) over at most 512 experts the gate/up launch
+    routes and plans itself (three launches), otherwise the router, the activation
+    terms and the route plan run in one launch before it for up to 32 tokens.
+    ``x [T, H]`` (fp16/bf16), ``logits [T, E]``; ``slot_map`` as
     in ``moe_layer``. Returns ``(out [T, H], RouterOutput)``; float32 by default."""
 
     device = x.device

@@ -3,7 +3,8 @@ identity with the one-token layer token by token (the verify-rows discipline
 of the reference, tests/test_gather_vqmm_verify_rows.py:1-33), the C oracle at
 the verify shapes of config 3, the float64 oracle with many routes per expert
 (several tiles and route chunks per expert), the combine's edge cases, and the
-layer from the logits (keep_moe_tiles_layer: router, terms and plan in one
+layer from the logits (keep_moe_tiles_layer: the gate/up launch routing and
+planning itself up to 128 routes, or router, terms and plan in one prologue
 launch up to 32 tokens) byte-identical to the router followed by the tiles."""
 
 import numpy as np
@@ -167,12 +168,15 @@ def small_pool(dev):
 
 
 @pytest.mark.parametrize("T, E, xdt, biased", [(2, 384, torch.float16, False), (8, 384, torch.float16, False),
-                                              (16, 100, torch.bfloat16, True), (32, 1000, torch.float16, True),
-                                              (33, 384, torch.float16, False), (64, 300, torch.bfloat16, True),
-                                              (65, 384, torch.float16, False)])
+                                              (16, 100, torch.bfloat16, True), (20, 384, torch.bfloat16, False),
+                                              (21, 500, torch.float16, True), (22, 384, torch.float16, False),
+                                              (32, 1000, torch.float16, True), (33, 384, torch.float16, False),
+                                              (64, 300, torch.bfloat16, True), (65, 384, torch.float16, False)])
 def test_tiles_layer_equals_router_then_tiles(dev, small_pool, T, E, xdt, biased):
-    """keep_moe_tiles_layer: the router's five outputs and the tiles' result, bit for bit, on both sides of
-    the fused-prologue limit (32 tokens), every router lane width, with and without biases and admission."""
+    """keep_moe_tiles_layer: the router's five outputs and the tiles' result, bit for bit, on every side of
+    its launch forms: routed gate/up (up to 128 routes and 512 experts; 20 and 21 tokens put two tokens on
+    some routing waves), the prologue (22 and 32 tokens), the router launch (33 and more); every router
+    lane width, with and without biases and admission."""
     from keep_amd.router import resident_bias
     H, I, k = 1024, 512, 6
     pool = tuple((p.codes[:E], p.scales[:E]) for p in small_pool)
@@ -216,3 +220,68 @@ def test_tiles_layer_slot_map_and_module(dev, small_pool):
                                top_k=k, bias_served=bias, slot_map=sm)
     out_m, r_m = moe(x, z)
     assert torch.equal(r_m.idx, r.idx) and torch.equal(out_m, want)
+
+
+@pytest.mark.parametrize("T", [8, 16])
+def test_tiles_layer_config3_shape(dev, pool, T):
+    """Config 3's shape (384 experts, 4096 / 2048, top-6) from the logits, routed gate/up: every K slice
+    forms its own terms, blocks cross tiles; bit for bit with the router followed by keep_moe_tiles."""
+    E, H, I, k = 384, 4096, 2048, 6
+    x = synth.rht_activations(T, H, seed=80 + T, device=dev)
+    z = synth.router_logits(T, E, seed=81 + T, device=dev)
+    z[3] = z[2]  # two tokens on the same experts: tiles of two routes
+    r = keep_amd.router_dual_topk(z, k)
+    want = keep_amd.moe_decode(x, r.idx, r.weight, *_pairs(pool))
+    out, r2 = keep_amd.moe_tiles_layer(x, z, *_pairs(pool), k=k)
+    assert torch.equal(r2.idx, r.idx) and torch.equal(r2.weight, r.weight)
+    assert torch.equal(out, want)
+
+
+def test_tiles_layer_absent_experts(dev, small_pool):
+    """A slot map without the residency bias: some selected experts have no pool row (slot -1), their
+    routes sort last and are not computed, and their tokens' outputs are NaN, exactly as the router
+    followed by keep_moe_tiles gives them (routed gate/up, 400 experts over 200 rows)."""
+    E, S, H, I, k, T = 400, 200, 1024, 512, 6, 12
+    pool = tuple((p.codes[:S], p.scales[:S]) for p in small_pool)
+    rng = np.random.default_rng(90)
+    sm_np = np.full(E, -1, dtype=np.int32)
+    sm_np[rng.choice(E, S, replace=False)] = np.arange(S, dtype=np.int32)
+    sm = torch.from_numpy(sm_np).to(dev)
+    x = synth.rht_activations(T, H, seed=91, device=dev)
+    z = synth.router_logits(T, E, seed=92, device=dev)
+    r = keep_amd.router_dual_topk(z, k, slot_map=sm, num_slots=S)
+    assert (r.idx < 0).any() and (r.idx >= 0).any()
+    want = keep_amd.moe_decode(x, r.idx, r.weight, *pool)
+    out, r2 = keep_amd.moe_tiles_layer(x, z, *pool, k=k, slot_map=sm)
+    assert torch.equal(r2.idx, r.idx) and torch.equal(r2.weight, r.weight)
+    nan = torch.isnan(want)
+    assert nan.any() and torch.equal(torch.isnan(out), nan)
+    assert torch.equal(out[~nan], want[~nan])
+
+
+def test_tiles_layer_near_ties_fall_back_to_exact_keys(dev, small_pool):
+    """Routed gate/up: its blocks select on the logits where the softmax certifies that order. Tokens whose
+    logits differ by one ulp with equal softmax scores (the larger logit on the higher index, so the logit
+    order and the score order disagree), at the first route, at the last route against the first left out,
+    and twice among the routes: the layer still equals the router followed by keep_moe_tiles bit for bit."""
+    E, H, I, k, T = 384, 1024, 512, 6, 8
+    pool = tuple((p.codes[:E], p.scales[:E]) for p in small_pool)
+    x = synth.rht_activations(T, H, seed=95, device=dev)
+    z = synth.router_logits(T, E, seed=96, device=dev) - 8.0
+    up1 = lambda v: float(np.nextafter(np.float32(v), np.float32(np.inf)))  # noqa: E731
+    z[0, 40], z[0, 300] = 0.0, float(np.finfo(np.float32).tiny)       # the first route
+    for j, e in enumerate((10, 11, 12, 13, 14)):                       # routes 0-4, then the sixth
+        z[1, e] = 5.0 - j
+    z[1, 100], z[1, 200] = 0.5, up1(0.5)
+    z[2, 9] = 5.0                                                      # two pairs among the routes
+    z[2, 7], z[2, 300] = 0.25, up1(0.25)
+    z[2, 8], z[2, 301] = 0.125, up1(0.125)
+    z[3, 40], z[3, 41] = 3.0, 3.0                                      # an exact tie
+    r = keep_amd.router_dual_topk(z, k)
+    # the cases bite: the score order puts the lower index first where the logit order would not
+    assert r.idx[0, 0].item() == 40 and r.idx[1, 5].item() == 100
+    assert r.idx[2, 1].item() == 7 and r.idx[2, 3].item() == 8
+    want = keep_amd.moe_decode(x, r.idx, r.weight, *pool)
+    out, r2 = keep_amd.moe_tiles_layer(x, z, *pool, k=k)
+    assert torch.equal(r2.idx, r.idx) and torch.equal(r2.weight, r.weight)
+    assert torch.equal(out, want)
