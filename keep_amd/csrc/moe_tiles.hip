@@ -669,6 +669,10 @@ __global__ __launch_bounds__(1024) void k_moeq_down_tiles(MTArgs a) {
   };
   auto read_a = [&]() {  // after the barrier that follows build_a
     if (dec) {
+      // the LDS addresses are rebuilt here, not kept across the unit loop: held, one is spilled, and its
+      // reload from scratch waits for every code load in flight
+      uint32_t g = lane >> 4;
+      asm volatile("" : "+v"(g));
       const q8v4* as = (const q8v4*)ash[sl] + (j & (2 * MT_TILE - 1)) * 16 + g * 4;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
