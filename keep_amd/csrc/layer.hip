@@ -131,7 +131,10 @@ __device__ __forceinline__ uint32_t fl_pos(uint32_t d) { return (d & 1u) * 4u + 
 // lane, NSL = I / 256 down K slices, RPW routes per down wave (RG = 16 / NSL
 // route groups of RPW routes: the waves w < NSL * RG own slice w % NSL and
 // route group w / NSL). G1: per-row gate and up scales (one scale group per
-// row), applied once to each row's sum instead of to every slice's partial.
+// row), applied once to each row's sum instead of to every slice's partial;
+// with RES the residual's gate and up scales are per row as well, and each
+// wave keeps its residual partials apart (in its own slice of the x-term
+// LDS, free once the wave holds its A operands) for the same fold.
 //
 // LDS is one array with the decode image at address 0, so a lookup address
 // is exactly the byte permute of q8_decode2 (no base to add).
@@ -142,7 +145,6 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   constexpr int QT = NT / 2;
   constexpr int RG = FL_WAVES / NSL;
   static_assert(RPW * 4 <= 16, "at most four routes per down wave (A rows 4 r + t)");
-  static_assert(!(RES && G1), "the nested tier scales every slice's partials (no per-row fold)");
   constexpr int O_DSH = TQR_BYTES;                      // down terms [wave][row 4 r + t][g * 4 + i]
   constexpr int O_ASH = O_DSH + FL_WAVES * 16 * 256;    // x terms [slice][term][g * 4 + i]
   constexpr int O_GRED = O_ASH + 16 * 3 * 256;          // gate/up partials [wave][tile][row]
@@ -156,6 +158,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
   uint4* dsh = (uint4*)(lds + O_DSH);
   uint4* ash = (uint4*)(lds + O_ASH);
   float* gred = (float*)(lds + O_GRED);
+  float* gres = (float*)(lds + O_ASH);  // RES and G1: wave w's residual partials [tile][row] at float w * 192 (its x-term slice)
   float* red = (float*)(lds + O_RED);
   float* s_inv4s = (float*)(lds + O_SMALL);
   int32_t* s_idx = (int32_t*)(lds + O_SMALL + 64);
@@ -364,11 +367,24 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       for (int t = 0; t < NT; ++t) {
         if (hrt[t >> 1] >= 0) {  // block-uniform
           qr[t] = ldg8_q(((t & 1) ? a.ruc : a.rgc) + (size_t)(rrow[t >> 1] + j) * C + kc0);
-          srr[t] = scale_raw((t & 1) ? a.rus : a.rgs, a.rsdt, (rrow[t >> 1] + j) * (uint32_t)a.rGh + rgrp);
+          if constexpr (!G1)
+            srr[t] = scale_raw((t & 1) ? a.rus : a.rgs, a.rsdt, (rrow[t >> 1] + j) * (uint32_t)a.rGh + rgrp);
         } else {
           qr[t] = make_uint2(0u, 0u);
-          srr[t] = 0u;
+          if constexpr (!G1) srr[t] = 0u;
         }
+      }
+      if constexpr (G1) {  // the residual row scales of the reducing lanes (as sr)
+        uint32_t rr = rrow[0];
+        int hu = hrt[0];
+#pragma unroll
+        for (int u = 1; u < QT; ++u) {
+          rr = (lane >> 4) == (uint32_t)u ? rrow[u] : rr;
+          hu = (lane >> 4) == (uint32_t)u ? hrt[u] : hu;
+        }
+        const bool ld = wv == 0 && lane < QT * 16 && hu >= 0;
+        srr[0] = ld ? scale_raw(a.rgs, a.rsdt, rr + j) : 0u;
+        srr[1] = ld ? scale_raw(a.rus, a.rsdt, rr + j) : 0u;
       }
     }
   };
@@ -455,7 +471,7 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
     q8v4 acc = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc = mfma_i8(A[i], B[i], acc);
-    float vres = 0.f;  // RES: the residual's scaled partial
+    float vres = 0.f;  // RES: the residual's scaled partial (G1: its unscaled partial, kept apart)
     if constexpr (RES) {
       if (hrt[t >> 1] >= 0) {  // block-uniform
         q8v4 R[4];
@@ -464,7 +480,11 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
 #pragma unroll
         for (int i = 0; i < 4; ++i) accr = mfma_i8(A[i], R[i], accr);
         const float dr = ((float)accr[0] + (float)accr[1] * 0.0078125f) + (float)accr[2] * 0.00006103515625f;
-        vres = dr * inv4s * scale_cvt(srr[t], a.rsdt, (rrow[t >> 1] + j) * (uint32_t)a.rGh + rgrp);
+        if constexpr (G1) {
+          if (lane < 16) gres[wv * 192 + t * 16 + (int)j] = dr * inv4s;
+        } else {
+          vres = dr * inv4s * scale_cvt(srr[t], a.rsdt, (rrow[t >> 1] + j) * (uint32_t)a.rGh + rgrp);
+        }
       }
     }
     if (lane < 16) {
@@ -549,6 +569,24 @@ __global__ __launch_bounds__(1024) void k_moe_layer1(const float* logits, const 
       for (int v = 1; v < QT; ++v) rb = u == (uint32_t)v ? rbase[v] : rb;
       gsum *= scale_cvt(sr[0], a.sdt, rb + jj);
       usum *= scale_cvt(sr[1], a.sdt, rb + jj);
+      if constexpr (RES) {
+        uint32_t rr = rrow[0];
+        int hu = hrt[0];
+#pragma unroll
+        for (int v = 1; v < QT; ++v) {
+          rr = u == (uint32_t)v ? rrow[v] : rr;
+          hu = u == (uint32_t)v ? hrt[v] : hu;
+        }
+        if (hu >= 0) {
+          float gr = 0.f, ur = 0.f;
+          for (int w = 0; w < 16; ++w) {
+            gr += gres[w * 192 + (int)(2 * u) * 16 + (int)jj];
+            ur += gres[w * 192 + (int)(2 * u + 1) * 16 + (int)jj];
+          }
+          gsum += gr * scale_cvt(srr[0], a.rsdt, rr + jj);
+          usum += ur * scale_cvt(srr[1], a.rsdt, rr + jj);
+        }
+      }
     }
     float hv = silu_mul(gsum, usum, a.limit);
     if (tq_bad || e < 0 || e >= a.S) hv = __builtin_nanf("");
@@ -815,15 +853,20 @@ void fl_launch(const float* logits, const float* bias_s, const float* bias_d, in
   a.spin_ticks = spin_ticks;
   a.out = out; a.odt = odt;
   a.xbf = x_dtype == KEEP_BF16;
-  if (nest) {  // every slice's partials scaled in place (no per-row fold)
+  if (nest) {  // per-row fold when base and residual scales are both per row, else every slice scaled in place
     a.hot = nest->hot; a.nhot = nest->nhot;
     a.rgc = nest->gc; a.ruc = nest->uc; a.rdc = nest->dc;
     a.rgs = nest->gs; a.rus = nest->us; a.rds = nest->ds; a.rsdt = nest->sdt;
     a.rGh = (int32_t)(4096 / nest->group_h); a.rgsz_h = (int32_t)nest->group_h;
     a.rGi = (int32_t)(I / nest->group_i); a.rgsz_i = (int32_t)nest->group_i;
     a.t8 = nest->t8;
-    if (E <= 384) fl_dispatch<6, false, true>(h, a, s);
-    else fl_dispatch<16, false, true>(h, a, s);
+    if (group_h == 4096 && nest->group_h == 4096) {  // per-row base and residual scales: the fold
+      if (E <= 384) fl_dispatch<6, true, true>(h, a, s);
+      else fl_dispatch<16, true, true>(h, a, s);
+    } else {
+      if (E <= 384) fl_dispatch<6, false, true>(h, a, s);
+      else fl_dispatch<16, false, true>(h, a, s);
+    }
     return;
   }
   const bool g1 = group_h == 4096;
