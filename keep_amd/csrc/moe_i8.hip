@@ -213,12 +213,28 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(const float* logits,
     }
   }
   const uint32_t grp = (uint32_t)(wv * 256) / (uint32_t)a.gsz_h;
-  ScaleRaw sr[NT];
+  // per-row gate and up scales (g1): a tile's slice partials are summed unscaled and the row scale
+  // applied once to the sum (a hot tile of the tier excepted: its residual has scales of its own), so
+  // only the reducing lanes (wave 0, lane 16 u + jj: row jj of q-tile u) load scale words
+  const bool g1 = a.gsz_h == 4096;
+  ScaleRaw sr[NT], srow[2] = {0u, 0u};
 #pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
-    sr[2 * u] = scale_raw(a.gs, a.sdt, si);
-    sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
+  for (int t = 0; t < NT; ++t) sr[t] = 0u;
+  if (!g1 || RES) {
+#pragma unroll
+    for (int u = 0; u < QT; ++u) {
+      const uint32_t si = (rbase[u] + j) * (uint32_t)a.Gh + grp;
+      sr[2 * u] = scale_raw(a.gs, a.sdt, si);
+      sr[2 * u + 1] = scale_raw(a.us, a.sdt, si);
+    }
+  }
+  if (g1) {
+    uint32_t rb = rbase[0];
+#pragma unroll
+    for (int u = 1; u < QT; ++u) rb = (lane >> 4) == (uint32_t)u ? rbase[u] : rb;
+    const bool ld = wv == 0 && lane < QT * 16;
+    srow[0] = ld ? scale_raw(a.gs, a.sdt, rb + j) : 0u;
+    srow[1] = ld ? scale_raw(a.us, a.sdt, rb + j) : 0u;
   }
   constexpr int PD = NT;  // tiles whose codes are loaded before the first decode
   const uint32_t kc0 = wv * 32 + g * 8;
@@ -303,9 +319,10 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(const float* logits,
       }
     }
     const uint32_t si = (rbase[t >> 1] + j) * (uint32_t)a.Gh + grp;
+    const bool fold = g1 && !(RES && hot_t[t >> 1]);  // block-uniform
     if (lane < 16) {
       const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
-      gred[(wv * NT + t) * 16 + j] = d * inv4s * scale_cvt(sr[t], a.sdt, si) + vr;
+      gred[(wv * NT + t) * 16 + j] = fold ? d * inv4s : d * inv4s * scale_cvt(sr[t], a.sdt, si) + vr;
     }
   }
   rt_lds_barrier();
@@ -316,6 +333,18 @@ __global__ __launch_bounds__(1024) void k_moeq_route_gateup(const float* logits,
     for (int w = 0; w < 16; ++w) {
       gsum += gred[(w * NT + 2 * u) * 16 + jj];
       usum += gred[(w * NT + 2 * u + 1) * 16 + jj];
+    }
+    bool hot_u = false;
+    if constexpr (RES) {
+#pragma unroll
+      for (int v = 0; v < QT; ++v) hot_u = u == (uint32_t)v ? hot_t[v] : hot_u;
+    }
+    if (g1 && !hot_u) {
+      uint32_t rb = rbase[0];
+#pragma unroll
+      for (int v = 1; v < QT; ++v) rb = u == (uint32_t)v ? rbase[v] : rb;
+      gsum *= scale_cvt(srow[0], a.sdt, rb + jj);
+      usum *= scale_cvt(srow[1], a.sdt, rb + jj);
     }
     if (qt < (uint32_t)a.qtiles) {
       const uint32_t q0 = qt * 16u;

@@ -372,13 +372,18 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a, MTRoute p)
     const bool n = uu >= (tic + 1) * rg_n;
     return (n ? nxt_row : cur_row) + (uint32_t)(uu - (n ? tic + 1 : tic) * rg_n) * 16u;
   };
-  // a unit's codes and its rows' scale words (the aligned word holding each)
+  // a unit's codes and its rows' scale words (the aligned word holding each). Per-row scales (g1): a
+  // row's slice partials are summed unscaled and its scale applied once to the sum by the SwiGLU lanes
+  // (wave 0's, which hold those rows' words), so the other waves load none
+  const bool g1 = a.gsz_h == a.H;
+  const bool ld_scale = !g1 || wv == 0;  // wave-uniform
   auto load_unit = [&](int u, Buf& b) {
     const uint32_t row = unit_row(u) + j;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       b.q[t] = ldg16_q((t ? a.uc : a.gc) + (size_t)row * C + kc0);
-      b.s[t] = ldg4_q((const char*)(t ? a.us : a.gs) + ((row * (uint32_t)a.Gh + grp) * sbytes & ~3u));
+      if (ld_scale) b.s[t] = ldg4_q((const char*)(t ? a.us : a.gs) + ((row * (uint32_t)a.Gh + grp) * sbytes & ~3u));
+      else b.s[t] = 0u;
     }
   };
   if (tl) s_td[lane] = MTTile{(uint32_t)tte * (uint32_t)a.I, ttc, {tr[0], tr[1], tr[2], tr[3]}};
@@ -494,7 +499,7 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a, MTRoute p)
 #pragma unroll
         for (int m = 0; m < 4; ++m) acc = mfma_i8(A[m], B[t][m], acc);
         const float d = ((float)acc[0] + (float)acc[1] * 0.0078125f) + (float)acc[2] * 0.00006103515625f;
-        if ((int)g < cur_nr) gred[par][wv][t][g][j] = d * inv * scl[t];
+        if ((int)g < cur_nr) gred[par][wv][t][g][j] = g1 ? d * inv : d * inv * scl[t];
       }
     }
     rt_lds_barrier();
@@ -509,6 +514,10 @@ __global__ __launch_bounds__(1024) void k_moeq_gateup_tiles(MTArgs a, MTRoute p)
       for (int w = 0; w < a.S; ++w) {
         gsum += gred[par][w][0][i][jj];
         usum += gred[par][w][1][i][jj];
+      }
+      if (g1) {  // this lane's own words: row jj of the unit
+        gsum *= scl[0];
+        usum *= scl[1];
       }
       float hv = silu_mul(gsum, usum, a.limit);
       if (tq_bad) hv = __builtin_nanf("");
