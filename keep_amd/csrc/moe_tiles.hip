@@ -30,11 +30,12 @@
 //
 // From the router logits (keep_moe_tiles_layer) with at most 128 routes and
 // 512 experts, launches 1 and 2 and the router fold into launch 3: every
-// gate/up block routes every token and plans the routes in LDS (block 0 also
-// writes the router's outputs and the plan for launches 4 and 5), and each
-// wave forms its K slice's x terms for the tile it enters. Up to 32 tokens
-// otherwise, one prologue launch routes, plans and builds the terms; beyond,
-// the router runs on its own launch.
+// gate/up block finds every token's served routes and plans them in LDS
+// (block t also writes token t's router outputs; blocks 0 and the last one
+// write the plan for launches 4 and 5), and each wave forms its K slice's x
+// terms for the tile it enters. Up to 32 tokens otherwise, one prologue
+// launch routes, plans and builds the terms; beyond, the router runs on its
+// own launch.
 #include "common.h"
 #include "moe_dev.h"
 #include "plan_dev.h"
